@@ -1,0 +1,58 @@
+"""ctypes binding of libhilda_spec.so (the C ABI declared in include/hilda_spec.h).
+
+The library is built in-tree by build_lib.py. There is no fallback: if the
+library is missing or a call fails, a RuntimeError is raised.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libhilda_spec.so"
+
+HS_OK = 0
+HS_F32, HS_BF16, HS_FP8_E4M3 = 0, 1, 2
+HS_ACCEPT_REFERENCE, HS_ACCEPT_FILTERED, HS_ACCEPT_GREEDY = 0, 1, 2
+
+_vp = ctypes.c_void_p
+_i32 = ctypes.c_int
+_i64 = ctypes.c_int64
+_sz = ctypes.c_size_t
+_f32 = ctypes.c_float
+
+# name -> (restype, argtypes); every symbol declared in include/hilda_spec.h
+SIGNATURES: dict[str, tuple] = {
+    "hs_status_string": (ctypes.c_char_p, [_i32]),
+    "hs_version": (_i32, []),
+    "hs_spec_accept_workspace_size": (_sz, [_i32, _i32, _i32]),
+    "hs_spec_accept": (_i32, [_vp, _i32, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp,
+                              _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "hs_sampler_workspace_size": (_sz, [_i32, _i32]),
+    "hs_sampler": (_i32, [_vp, _i32, _i64, _i32, _i32, _vp, _vp, _vp, _i32, _vp, _i64, _i32,
+                          _vp, _vp, _vp, _vp, _sz, _vp]),
+}
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Loads the HIP library (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH.name} is not built; run `python hilda-vllm_amd/build_lib.py` "
+                "(or __graft_entry__.build())")
+        L = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(status: int, what: str) -> None:
+    if status != HS_OK:
+        msg = lib().hs_status_string(status).decode()
+        raise RuntimeError(f"{what} failed: {msg} (status {status})")

@@ -1,0 +1,188 @@
+"""torch-facing wrappers of the C ABI (device memory and streams come from torch).
+
+Each wrapper validates shapes on the host, passes raw device pointers and the
+current HIP stream to libhilda_spec.so and raises RuntimeError on any non-zero
+status. Workspaces are allocated once per (device, kind), zero-filled, and
+reused: the kernels leave their counters zeroed after every call.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib as L
+
+_MODES = {"reference": L.HS_ACCEPT_REFERENCE, "filtered": L.HS_ACCEPT_FILTERED,
+          "greedy": L.HS_ACCEPT_GREEDY}
+_WS: dict = {}
+
+
+def workspace(device: torch.device, nbytes: int, kind: str) -> torch.Tensor:
+    key = (device.index, kind)
+    ws = _WS.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+        _WS[key] = ws
+    return ws
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _logit_dtype(t: torch.Tensor) -> int:
+    if t.dtype == torch.float32:
+        return L.HS_F32
+    if t.dtype == torch.bfloat16:
+        return L.HS_BF16
+    raise TypeError(f"logits must be float32 or bfloat16, got {t.dtype}")
+
+
+def _mode(mode) -> int:
+    if isinstance(mode, str):
+        if mode not in _MODES:
+            raise ValueError(f"unknown mode {mode!r}")
+        return _MODES[mode]
+    return int(mode)
+
+
+def _need_cuda(*ts):
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError("all tensors must live on the GPU")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError("all tensors must live on the same GPU")
+    return dev
+
+
+def _rows2d(t: torch.Tensor, rows: int, V: int) -> tuple[torch.Tensor, int]:
+    """View t as `rows` rows of V contiguous elements with one row stride."""
+    t2 = t.reshape(rows, V) if t.dim() != 2 else t
+    if t2.stride(1) != 1 or t2.shape != (rows, V):
+        t2 = t2.contiguous()
+    return t2, t2.stride(0)
+
+
+def spec_accept(target_logits: torch.Tensor, draft_probs: torch.Tensor | None,
+                draft_tokens: torch.Tensor, temperatures: torch.Tensor | None,
+                u_accept: torch.Tensor | None, u_resample: torch.Tensor | None, *,
+                mode="reference", top_ks: torch.Tensor | None = None,
+                top_ps: torch.Tensor | None = None, row_stats: bool = False):
+    """Fused acceptance sampler (drop-in for model_runner.py:387-428).
+
+    target_logits [B, gamma+1, V] f32/bf16, draft_probs [B, gamma, V] f32,
+    draft_tokens [B, gamma] int64, temperatures [B] f32, u_accept [B, gamma],
+    u_resample [B]. Returns (num_accepted int32 [B], out_tokens int64
+    [B, gamma+1], out_len int32 [B]) and, with row_stats=True, a 4th tensor
+    [B*(gamma+1), 2] with the max and normaliser of every target row.
+    """
+    m = _mode(mode)
+    dev = _need_cuda(target_logits, draft_probs, draft_tokens, temperatures, u_accept,
+                     u_resample, top_ks, top_ps)
+    if target_logits.dim() != 3:
+        raise ValueError("target_logits must be [B, gamma+1, V]")
+    B, R, V = target_logits.shape
+    gamma = R - 1
+    if gamma < 1:
+        raise ValueError("need at least one draft token")
+    if tuple(draft_tokens.shape) != (B, gamma):
+        raise ValueError(f"draft_tokens must be [{B}, {gamma}]")
+    lg, lstride = _rows2d(target_logits, B * R, V)
+    dt = draft_tokens.to(torch.int64).contiguous()
+    q = None
+    qstride = V
+    if m != L.HS_ACCEPT_GREEDY:
+        if draft_probs is None or tuple(draft_probs.shape) != (B, gamma, V):
+            raise ValueError(f"draft_probs must be [{B}, {gamma}, {V}]")
+        if draft_probs.dtype != torch.float32:
+            raise TypeError("draft_probs must be float32")
+        q, qstride = _rows2d(draft_probs, B * gamma, V)
+        temperatures = temperatures.to(torch.float32).contiguous()
+        u_accept = u_accept.to(torch.float32).reshape(B, gamma).contiguous()
+        u_resample = u_resample.to(torch.float32).reshape(B).contiguous()
+    if m == L.HS_ACCEPT_FILTERED:
+        if top_ks is None or top_ps is None:
+            raise ValueError("filtered mode needs top_ks and top_ps")
+        top_ks = top_ks.to(torch.int32).contiguous()
+        top_ps = top_ps.to(torch.float32).contiguous()
+    nacc = torch.empty(B, dtype=torch.int32, device=dev)
+    out = torch.empty((B, R), dtype=torch.int64, device=dev)
+    olen = torch.empty(B, dtype=torch.int32, device=dev)
+    stats = torch.empty((B * R, 2), dtype=torch.float32, device=dev) if row_stats else None
+    lib = L.lib()
+    nbytes = lib.hs_spec_accept_workspace_size(B, gamma, V)
+    ws = workspace(dev, nbytes, "spec_accept")
+
+    def p(t):
+        return None if t is None else t.data_ptr()
+
+    rc = lib.hs_spec_accept(p(lg), _logit_dtype(lg), lstride, p(q), qstride, p(dt),
+                            p(temperatures) if m != L.HS_ACCEPT_GREEDY else None,
+                            p(top_ks) if m == L.HS_ACCEPT_FILTERED else None,
+                            p(top_ps) if m == L.HS_ACCEPT_FILTERED else None,
+                            p(u_accept) if m != L.HS_ACCEPT_GREEDY else None,
+                            p(u_resample) if m != L.HS_ACCEPT_GREEDY else None,
+                            B, gamma, V, m, p(nacc), p(out), p(olen), p(stats), ws.data_ptr(),
+                            ws.numel(), _stream(dev))
+    L.check(rc, "hs_spec_accept")
+    if row_stats:
+        return nacc, out, olen, stats
+    return nacc, out, olen
+
+
+def sample_rows(logits: torch.Tensor, temperatures: torch.Tensor | None = None,
+                top_ks: torch.Tensor | None = None, top_ps: torch.Tensor | None = None, *,
+                mode="reference", uniforms: torch.Tensor | None = None, want_probs: bool = False,
+                out_kind: int = 0, row_stats: bool = False):
+    """Row sampler (Sampler.forward / draft probabilities).
+
+    Returns dict(probs=[rows, V] f32 or None, tokens=[rows] int64 or None,
+    row_stats=[rows, 2] or None). out_kind 1 returns the masked logits of the
+    top-k/top-p filters instead of probabilities.
+    """
+    m = _mode(mode)
+    dev = _need_cuda(logits, temperatures, top_ks, top_ps, uniforms)
+    if logits.dim() != 2:
+        raise ValueError("logits must be [rows, V]")
+    rows, V = logits.shape
+    lg, lstride = _rows2d(logits, rows, V)
+    if m != L.HS_ACCEPT_GREEDY:
+        if temperatures is None:
+            raise ValueError("temperatures required")
+        temperatures = temperatures.to(torch.float32).reshape(rows).contiguous()
+    if m == L.HS_ACCEPT_FILTERED:
+        if top_ks is None or top_ps is None:
+            raise ValueError("filtered mode needs top_ks and top_ps")
+        top_ks = top_ks.to(torch.int32).reshape(rows).contiguous()
+        top_ps = top_ps.to(torch.float32).reshape(rows).contiguous()
+    probs = None
+    if want_probs and m != L.HS_ACCEPT_GREEDY:
+        probs = torch.empty((rows, V), dtype=torch.float32, device=dev)
+    toks = None
+    if m == L.HS_ACCEPT_GREEDY or uniforms is not None:
+        toks = torch.empty(rows, dtype=torch.int64, device=dev)
+    if uniforms is not None:
+        uniforms = uniforms.to(torch.float32).reshape(rows).contiguous()
+    if m == L.HS_ACCEPT_GREEDY and uniforms is None:
+        uniforms_ptr = None
+    else:
+        uniforms_ptr = None if uniforms is None else uniforms.data_ptr()
+    stats = torch.empty((rows, 2), dtype=torch.float32, device=dev) if row_stats else None
+    lib = L.lib()
+    ws = workspace(dev, lib.hs_sampler_workspace_size(rows, V), "sampler")
+
+    def p(t):
+        return None if t is None else t.data_ptr()
+
+    rc = lib.hs_sampler(p(lg), _logit_dtype(lg), lstride, rows, V, p(temperatures),
+                        p(top_ks) if m == L.HS_ACCEPT_FILTERED else None,
+                        p(top_ps) if m == L.HS_ACCEPT_FILTERED else None, m, p(probs),
+                        V if probs is not None else 0, int(out_kind),
+                        uniforms_ptr if m != L.HS_ACCEPT_GREEDY else None,
+                        p(toks), p(stats), ws.data_ptr(), ws.numel(), _stream(dev))
+    L.check(rc, "hs_sampler")
+    return dict(probs=probs, tokens=toks, row_stats=stats)

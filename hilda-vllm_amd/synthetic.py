@@ -1,0 +1,123 @@
+"""Seeded synthetic workloads of the verify path (numpy, host side).
+
+The shapes and distributions follow the benchmark configurations of the verify
+path: config 0 (one sequence, fp32 logits), config 1 (batched bf16 logits with
+per-sequence sampling settings) and config 2 (paged attention). Arrays come
+from numpy's PCG64 generator so the same seed gives the same bytes on every
+machine; `digest()` fingerprints a workload.
+"""
+from __future__ import annotations
+
+import hashlib
+
+import numpy as np
+
+VOCAB = 151936
+
+
+def _rng(seed: int) -> np.random.Generator:
+    return np.random.Generator(np.random.PCG64(seed))
+
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + (((u >> 16) & 1) + 0x7FFF)) >> 16).astype(np.uint16)
+
+
+def bf16_bits_to_f32(b: np.ndarray) -> np.ndarray:
+    return (b.astype(np.uint32) << 16).view(np.float32)
+
+
+def softmax64(x: np.ndarray) -> np.ndarray:
+    z = x.astype(np.float64)
+    z = z - z.max(axis=-1, keepdims=True)
+    e = np.exp(z)
+    return e / e.sum(axis=-1, keepdims=True)
+
+
+def filtered_probs64(logits: np.ndarray, temperature: float, top_k: int, top_p: float):
+    """float64 top-k / top-p distribution of one row (draft-side input only)."""
+    x = logits.astype(np.float64) / temperature
+    V = x.shape[-1]
+    order = np.lexsort((np.arange(V), -x))
+    keep = np.ones(V, bool)
+    if 0 < top_k < V:
+        keep[:] = False
+        keep[order[:top_k]] = True
+    if top_p < 1.0:
+        xs = np.where(keep[order], x[order], -np.inf)
+        p = np.exp(xs - xs[0])
+        p /= p.sum()
+        c = np.cumsum(p)
+        ks = c < top_p
+        ks[0] = True
+        keep[:] = False
+        keep[order[ks]] = True
+    z = np.where(keep, x, -np.inf)
+    e = np.exp(z - z.max())
+    return e / e.sum()
+
+
+def _inv_cdf(p: np.ndarray, u: float) -> int:
+    c = np.cumsum(p)
+    return int(min(np.searchsorted(c, u * c[-1], side="right"), p.shape[0] - 1))
+
+
+def accept_workload(batch: int, gamma: int, vocab: int = VOCAB, seed: int = 0,
+                    dtype: str = "f32", temperature=1.0, top_k=0, top_p=1.0,
+                    per_seq_settings: bool = False, mode: str = "reference") -> dict:
+    """Inputs of one fused acceptance call.
+
+    Target logits ~ N(0, 2^2) [B, gamma+1, V]; draft logits = target[:, :gamma]
+    + N(0, 1). Draft probabilities are the draft distribution (filtered in
+    filtered mode) and the draft tokens are drawn from it. Uniforms u_accept
+    [B, gamma] and u_resample [B] come from the same seeded stream.
+    With per_seq_settings, T ~ U[0.5, 1.2], top_k in {0, 20, 50} and
+    top_p in {1.0, 0.9, 0.8} per sequence.
+    dtype "bf16" rounds the logits to bf16 (logits_bits holds the patterns).
+    """
+    rng = _rng(seed)
+    target = (rng.standard_normal((batch, gamma + 1, vocab), dtype=np.float32) * 2.0)
+    noise = rng.standard_normal((batch, gamma, vocab), dtype=np.float32)
+    draft = target[:, :gamma] + noise
+    if dtype == "bf16":
+        tb = f32_to_bf16_bits(target)
+        target = bf16_bits_to_f32(tb)
+        draft = bf16_bits_to_f32(f32_to_bf16_bits(draft))
+    else:
+        tb = None
+    if per_seq_settings:
+        temps = rng.uniform(0.5, 1.2, size=batch).astype(np.float32)
+        top_ks = rng.choice(np.array([0, 20, 50], np.int32), size=batch)
+        top_ps = rng.choice(np.array([1.0, 0.9, 0.8], np.float32), size=batch)
+    else:
+        temps = np.full(batch, temperature, np.float32)
+        top_ks = np.full(batch, top_k, np.int32)
+        top_ps = np.full(batch, top_p, np.float32)
+    q = np.empty((batch, gamma, vocab), np.float32)
+    dtok = np.empty((batch, gamma), np.int64)
+    for b in range(batch):
+        for j in range(gamma):
+            if mode == "filtered":
+                p = filtered_probs64(draft[b, j], float(temps[b]), int(top_ks[b]),
+                                     float(top_ps[b]))
+            else:
+                p = softmax64(draft[b, j] / np.float64(temps[b]))
+            q[b, j] = p.astype(np.float32)
+            dtok[b, j] = _inv_cdf(p, rng.random())
+    u_acc = rng.random((batch, gamma), dtype=np.float32)
+    u_res = rng.random(batch, dtype=np.float32)
+    return dict(logits=target.astype(np.float32), logits_bits=tb, draft_probs=q,
+                draft_tokens=dtok, temperatures=temps, top_ks=top_ks.astype(np.int32),
+                top_ps=top_ps.astype(np.float32), u_accept=u_acc, u_resample=u_res,
+                dtype=dtype, mode=mode)
+
+
+def digest(arrays: dict) -> str:
+    h = hashlib.sha256()
+    for k in sorted(arrays):
+        v = arrays[k]
+        if isinstance(v, np.ndarray):
+            h.update(k.encode())
+            h.update(np.ascontiguousarray(v).tobytes())
+    return h.hexdigest()

@@ -1,0 +1,111 @@
+/*
+ * hilda_spec.h - C ABI of the MI355X (gfx950) speculative-decoding verify path.
+ *
+ * Every entry point takes plain device pointers, element strides and sizes, a
+ * caller-owned workspace and a HIP stream (passed as void*, it is a
+ * hipStream_t). Each returns 0 on success or a negative HS_ERR_* code; none of
+ * them synchronises the stream or allocates device memory.
+ *
+ * Workspaces: query the size with the matching *_workspace_size() function,
+ * allocate it once, fill it with zeros once, and reuse it. Every successful
+ * call leaves the counter region zeroed again, so no memset is needed between
+ * calls (the calls are therefore safe to record into a HIP graph). Two calls
+ * that share one workspace must not overlap in time.
+ */
+#ifndef HILDA_SPEC_H
+#define HILDA_SPEC_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define HS_OK 0
+#define HS_ERR_INVALID (-1)     /* bad size, null pointer or enum value      */
+#define HS_ERR_WORKSPACE (-2)   /* workspace too small                        */
+#define HS_ERR_LAUNCH (-3)      /* kernel launch failed (hipGetLastError)     */
+#define HS_ERR_UNSUPPORTED (-4) /* valid request this build does not support */
+
+/* element types */
+#define HS_F32 0
+#define HS_BF16 1
+#define HS_FP8_E4M3 2
+
+/* acceptance modes */
+#define HS_ACCEPT_REFERENCE 0 /* temperature-only softmax (model_runner.py:398) */
+#define HS_ACCEPT_FILTERED 1  /* temperature, top-k, top-p (sampler.py:20-49)   */
+#define HS_ACCEPT_GREEDY 2    /* argmax match; temperature ignored             */
+
+/* Human-readable text for a status code (static storage). */
+const char* hs_status_string(int status);
+
+/* Library version, (major << 16) | minor. */
+int hs_version(void);
+
+/* ------------------------------------------------------------------------ */
+/* Fused acceptance sampler.                                                 */
+/*                                                                          */
+/* Replaces the per-sequence rejection-sampling loop of                      */
+/* ModelRunner.run_verify, mini_vllm/engine/model_runner.py:387-428, with    */
+/* the torch RNG calls (torch.rand at :407, torch.multinomial at :412,:425)  */
+/* replaced by the explicit uniforms u_accept and u_resample.               */
+/*                                                                          */
+/* target_logits : [batch, gamma+1, vocab] rows of dtype HS_F32 or HS_BF16;  */
+/*                 row (b, j) starts at element (b*(gamma+1)+j)*row_stride.  */
+/* draft_probs   : [batch, gamma, vocab] f32; row (b, j) at                 */
+/*                 (b*gamma+j)*draft_row_stride. Unused (may be NULL) in     */
+/*                 greedy mode. In filtered mode it must hold the filtered   */
+/*                 draft distribution the draft tokens were drawn from.     */
+/* draft_tokens  : [batch, gamma] int64.                                     */
+/* temperatures  : [batch] f32 (> 0 unless greedy); top_ks [batch] int32     */
+/*                 (<= 0 or >= vocab: off); top_ps [batch] f32 (>= 1: off).  */
+/*                 top_ks/top_ps are read in filtered mode only.            */
+/* u_accept      : [batch, gamma] f32 in [0,1); u_resample [batch] f32.     */
+/* outputs       : num_accepted [batch] int32, out_tokens [batch, gamma+1]   */
+/*                 int64 (-1 after the last emitted token), out_len [batch]. */
+/* row_stats     : optional [batch*(gamma+1), 2] f32: per target row the     */
+/*                 softmax max and normaliser over the kept set.            */
+/* ------------------------------------------------------------------------ */
+size_t hs_spec_accept_workspace_size(int batch, int gamma, int vocab);
+
+int hs_spec_accept(const void* target_logits, int logits_dtype, int64_t logits_row_stride,
+                   const float* draft_probs, int64_t draft_row_stride,
+                   const int64_t* draft_tokens, const float* temperatures,
+                   const int32_t* top_ks, const float* top_ps,
+                   const float* u_accept, const float* u_resample,
+                   int batch, int gamma, int vocab, int mode,
+                   int32_t* num_accepted, int64_t* out_tokens, int32_t* out_len,
+                   float* row_stats, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Row sampler: Sampler.forward, mini_vllm/layers/sampler.py:13-25, and the  */
+/* draft-probability producer softmax(logits/T) of run_draft_decode,         */
+/* mini_vllm/engine/model_runner.py:312-313.                                 */
+/*                                                                          */
+/* mode: HS_ACCEPT_REFERENCE (temperature only), HS_ACCEPT_FILTERED          */
+/* (temperature, top-k, top-p) or HS_ACCEPT_GREEDY (argmax, lowest index on  */
+/* ties; probs_out must be NULL).                                            */
+/* probs_out (optional): [rows, vocab] f32. out_kind 0 writes the           */
+/* probabilities of the (filtered) distribution; out_kind 1 writes logits/T  */
+/* inside the kept set and -inf outside it, i.e. the masked logits of        */
+/* Sampler._apply_top_k/_apply_top_p (sampler.py:27-49).                    */
+/* uniforms + tokens_out (optional, both or neither): one                    */
+/* uniform per row drives an inverse-CDF draw that replaces the exponential- */
+/* race draw of sampler.py:24.                                               */
+/* ------------------------------------------------------------------------ */
+size_t hs_sampler_workspace_size(int rows, int vocab);
+
+int hs_sampler(const void* logits, int logits_dtype, int64_t logits_row_stride,
+               int rows, int vocab, const float* temperatures, const int32_t* top_ks,
+               const float* top_ps, int mode, float* probs_out, int64_t probs_row_stride,
+               int out_kind, const float* uniforms, int64_t* tokens_out, float* row_stats,
+               void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HILDA_SPEC_H */
