@@ -8,6 +8,7 @@ namespace hs {
 constexpr int kMaxGamma = 32;     // drafts per sequence handled by one wave
 constexpr int kFilterThreads = 512;
 constexpr int kCand = 4096;       // LDS candidate capacity of the filter kernel
+constexpr int kMaxRows = 65535;   // rows (and units) per call: grid.y limit
 
 enum : int { kFinRow = 0, kFinDecide = 1, kFinPlain = 2 };
 enum : int { kKindNone = 0, kKindResidual = 1, kKindBonus = 2, kKindPlain = 3 };

@@ -354,17 +354,20 @@ __global__ __launch_bounds__(64) void k_sample(Problem P, AcceptArgs A, Work W, 
 // ---------------------------------------------------------------------------
 static inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
+// The ticket counters come first, at fixed offsets for every shape (one slot
+// per possible row/unit), so the "counters are left zero" invariant holds
+// across calls of different shapes that share one workspace.
 Layout make_layout(int units, int rows, int nchunk) {
   Layout L;
   size_t off = 0;
+  L.rowctr = off; off = align_up(off + (size_t)kMaxRows * sizeof(uint32_t), 256);
+  L.unitctr = off; off = align_up(off + (size_t)kMaxRows * sizeof(uint32_t), 256);
+  L.sampctr = off; off = align_up(off + (size_t)kMaxRows * sizeof(uint32_t), 256);
   L.part = off; off = align_up(off + (size_t)rows * nchunk * sizeof(ChunkStat), 256);
   L.desc = off; off = align_up(off + (size_t)rows * sizeof(RowDesc), 256);
   L.st = off; off = align_up(off + (size_t)units * sizeof(SeqState), 256);
   L.spart = off; off = align_up(off + (size_t)units * nchunk * sizeof(SampPart), 256);
   L.filt = off; off = align_up(off + (size_t)rows * sizeof(FilterScratch), 256);
-  L.rowctr = off; off = align_up(off + (size_t)rows * sizeof(uint32_t), 256);
-  L.unitctr = off; off = align_up(off + (size_t)units * sizeof(uint32_t), 256);
-  L.sampctr = off; off = align_up(off + (size_t)units * sizeof(uint32_t), 256);
   L.total = off;
   return L;
 }
@@ -488,7 +491,7 @@ int hs_spec_accept(const void* target_logits, int logits_dtype, int64_t logits_r
                    int32_t* num_accepted, int64_t* out_tokens, int32_t* out_len,
                    float* row_stats, void* workspace, size_t workspace_bytes, void* stream) {
   if (batch <= 0 || gamma <= 0 || gamma > kMaxGamma || vocab <= 0) return HS_ERR_INVALID;
-  if ((int64_t)batch * (gamma + 1) > 65535) return HS_ERR_UNSUPPORTED;
+  if ((int64_t)batch * (gamma + 1) > kMaxRows) return HS_ERR_UNSUPPORTED;
   if (mode != HS_ACCEPT_REFERENCE && mode != HS_ACCEPT_FILTERED && mode != HS_ACCEPT_GREEDY)
     return HS_ERR_INVALID;
   if (logits_dtype != HS_F32 && logits_dtype != HS_BF16) return HS_ERR_INVALID;
@@ -541,7 +544,8 @@ int hs_sampler(const void* logits, int logits_dtype, int64_t logits_row_stride, 
                float* probs_out, int64_t probs_row_stride, int out_kind, const float* uniforms,
                int64_t* tokens_out, float* row_stats, void* workspace, size_t workspace_bytes,
                void* stream) {
-  if (rows <= 0 || rows > 65535 || vocab <= 0) return HS_ERR_INVALID;
+  if (rows <= 0 || vocab <= 0) return HS_ERR_INVALID;
+  if (rows > kMaxRows) return HS_ERR_UNSUPPORTED;
   if (mode != HS_ACCEPT_REFERENCE && mode != HS_ACCEPT_FILTERED && mode != HS_ACCEPT_GREEDY)
     return HS_ERR_INVALID;
   if (logits_dtype != HS_F32 && logits_dtype != HS_BF16) return HS_ERR_INVALID;

@@ -7,10 +7,12 @@
  * them synchronises the stream or allocates device memory.
  *
  * Workspaces: query the size with the matching *_workspace_size() function,
- * allocate it once, fill it with zeros once, and reuse it. Every successful
- * call leaves the counter region zeroed again, so no memset is needed between
- * calls (the calls are therefore safe to record into a HIP graph). Two calls
- * that share one workspace must not overlap in time.
+ * allocate it once, fill it with zeros once, and reuse it. The counters live
+ * at fixed offsets at the start of the workspace and every successful call
+ * leaves them zeroed again, so no memset is needed between calls, also when
+ * consecutive calls differ in shape (the calls are therefore safe to record
+ * into a HIP graph). Two calls that share one workspace must not overlap in
+ * time.
  */
 #ifndef HILDA_SPEC_H
 #define HILDA_SPEC_H

@@ -207,3 +207,13 @@ def test_repeated_calls_reuse_workspace(hv, orc, cuda):
     outs = [_run_both(hv, orc, w, cuda, "reference")[0][1] for _ in range(3)]
     for o in outs[1:]:
         np.testing.assert_array_equal(o, outs[0])
+
+
+def test_shape_changes_share_workspace(hv, orc, cuda):
+    """Calls of different (B, gamma, V) reuse one workspace; the ticket
+    counters must still start from zero on every call."""
+    shapes = [(8, 5, 30000), (2, 1, 4097), (16, 3, 2048), (1, 7, 151936), (8, 1, 30000)]
+    for i, (B, g, V) in enumerate(shapes):
+        w = hv.synthetic.accept_workload(B, g, vocab=V, seed=400 + i)
+        got, ref = _run_both(hv, orc, w, cuda, "reference")
+        _assert_same(got, ref)
