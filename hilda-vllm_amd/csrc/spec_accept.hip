@@ -4,21 +4,23 @@
 // (mini_vllm/engine/model_runner.py:387-428) and the sampling ops of
 // Sampler.forward (mini_vllm/layers/sampler.py:13-49).
 //
-// Pipeline of one hs_spec_accept call (B sequences, gamma drafts, V vocab):
-//   1. k_row_stats  grid (nsplit, B*(gamma+1)), one wave per workgroup.
-//      Each wave streams 2048-element chunks of a target row once from HBM
-//      and writes the chunk max m_c and the exact fixed-point sum
-//      E_c = sum_i floor(2^44 * exp(x_i - m_c)). The last workgroup of a row
-//      (atomic ticket) folds the chunk partials into the row max M and the
-//      normaliser S; the last row of a sequence then runs the accept test
-//      for all gamma drafts in one wave and records where to resample.
-//   2. (filtered mode) k_row_filter: one workgroup per row finds the top-k /
-//      top-p boundary (spec_filter.hip).
-//   3. k_sample     grid (nsplit, B): streams only the resample row (target
-//      row r, and draft row r for a residual) and writes per-chunk exact
-//      weight sums; the last workgroup locates the chunk holding the
-//      inverse-CDF point and rescans that one chunk to find the token.
-// Greedy mode uses k_row_argmax instead of 1-3.
+// One hs_spec_accept call (B sequences, gamma drafts, V vocab) is a short
+// chain of launches with no communication between workgroups of a launch
+// (on gfx950 a cross-XCD release/acquire costs an L2 write-back plus an L2
+// invalidate per workgroup; kernel boundaries are cheaper):
+//   1. k_chunk_stats   one 256-thread workgroup per 2048-element chunk of a
+//      target row: chunk max m_c and E_c = sum floor(2^44 exp(x_i - m_c)).
+//      Target logits are read from HBM exactly once here.
+//   2. (filtered mode) k_row_filter, spec_filter.hip: top-k / top-p kept set
+//      and normaliser per row.
+//   3. k_sample_part   grid (splits, B). Every workgroup first recomputes the
+//      decision of its sequence from the chunk partials (a few hundred
+//      values, deterministic, so all workgroups agree without talking), then
+//      streams its share of the resample row (target row r, plus draft row r
+//      for a residual) and writes exact per-chunk weight sums.
+//   4. k_sample_final  one workgroup per sequence: locates the chunk holding
+//      the inverse-CDF point and rescans that one chunk to find the token.
+// Greedy mode: k_chunk_argmax then k_greedy_final.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <string.h>
@@ -30,147 +32,123 @@
 
 namespace hs {
 
-template <typename T>
-__global__ __launch_bounds__(64) void k_row_stats(Problem P, AcceptArgs A, Work W, int fin,
-                                                  float* row_stats) {
-  const int row = blockIdx.y;
-  const int split = blockIdx.x;
-  const int lane = threadIdx.x;
-  const int unit = row / P.rows_per_unit;
-  const float Tt = P.temps[unit];
-  const T* rp = reinterpret_cast<const T*>(P.logits) + (int64_t)row * P.row_stride;
-  const bool vec_ok = ((reinterpret_cast<uintptr_t>(rp) & 15u) == 0);
-  const int c_begin = (int)((int64_t)split * P.nchunk / P.nsplit);
-  const int c_end = (int)((int64_t)(split + 1) * P.nchunk / P.nsplit);
+constexpr int kT = kChunkThreads;  // 256 threads, 8 elements each, per chunk
 
-  for (int c = c_begin; c < c_end; ++c) {
-    const int64_t c0 = (int64_t)c * kChunk;
-    float x[kChunkGroups][8];
-#pragma unroll
-    for (int g = 0; g < kChunkGroups; ++g) load8<T>(rp, elem_idx(c0, g, lane, 0), P.V, vec_ok, x[g]);
+// ---------------------------------------------------------------------------
+// 1. chunk statistics
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(kT) void k_chunk_stats(Problem P, Work W) {
+  __shared__ float s_m[kT / kWave];
+  __shared__ uint64_t s_e[kT / kWave];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int64_t items = (int64_t)P.units * P.rows_per_unit * P.nchunk;
+  for (int64_t it = blockIdx.x; it < items; it += gridDim.x) {
+    const int row = (int)(it / P.nchunk);
+    const int c = (int)(it % P.nchunk);
+    const int unit = row / P.rows_per_unit;
+    const float Tt = P.temps[unit];
+    const float rT = 1.0f / Tt;
+    const bool fast = hs_rcp_ok(Tt);
+    const T* rp = reinterpret_cast<const T*>(P.logits) + (int64_t)row * P.row_stride;
+    const bool vec_ok = ((reinterpret_cast<uintptr_t>(rp) & 15u) == 0);
+    const int64_t i0 = chunk_elem(c, tid, 0);
+    float x[8];
+    load8<T>(rp, i0, P.V, vec_ok, x);
     float m = -INFINITY;
 #pragma unroll
-    for (int g = 0; g < kChunkGroups; ++g)
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        x[g][k] = hs_div_t(x[g][k], Tt);
-        if (elem_idx(c0, g, lane, k) < P.V) m = fmaxf(m, x[g][k]);
-      }
+    for (int k = 0; k < 8; ++k) {
+      x[k] = hs_div_temp(x[k], Tt, rT, fast);
+      if (i0 + k < P.V) m = fmaxf(m, x[k]);
+    }
     m = wave_max_f32(m);
-    uint64_t e = 0;
+    if (lane == 0) s_m[wid] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
+    uint32_t hi = 0, lo = 0;
 #pragma unroll
-    for (int g = 0; g < kChunkGroups; ++g)
-#pragma unroll
-      for (int k = 0; k < 8; ++k)
-        if (elem_idx(c0, g, lane, k) < P.V) e += hs_fx44(hs_exp(x[g][k] - m));
-    e = wave_sum_u64(e);
-    if (lane == 0) {
+    for (int k = 0; k < 8; ++k)
+      if (i0 + k < P.V) hs_fx44_split(hs_exp(x[k] - m), hi, lo);
+    uint64_t e = wave_sum_u64(hs_join44(hi, lo));
+    if (lane == 0) s_e[wid] = e;
+    __syncthreads();
+    if (tid == 0) {
       ChunkStat cs;
       cs.m = m;
       cs.pad = 0;
-      cs.e = e;
-      W.part[(int64_t)row * P.nchunk + c] = cs;
-    }
-  }
-
-  if (!last_ticket(W.rowctr + row, (uint32_t)P.nsplit, lane)) return;
-  fold_row<T>(P, W, row, lane, row_stats);
-
-  if (fin == kFinDecide) {
-    if (!last_ticket(W.unitctr + unit, (uint32_t)P.rows_per_unit, lane)) return;
-    decide_unit<T>(P, A, W, unit, lane);
-  } else if (fin == kFinPlain) {
-    if (lane == 0) {
-      SeqState s;
-      s.kind = kKindPlain;
-      s.row = row;
-      s.qrow = -1;
-      s.nacc = 0;
-      s.pad[0] = s.pad[1] = s.pad[2] = s.pad[3] = 0;
-      W.st[unit] = s;
+      cs.e = s_e[0] + s_e[1] + s_e[2] + s_e[3];
+      W.part[it] = cs;
     }
   }
 }
 
-// ---------------------------------------------------------------------------
-// greedy: argmax over raw logits (lowest index on ties)
-// ---------------------------------------------------------------------------
+// greedy: argmax over raw logits, lowest index on ties
 template <typename T>
-__global__ __launch_bounds__(64) void k_row_argmax(Problem P, AcceptArgs A, Work W, int fin,
-                                                   int64_t* tokens_out) {
-  const int row = blockIdx.y;
-  const int split = blockIdx.x;
-  const int lane = threadIdx.x;
-  const int unit = row / P.rows_per_unit;
-  const T* rp = reinterpret_cast<const T*>(P.logits) + (int64_t)row * P.row_stride;
-  const bool vec_ok = ((reinterpret_cast<uintptr_t>(rp) & 15u) == 0);
-  const int c_begin = (int)((int64_t)split * P.nchunk / P.nsplit);
-  const int c_end = (int)((int64_t)(split + 1) * P.nchunk / P.nsplit);
-
-  for (int c = c_begin; c < c_end; ++c) {
-    const int64_t c0 = (int64_t)c * kChunk;
+__global__ __launch_bounds__(kT) void k_chunk_argmax(Problem P, Work W) {
+  __shared__ uint64_t s_b[kT / kWave];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int64_t items = (int64_t)P.units * P.rows_per_unit * P.nchunk;
+  for (int64_t it = blockIdx.x; it < items; it += gridDim.x) {
+    const int row = (int)(it / P.nchunk);
+    const int c = (int)(it % P.nchunk);
+    const T* rp = reinterpret_cast<const T*>(P.logits) + (int64_t)row * P.row_stride;
+    const bool vec_ok = ((reinterpret_cast<uintptr_t>(rp) & 15u) == 0);
+    const int64_t i0 = chunk_elem(c, tid, 0);
+    float v[8];
+    load8<T>(rp, i0, P.V, vec_ok, v);
     uint64_t best = 0;
 #pragma unroll
-    for (int g = 0; g < kChunkGroups; ++g) {
-      float v[8];
-      load8<T>(rp, elem_idx(c0, g, lane, 0), P.V, vec_ok, v);
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        int64_t i = elem_idx(c0, g, lane, k);
-        if (i < P.V) {
-          uint64_t pk = ((uint64_t)hs_key(v[k]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
-          best = pk > best ? pk : best;
-        }
+    for (int k = 0; k < 8; ++k) {
+      const int64_t i = i0 + k;
+      if (i < P.V) {
+        uint64_t pk = ((uint64_t)hs_key(v[k]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
+        best = pk > best ? pk : best;
       }
     }
     best = wave_max_u64(best);
-    if (lane == 0) {
+    if (lane == 0) s_b[wid] = best;
+    __syncthreads();
+    if (tid == 0) {
+      uint64_t b = s_b[0];
+      for (int w = 1; w < kT / kWave; ++w) b = s_b[w] > b ? s_b[w] : b;
       ChunkStat cs;
       cs.m = 0.0f;
       cs.pad = 0;
-      cs.e = best;
-      W.part[(int64_t)row * P.nchunk + c] = cs;
+      cs.e = b;
+      W.part[it] = cs;
     }
+    __syncthreads();
   }
+}
 
-  if (!last_ticket(W.rowctr + row, (uint32_t)P.nsplit, lane)) return;
-  {
-    const ChunkStat* cp = W.part + (int64_t)row * P.nchunk;
+// one wave per unit: per-row argmax, then the greedy acceptance
+__global__ __launch_bounds__(kWave) void k_greedy_final(Problem P, AcceptArgs A, Work W,
+                                                        int64_t* tokens_out) {
+  const int unit = blockIdx.x;
+  const int lane = threadIdx.x;
+  const int R = P.rows_per_unit;
+  __shared__ int s_tok[kMaxGamma + 1];
+  for (int j = 0; j < R; ++j) {
+    const ChunkStat* cp = W.part + (int64_t)(unit * R + j) * P.nchunk;
     uint64_t best = 0;
     for (int c = lane; c < P.nchunk; c += kWave) best = cp[c].e > best ? cp[c].e : best;
     best = wave_max_u64(best);
-    int tok = (int)(0xffffffffu - (uint32_t)(best & 0xffffffffull));
-    if (lane == 0) {
-      RowDesc d;
-      d.m = hs_unkey((uint32_t)(best >> 32));
-      d.s = 1.0f;
-      d.tkey = 0u;
-      d.tidx = 0x7fffffff;
-      d.all = 1;
-      d.token = tok;
-      d.s_full = 1.0f;
-      d.pad = 0;
-      W.desc[row] = d;
-      if (fin == kFinPlain && tokens_out) tokens_out[row] = tok;
-    }
+    if (lane == 0) s_tok[j] = (int)(0xffffffffu - (uint32_t)(best & 0xffffffffull));
   }
-  if (fin != kFinDecide) return;
-  if (!last_ticket(W.unitctr + unit, (uint32_t)P.rows_per_unit, lane)) return;
-
-  // greedy acceptance: draft j accepted iff it equals the target argmax of row j
+  __syncthreads();
+  if (!A.tok_out) {  // row sampler: one row per unit
+    if (lane == 0) tokens_out[unit] = s_tok[0];
+    return;
+  }
   const int g = A.gamma;
   bool rej = false;
-  if (lane < g) {
-    int64_t d = A.dtok[(int64_t)unit * g + lane];
-    int t = W.desc[(int64_t)unit * (g + 1) + lane].token;
-    rej = (d != (int64_t)t);
-  }
-  uint64_t mask = __ballot(rej);
-  int r = mask ? (__ffsll((long long)mask) - 1) : g;
+  if (lane < g) rej = (A.dtok[(int64_t)unit * g + lane] != (int64_t)s_tok[lane]);
+  const uint64_t mask = __ballot(rej);
+  const int r = mask ? (__ffsll((long long)mask) - 1) : g;
   if (lane <= g) {
     int64_t v;
     if (lane < r) v = A.dtok[(int64_t)unit * g + lane];
-    else if (lane == r) v = W.desc[(int64_t)unit * (g + 1) + r].token;
+    else if (lane == r) v = s_tok[r];
     else v = -1;
     A.tok_out[(int64_t)unit * (g + 1) + lane] = v;
   }
@@ -181,46 +159,89 @@ __global__ __launch_bounds__(64) void k_row_argmax(Problem P, AcceptArgs A, Work
 }
 
 // ---------------------------------------------------------------------------
-// sample: inverse-CDF draw from one row per unit (bonus/plain) or from the
-// residual max(P - Q, 0) (reject)
+// 3. decision + resample partial sums
 // ---------------------------------------------------------------------------
+// Decision of one unit from row descriptors held in LDS (one wave).
 template <typename T>
-__device__ __forceinline__ void unit_weights(const Problem& P, const RowDesc& D, float Tt,
-                                             const float (&v)[8], const float (&q)[8],
-                                             bool residual, bool masked, int64_t i0,
-                                             uint64_t (&wres)[8], uint64_t (&wp)[8],
-                                             float (&pr)[8]) {
-#pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const int64_t i = i0 + k;
-    float p = 0.0f, xm = -INFINITY;
-    if (i < P.V) {
-      const float x = hs_div_t(v[k], Tt);
-      if (desc_keep(D, hs_key(x), i)) {
-        p = hs_exp(x - D.m) / D.s;
-        xm = x;
-      }
+__device__ void decide_from(const Problem& P, const AcceptArgs& A, const RowDesc* sd, int unit,
+                            int lane, SeqState* out) {
+  const int g = A.gamma;
+  bool rej = false;
+  if (lane < g) {
+    const int64_t d = A.dtok[(int64_t)unit * g + lane];
+    float pt = 0.0f, pd = 0.0f;
+    if (d >= 0 && d < P.V) {
+      const int64_t row = (int64_t)unit * (g + 1) + lane;
+      const T* rp = reinterpret_cast<const T*>(P.logits) + row * P.row_stride;
+      const float x = hs_div_t(ld1<T>(rp + d), P.temps[unit]);
+      pt = desc_prob(sd[lane], x, d);
+      pd = A.q[((int64_t)unit * g + lane) * A.q_stride + d];
     }
-    pr[k] = masked ? xm : p;
-    wp[k] = hs_fx44(p);
-    wres[k] = residual ? hs_fx44(fmaxf(p - q[k], 0.0f)) : 0ull;
+    const float ratio = pt / fmaxf(pd, 1e-10f);
+    const float a = fminf(ratio, 1.0f);
+    rej = !(A.u_acc[(int64_t)unit * g + lane] < a);
+  }
+  const uint64_t mask = __ballot(rej);
+  const int r = mask ? (__ffsll((long long)mask) - 1) : g;
+  if (lane == 0) {
+    out->kind = (r < g) ? kKindResidual : kKindBonus;
+    out->row = unit * (g + 1) + r;
+    out->qrow = unit * g + r;
+    out->nacc = r;
   }
 }
 
 template <typename T>
-__global__ __launch_bounds__(64) void k_sample(Problem P, AcceptArgs A, Work W, SampleOut O) {
+__global__ __launch_bounds__(kT) void k_sample_part(Problem P, AcceptArgs A, Work W, SampleOut O,
+                                                    int mode, int desc_ready) {
+  __shared__ RowDesc s_desc[kMaxGamma + 1];
+  __shared__ SeqState s_st;
+  __shared__ uint64_t s_w[kT / kWave], s_p[kT / kWave];
   const int unit = blockIdx.y;
   const int split = blockIdx.x;
-  const int lane = threadIdx.x;
-  const SeqState st = W.st[unit];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int R = P.rows_per_unit;
+  const bool spec = (A.tok_out != nullptr);
+  (void)mode;
+
+  // descriptors of the unit's rows: from the filter kernel or folded here
+  if (desc_ready) {
+    for (int j = tid; j < R; j += kT) s_desc[j] = W.desc[(int64_t)unit * R + j];
+  } else {
+    for (int j = wid; j < R; j += kT / kWave) {
+      RowDesc d = fold_row_desc(P, W, unit * R + j, lane);
+      if (lane == 0) s_desc[j] = d;
+    }
+  }
+  __syncthreads();
+  if (wid == 0) {
+    if (spec) {
+      decide_from<T>(P, A, s_desc, unit, lane, &s_st);
+    } else if (lane == 0) {
+      s_st.kind = kKindPlain;
+      s_st.row = unit;
+      s_st.qrow = -1;
+      s_st.nacc = 0;
+    }
+  }
+  __syncthreads();
+  const SeqState st = s_st;
+  if (split == 0 && tid == 0) W.st[unit] = st;
+  if (split == 0 && O.row_stats && tid < R) {
+    const int64_t row = (int64_t)unit * R + tid;
+    O.row_stats[2 * row] = s_desc[tid].m;
+    O.row_stats[2 * row + 1] = s_desc[tid].s;
+  }
+  if (split == 0 && !desc_ready && tid < R) W.desc[(int64_t)unit * R + tid] = s_desc[tid];
+
   const int row = st.row;
-  // the state is written by the preceding kernel of this call; anything out
-  // of range means there is nothing to draw for this unit
-  if (st.kind == kKindNone || row < 0 || row >= P.units * P.rows_per_unit) return;
-  if (st.kind == kKindResidual && (st.qrow < 0 || st.qrow >= P.units * A.gamma)) return;
   const bool residual = (st.kind == kKindResidual);
-  const RowDesc D = W.desc[row];
-  const float Tt = P.temps[row / P.rows_per_unit];
+  const RowDesc D = s_desc[row - unit * R];
+  const float Tt = P.temps[unit];
+  const float rT = 1.0f / Tt;
+  const bool fastT = hs_rcp_ok(Tt);
+  const float rS = 1.0f / D.s;
+  const bool fastS = hs_rcp_ok(D.s);
   const T* rp = reinterpret_cast<const T*>(P.logits) + (int64_t)row * P.row_stride;
   const bool vec_ok = ((reinterpret_cast<uintptr_t>(rp) & 15u) == 0);
   const float* qp = residual ? A.q + (int64_t)st.qrow * A.q_stride : nullptr;
@@ -232,121 +253,178 @@ __global__ __launch_bounds__(64) void k_sample(Problem P, AcceptArgs A, Work W, 
   const int c_end = (int)((int64_t)(split + 1) * P.nchunk / P.nsplit);
 
   for (int c = c_begin; c < c_end; ++c) {
-    const int64_t c0 = (int64_t)c * kChunk;
-    uint64_t sw = 0, sp = 0;
+    const int64_t i0 = chunk_elem(c, tid, 0);
+    float v[8], q[8], pr[8];
+    load8<T>(rp, i0, P.V, vec_ok, v);
+    if (residual) load8_f32(qp, i0, P.V, q_vec, q);
+    uint32_t whi = 0, wlo = 0, phi = 0, plo = 0;
 #pragma unroll
-    for (int g = 0; g < kChunkGroups; ++g) {
-      const int64_t i0 = elem_idx(c0, g, lane, 0);
-      float v[8], q[8], pr[8];
-      uint64_t wres[8], wp[8];
-      load8<T>(rp, i0, P.V, vec_ok, v);
-      if (residual) load8_f32(qp, i0, P.V, q_vec, q);
-      else {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) q[k] = 0.0f;
-      }
-      unit_weights<T>(P, D, Tt, v, q, residual, masked, i0, wres, wp, pr);
-      if (pout) store8_f32(pout, i0, P.V, p_vec, pr);
-#pragma unroll
-      for (int k = 0; k < 8; ++k) { sw += wres[k]; sp += wp[k]; }
-    }
-    sw = wave_sum_u64(sw);
-    sp = wave_sum_u64(sp);
-    if (lane == 0) {
-      SampPart s;
-      s.w = sw;
-      s.p = sp;
-      W.spart[(int64_t)unit * P.nchunk + c] = s;
-    }
-  }
-  if (!O.sample) return;
-  if (!last_ticket(W.sampctr + unit, (uint32_t)P.nsplit, lane)) return;
-
-  // totals and the choice between residual and plain weights (model_runner.py:419-424)
-  const SampPart* spp = W.spart + (int64_t)unit * P.nchunk;
-  uint64_t wt = 0, pt = 0;
-  for (int c = lane; c < P.nchunk; c += kWave) { wt += spp[c].w; pt += spp[c].p; }
-  wt = wave_sum_u64(wt);
-  pt = wave_sum_u64(pt);
-  const bool use_res = residual && (hs_f32_of_u64(wt) * kTwoM44 > 1e-10f);
-  const uint64_t total = use_res ? wt : pt;
-  const float u = O.uniforms[unit];
-  const uint64_t t = hs_mulshift24(hs_u24(u), total);
-
-  // chunk holding the draw
-  int cstar = -1;
-  uint64_t before = 0, running = 0;
-  for (int cb = 0; cb < P.nchunk && cstar < 0; cb += kWave) {
-    int c = cb + lane;
-    uint64_t val = 0;
-    if (c < P.nchunk) val = use_res ? spp[c].w : spp[c].p;
-    uint64_t incl = wave_incl_scan_u64(val, lane);
-    uint64_t m = __ballot(running + incl > t);
-    if (m) {
-      int l = __ffsll((long long)m) - 1;
-      uint64_t incl_l = __shfl(incl, l, 64);
-      uint64_t val_l = __shfl(val, l, 64);
-      cstar = cb + l;
-      before = running + incl_l - val_l;
-    } else {
-      running += __shfl(incl, 63, 64);
-    }
-  }
-
-  int64_t token = -1;
-  if (cstar >= 0) {
-    const uint64_t trel = t - before;
-    const int64_t c0 = (int64_t)cstar * kChunk;
-    uint64_t base = 0;
-    for (int g = 0; g < kChunkGroups; ++g) {
-      const int64_t i0 = elem_idx(c0, g, lane, 0);
-      float v[8], q[8], pr[8];
-      uint64_t wres[8], wp[8];
-      load8<T>(rp, i0, P.V, vec_ok, v);
-      if (residual) load8_f32(qp, i0, P.V, q_vec, q);
-      else {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) q[k] = 0.0f;
-      }
-      unit_weights<T>(P, D, Tt, v, q, residual, masked, i0, wres, wp, pr);
-      uint64_t s = 0;
-#pragma unroll
-      for (int k = 0; k < 8; ++k) s += use_res ? wres[k] : wp[k];
-      uint64_t incl = wave_incl_scan_u64(s, lane);
-      uint64_t m = __ballot(base + incl > trel);
-      if (m) {
-        int l = __ffsll((long long)m) - 1;
-        int64_t found = -1;
-        if (lane == l) {
-          uint64_t acc = base + incl - s;
-#pragma unroll
-          for (int k = 0; k < 8; ++k) {
-            acc += use_res ? wres[k] : wp[k];
-            if (found < 0 && acc > trel) found = i0 + k;
-          }
+    for (int k = 0; k < 8; ++k) {
+      const int64_t i = i0 + k;
+      float p = 0.0f, xm = -INFINITY;
+      if (i < P.V) {
+        const float x = hs_div_temp(v[k], Tt, rT, fastT);
+        if (desc_keep(D, hs_key(x), i)) {
+          const float e = hs_exp(x - D.m);
+          p = fastS ? hs_div_rcp(e, D.s, rS) : e / D.s;
+          xm = x;
         }
-        token = (int64_t)__shfl((long long)found, l, 64);
-        break;
       }
-      base += __shfl(incl, 63, 64);
+      pr[k] = masked ? xm : p;
+      hs_fx44_split(p, phi, plo);
+      if (residual) hs_fx44_split(fmaxf(p - q[k], 0.0f), whi, wlo);
+    }
+    if (pout) store8_f32(pout, i0, P.V, p_vec, pr);
+    if (O.sample) {
+      const uint64_t sw = wave_sum_u64(hs_join44(whi, wlo));
+      const uint64_t sp = wave_sum_u64(hs_join44(phi, plo));
+      if (lane == 0) {
+        s_w[wid] = sw;
+        s_p[wid] = sp;
+      }
+      __syncthreads();
+      if (tid == 0) {
+        SampPart s;
+        s.w = s_w[0] + s_w[1] + s_w[2] + s_w[3];
+        s.p = s_p[0] + s_p[1] + s_p[2] + s_p[3];
+        W.spart[(int64_t)unit * P.nchunk + c] = s;
+      }
+      __syncthreads();
     }
   }
+}
 
+// ---------------------------------------------------------------------------
+// 4. final inverse-CDF search
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(kT) void k_sample_final(Problem P, AcceptArgs A, Work W,
+                                                     SampleOut O) {
+  __shared__ uint64_t s_tot[2];
+  __shared__ int s_cstar;
+  __shared__ uint64_t s_before;
+  __shared__ uint64_t s_ws[kT / kWave];
+  __shared__ long long s_tok;
+  const int unit = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const SeqState st = W.st[unit];
+  const int R = P.rows_per_unit;
+  const int row = st.row;
+  if (st.kind == kKindNone || row < unit * R || row >= (unit + 1) * R) return;
+  const bool residual = (st.kind == kKindResidual);
+  const SampPart* spp = W.spart + (int64_t)unit * P.nchunk;
+
+  if (wid == 0) {
+    uint64_t wt = 0, pt = 0;
+    for (int c = lane; c < P.nchunk; c += kWave) {
+      wt += spp[c].w;
+      pt += spp[c].p;
+    }
+    wt = wave_sum_u64(wt);
+    pt = wave_sum_u64(pt);
+    // residual normalisation or fallback to P[r] (model_runner.py:419-424)
+    const bool use_res = residual && (hs_f32_of_u64(wt) * kTwoM44 > 1e-10f);
+    const uint64_t total = use_res ? wt : pt;
+    const uint64_t t = hs_mulshift24(hs_u24(O.uniforms[unit]), total);
+    int cstar = -1;
+    uint64_t before = 0, running = 0;
+    for (int cb = 0; cb < P.nchunk && cstar < 0; cb += kWave) {
+      const int c = cb + lane;
+      uint64_t val = 0;
+      if (c < P.nchunk) val = use_res ? spp[c].w : spp[c].p;
+      const uint64_t incl = wave_incl_scan_u64(val, lane);
+      const uint64_t m = __ballot(running + incl > t);
+      if (m) {
+        const int l = __ffsll((long long)m) - 1;
+        const uint64_t incl_l = __shfl(incl, l, 64);
+        const uint64_t val_l = __shfl(val, l, 64);
+        cstar = cb + l;
+        before = running + incl_l - val_l;
+      } else {
+        running += __shfl(incl, 63, 64);
+      }
+    }
+    if (lane == 0) {
+      s_tot[0] = use_res ? 1ull : 0ull;
+      s_tot[1] = t;
+      s_cstar = cstar;
+      s_before = before;
+      s_tok = -1;
+    }
+  }
+  __syncthreads();
+  const int cstar = s_cstar;
+  if (cstar >= 0) {
+    const bool use_res = s_tot[0] != 0;
+    const uint64_t trel = s_tot[1] - s_before;
+    const RowDesc D = W.desc[row];
+    const float Tt = P.temps[unit];
+    const float rT = 1.0f / Tt;
+    const bool fastT = hs_rcp_ok(Tt);
+    const float rS = 1.0f / D.s;
+    const bool fastS = hs_rcp_ok(D.s);
+    const T* rp = reinterpret_cast<const T*>(P.logits) + (int64_t)row * P.row_stride;
+    const bool vec_ok = ((reinterpret_cast<uintptr_t>(rp) & 15u) == 0);
+    const float* qp = residual ? A.q + (int64_t)st.qrow * A.q_stride : nullptr;
+    const bool q_vec = residual && ((reinterpret_cast<uintptr_t>(qp) & 15u) == 0);
+    const int64_t i0 = chunk_elem(cstar, tid, 0);
+    float v[8], q[8];
+    uint64_t w[8];
+    load8<T>(rp, i0, P.V, vec_ok, v);
+    if (residual) load8_f32(qp, i0, P.V, q_vec, q);
+    uint64_t s = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int64_t i = i0 + k;
+      float p = 0.0f;
+      if (i < P.V) {
+        const float x = hs_div_temp(v[k], Tt, rT, fastT);
+        if (desc_keep(D, hs_key(x), i)) {
+          const float e = hs_exp(x - D.m);
+          p = fastS ? hs_div_rcp(e, D.s, rS) : e / D.s;
+        }
+      }
+      const float wt = use_res ? fmaxf(p - q[k], 0.0f) : p;
+      uint32_t hi = 0, lo = 0;
+      hs_fx44_split(wt, hi, lo);
+      w[k] = hs_join44(hi, lo);
+      s += w[k];
+    }
+    // block-wide inclusive scan in element order (thread order)
+    const uint64_t incl = wave_incl_scan_u64(s, lane);
+    if (lane == 63) s_ws[wid] = incl;
+    __syncthreads();
+    uint64_t off = 0;
+    for (int ww = 0; ww < wid; ++ww) off += s_ws[ww];
+    const uint64_t lo_ = off + incl - s;
+    if (lo_ <= trel && trel < off + incl) {
+      uint64_t acc = lo_;
+      for (int k = 0; k < 8; ++k) {
+        acc += w[k];
+        if (acc > trel) {
+          s_tok = (long long)(i0 + k);
+          break;
+        }
+      }
+    }
+    __syncthreads();
+  }
+  const int64_t token = (int64_t)s_tok;
   if (A.tok_out) {
     const int gm = A.gamma;
-    if (lane <= gm) {
+    if (tid <= gm) {
       int64_t v;
-      if (lane < st.nacc) v = A.dtok[(int64_t)unit * gm + lane];
-      else if (lane == st.nacc) v = token;
+      if (tid < st.nacc) v = A.dtok[(int64_t)unit * gm + tid];
+      else if (tid == st.nacc) v = token;
       else v = -1;
-      A.tok_out[(int64_t)unit * (gm + 1) + lane] = v;
+      A.tok_out[(int64_t)unit * (gm + 1) + tid] = v;
     }
-    if (lane == 0) {
+    if (tid == 0) {
       A.nacc_out[unit] = st.nacc;
       A.len_out[unit] = st.nacc + 1;
     }
   }
-  if (O.tokens && lane == 0) O.tokens[unit] = token;
+  if (O.tokens && tid == 0) O.tokens[unit] = token;
 }
 
 // ---------------------------------------------------------------------------
@@ -354,15 +432,9 @@ __global__ __launch_bounds__(64) void k_sample(Problem P, AcceptArgs A, Work W, 
 // ---------------------------------------------------------------------------
 static inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
-// The ticket counters come first, at fixed offsets for every shape (one slot
-// per possible row/unit), so the "counters are left zero" invariant holds
-// across calls of different shapes that share one workspace.
 Layout make_layout(int units, int rows, int nchunk) {
   Layout L;
   size_t off = 0;
-  L.rowctr = off; off = align_up(off + (size_t)kMaxRows * sizeof(uint32_t), 256);
-  L.unitctr = off; off = align_up(off + (size_t)kMaxRows * sizeof(uint32_t), 256);
-  L.sampctr = off; off = align_up(off + (size_t)kMaxRows * sizeof(uint32_t), 256);
   L.part = off; off = align_up(off + (size_t)rows * nchunk * sizeof(ChunkStat), 256);
   L.desc = off; off = align_up(off + (size_t)rows * sizeof(RowDesc), 256);
   L.st = off; off = align_up(off + (size_t)units * sizeof(SeqState), 256);
@@ -380,82 +452,56 @@ Work bind_work(void* ws, const Layout& L) {
   W.st = reinterpret_cast<SeqState*>(b + L.st);
   W.spart = reinterpret_cast<SampPart*>(b + L.spart);
   W.filt = reinterpret_cast<FilterScratch*>(b + L.filt);
-  W.rowctr = reinterpret_cast<uint32_t*>(b + L.rowctr);
-  W.unitctr = reinterpret_cast<uint32_t*>(b + L.unitctr);
-  W.sampctr = reinterpret_cast<uint32_t*>(b + L.sampctr);
   return W;
 }
 
 static inline int nchunk_of(int V) { return (V + kChunk - 1) / kChunk; }
 
-static int pick_split(int units_or_rows, int nchunk) {
-  const int target = 2048;  // waves in flight across 256 CUs
-  int s = (target + units_or_rows - 1) / units_or_rows;
+static int grid_items(int64_t items) {
+  const int64_t cap = 4096;  // 16 workgroups per CU on 256 CUs
+  return (int)(items < cap ? items : cap);
+}
+
+static int pick_split(int units, int nchunk) {
+  const int target = 1024;  // workgroups of k_sample_part
+  int s = (target + units - 1) / units;
   if (s < 1) s = 1;
   if (s > nchunk) s = nchunk;
   return s;
 }
 
-template <typename T>
-int launch_accept(const Problem& P0, const AcceptArgs& A, const Work& W, int mode, float* row_stats,
-                  const float* u_res, hipStream_t stream) {
-  Problem P = P0;
-  const int rows = P.units * P.rows_per_unit;
-  P.nsplit = pick_split(rows, P.nchunk);
-  dim3 g1(P.nsplit, rows);
-  if (mode == HS_ACCEPT_GREEDY) {
-    hipLaunchKernelGGL(k_row_argmax<T>, g1, dim3(64), 0, stream, P, A, W, (int)kFinDecide,
-                       (int64_t*)nullptr);
-    return hipGetLastError() == hipSuccess ? HS_OK : HS_ERR_LAUNCH;
-  }
-  const int fin = (mode == HS_ACCEPT_FILTERED) ? kFinRow : kFinDecide;
-  hipLaunchKernelGGL(k_row_stats<T>, g1, dim3(64), 0, stream, P, A, W, fin, row_stats);
-  if (mode == HS_ACCEPT_FILTERED) {
-    int rc = launch_filter<T>(P, A, W, /*decide=*/1, row_stats, stream);
-    if (rc != HS_OK) return rc;
-  }
-  Problem P2 = P;
-  P2.nsplit = pick_split(P.units, P.nchunk);
-  SampleOut O;
-  O.probs = nullptr;
-  O.probs_stride = 0;
-  O.out_kind = 0;
-  O.uniforms = u_res;
-  O.tokens = nullptr;
-  O.sample = 1;
-  hipLaunchKernelGGL(k_sample<T>, dim3(P2.nsplit, P.units), dim3(64), 0, stream, P2, A, W, O);
-  return hipGetLastError() == hipSuccess ? HS_OK : HS_ERR_LAUNCH;
-}
+static inline int launch_ok() { return hipGetLastError() == hipSuccess ? HS_OK : HS_ERR_LAUNCH; }
 
 template <typename T>
-int launch_sampler(const Problem& P0, const Work& W, int mode, float* probs, int64_t probs_stride,
-                   int out_kind, const float* uniforms, int64_t* tokens, float* row_stats,
-                   hipStream_t stream) {
+int run_sampler_chain(const Problem& P0, const AcceptArgs& A, const Work& W, int mode,
+                      SampleOut O, hipStream_t stream) {
   Problem P = P0;
-  const int rows = P.units;
-  P.nsplit = pick_split(rows, P.nchunk);
-  AcceptArgs A;
-  memset(&A, 0, sizeof(A));
-  dim3 g1(P.nsplit, rows);
+  const int rows = P.units * P.rows_per_unit;
+  const int64_t items = (int64_t)rows * P.nchunk;
   if (mode == HS_ACCEPT_GREEDY) {
-    hipLaunchKernelGGL(k_row_argmax<T>, g1, dim3(64), 0, stream, P, A, W, (int)kFinPlain, tokens);
-    return hipGetLastError() == hipSuccess ? HS_OK : HS_ERR_LAUNCH;
+    hipLaunchKernelGGL(k_chunk_argmax<T>, dim3(grid_items(items)), dim3(kT), 0, stream, P, W);
+    hipLaunchKernelGGL(k_greedy_final, dim3(P.units), dim3(kWave), 0, stream, P, A, W, O.tokens);
+    return launch_ok();
   }
-  hipLaunchKernelGGL(k_row_stats<T>, g1, dim3(64), 0, stream, P, A, W, (int)kFinPlain, row_stats);
-  if (mode == HS_ACCEPT_FILTERED) {
-    int rc = launch_filter<T>(P, A, W, /*decide=*/0, row_stats, stream);
+  hipLaunchKernelGGL(k_chunk_stats<T>, dim3(grid_items(items)), dim3(kT), 0, stream, P, W);
+  const bool filtered = (mode == HS_ACCEPT_FILTERED);
+  if (filtered) {
+    int rc = launch_filter<T>(P, W, O.row_stats, stream);
     if (rc != HS_OK) return rc;
   }
-  if (!probs && !tokens) return hipGetLastError() == hipSuccess ? HS_OK : HS_ERR_LAUNCH;
-  SampleOut O;
-  O.probs = probs;
-  O.probs_stride = probs_stride;
-  O.out_kind = out_kind;
-  O.uniforms = uniforms;
-  O.tokens = tokens;
-  O.sample = tokens ? 1 : 0;
-  hipLaunchKernelGGL(k_sample<T>, dim3(P.nsplit, rows), dim3(64), 0, stream, P, A, W, O);
-  return hipGetLastError() == hipSuccess ? HS_OK : HS_ERR_LAUNCH;
+  if (!O.probs && !O.sample) {
+    // statistics only: one workgroup per unit folds the rows for row_stats
+    P.nsplit = P.nchunk;  // no chunk lies in split 0's range when nsplit > nchunk - 1
+    hipLaunchKernelGGL(k_sample_part<T>, dim3(1, P.units), dim3(kT), 0, stream, P, A, W, O, mode,
+                       filtered ? 1 : 0);
+    return launch_ok();
+  }
+  P.nsplit = pick_split(P.units, P.nchunk);
+  hipLaunchKernelGGL(k_sample_part<T>, dim3(P.nsplit, P.units), dim3(kT), 0, stream, P, A, W, O,
+                     mode, filtered ? 1 : 0);
+  if (O.sample)
+    hipLaunchKernelGGL(k_sample_final<T>, dim3(P.units), dim3(kT), 0, stream, P, A, W, O);
+  return launch_ok();
 }
 
 }  // namespace hs
@@ -475,7 +521,7 @@ const char* hs_status_string(int status) {
   }
 }
 
-int hs_version(void) { return (0 << 16) | 1; }
+int hs_version(void) { return (0 << 16) | 2; }
 
 size_t hs_spec_accept_workspace_size(int batch, int gamma, int vocab) {
   if (batch <= 0 || gamma <= 0 || vocab <= 0) return 0;
@@ -491,7 +537,7 @@ int hs_spec_accept(const void* target_logits, int logits_dtype, int64_t logits_r
                    int32_t* num_accepted, int64_t* out_tokens, int32_t* out_len,
                    float* row_stats, void* workspace, size_t workspace_bytes, void* stream) {
   if (batch <= 0 || gamma <= 0 || gamma > kMaxGamma || vocab <= 0) return HS_ERR_INVALID;
-  if ((int64_t)batch * (gamma + 1) > kMaxRows) return HS_ERR_UNSUPPORTED;
+  if (batch > kMaxRows) return HS_ERR_UNSUPPORTED;
   if (mode != HS_ACCEPT_REFERENCE && mode != HS_ACCEPT_FILTERED && mode != HS_ACCEPT_GREEDY)
     return HS_ERR_INVALID;
   if (logits_dtype != HS_F32 && logits_dtype != HS_BF16) return HS_ERR_INVALID;
@@ -527,11 +573,18 @@ int hs_spec_accept(const void* target_logits, int logits_dtype, int64_t logits_r
   A.nacc_out = num_accepted;
   A.tok_out = out_tokens;
   A.len_out = out_len;
+  SampleOut O;
+  O.probs = nullptr;
+  O.probs_stride = 0;
+  O.out_kind = 0;
+  O.uniforms = u_resample;
+  O.tokens = nullptr;
+  O.sample = 1;
+  O.row_stats = row_stats;
   Work W = bind_work(workspace, L);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (logits_dtype == HS_F32)
-    return launch_accept<float>(P, A, W, mode, row_stats, u_resample, s);
-  return launch_accept<uint16_t>(P, A, W, mode, row_stats, u_resample, s);
+  if (logits_dtype == HS_F32) return run_sampler_chain<float>(P, A, W, mode, O, s);
+  return run_sampler_chain<uint16_t>(P, A, W, mode, O, s);
 }
 
 size_t hs_sampler_workspace_size(int rows, int vocab) {
@@ -575,13 +628,20 @@ int hs_sampler(const void* logits, int logits_dtype, int64_t logits_row_stride, 
   P.temps = temperatures;
   P.top_ks = top_ks;
   P.top_ps = top_ps;
+  AcceptArgs A;
+  memset(&A, 0, sizeof(A));
+  SampleOut O;
+  O.probs = probs_out;
+  O.probs_stride = probs_row_stride;
+  O.out_kind = out_kind;
+  O.uniforms = uniforms;
+  O.tokens = tokens_out;
+  O.sample = (mode != HS_ACCEPT_GREEDY && tokens_out) ? 1 : 0;
+  O.row_stats = row_stats;
   Work W = bind_work(workspace, L);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (logits_dtype == HS_F32)
-    return launch_sampler<float>(P, W, mode, probs_out, probs_row_stride, out_kind, uniforms,
-                                 tokens_out, row_stats, s);
-  return launch_sampler<uint16_t>(P, W, mode, probs_out, probs_row_stride, out_kind, uniforms,
-                                  tokens_out, row_stats, s);
+  if (logits_dtype == HS_F32) return run_sampler_chain<float>(P, A, W, mode, O, s);
+  return run_sampler_chain<uint16_t>(P, A, W, mode, O, s);
 }
 
 }  // extern "C"

@@ -19,7 +19,7 @@
 //   2. top-p: the same scheme with exact mass histograms (u64 LDS atomics);
 //      ties at the final key are resolved in closed form (equal keys have
 //      equal mass) plus one index-ordered pass when a tie is split.
-// The last row of a sequence then runs the acceptance test (decide_unit).
+// The acceptance test runs afterwards in k_sample_part (spec_accept.hip).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -299,9 +299,9 @@ __device__ void lds_top_p(FilterSmem& sm, int n, float M, float sA, bool p_on, u
 }
 
 template <typename T>
-__global__ __launch_bounds__(kFT) void k_row_filter(Problem P, AcceptArgs A, Work W, int decide,
-                                                    float* row_stats) {
+__global__ __launch_bounds__(kFT) void k_row_filter(Problem P, Work W, float* row_stats) {
   __shared__ FilterSmem sm;
+  __shared__ RowDesc s_fold;
   const int row = blockIdx.x;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wid = tid >> 6;
@@ -313,8 +313,20 @@ __global__ __launch_bounds__(kFT) void k_row_filter(Problem P, AcceptArgs A, Wor
   const bool k_on = keff < V;
   const bool p_on = pp < 1.0f;
 
+  if (wid == 0) {
+    const RowDesc d = fold_row_desc(P, W, row, lane);
+    if (lane == 0) s_fold = d;
+  }
+  __syncthreads();
+  if (!(k_on || p_on) && tid == 0) {
+    W.desc[row] = s_fold;
+    if (row_stats) {
+      row_stats[2 * (int64_t)row] = s_fold.m;
+      row_stats[2 * (int64_t)row + 1] = s_fold.s;
+    }
+  }
   if (k_on || p_on) {
-    RowDesc D = W.desc[row];
+    RowDesc D = s_fold;
     RowCtx<T> C;
     C.rp = reinterpret_cast<const T*>(P.logits) + (int64_t)row * P.row_stride;
     C.vec_ok = ((reinterpret_cast<uintptr_t>(C.rp) & 15u) == 0);
@@ -560,29 +572,22 @@ __global__ __launch_bounds__(kFT) void k_row_filter(Problem P, AcceptArgs A, Wor
       fs.path = cand_ready ? 1 : 0;
       fs.pad[0] = fs.pad[1] = 0;
       W.filt[row] = fs;
-      if (row_stats) row_stats[2 * (int64_t)row + 1] = sB;
+      if (row_stats) {
+        row_stats[2 * (int64_t)row] = d.m;
+        row_stats[2 * (int64_t)row + 1] = sB;
+      }
     }
   }
-
-  if (!decide) return;
-  __syncthreads();
-  if (wid != 0) return;
-  if (!last_ticket(W.unitctr + unit, (uint32_t)P.rows_per_unit, lane)) return;
-  decide_unit<T>(P, A, W, unit, lane);
 }
 
 template <typename T>
-int launch_filter(const Problem& P, const AcceptArgs& A, const Work& W, int decide,
-                  float* row_stats, hipStream_t stream) {
+int launch_filter(const Problem& P, const Work& W, float* row_stats, hipStream_t stream) {
   const int rows = P.units * P.rows_per_unit;
-  hipLaunchKernelGGL(k_row_filter<T>, dim3(rows), dim3(kFT), 0, stream, P, A, W, decide,
-                     row_stats);
+  hipLaunchKernelGGL(k_row_filter<T>, dim3(rows), dim3(kFT), 0, stream, P, W, row_stats);
   return hipGetLastError() == hipSuccess ? HS_OK : HS_ERR_LAUNCH;
 }
 
-template int launch_filter<float>(const Problem&, const AcceptArgs&, const Work&, int, float*,
-                                  hipStream_t);
-template int launch_filter<uint16_t>(const Problem&, const AcceptArgs&, const Work&, int, float*,
-                                     hipStream_t);
+template int launch_filter<float>(const Problem&, const Work&, float*, hipStream_t);
+template int launch_filter<uint16_t>(const Problem&, const Work&, float*, hipStream_t);
 
 }  // namespace hs

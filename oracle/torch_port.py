@@ -1,0 +1,58 @@
+"""torch-CPU restatement of the reference acceptance loop (CPU baseline only).
+
+TEST INFRASTRUCTURE: used by bench.py's cpu_baseline leg and by tests that
+compare it with the C oracle; never by the product path.
+
+It follows ModelRunner.run_verify's per-sequence loop,
+mini_vllm/engine/model_runner.py:391-428, operation by operation on torch
+CPU tensors, with torch.rand (:407) and torch.multinomial (:412, :425)
+replaced by the explicit uniforms u_accept / u_resample (inverse CDF over the
+normalised weights, torch.searchsorted).
+"""
+from __future__ import annotations
+
+import torch
+
+
+def _draw(weights: torch.Tensor, u: float) -> int:
+    c = torch.cumsum(weights.double(), 0)
+    i = int(torch.searchsorted(c, torch.tensor([u * float(c[-1])], dtype=torch.float64),
+                               right=True)[0])
+    return min(i, weights.shape[0] - 1)
+
+
+def run_verify_accept(logits: torch.Tensor, draft_probs: torch.Tensor,
+                      draft_tokens: torch.Tensor, temperatures: torch.Tensor,
+                      u_accept: torch.Tensor, u_resample: torch.Tensor):
+    """logits [B, gamma+1, V], draft_probs [B, gamma, V] -> list[(tokens, n_acc)]."""
+    results = []
+    B = logits.shape[0]
+    for i in range(B):
+        seq_logits = logits[i]
+        num_draft = draft_tokens.shape[1]
+        temperature = float(temperatures[i])
+        target_probs = torch.softmax(seq_logits.float() / temperature, dim=-1)
+        draft_tok_ids = draft_tokens[i].to(torch.int64)
+        draft_probs_stacked = draft_probs[i]
+        p_target = target_probs[:num_draft].gather(1, draft_tok_ids.unsqueeze(1)).squeeze(1)
+        p_draft = draft_probs_stacked.gather(1, draft_tok_ids.unsqueeze(1)).squeeze(1)
+        accept_probs = torch.clamp(p_target / p_draft.clamp(min=1e-10), max=1.0)
+        accepted_mask = u_accept[i] < accept_probs
+        if bool(accepted_mask.all()):
+            accepted = draft_tok_ids.tolist()
+            accepted.append(_draw(target_probs[num_draft], float(u_resample[i])))
+            n_acc = num_draft
+        else:
+            first_reject = int((~accepted_mask).nonzero(as_tuple=True)[0][0])
+            accepted = draft_tok_ids[:first_reject].tolist()
+            n_acc = first_reject
+            adjusted = torch.clamp(target_probs[first_reject] - draft_probs_stacked[first_reject],
+                                   min=0)
+            s = adjusted.sum()
+            if s > 1e-10:
+                adjusted = adjusted / s
+            else:
+                adjusted = target_probs[first_reject]
+            accepted.append(_draw(adjusted, float(u_resample[i])))
+        results.append((accepted, n_acc))
+    return results
