@@ -30,6 +30,12 @@ SIGNATURES: dict[str, tuple] = {
     "hs_sampler_workspace_size": (_sz, [_i32, _i32]),
     "hs_sampler": (_i32, [_vp, _i32, _i64, _i32, _i32, _vp, _vp, _vp, _i32, _vp, _i64, _i32,
                           _vp, _vp, _vp, _vp, _sz, _vp]),
+    "hs_verify_attention_workspace_size": (_sz, [_i32, _i32, _i32, _i32, _i32]),
+    "hs_verify_attention": (_i32, [_vp, _i64, _i64, _vp, _vp, _i32, _i64, _i64, _i64, _f32, _f32,
+                                   _vp, _i64, _i32, _i32, _vp, _vp, _i32, _i32, _i32, _i32, _i32,
+                                   _i32, _i32, _f32, _vp, _i64, _i64, _vp, _sz, _vp]),
+    "hs_store_kvcache": (_i32, [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i32, _i64, _i64,
+                                _i64, _f32, _f32, _vp, _i32, _i32, _i32, _i32, _i32, _vp]),
 }
 
 _lib = None

@@ -1,0 +1,472 @@
+// gamma+1-query paged-attention verify kernel for gfx950 (MFMA 16x16x32 bf16).
+//
+// Replaces the verify branch of Attention.forward,
+// mini_vllm/layers/attention.py:145-160 (flash_attn_varlen_func over the
+// paged cache with block_table, causal=True, softmax_scale = D^-0.5), and is
+// also usable for decode (q_len 1) and prefill (q_len > gamma+1).
+//
+// Work decomposition: a workgroup (4 waves) owns one (sequence, kv head,
+// 16-row query tile, key split). The query tile holds the G = Hq/Hkv query
+// heads of up to 16/G consecutive query tokens, so one K/V head is streamed
+// once for all of them (GQA). Each wave walks 32-key windows of the split:
+//   S^T[32 keys x 16 rows] = K (A operand, 16-byte loads straight from the
+//                             paged cache) x Q^T (B operand, registers)
+//   online softmax in the S^T layout (one query row per lane column),
+//   O^T[128 x 16] += V^T (A operand, from a per-wave transposed LDS tile)
+//                    x P^T (B operand: the exp2'd S^T values of the lane),
+// so P never leaves registers. Causal alignment is bottom-right: query token
+// i of a sequence with Lq queries and Lk keys sees keys 0 .. Lk - Lq + i.
+// FP8 (e4m3fn) caches are decoded exactly to bf16 in registers; the per-tensor
+// k/v scales are folded into the softmax scale and the output.
+// Splits of one query tile are merged by k_attn_combine.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/hilda_spec.h"
+
+namespace hs {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kAW = 4;          // waves per workgroup
+constexpr int kAT = kAW * 64;   // threads per workgroup
+constexpr int kD = 128;         // head dim
+constexpr int kWin = 32;        // keys per window
+constexpr int kRows = 16;       // query rows per tile
+constexpr int kVtStride = 40;   // LDS row stride (bf16) of the transposed V tile
+
+struct AttnArgs {
+  const uint16_t* q;
+  int64_t q_st, q_sh;
+  const uint8_t* kc;
+  const uint8_t* vc;
+  int fp8;
+  int64_t c_sb, c_st, c_sh;  // element strides of the caches
+  float v_scale;
+  const int32_t* bt;
+  int64_t bt_stride;
+  int bt_width;   // entries per block-table row
+  int num_blocks;
+  const int32_t* cu_q;
+  const int32_t* cu_k;
+  int B, Hkv, G, block_size, qtiles, nsplit, split_len;
+  float scale_log2;          // softmax_scale * k_scale * log2(e)
+  uint16_t* out;
+  int64_t o_st, o_sh;
+  float* part_o;             // [B, Hkv, qtiles, nsplit, 16, 128]
+  float* part_ml;            // [B, Hkv, qtiles, nsplit, 16, 2]
+};
+
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// 8 fp8 e4m3fn bytes -> 8 bf16 (exact: every e4m3fn value is a bf16 value)
+__device__ __forceinline__ bf16x8_t fp8x8_to_bf16(uint2 raw) {
+  union {
+    uint32_t u[4];
+    bf16x8_t v;
+  } r;
+  const auto a = __builtin_amdgcn_cvt_pk_f32_fp8((int)raw.x, false);
+  const auto b = __builtin_amdgcn_cvt_pk_f32_fp8((int)raw.x, true);
+  const auto c = __builtin_amdgcn_cvt_pk_f32_fp8((int)raw.y, false);
+  const auto d = __builtin_amdgcn_cvt_pk_f32_fp8((int)raw.y, true);
+  r.u[0] = (__float_as_uint(a[0]) >> 16) | (__float_as_uint(a[1]) & 0xffff0000u);
+  r.u[1] = (__float_as_uint(b[0]) >> 16) | (__float_as_uint(b[1]) & 0xffff0000u);
+  r.u[2] = (__float_as_uint(c[0]) >> 16) | (__float_as_uint(c[1]) & 0xffff0000u);
+  r.u[3] = (__float_as_uint(d[0]) >> 16) | (__float_as_uint(d[1]) & 0xffff0000u);
+  return r.v;
+}
+
+__device__ __forceinline__ bf16x8_t u4_to_bf16x8(uint4 u) {
+  union {
+    uint4 u;
+    bf16x8_t v;
+  } r;
+  r.u = u;
+  return r.v;
+}
+
+// 8 consecutive head-dim elements of one cached token as bf16x8
+template <bool kFp8>
+__device__ __forceinline__ bf16x8_t load_kv8(const uint8_t* base, int64_t elem_off) {
+  if constexpr (kFp8) {
+    const uint2 raw = *reinterpret_cast<const uint2*>(base + elem_off);
+    return fp8x8_to_bf16(raw);
+  } else {
+    const uint4 raw = *reinterpret_cast<const uint4*>(base + elem_off * 2);
+    return u4_to_bf16x8(raw);
+  }
+}
+
+template <bool kFp8>
+__global__ __launch_bounds__(kAT) void k_verify_attn(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t s_vt[kAW][kD * kVtStride];
+  __shared__ float s_m[kAW][kRows], s_l[kAW][kRows];
+  __shared__ float s_o[kAW][kRows * kD];
+
+  const int split = blockIdx.x;
+  const int kvh = blockIdx.y / a.qtiles;
+  const int qt = blockIdx.y % a.qtiles;
+  const int b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int n = lane & 15;  // query row of this lane (B-operand column)
+  const int g = lane >> 4;  // k-group of this lane
+
+  const int qs = a.cu_q[b];
+  const int Lq = a.cu_q[b + 1] - qs;
+  const int Lk = a.cu_k[b + 1] - a.cu_k[b];
+  const int rows = Lq * a.G;
+  const int r0 = qt * kRows;
+  if (r0 >= rows || Lk <= 0) return;
+  const int nsplit_b = (Lk + a.split_len - 1) / a.split_len;
+  if (split >= nsplit_b) return;
+
+  const int lo = split * a.split_len;
+  int hi = lo + a.split_len < Lk ? lo + a.split_len : Lk;
+  {
+    const int last_row = (r0 + kRows - 1 < rows - 1) ? r0 + kRows - 1 : rows - 1;
+    const int lim = Lk - Lq + last_row / a.G + 1;  // keys visible to the tile's last token
+    if (lim < hi) hi = lim;
+  }
+
+  // query row of this lane
+  const int r = r0 + n;
+  const bool r_ok = r < rows;
+  const int qi = r_ok ? r / a.G : 0;
+  const int qh = kvh * a.G + (r_ok ? r % a.G : 0);
+  const int lim_r = Lk - Lq + qi;  // last visible key of this row
+  bf16x8_t qv[4];
+#pragma unroll
+  for (int ds = 0; ds < 4; ++ds) {
+    if (r_ok) {
+      const uint16_t* qp = a.q + (int64_t)(qs + qi) * a.q_st + (int64_t)qh * a.q_sh + ds * 32 + g * 8;
+      qv[ds] = u4_to_bf16x8(*reinterpret_cast<const uint4*>(qp));
+    } else {
+      qv[ds] = u4_to_bf16x8(make_uint4(0, 0, 0, 0));
+    }
+  }
+
+  float m = -INFINITY, lsum = 0.0f;
+  f32x4_t oacc[8];
+#pragma unroll
+  for (int db = 0; db < 8; ++db) oacc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  uint16_t* vt = s_vt[wid];
+
+  for (int ws = lo + wid * kWin; ws < hi; ws += kAW * kWin) {
+    const int blk_idx = ws / a.block_size;
+    const int blk = (blk_idx < a.bt_width) ? a.bt[(int64_t)b * a.bt_stride + blk_idx] : -1;
+    const bool blk_ok = (blk >= 0 && blk < a.num_blocks);
+    const int slot0 = ws - blk_idx * a.block_size;
+    const int64_t blk_base = (int64_t)blk * a.c_sb + (int64_t)kvh * a.c_sh;
+
+    // K as the A operand: row rho = n holds key ws + 8*(n/4) + 4*kb + (n%4)
+    bf16x8_t ka[2][4];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const int kl = 8 * (n >> 2) + 4 * kb + (n & 3);
+      const bool ok = blk_ok && (ws + kl < hi);
+      const int64_t off = blk_base + (int64_t)(slot0 + kl) * a.c_st + g * 8;
+#pragma unroll
+      for (int ds = 0; ds < 4; ++ds)
+        ka[kb][ds] = ok ? load_kv8<kFp8>(a.kc, off + ds * 32)
+                        : u4_to_bf16x8(make_uint4(0, 0, 0, 0));
+    }
+    // V rows of the window: load i holds key ws + 4*i + g, dims 8*n .. 8*n+7
+    bf16x8_t vv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int kl = 4 * i + g;
+      const bool ok = blk_ok && (ws + kl < hi);
+      const int64_t off = blk_base + (int64_t)(slot0 + kl) * a.c_st + n * 8;
+      vv[i] = ok ? load_kv8<kFp8>(a.vc, off) : u4_to_bf16x8(make_uint4(0, 0, 0, 0));
+    }
+
+    // S^T = K Q^T for the two 16-key blocks
+    f32x4_t st[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ds = 0; ds < 4; ++ds)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[kb][ds], qv[ds], acc, 0, 0, 0);
+      st[kb] = acc;
+    }
+    // lane holds row n, keys ws + 8g + 4kb + j
+    float sv[8];
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int key = ws + 8 * g + 4 * kb + j;
+        float v = st[kb][j] * a.scale_log2;
+        if (!r_ok || key >= hi || key > lim_r) v = -INFINITY;
+        sv[kb * 4 + j] = v;
+        mloc = fmaxf(mloc, v);
+      }
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+    const float m_new = fmaxf(m, mloc);
+    const float base = (m_new == -INFINITY) ? 0.0f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m - base);
+    m = m_new;
+    float psum = 0.0f;
+    union {
+      uint16_t h[8];
+      bf16x8_t v;
+    } pb;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const float p = __builtin_amdgcn_exp2f(sv[t] - base);
+      psum += p;
+      pb.h[t] = f32_to_bf16_rne(p);
+    }
+    lsum = lsum * alpha + psum;
+#pragma unroll
+    for (int db = 0; db < 8; ++db) oacc[db] *= alpha;
+
+    // V^T into LDS: vt[d][key]
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      union {
+        bf16x8_t v;
+        uint16_t h[8];
+      } u;
+      u.v = vv[i];
+      const int kl = 4 * i + g;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) vt[(n * 8 + t) * kVtStride + kl] = u.h[t];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // O^T[d][row] += V^T[d][keys 8g..8g+7] * P^T
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+      const uint4 av = *reinterpret_cast<const uint4*>(&vt[(db * 16 + n) * kVtStride + 8 * g]);
+      oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(u4_to_bf16x8(av), pb.v, oacc[db], 0, 0, 0);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+
+  // per-row totals of this wave
+  lsum += __shfl_xor(lsum, 16, 64);
+  lsum += __shfl_xor(lsum, 32, 64);
+  if (g == 0) {
+    s_m[wid][n] = m;
+    s_l[wid][n] = lsum;
+  }
+  // O^T layout: lane holds O[row n][d = db*16 + 4g + j]
+#pragma unroll
+  for (int db = 0; db < 8; ++db)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s_o[wid][n * kD + db * 16 + 4 * g + j] = oacc[db][j];
+  __syncthreads();
+
+  // merge the 4 waves: thread handles row tid/16, dims (tid%16)*8 .. +8
+  const int row = tid >> 4;
+  const int d0 = (tid & 15) * 8;
+  float M = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < kAW; ++w) M = fmaxf(M, s_m[w][row]);
+  const float Mb = (M == -INFINITY) ? 0.0f : M;
+  float L = 0.0f, f[kAW];
+#pragma unroll
+  for (int w = 0; w < kAW; ++w) {
+    f[w] = __builtin_amdgcn_exp2f(s_m[w][row] - Mb);
+    L += s_l[w][row] * f[w];
+  }
+  float o[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kAW; ++w) acc += s_o[w][row * kD + d0 + t] * f[w];
+    o[t] = acc;
+  }
+  const int rr = r0 + row;
+  if (rr >= rows) return;
+  const int oi = rr / a.G, oh = kvh * a.G + rr % a.G;
+  if (nsplit_b == 1) {
+    const float inv = (L > 0.0f) ? a.v_scale / L : 0.0f;
+    union {
+      uint16_t h[8];
+      uint4 u;
+    } ob;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) ob.h[t] = f32_to_bf16_rne(o[t] * inv);
+    *reinterpret_cast<uint4*>(a.out + (int64_t)(qs + oi) * a.o_st + (int64_t)oh * a.o_sh + d0) = ob.u;
+  } else {
+    const int64_t pidx =
+        ((((int64_t)b * a.Hkv + kvh) * a.qtiles + qt) * a.nsplit + split) * kRows + row;
+    float* po = a.part_o + pidx * kD + d0;
+    *reinterpret_cast<float4*>(po) = make_float4(o[0], o[1], o[2], o[3]);
+    *reinterpret_cast<float4*>(po + 4) = make_float4(o[4], o[5], o[6], o[7]);
+    if ((tid & 15) == 0) {
+      a.part_ml[pidx * 2] = M;
+      a.part_ml[pidx * 2 + 1] = L;
+    }
+  }
+}
+
+// merges the key splits of every (sequence, kv head, query tile)
+__global__ __launch_bounds__(kAT) void k_attn_combine(AttnArgs a) {
+  const int kvh = blockIdx.y / a.qtiles;
+  const int qt = blockIdx.y % a.qtiles;
+  const int b = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int qs = a.cu_q[b];
+  const int Lq = a.cu_q[b + 1] - qs;
+  const int Lk = a.cu_k[b + 1] - a.cu_k[b];
+  const int rows = Lq * a.G;
+  const int r0 = qt * kRows;
+  if (r0 >= rows || Lk <= 0) return;
+  const int ns = (Lk + a.split_len - 1) / a.split_len;
+  if (ns <= 1) return;
+  const int row = tid >> 4;
+  const int d0 = (tid & 15) * 8;
+  const int rr = r0 + row;
+  if (rr >= rows) return;
+  const int64_t base = (((int64_t)b * a.Hkv + kvh) * a.qtiles + qt) * a.nsplit;
+  float M = -INFINITY;
+  for (int s = 0; s < ns; ++s) M = fmaxf(M, a.part_ml[((base + s) * kRows + row) * 2]);
+  const float Mb = (M == -INFINITY) ? 0.0f : M;
+  float L = 0.0f, o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int s = 0; s < ns; ++s) {
+    const int64_t pidx = (base + s) * kRows + row;
+    const float f = __builtin_amdgcn_exp2f(a.part_ml[pidx * 2] - Mb);
+    L += a.part_ml[pidx * 2 + 1] * f;
+    const float4 x0 = *reinterpret_cast<const float4*>(a.part_o + pidx * kD + d0);
+    const float4 x1 = *reinterpret_cast<const float4*>(a.part_o + pidx * kD + d0 + 4);
+    o[0] += x0.x * f; o[1] += x0.y * f; o[2] += x0.z * f; o[3] += x0.w * f;
+    o[4] += x1.x * f; o[5] += x1.y * f; o[6] += x1.z * f; o[7] += x1.w * f;
+  }
+  const float inv = (L > 0.0f) ? a.v_scale / L : 0.0f;
+  const int oi = rr / a.G, oh = kvh * a.G + rr % a.G;
+  union {
+    uint16_t h[8];
+    uint4 u;
+  } ob;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) ob.h[t] = f32_to_bf16_rne(o[t] * inv);
+  *reinterpret_cast<uint4*>(a.out + (int64_t)(qs + oi) * a.o_st + (int64_t)oh * a.o_sh + d0) = ob.u;
+}
+
+static void attn_plan(int B, int Hkv, int qtiles, int max_seqlen_k, int* nsplit, int* split_len) {
+  const int64_t tiles = (int64_t)B * Hkv * qtiles;
+  const int64_t target = 1024;  // workgroups in flight across 256 CUs
+  int64_t want = (target + tiles - 1) / tiles;
+  if (want < 1) want = 1;
+  int64_t len = (max_seqlen_k + want - 1) / want;
+  len = (len + 127) / 128 * 128;
+  if (len < 128) len = 128;
+  *split_len = (int)len;
+  *nsplit = (int)((max_seqlen_k + len - 1) / len);
+  if (*nsplit < 1) *nsplit = 1;
+}
+
+}  // namespace hs
+
+using namespace hs;
+
+extern "C" {
+
+size_t hs_verify_attention_workspace_size(int num_seqs, int num_q_heads, int num_kv_heads,
+                                          int max_seqlen_q, int max_seqlen_k) {
+  if (num_seqs <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 || max_seqlen_q <= 0 ||
+      max_seqlen_k <= 0 || num_q_heads % num_kv_heads)
+    return 0;
+  const int G = num_q_heads / num_kv_heads;
+  const int qtiles = (max_seqlen_q * G + kRows - 1) / kRows;
+  int nsplit, split_len;
+  attn_plan(num_seqs, num_kv_heads, qtiles, max_seqlen_k, &nsplit, &split_len);
+  const size_t parts = (size_t)num_seqs * num_kv_heads * qtiles * nsplit * kRows;
+  return parts * kD * sizeof(float) + parts * 2 * sizeof(float) + 256;
+}
+
+int hs_verify_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                        const void* k_cache, const void* v_cache, int kv_dtype,
+                        int64_t cache_stride_block, int64_t cache_stride_tok,
+                        int64_t cache_stride_head, float k_scale, float v_scale,
+                        const int32_t* block_tables, int64_t block_table_stride,
+                        int block_table_width, int num_blocks,
+                        const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int num_seqs,
+                        int max_seqlen_q, int max_seqlen_k, int num_q_heads, int num_kv_heads,
+                        int head_dim, int block_size, float softmax_scale, void* out,
+                        int64_t out_stride_tok, int64_t out_stride_head, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  if (!q || !k_cache || !v_cache || !block_tables || !cu_seqlens_q || !cu_seqlens_k || !out)
+    return HS_ERR_INVALID;
+  if (num_seqs <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || max_seqlen_q <= 0 ||
+      max_seqlen_k <= 0 || num_blocks <= 0 || block_size <= 0 || block_table_width <= 0 ||
+      block_table_stride < block_table_width)
+    return HS_ERR_INVALID;
+  if (num_q_heads % num_kv_heads) return HS_ERR_INVALID;
+  if (head_dim != kD) return HS_ERR_UNSUPPORTED;
+  if (block_size % kWin) return HS_ERR_UNSUPPORTED;
+  if (kv_dtype != HS_BF16 && kv_dtype != HS_FP8_E4M3) return HS_ERR_INVALID;
+  const int G = num_q_heads / num_kv_heads;
+  if (G > kRows) return HS_ERR_UNSUPPORTED;
+  // 16-byte alignment of every row the kernel loads or stores
+  const int esz = (kv_dtype == HS_BF16) ? 2 : 1;
+  if ((q_stride_tok % 8) || (q_stride_head % 8) || (out_stride_tok % 8) || (out_stride_head % 8))
+    return HS_ERR_UNSUPPORTED;
+  if (((cache_stride_block * esz) % 16) || ((cache_stride_tok * esz) % 16) ||
+      ((cache_stride_head * esz) % 16))
+    return HS_ERR_UNSUPPORTED;
+  if (((uintptr_t)q | (uintptr_t)out | (uintptr_t)k_cache | (uintptr_t)v_cache) & 15)
+    return HS_ERR_UNSUPPORTED;
+  const size_t need = hs_verify_attention_workspace_size(num_seqs, num_q_heads, num_kv_heads,
+                                                         max_seqlen_q, max_seqlen_k);
+  AttnArgs a;
+  a.qtiles = (max_seqlen_q * G + kRows - 1) / kRows;
+  attn_plan(num_seqs, num_kv_heads, a.qtiles, max_seqlen_k, &a.nsplit, &a.split_len);
+  if (a.nsplit > 1 && (!workspace || workspace_bytes < need)) return HS_ERR_WORKSPACE;
+  if ((int64_t)num_kv_heads * a.qtiles > 65535 || num_seqs > 65535) return HS_ERR_UNSUPPORTED;
+  a.q = static_cast<const uint16_t*>(q);
+  a.q_st = q_stride_tok;
+  a.q_sh = q_stride_head;
+  a.kc = static_cast<const uint8_t*>(k_cache);
+  a.vc = static_cast<const uint8_t*>(v_cache);
+  a.fp8 = (kv_dtype == HS_FP8_E4M3);
+  a.c_sb = cache_stride_block;
+  a.c_st = cache_stride_tok;
+  a.c_sh = cache_stride_head;
+  a.v_scale = a.fp8 ? v_scale : 1.0f;
+  a.bt = block_tables;
+  a.bt_stride = block_table_stride;
+  a.bt_width = block_table_width;
+  a.num_blocks = num_blocks;
+  a.cu_q = cu_seqlens_q;
+  a.cu_k = cu_seqlens_k;
+  a.B = num_seqs;
+  a.Hkv = num_kv_heads;
+  a.G = G;
+  a.block_size = block_size;
+  a.scale_log2 = softmax_scale * (a.fp8 ? k_scale : 1.0f) * 1.4426950408889634f;
+  a.out = static_cast<uint16_t*>(out);
+  a.o_st = out_stride_tok;
+  a.o_sh = out_stride_head;
+  const size_t parts = (size_t)num_seqs * num_kv_heads * a.qtiles * a.nsplit * kRows;
+  a.part_o = static_cast<float*>(workspace);
+  a.part_ml = workspace ? static_cast<float*>(workspace) + parts * kD : nullptr;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  dim3 grid(a.nsplit, num_kv_heads * a.qtiles, num_seqs);
+  if (a.fp8)
+    hipLaunchKernelGGL(k_verify_attn<true>, grid, dim3(kAT), 0, s, a);
+  else
+    hipLaunchKernelGGL(k_verify_attn<false>, grid, dim3(kAT), 0, s, a);
+  if (a.nsplit > 1)
+    hipLaunchKernelGGL(k_attn_combine, dim3(num_seqs, num_kv_heads * a.qtiles), dim3(kAT), 0, s,
+                       a);
+  return hipGetLastError() == hipSuccess ? HS_OK : HS_ERR_LAUNCH;
+}
+
+}  // extern "C"

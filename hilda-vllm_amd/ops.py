@@ -2,8 +2,9 @@
 
 Each wrapper validates shapes on the host, passes raw device pointers and the
 current HIP stream to libhilda_spec.so and raises RuntimeError on any non-zero
-status. Workspaces are allocated once per (device, kind), zero-filled, and
-reused: the kernels leave their counters zeroed after every call.
+status. Workspaces (intermediate partial results only, no initialisation
+needed) are allocated once per (device, kind) and reused; calls on one device
+are ordered by the current stream.
 """
 from __future__ import annotations
 
@@ -186,3 +187,83 @@ def sample_rows(logits: torch.Tensor, temperatures: torch.Tensor | None = None,
                         p(toks), p(stats), ws.data_ptr(), ws.numel(), _stream(dev))
     L.check(rc, "hs_sampler")
     return dict(probs=probs, tokens=toks, row_stats=stats)
+
+
+_KV_DTYPES = {torch.bfloat16: L.HS_BF16, torch.float8_e4m3fn: L.HS_FP8_E4M3}
+
+
+def _kv_code(cache: torch.Tensor) -> int:
+    if cache.dtype not in _KV_DTYPES:
+        raise TypeError(f"KV cache must be bfloat16 or float8_e4m3fn, got {cache.dtype}")
+    return _KV_DTYPES[cache.dtype]
+
+
+def verify_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                     block_tables: torch.Tensor, cu_seqlens_q: torch.Tensor,
+                     cu_seqlens_k: torch.Tensor, max_seqlen_q: int, max_seqlen_k: int,
+                     softmax_scale: float, *, k_scale: float = 1.0, v_scale: float = 1.0,
+                     out: torch.Tensor | None = None) -> torch.Tensor:
+    """Paged causal attention over the KV cache (attention.py:145-160 semantics).
+
+    q [tokens, Hq, 128] bf16; k_cache/v_cache [num_blocks, block_size, Hkv, 128]
+    bf16 or float8_e4m3fn (dequantised as code * k_scale / v_scale);
+    block_tables int32 [B, W]; cu_seqlens_q/k int32 [B+1].
+    """
+    dev = _need_cuda(q, k_cache, v_cache, block_tables, cu_seqlens_q, cu_seqlens_k, out)
+    if q.dtype != torch.bfloat16 or q.dim() != 3 or q.stride(2) != 1:
+        raise ValueError("q must be [tokens, heads, head_dim] bf16 with contiguous head_dim")
+    if k_cache.shape != v_cache.shape or k_cache.dtype != v_cache.dtype:
+        raise ValueError("k_cache and v_cache must match")
+    if k_cache.stride() != v_cache.stride() or k_cache.stride(3) != 1:
+        raise ValueError("k_cache and v_cache need identical strides with contiguous head_dim")
+    nb, bs, Hkv, D = k_cache.shape
+    N, Hq, Dq = q.shape
+    if Dq != D:
+        raise ValueError("head_dim mismatch")
+    B = cu_seqlens_q.numel() - 1
+    bt = block_tables if block_tables.dtype == torch.int32 else block_tables.to(torch.int32)
+    if bt.dim() != 2 or bt.shape[0] < B or bt.stride(1) != 1:
+        bt = bt.contiguous()
+    cq = cu_seqlens_q.to(torch.int32).contiguous()
+    ck = cu_seqlens_k.to(torch.int32).contiguous()
+    if out is None:
+        out = torch.empty((N, Hq, D), dtype=torch.bfloat16, device=dev)
+    lib = L.lib()
+    nbytes = lib.hs_verify_attention_workspace_size(B, Hq, Hkv, int(max_seqlen_q),
+                                                    int(max_seqlen_k))
+    ws = workspace(dev, nbytes, "attention")
+    rc = lib.hs_verify_attention(
+        q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(),
+        _kv_code(k_cache), k_cache.stride(0), k_cache.stride(1), k_cache.stride(2),
+        float(k_scale), float(v_scale), bt.data_ptr(), bt.stride(0), bt.shape[1], nb,
+        cq.data_ptr(), ck.data_ptr(), B, int(max_seqlen_q), int(max_seqlen_k), Hq, Hkv, D, bs,
+        float(softmax_scale), out.data_ptr(), out.stride(0), out.stride(1), ws.data_ptr(),
+        ws.numel(), _stream(dev))
+    L.check(rc, "hs_verify_attention")
+    return out
+
+
+def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
+                  v_cache: torch.Tensor, slot_mapping: torch.Tensor, *, k_scale: float = 1.0,
+                  v_scale: float = 1.0) -> None:
+    """Writes key/value [N, Hkv, 128] bf16 into the paged cache (attention.py:59-90)."""
+    dev = _need_cuda(key, value, k_cache, v_cache, slot_mapping)
+    if key.dtype != torch.bfloat16 or value.dtype != torch.bfloat16:
+        raise TypeError("key/value must be bfloat16")
+    N, Hkv, D = key.shape
+    if slot_mapping.numel() != N:
+        raise ValueError("slot_mapping must have one entry per token")
+    if key.stride(2) != 1 or value.stride(2) != 1:
+        raise ValueError("head_dim must be contiguous")
+    if k_cache.stride() != v_cache.stride() or k_cache.stride(3) != 1:
+        raise ValueError("k_cache and v_cache need identical strides with contiguous head_dim")
+    nb, bs, Hc, Dc = k_cache.shape
+    if (Hc, Dc) != (Hkv, D):
+        raise ValueError("cache geometry mismatch")
+    sm = slot_mapping.to(torch.int32).contiguous()
+    rc = L.lib().hs_store_kvcache(
+        key.data_ptr(), key.stride(0), key.stride(1), value.data_ptr(), value.stride(0),
+        value.stride(1), k_cache.data_ptr(), v_cache.data_ptr(), _kv_code(k_cache),
+        k_cache.stride(0), k_cache.stride(1), k_cache.stride(2), float(k_scale), float(v_scale),
+        sm.data_ptr(), N, Hkv, D, bs, nb, _stream(dev))
+    L.check(rc, "hs_store_kvcache")

@@ -121,3 +121,48 @@ def digest(arrays: dict) -> str:
             h.update(k.encode())
             h.update(np.ascontiguousarray(v).tobytes())
     return h.hexdigest()
+
+
+def attention_workload(batch: int = 64, q_len: int = 4, num_q_heads: int = 16,
+                       num_kv_heads: int = 8, head_dim: int = 128, block_size: int = 256,
+                       min_len: int = 64, max_len: int = 2048, seed: int = 0,
+                       spare_blocks: int = 3, lens=None) -> dict:
+    """Paged verify attention inputs (config 2 by default).
+
+    Context lengths Lk ~ U[min_len, max_len] (or `lens`), q_len query tokens per
+    sequence (the last q_len positions), blocks of block_size tokens assigned
+    by a random permutation; Q, K, V ~ N(0, 1) rounded to bf16. Cache slots
+    past each sequence's length hold NaN so reads beyond Lk are detectable.
+    """
+    rng = _rng(seed)
+    if lens is None:
+        lens = rng.integers(min_len, max_len + 1, size=batch)
+    lens = np.asarray(lens, np.int64)
+    q_lens = np.minimum(np.full(batch, q_len, np.int64), lens)
+    nblk = (lens + block_size - 1) // block_size
+    num_blocks = int(nblk.sum()) + spare_blocks
+    perm = rng.permutation(num_blocks).astype(np.int32)
+    W = int(nblk.max())
+    bt = np.full((batch, W), -1, np.int32)
+    off = 0
+    for b in range(batch):
+        bt[b, :nblk[b]] = perm[off:off + nblk[b]]
+        off += nblk[b]
+    kc = rng.standard_normal((num_blocks, block_size, num_kv_heads, head_dim), dtype=np.float32)
+    vc = rng.standard_normal((num_blocks, block_size, num_kv_heads, head_dim), dtype=np.float32)
+    kc = bf16_bits_to_f32(f32_to_bf16_bits(kc))
+    vc = bf16_bits_to_f32(f32_to_bf16_bits(vc))
+    for b in range(batch):
+        last = bt[b, nblk[b] - 1]
+        used = lens[b] - (nblk[b] - 1) * block_size
+        kc[last, used:] = np.nan
+        vc[last, used:] = np.nan
+    N = int(q_lens.sum())
+    q = bf16_bits_to_f32(f32_to_bf16_bits(
+        rng.standard_normal((N, num_q_heads, head_dim), dtype=np.float32)))
+    cu_q = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    cu_k = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    return dict(q=q, k_cache=kc, v_cache=vc, block_tables=bt, cu_seqlens_q=cu_q,
+                cu_seqlens_k=cu_k, max_seqlen_q=int(q_lens.max()), max_seqlen_k=int(lens.max()),
+                softmax_scale=float(head_dim) ** -0.5, lens=lens, q_lens=q_lens,
+                num_blocks=num_blocks, block_size=block_size)

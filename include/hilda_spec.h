@@ -6,13 +6,12 @@
  * hipStream_t). Each returns 0 on success or a negative HS_ERR_* code; none of
  * them synchronises the stream or allocates device memory.
  *
- * Workspaces: query the size with the matching *_workspace_size() function,
- * allocate it once, fill it with zeros once, and reuse it. The counters live
- * at fixed offsets at the start of the workspace and every successful call
- * leaves them zeroed again, so no memset is needed between calls, also when
- * consecutive calls differ in shape (the calls are therefore safe to record
- * into a HIP graph). Two calls that share one workspace must not overlap in
- * time.
+ * Workspaces: query the size with the matching *_workspace_size() function
+ * and pass a buffer at least that large. A workspace only carries partial
+ * results from one launch of a call to the next launch of the same call: it
+ * needs no initialisation and no clearing between calls (so the calls can be
+ * recorded into a HIP graph). Two calls that share one workspace must not
+ * overlap in time.
  */
 #ifndef HILDA_SPEC_H
 #define HILDA_SPEC_H
@@ -105,6 +104,59 @@ int hs_sampler(const void* logits, int logits_dtype, int64_t logits_row_stride,
                const float* top_ps, int mode, float* probs_out, int64_t probs_row_stride,
                int out_kind, const float* uniforms, int64_t* tokens_out, float* row_stats,
                void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* gamma+1-query paged-attention verify.                                     */
+/*                                                                          */
+/* Replaces the verify branch of Attention.forward,                          */
+/* mini_vllm/layers/attention.py:145-160: flash_attn_varlen_func(q, k_cache, */
+/* v_cache, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,          */
+/* softmax_scale, causal=True, block_table) with bottom-right causal         */
+/* alignment (query i of a sequence sees keys 0 .. Lk - Lq + i). Also serves */
+/* decode (q_len 1) and prefill.                                             */
+/*                                                                          */
+/* q, out      : [tokens, num_q_heads, 128] bf16 with element strides        */
+/*               (token, head); head elements contiguous, 16-byte aligned.   */
+/* k/v cache   : [num_blocks, block_size, num_kv_heads, 128] bf16 or fp8      */
+/*               e4m3fn (kv_dtype HS_BF16 / HS_FP8_E4M3), element strides    */
+/*               (block, token, head); fp8 values dequantise as code*scale.  */
+/* block_tables: int32 [num_seqs, block_table_width] (row stride given);     */
+/*               entries outside [0, num_blocks) are treated as empty.       */
+/* cu_seqlens_q/k: int32 [num_seqs + 1] prefix sums of query/key lengths.    */
+/* The workspace (size from hs_verify_attention_workspace_size) holds the    */
+/* partial results of key splits; it needs no initialisation.                */
+/* ------------------------------------------------------------------------ */
+size_t hs_verify_attention_workspace_size(int num_seqs, int num_q_heads, int num_kv_heads,
+                                          int max_seqlen_q, int max_seqlen_k);
+
+int hs_verify_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                        const void* k_cache, const void* v_cache, int kv_dtype,
+                        int64_t cache_stride_block, int64_t cache_stride_tok,
+                        int64_t cache_stride_head, float k_scale, float v_scale,
+                        const int32_t* block_tables, int64_t block_table_stride,
+                        int block_table_width, int num_blocks, const int32_t* cu_seqlens_q,
+                        const int32_t* cu_seqlens_k, int num_seqs, int max_seqlen_q,
+                        int max_seqlen_k, int num_q_heads, int num_kv_heads, int head_dim,
+                        int block_size, float softmax_scale, void* out, int64_t out_stride_tok,
+                        int64_t out_stride_head, void* workspace, size_t workspace_bytes,
+                        void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* KV-cache store: store_kvcache, mini_vllm/layers/attention.py:59-90, and   */
+/* the FP8 store the reference imports from an external package             */
+/* (attention.py:17-56, absent from the reference tree).                    */
+/* key/value [num_tokens, num_kv_heads, 128] bf16; token i goes to cache slot */
+/* slot_mapping[i] = block * block_size + offset; slots < 0 (the reference's */
+/* -1) and blocks >= num_blocks are skipped. FP8 stores                      */
+/* sat_e4m3fn(x / scale): round to nearest even, saturated to +-448.         */
+/* ------------------------------------------------------------------------ */
+int hs_store_kvcache(const void* key, int64_t key_stride_tok, int64_t key_stride_head,
+                     const void* value, int64_t value_stride_tok, int64_t value_stride_head,
+                     void* k_cache, void* v_cache, int kv_dtype, int64_t cache_stride_block,
+                     int64_t cache_stride_tok, int64_t cache_stride_head, float k_scale,
+                     float v_scale, const int32_t* slot_mapping, int num_tokens,
+                     int num_kv_heads, int head_dim, int block_size, int num_blocks,
+                     void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,152 @@
+"""GPU parity of the paged verify attention and the KV-cache store.
+
+The HIP kernels run through the C ABI and are compared with the float64
+oracle (oracle/attn.py) on identical inputs. Attention outputs are bf16 and
+must agree within 2e-2 (absolute + relative); the BF16 store is a bit-exact
+copy and the FP8 store must equal the oracle's codec bit for bit.
+"""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-2
+
+
+@pytest.fixture(scope="module")
+def attn(orc):
+    from oracle import attn as A
+    return A
+
+
+def _bf16(x, dev):
+    from importlib import import_module
+    hv = import_module("hilda-vllm_amd")
+    bits = hv.synthetic.f32_to_bf16_bits(np.ascontiguousarray(x, np.float32))
+    return torch.from_numpy(bits.view(np.int16)).to(dev).view(torch.bfloat16)
+
+
+def _run(hv, attn, w, cuda, kv="bf16", q_strided=False):
+    dev = cuda
+    if kv == "fp8":
+        ks = float(np.nanmax(np.abs(w["k_cache"]))) / 448.0
+        vs = float(np.nanmax(np.abs(w["v_cache"]))) / 448.0
+        kq = attn.e4m3fn_quantize(w["k_cache"], ks)
+        vq = attn.e4m3fn_quantize(w["v_cache"], vs)
+        kc = torch.from_numpy(kq).to(dev).view(torch.float8_e4m3fn)
+        vc = torch.from_numpy(vq).to(dev).view(torch.float8_e4m3fn)
+        kref = attn.dequant(kq, ks)
+        vref = attn.dequant(vq, vs)
+    else:
+        ks = vs = 1.0
+        kc = _bf16(w["k_cache"], dev)
+        vc = _bf16(w["v_cache"], dev)
+        kref, vref = w["k_cache"], w["v_cache"]
+    q = _bf16(w["q"], dev)
+    if q_strided:  # q as the first slice of a fused qkv projection
+        N, Hq, D = q.shape
+        big = torch.zeros((N, Hq + 2 * 8, D), dtype=torch.bfloat16, device=dev)
+        big[:, :Hq] = q
+        q = big[:, :Hq]
+    out = hv.ops.verify_attention(
+        q, kc, vc, torch.from_numpy(w["block_tables"]).to(dev),
+        torch.from_numpy(w["cu_seqlens_q"]).to(dev), torch.from_numpy(w["cu_seqlens_k"]).to(dev),
+        w["max_seqlen_q"], w["max_seqlen_k"], w["softmax_scale"], k_scale=ks, v_scale=vs)
+    torch.cuda.synchronize()
+    ref = attn.paged_attention(w["q"], kref, vref, w["block_tables"], w["cu_seqlens_q"],
+                               w["cu_seqlens_k"], w["softmax_scale"])
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    err = np.abs(got - ref)
+    bad = err > TOL + TOL * np.abs(ref)
+    assert not bad.any(), (err.max(), np.argwhere(bad)[:5])
+    return err.max()
+
+
+def test_config2_bf16(hv, attn, cuda):
+    print("config2 bf16 B=64", flush=True)
+    w = hv.synthetic.attention_workload(seed=0)
+    _run(hv, attn, w, cuda)
+
+
+def test_config2_fp8(hv, attn, cuda):
+    print("config2 fp8 B=64", flush=True)
+    w = hv.synthetic.attention_workload(seed=1)
+    _run(hv, attn, w, cuda, kv="fp8")
+
+
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (16, 8), (8, 8)])
+def test_decode_single_query(hv, attn, cuda, hq, hkv):
+    w = hv.synthetic.attention_workload(batch=12, q_len=1, num_q_heads=hq, num_kv_heads=hkv,
+                                        min_len=1, max_len=700, seed=2)
+    _run(hv, attn, w, cuda)
+
+
+def test_prefill_long_queries(hv, attn, cuda):
+    w = hv.synthetic.attention_workload(batch=3, q_len=64, num_q_heads=32, num_kv_heads=8,
+                                        min_len=64, max_len=400, seed=3)
+    _run(hv, attn, w, cuda)
+
+
+def test_ragged_query_lengths_and_strided_q(hv, attn, cuda):
+    w = hv.synthetic.attention_workload(batch=6, q_len=5, num_q_heads=16, num_kv_heads=8,
+                                        min_len=5, max_len=900, seed=4, lens=None)
+    # make query lengths ragged: shrink some and rebuild the prefix sums
+    ql = np.array([5, 1, 3, 5, 2, 4])
+    keep = np.concatenate([np.arange(w["cu_seqlens_q"][b], w["cu_seqlens_q"][b] + ql[b])
+                           for b in range(6)])
+    w["q"] = np.ascontiguousarray(w["q"][keep])
+    w["cu_seqlens_q"] = np.concatenate([[0], np.cumsum(ql)]).astype(np.int32)
+    w["max_seqlen_q"] = int(ql.max())
+    _run(hv, attn, w, cuda, q_strided=True)
+
+
+@pytest.mark.parametrize("kv", ["bf16", "fp8"])
+def test_small_blocks_and_short_contexts(hv, attn, cuda, kv):
+    w = hv.synthetic.attention_workload(batch=9, q_len=4, num_q_heads=32, num_kv_heads=8,
+                                        block_size=32, lens=[4, 5, 31, 32, 33, 64, 65, 100, 257],
+                                        seed=5)
+    _run(hv, attn, w, cuda, kv=kv)
+
+
+def test_batch1_verify_shape_of_8b_target(hv, attn, cuda):
+    """B=1, gamma+1=4 queries, 32 Q / 8 KV heads: the verify shape of config 3."""
+    w = hv.synthetic.attention_workload(batch=1, q_len=4, num_q_heads=32, num_kv_heads=8,
+                                        lens=[324], seed=6)
+    _run(hv, attn, w, cuda)
+
+
+@pytest.mark.parametrize("kv", ["bf16", "fp8"])
+def test_store_kvcache(hv, attn, cuda, kv):
+    rng = np.random.default_rng(7)
+    nb, bs, H, D = 6, 32, 8, 128
+    N = 40
+    key = rng.standard_normal((N, H, D)).astype(np.float32) * 3
+    val = rng.standard_normal((N, H, D)).astype(np.float32) * 3
+    key = hv.synthetic.bf16_bits_to_f32(hv.synthetic.f32_to_bf16_bits(key))
+    val = hv.synthetic.bf16_bits_to_f32(hv.synthetic.f32_to_bf16_bits(val))
+    slots = rng.permutation(nb * bs)[:N].astype(np.int32)
+    slots[[3, 17]] = -1
+    if kv == "bf16":
+        kc = torch.zeros((nb, bs, H, D), dtype=torch.bfloat16, device=cuda)
+        vc = torch.zeros_like(kc)
+        hv.ops.store_kvcache(_bf16(key, cuda), _bf16(val, cuda), kc, vc,
+                             torch.from_numpy(slots).to(cuda))
+        ek = np.zeros((nb, bs, H, D), np.float32)
+        ev = np.zeros_like(ek)
+        attn.store_kvcache(key, val, ek, ev, slots)
+        np.testing.assert_array_equal(kc.float().cpu().numpy(), ek)
+        np.testing.assert_array_equal(vc.float().cpu().numpy(), ev)
+    else:
+        ks, vs = 0.021, 0.017
+        kc = torch.zeros((nb, bs, H, D), dtype=torch.uint8, device=cuda).view(torch.float8_e4m3fn)
+        vc = torch.zeros_like(kc)
+        hv.ops.store_kvcache(_bf16(key, cuda), _bf16(val, cuda), kc, vc,
+                             torch.from_numpy(slots).to(cuda), k_scale=ks, v_scale=vs)
+        ek = np.zeros((nb, bs, H, D), np.uint8)
+        ev = np.zeros_like(ek)
+        attn.store_kvcache(attn.e4m3fn_quantize(key, ks), attn.e4m3fn_quantize(val, vs), ek, ev,
+                           slots)
+        np.testing.assert_array_equal(kc.view(torch.uint8).cpu().numpy(), ek)
+        np.testing.assert_array_equal(vc.view(torch.uint8).cpu().numpy(), ev)
