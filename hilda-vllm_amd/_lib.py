@@ -38,6 +38,27 @@ SIGNATURES: dict[str, tuple] = {
                                 _i64, _f32, _f32, _vp, _i32, _i32, _i32, _i32, _i32, _vp]),
 }
 
+
+
+class SpecState(ctypes.Structure):
+    """Mirror of hs_spec_state (include/hilda_spec.h)."""
+    _fields_ = [(n, ctypes.c_void_p) for n in (
+        "context_lens", "num_prompt", "max_tokens", "ignore_eos", "finished", "block_tables",
+        "num_seq_blocks", "tokens", "free_ring", "free_hdr", "ref_count")] + [
+        ("B", ctypes.c_int32), ("W", ctypes.c_int32), ("T", ctypes.c_int32),
+        ("num_blocks", ctypes.c_int32), ("block_size", ctypes.c_int32), ("pad", ctypes.c_int32),
+        ("eos", ctypes.c_int64)]
+
+
+_sp = ctypes.POINTER(SpecState)
+SIGNATURES.update({
+    "hs_spec_prealloc": (_i32, [_sp, _i32, _vp, _vp, _vp]),
+    "hs_verify_prepare": (_i32, [_sp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "hs_spec_commit_workspace_size": (_sz, [_i32, _i32, _i32]),
+    "hs_spec_commit": (_i32, [_sp, _i32, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _sz, _vp]),
+    "hs_zero_kv_slots": (_i32, [_vp, _i64, _i32, _i64, _i64, _i64, _vp, _i32, _vp]),
+})
+
 _lib = None
 
 

@@ -267,3 +267,113 @@ def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
         k_cache.stride(0), k_cache.stride(1), k_cache.stride(2), float(k_scale), float(v_scale),
         sm.data_ptr(), N, Hkv, D, bs, nb, _stream(dev))
     L.check(rc, "hs_store_kvcache")
+
+
+class SpecStateTensors:
+    """Device-resident bookkeeping state of a batch (layout of hs_spec_state).
+
+    Fields mirror Sequence / BlockManager (sequence.py:14-132,
+    block_manager.py:26-115): context_lens, num_prompt, max_tokens, ignore_eos,
+    finished, block_tables [B, W] (-1 padded), num_seq_blocks, tokens [B, T],
+    free_ring [num_blocks] + free_hdr (head, count), ref_count [num_blocks].
+    """
+
+    FIELDS = ("context_lens", "num_prompt", "max_tokens", "ignore_eos", "finished",
+              "block_tables", "num_seq_blocks", "tokens", "free_ring", "free_hdr", "ref_count")
+
+    def __init__(self, B: int, W: int, T: int, num_blocks: int, block_size: int, eos: int,
+                 device):
+        i32 = dict(dtype=torch.int32, device=device)
+        self.B, self.W, self.T = B, W, T
+        self.num_blocks, self.block_size, self.eos = num_blocks, block_size, int(eos)
+        self.context_lens = torch.zeros(B, **i32)
+        self.num_prompt = torch.zeros(B, **i32)
+        self.max_tokens = torch.zeros(B, **i32)
+        self.ignore_eos = torch.zeros(B, **i32)
+        self.finished = torch.zeros(B, **i32)
+        self.block_tables = torch.full((B, W), -1, **i32)
+        self.num_seq_blocks = torch.zeros(B, **i32)
+        self.tokens = torch.zeros((B, T), dtype=torch.int64, device=device)
+        self.free_ring = torch.arange(num_blocks, **i32)
+        self.free_hdr = torch.tensor([0, num_blocks], **i32)
+        self.ref_count = torch.zeros(num_blocks, **i32)
+        self.commit_ws = torch.zeros(
+            L.lib().hs_spec_commit_workspace_size(B, W, num_blocks), dtype=torch.uint8,
+            device=device)
+
+    def struct(self) -> "L.SpecState":
+        st = L.SpecState()
+        for f in self.FIELDS:
+            setattr(st, f, getattr(self, f).data_ptr())
+        st.B, st.W, st.T = self.B, self.W, self.T
+        st.num_blocks, st.block_size, st.eos = self.num_blocks, self.block_size, self.eos
+        return st
+
+
+def spec_prealloc(state: SpecStateTensors, gamma: int) -> torch.Tensor:
+    """llm_engine.py:111-128 on the device; returns eligible int32 [B]."""
+    dev = state.context_lens.device
+    elig = torch.empty(state.B, dtype=torch.int32, device=dev)
+    st = state.struct()
+    L.check(L.lib().hs_spec_prealloc(ctypes_ref(st), int(gamma), elig.data_ptr(), None,
+                                     _stream(dev)), "hs_spec_prealloc")
+    return elig
+
+
+def verify_prepare(state: SpecStateTensors, draft_tokens: torch.Tensor, gamma: int):
+    """model_runner.py:339-362 on the device.
+
+    Returns (input_ids, positions, slot_mapping, cu_seqlens_q, cu_seqlens_k)."""
+    dev = state.context_lens.device
+    B, R = state.B, gamma + 1
+    ids = torch.empty(B * R, dtype=torch.int64, device=dev)
+    pos = torch.empty(B * R, dtype=torch.int64, device=dev)
+    slots = torch.empty(B * R, dtype=torch.int32, device=dev)
+    cq = torch.empty(B + 1, dtype=torch.int32, device=dev)
+    ck = torch.empty(B + 1, dtype=torch.int32, device=dev)
+    dt = draft_tokens.to(torch.int64).contiguous() if gamma > 0 else None
+    st = state.struct()
+    L.check(L.lib().hs_verify_prepare(ctypes_ref(st), None if dt is None else dt.data_ptr(),
+                                      int(gamma), ids.data_ptr(), pos.data_ptr(),
+                                      slots.data_ptr(), cq.data_ptr(), ck.data_ptr(),
+                                      _stream(dev)), "hs_verify_prepare")
+    return ids, pos, slots, cq, ck
+
+
+def spec_commit(state: SpecStateTensors, gamma: int, out_tokens: torch.Tensor,
+                out_len: torch.Tensor, *, dirty_mode: int | None = None):
+    """llm_engine.py:146-195 on the device. Returns (appended, dirty_slots or None)."""
+    dev = state.context_lens.device
+    app = torch.empty(state.B, dtype=torch.int32, device=dev)
+    dirty = None
+    if dirty_mode is not None:
+        dirty = torch.empty((state.B, gamma + 1), dtype=torch.int32, device=dev)
+    ot = out_tokens.to(torch.int64).contiguous()
+    ol = out_len.to(torch.int32).contiguous()
+    st = state.struct()
+    L.check(L.lib().hs_spec_commit(ctypes_ref(st), int(gamma), None, ot.data_ptr(),
+                                   ol.data_ptr(), app.data_ptr(),
+                                   None if dirty is None else dirty.data_ptr(),
+                                   int(dirty_mode or 0), state.commit_ws.data_ptr(),
+                                   state.commit_ws.numel(), _stream(dev)), "hs_spec_commit")
+    return app, dirty
+
+
+def zero_kv_slots(cache: torch.Tensor, slots: torch.Tensor) -> None:
+    """Zero the rows of `slots` in every plane of a [P..., num_blocks, block_size, H, D] cache
+    (cleanup_rejected_kv_slots, model_runner.py:467-481)."""
+    dev = _need_cuda(cache, slots)
+    nb, bs, H, D = cache.shape[-4:]
+    planes = cache.numel() // (nb * bs * H * D)
+    esz = cache.element_size()
+    if not cache.is_contiguous():
+        raise ValueError("cache must be contiguous")
+    s = slots.to(torch.int32).reshape(-1).contiguous()
+    L.check(L.lib().hs_zero_kv_slots(cache.data_ptr(), nb * bs * H * D * esz, planes,
+                                     H * D * esz, H * D * esz, nb * bs, s.data_ptr(), s.numel(),
+                                     _stream(dev)), "hs_zero_kv_slots")
+
+
+def ctypes_ref(st):
+    import ctypes
+    return ctypes.byref(st)

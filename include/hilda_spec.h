@@ -158,6 +158,80 @@ int hs_store_kvcache(const void* key, int64_t key_stride_tok, int64_t key_stride
                      int num_kv_heads, int head_dim, int block_size, int num_blocks,
                      void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* Device-resident bookkeeping of the speculative step.                      */
+/*                                                                          */
+/* The state mirrors Sequence (mini_vllm/engine/sequence.py:14-132) and      */
+/* BlockManager (block_manager.py:26-115) for a batch of B sequences:        */
+/* context_lens = len(seq), num_prompt, max_tokens, ignore_eos (0/1),        */
+/* finished (0/1), block_tables [B, W] (-1 padded) with num_seq_blocks, the  */
+/* token history tokens [B, T] (T must exceed the longest sequence), the     */
+/* free-block deque as a ring free_ring[num_blocks] with free_hdr = {head,    */
+/* count} (pop at head, append at head+count), and ref_count[num_blocks].    */
+/* All pointers are device pointers; the struct itself lives on the host.    */
+/* ------------------------------------------------------------------------ */
+typedef struct hs_spec_state {
+  int32_t* context_lens;
+  int32_t* num_prompt;
+  int32_t* max_tokens;
+  int32_t* ignore_eos;
+  int32_t* finished;
+  int32_t* block_tables;
+  int32_t* num_seq_blocks;
+  int64_t* tokens;
+  int32_t* free_ring;
+  int32_t* free_hdr;
+  int32_t* ref_count;
+  int32_t B, W, T, num_blocks, block_size;
+  int32_t pad;
+  int64_t eos;
+} hs_spec_state;
+
+/* Pre-allocation of blocks for len + gamma + 1 tokens,                      */
+/* mini_vllm/engine/llm_engine.py:111-128: sequences in order, blocks popped */
+/* from the front of the free deque with ref_count 1; a sequence is skipped  */
+/* (eligible[b] = 0) when the free count is short or it is finished.         */
+/* *status is set to 1 if a table row is too narrow (optional pointer).      */
+int hs_spec_prealloc(const hs_spec_state* state, int gamma, int32_t* eligible, int32_t* status,
+                     void* stream);
+
+/* Verify staging, mini_vllm/engine/model_runner.py:339-362: per sequence the */
+/* gamma+1 tokens [last_token, drafts], positions len-1+j, slot_mapping       */
+/* (block*block_size + pos%block_size, or -1 past the table),                */
+/* cu_seqlens_q (steps of gamma+1) and cu_seqlens_k (len + gamma each).       */
+int hs_verify_prepare(const hs_spec_state* state, const int64_t* draft_tokens, int gamma,
+                      int64_t* input_ids, int64_t* positions, int32_t* slot_mapping,
+                      int32_t* cu_seqlens_q, int32_t* cu_seqlens_k, void* stream);
+
+/* Commit and rollback after acceptance, mini_vllm/engine/llm_engine.py:     */
+/* 146-195: append out_tokens[b, :out_len[b]] one by one, stopping at EOS    */
+/* (unless ignore_eos) or max_tokens (sequence finished: all blocks released */
+/* last-first, block_manager.py:84-92); then unfinished sequences drop tail  */
+/* blocks beyond ceil(len / block_size). Released blocks whose reference     */
+/* count reaches 0 are appended to the free deque in the reference's order   */
+/* (all finishes in sequence order, then all trims in sequence order).       */
+/* appended[b] (optional) = tokens appended. dirty_slots (optional,          */
+/* [B, gamma+1], -1 padded) lists the KV slots of rejected drafts            */
+/* (model_runner.py:439-464): dirty_mode 0 uses the reference range          */
+/* [len, old_len + gamma + 1), dirty_mode 1 the exact range                  */
+/* [len - 1, old_len + gamma). num_accepted is not needed (may be NULL).     */
+/* The workspace must be zero-filled before its first use; every call leaves */
+/* it zero-filled.                                                           */
+size_t hs_spec_commit_workspace_size(int batch, int table_width, int num_blocks);
+int hs_spec_commit(const hs_spec_state* state, int gamma, const int32_t* num_accepted,
+                   const int64_t* out_tokens, const int32_t* out_len, int32_t* appended,
+                   int32_t* dirty_slots, int dirty_mode, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
+/* Zeroes row_bytes at every slot of slots[] (entries < 0 skipped) in each of */
+/* num_planes planes (e.g. the 2*L (K|V, layer) planes of a                  */
+/* [2, L, num_blocks, block_size, H, D] cache): byte offset                  */
+/* plane * plane_bytes + slot * slot_bytes. Replaces the per-layer index     */
+/* assignments of cleanup_rejected_kv_slots, model_runner.py:467-481.        */
+int hs_zero_kv_slots(void* cache, int64_t plane_bytes, int num_planes, int64_t slot_bytes,
+                     int64_t row_bytes, int64_t slots_per_plane, const int32_t* slots,
+                     int num_slots, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
