@@ -160,6 +160,56 @@ __global__ __launch_bounds__(kCT) void k_prepare(hs_spec_state s, const int64_t*
   }
 }
 
+// draft step staging: model_runner.py:294-310 (step j feeds the previous draft
+// token, or last_token for j = 0, at position len - 1 + j). With lookback, step
+// 0 feeds the two last tokens (positions len-2, len-1): after a step that
+// accepted every draft, the draft model never saw the last accepted draft,
+// and this fills that KV slot.
+__global__ __launch_bounds__(kCT) void k_draft_prepare(hs_spec_state s, const int64_t* draft,
+                                                       int draft_stride, int step, int lookback,
+                                                       int64_t* input_ids, int64_t* positions,
+                                                       int32_t* slot_mapping, int32_t* cu_q,
+                                                       int32_t* cu_k) {
+  __shared__ int s_w[kCW];
+  const int tid = threadIdx.x;
+  const int R = (step == 0 && lookback) ? 2 : 1;
+  int carry = 0;
+  for (int base = 0; base < s.B; base += kCT) {
+    const int b = base + tid;
+    int lk = 0;
+    if (b < s.B) {
+      const int len = s.context_lens[b];
+      const int cur = len + step;
+      lk = cur;
+      const int nblk = s.num_seq_blocks[b];
+      for (int r = 0; r < R; ++r) {
+        const int back = R - 1 - r;  // 1 for the look-back row
+        int64_t tok;
+        if (step == 0) tok = s.tokens[(int64_t)b * s.T + (len - 1 - back >= 0 ? len - 1 - back : 0)];
+        else tok = draft[(int64_t)b * draft_stride + step - 1];
+        const int pos = cur - 1 - back;
+        const int bi = pos / s.block_size;
+        const int o = b * R + r;
+        input_ids[o] = tok;
+        positions[o] = pos;
+        slot_mapping[o] = (pos >= 0 && bi < nblk)
+                              ? s.block_tables[(int64_t)b * s.W + bi] * s.block_size +
+                                    pos % s.block_size
+                              : -1;
+      }
+      cu_q[b] = b * R;
+    }
+    int total;
+    const int ex = cscan_excl(lk, s_w, &total);
+    if (b < s.B) cu_k[b] = carry + ex;
+    carry += total;
+  }
+  if (tid == 0) {
+    cu_q[s.B] = s.B * R;
+    cu_k[s.B] = carry;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // commit + rollback: llm_engine.py:146-195, block_manager.py:84-92
 // ---------------------------------------------------------------------------
@@ -356,6 +406,21 @@ int hs_verify_prepare(const hs_spec_state* state, const int64_t* draft_tokens, i
   hipLaunchKernelGGL(k_prepare, dim3(1), dim3(kCT), 0, reinterpret_cast<hipStream_t>(stream),
                      *state, draft_tokens, gamma, input_ids, positions, slot_mapping,
                      cu_seqlens_q, cu_seqlens_k);
+  return hipGetLastError() == hipSuccess ? HS_OK : HS_ERR_LAUNCH;
+}
+
+int hs_draft_prepare(const hs_spec_state* state, const int64_t* draft_tokens, int draft_stride,
+                     int step, int lookback, int64_t* input_ids, int64_t* positions,
+                     int32_t* slot_mapping, int32_t* cu_seqlens_q, int32_t* cu_seqlens_k,
+                     void* stream) {
+  if (!state_ok(state) || step < 0 || (step > 0 && (!draft_tokens || draft_stride < step)) ||
+      !input_ids || !positions || !slot_mapping || !cu_seqlens_q || !cu_seqlens_k ||
+      (lookback != 0 && lookback != 1))
+    return HS_ERR_INVALID;
+  hipLaunchKernelGGL(k_draft_prepare, dim3(1), dim3(kCT), 0,
+                     reinterpret_cast<hipStream_t>(stream), *state, draft_tokens, draft_stride,
+                     step, lookback, input_ids, positions, slot_mapping, cu_seqlens_q,
+                     cu_seqlens_k);
   return hipGetLastError() == hipSuccess ? HS_OK : HS_ERR_LAUNCH;
 }
 

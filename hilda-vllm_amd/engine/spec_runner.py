@@ -1,0 +1,242 @@
+"""Speculative-decoding runner on one MI355X.
+
+Restates the spec path of mini_vllm/engine/model_runner.py (KV-cache
+allocation and binding :141-247, run_draft_prefill :249-279, run_draft_decode
+:281-319, run_verify :321-437) and of LLMEngine.step (llm_engine.py:104-208)
+around the gfx950 kernels:
+  * all per-step bookkeeping is device-resident (hs_spec_prealloc,
+    hs_draft_prepare, hs_verify_prepare, hs_spec_commit), so a step needs no
+    host staging loop and no host synchronisation;
+  * the draft loop samples each draft token and writes the draft
+    probabilities with one hs_sampler call per step;
+  * verify runs the target over gamma+1 tokens, the LM head over all rows and
+    the fused acceptance (hs_spec_accept) with explicit uniforms;
+  * the draft phase and the verify phase can each be captured once into a HIP
+    graph and replayed.
+Uniforms are drawn on the device from torch's generator (graph-safe).
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from .. import ops
+from ..layers.sampler import Sampler
+from ..utils.context import reset_context, set_context
+
+
+class SpecRunner:
+
+    def __init__(self, target, draft, *, batch: int, gamma: int, max_model_len: int = 4096,
+                 block_size: int = 256, kv_cache_dtype: str = "auto", num_blocks: int | None = None,
+                 temperature: float = 1.0, top_k: int = 0, top_p: float = 1.0,
+                 mode: str = "reference", eos: int = -1, k_scale: float = 1.0,
+                 v_scale: float = 1.0, device="cuda"):
+        self.target, self.draft = target, draft
+        self.B, self.gamma = batch, gamma
+        self.bs = block_size
+        self.max_model_len = max_model_len
+        self.W = math.ceil((max_model_len + gamma + 2) / block_size)
+        self.num_blocks = num_blocks or batch * self.W + 2
+        self.mode = mode
+        self.device = torch.device(device)
+        self.V = target.g.vocab
+        dev = self.device
+        kv_dtype = torch.float8_e4m3fn if kv_cache_dtype == "fp8" else torch.bfloat16
+        tg, dg = target.g, draft.g
+        self.kv = torch.zeros((2, len(target.layers), self.num_blocks, block_size,
+                               tg.num_kv_heads, tg.head_dim), dtype=kv_dtype, device=dev)
+        self.dkv = torch.zeros((2, len(draft.layers), self.num_blocks, block_size,
+                                dg.num_kv_heads, dg.head_dim), dtype=torch.bfloat16, device=dev)
+        kmax = max_model_len + gamma + 2
+        for i, a in enumerate(target.attention_layers()):
+            a.k_cache, a.v_cache = self.kv[0, i], self.kv[1, i]
+            a.kv_cache_dtype = kv_cache_dtype
+            a.k_scale, a.v_scale = k_scale, v_scale
+            a.max_model_len = kmax
+        for i, a in enumerate(draft.attention_layers()):
+            a.k_cache, a.v_cache = self.dkv[0, i], self.dkv[1, i]
+            a.kv_cache_dtype = "auto"
+            a.max_model_len = kmax
+        self.state = ops.SpecStateTensors(batch, self.W, kmax + 1, self.num_blocks, block_size,
+                                          eos, dev)
+        f32 = dict(dtype=torch.float32, device=dev)
+        self.temps = torch.full((batch,), float(temperature), **f32)
+        self.top_ks = torch.full((batch,), int(top_k), dtype=torch.int32, device=dev)
+        self.top_ps = torch.full((batch,), float(top_p), **f32)
+        self.draft_tokens = torch.zeros((batch, gamma), dtype=torch.int64, device=dev)
+        self.draft_probs = torch.zeros((batch, gamma, self.V), **f32)
+        self.tok_scratch = torch.zeros(batch, dtype=torch.int64, device=dev)
+        self.u_draft = torch.zeros((gamma, batch), **f32)
+        self.u_acc = torch.zeros((batch, gamma), **f32)
+        self.u_res = torch.zeros(batch, **f32)
+        self.d_stage = self._stage_bufs(batch)
+        self.d_stage0 = self._stage_bufs(2 * batch)
+        self.sampler = Sampler()
+        self.graphs = None
+        self.last = None
+
+    def _stage_bufs(self, rows):
+        dev = self.device
+        return (torch.zeros(rows, dtype=torch.int64, device=dev),
+                torch.zeros(rows, dtype=torch.int64, device=dev),
+                torch.zeros(rows, dtype=torch.int32, device=dev),
+                torch.zeros(self.B + 1, dtype=torch.int32, device=dev),
+                torch.zeros(self.B + 1, dtype=torch.int32, device=dev))
+
+    # ------------------------------------------------------------------ setup
+    def load_prompts(self, prompts: list[list[int]], max_tokens: int = 1 << 30,
+                     ignore_eos: bool = True):
+        """Allocates prompt blocks from the front of the free list (block_manager.py:59-82
+        without prefix reuse: random prompts never share a full block)."""
+        assert len(prompts) == self.B
+        st = self.state
+        free = list(range(self.num_blocks))
+        tables, nblk = [], []
+        for p in prompts:
+            n = math.ceil(len(p) / self.bs)
+            tables.append(free[:n])
+            free = free[n:]
+            nblk.append(n)
+        dev = self.device
+        bt = torch.full((self.B, self.W), -1, dtype=torch.int32)
+        tok = torch.zeros((self.B, st.T), dtype=torch.int64)
+        for i, (p, t) in enumerate(zip(prompts, tables)):
+            bt[i, :len(t)] = torch.tensor(t, dtype=torch.int32)
+            tok[i, :len(p)] = torch.tensor(p, dtype=torch.int64)
+        st.block_tables.copy_(bt)
+        st.tokens.copy_(tok)
+        st.num_seq_blocks.copy_(torch.tensor(nblk, dtype=torch.int32))
+        st.context_lens.copy_(torch.tensor([len(p) for p in prompts], dtype=torch.int32))
+        st.num_prompt.copy_(torch.tensor([len(p) for p in prompts], dtype=torch.int32))
+        st.max_tokens.fill_(max_tokens)
+        st.ignore_eos.fill_(int(ignore_eos))
+        st.finished.zero_()
+        ring = torch.zeros(self.num_blocks, dtype=torch.int32)
+        ring[:len(free)] = torch.tensor(free, dtype=torch.int32)
+        st.free_ring.copy_(ring)
+        st.free_hdr.copy_(torch.tensor([0, len(free)], dtype=torch.int32))
+        ref = torch.zeros(self.num_blocks, dtype=torch.int32)
+        for t in tables:
+            ref[t] = 1
+        st.ref_count.copy_(ref)
+        self.prompts = prompts
+        del dev
+
+    @torch.inference_mode()
+    def prefill(self):
+        """Target prefill + first token, then draft prefill (model_runner.py:249-279)."""
+        dev = self.device
+        lens = [len(p) for p in self.prompts]
+        ids = torch.tensor([t for p in self.prompts for t in p], dtype=torch.int64, device=dev)
+        pos = torch.tensor([i for n in lens for i in range(n)], dtype=torch.int64, device=dev)
+        bt = self.state.block_tables.cpu()
+        slots = torch.tensor([int(bt[b, i // self.bs]) * self.bs + i % self.bs
+                              for b, n in enumerate(lens) for i in range(n)],
+                             dtype=torch.int32, device=dev)
+        cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0).tolist()), dtype=torch.int32,
+                          device=dev)
+        set_context(True, cu, cu, max(lens), max(lens), slots, None, self.state.block_tables)
+        h = self.target(ids, pos)
+        last = h[cu[1:].long() - 1]
+        logits = self.target.compute_logits(last)
+        first = self.sampler(logits, self.temps, self.top_ks, self.top_ps)
+        set_context(True, cu, cu, max(lens), max(lens), slots, None, self.state.block_tables)
+        self.draft(ids, pos)
+        reset_context()
+        out = first.view(self.B, 1)
+        ops.spec_commit(self.state, 0, out, torch.ones(self.B, dtype=torch.int32, device=dev))
+        torch.cuda.synchronize()
+
+    # ------------------------------------------------------------------ phases
+    def draft_phase(self):
+        """Pre-allocation (llm_engine.py:111-128) and gamma draft steps
+        (model_runner.py:294-318)."""
+        st = self.state
+        ops.spec_prealloc(st, self.gamma)
+        self.u_draft.uniform_()
+        mode = "filtered" if self.mode == "filtered" else "reference"
+        for j in range(self.gamma):
+            if j == 0:
+                # two queries: the previous token (fills the draft K/V the last step
+                # left out when it accepted every draft) and the last token
+                ids, pos, slots, cq, ck = ops.draft_prepare(st, None, 0, out=self.d_stage0,
+                                                            lookback=True)
+                set_context(True, cq, ck, 2, 0, slots, None, st.block_tables)
+                h = self.draft(ids, pos)[1::2]
+            else:
+                ids, pos, slots, cq, ck = ops.draft_prepare(st, self.draft_tokens, j,
+                                                            out=self.d_stage)
+                set_context(False, cq, ck, 1, 0, slots, None, st.block_tables)
+                h = self.draft(ids, pos)
+            logits = self.draft.compute_logits(h)
+            if self.mode == "greedy":
+                ops.sample_rows(logits, mode="greedy", tokens_out=self.tok_scratch)
+            else:
+                ops.sample_rows(logits, self.temps, self.top_ks, self.top_ps, mode=mode,
+                                uniforms=self.u_draft[j], probs_out=self.draft_probs[:, j],
+                                tokens_out=self.tok_scratch)
+            self.draft_tokens[:, j].copy_(self.tok_scratch)
+        reset_context()
+
+    def verify_phase(self):
+        """Verify forward + LM head over all gamma+1 rows + fused acceptance
+        (model_runner.py:329-428) + commit/rollback (llm_engine.py:146-181)."""
+        st, g = self.state, self.gamma
+        ids, pos, slots, cq, ck = ops.verify_prepare(st, self.draft_tokens, g)
+        set_context(True, cq, ck, g + 1, 0, slots, None, st.block_tables)
+        h = self.target(ids, pos)
+        reset_context()
+        logits = self.target.compute_logits(h).view(self.B, g + 1, self.V)
+        self.u_acc.uniform_()
+        self.u_res.uniform_()
+        nacc, out, olen = ops.spec_accept(logits, self.draft_probs, self.draft_tokens, self.temps,
+                                          self.u_acc, self.u_res, mode=self.mode,
+                                          top_ks=self.top_ks, top_ps=self.top_ps)
+        ops.spec_commit(st, g, out, olen)
+        self.last = (nacc, out, olen)
+
+    def step(self):
+        self.draft_phase()
+        self.verify_phase()
+
+    # ------------------------------------------------------------------ graphs
+    def capture(self):
+        """Records the draft phase and the verify phase into two HIP graphs.
+        The caller must have run at least one eager step (workspaces exist)."""
+        torch.cuda.synchronize()
+        snap = self._snapshot()
+        gd, gv = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream(device=self.device)
+        s.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(gd, stream=s):
+                self.draft_phase()
+            with torch.cuda.graph(gv, stream=s, pool=gd.pool()):
+                self.verify_phase()
+        torch.cuda.current_stream(self.device).wait_stream(s)
+        torch.cuda.synchronize()
+        self._restore(snap)  # capture executed nothing, but keep the state exact
+        self.graphs = (gd, gv)
+
+    def replay(self):
+        gd, gv = self.graphs
+        gd.replay()
+        gv.replay()
+
+    def _snapshot(self):
+        st = self.state
+        return {f: getattr(st, f).clone() for f in st.FIELDS}
+
+    def _restore(self, snap):
+        for f, t in snap.items():
+            getattr(self.state, f).copy_(t)
+
+    # ------------------------------------------------------------------ results
+    def lengths(self) -> list[int]:
+        return self.state.context_lens.cpu().tolist()
+
+    def tokens(self, b: int) -> list[int]:
+        n = int(self.state.context_lens[b])
+        return self.state.tokens[b, :n].cpu().tolist()

@@ -1,0 +1,86 @@
+"""Attention layer and KV store backed by the gfx950 kernels.
+
+Drop-in for mini_vllm/layers/attention.py: the same constructor
+Attention(num_heads, head_dim, scale, num_kv_heads), the same module
+attributes bound by the model runner (k_cache, v_cache, kv_cache_dtype) and
+the same store_kvcache(key, value, k_cache, v_cache, slot_mapping) function.
+forward(q, k, v) stores k/v at context.slot_mapping (attention.py:145) and then
+attends over the paged cache through context.block_tables:
+  * prefill / verify (context.is_prefill): cu_seqlens_q/k as given
+    (attention.py:147-160, bottom-right causal);
+  * decode: one query per sequence with context.context_lens keys
+    (attention.py:162-170); cu_seqlens_k is taken from context.cu_seqlens_k
+    when the caller staged it on the device, else built from context_lens.
+kv_cache_dtype "fp8" means float8_e4m3fn caches with per-tensor scales
+k_scale / v_scale, used by every phase (the reference keeps a separate BF16
+prefill cache for verify, attention.py:114-131; one FP8 cache keeps the
+accepted tokens' K/V in the cache decode reads).
+"""
+from __future__ import annotations
+
+
+import torch
+from torch import nn
+
+from ..utils.context import get_context
+
+from .. import ops as _ops
+
+
+def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
+                  v_cache: torch.Tensor, slot_mapping: torch.Tensor, k_scale: float = 1.0,
+                  v_scale: float = 1.0) -> None:
+    """attention.py:83-90: write K/V rows of N tokens to their cache slots (-1 skipped)."""
+    N, num_heads, head_dim = key.shape
+    assert key.stride(-1) == 1 and value.stride(-1) == 1
+    assert slot_mapping.numel() == N
+    _ops.store_kvcache(key, value, k_cache, v_cache, slot_mapping, k_scale=k_scale,
+                       v_scale=v_scale)
+
+
+class Attention(nn.Module):
+
+    def __init__(self, num_heads, head_dim, scale, num_kv_heads):
+        super().__init__()
+        self.num_heads = num_heads
+        self.head_dim = head_dim
+        self.scale = scale
+        self.num_kv_heads = num_kv_heads
+        self.kv_cache_dtype = "auto"
+        self.k_cache = self.v_cache = torch.tensor([])
+        self.k_scale = 1.0
+        self.v_scale = 1.0
+        # upper bound of keys per sequence used to size the launch (set by the runner
+        # for graph capture; 0 means "use the context's max_seqlen_k")
+        self.max_model_len = 0
+
+    def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+        ctx = get_context()
+        k_cache, v_cache = self.k_cache, self.v_cache
+        if not (k_cache.numel() and v_cache.numel()):
+            raise RuntimeError("Attention needs a bound KV cache (k_cache / v_cache)")
+        if ctx.block_tables is None:
+            raise RuntimeError("Attention needs context.block_tables (paged KV)")
+        q = q.view(-1, self.num_heads, self.head_dim)
+        k = k.view(-1, self.num_kv_heads, self.head_dim)
+        v = v.view(-1, self.num_kv_heads, self.head_dim)
+        store_kvcache(k, v, k_cache, v_cache, ctx.slot_mapping, self.k_scale, self.v_scale)
+        if ctx.is_prefill:
+            cu_q, cu_k = ctx.cu_seqlens_q, ctx.cu_seqlens_k
+            max_q, max_k = ctx.max_seqlen_q, ctx.max_seqlen_k
+        else:
+            B = q.shape[0]
+            cu_q = ctx.cu_seqlens_q
+            if cu_q is None:
+                cu_q = torch.arange(B + 1, dtype=torch.int32, device=q.device)
+            if ctx.cu_seqlens_k is not None:
+                cu_k = ctx.cu_seqlens_k
+            else:
+                cu_k = torch.zeros(B + 1, dtype=torch.int32, device=q.device)
+                torch.cumsum(ctx.context_lens.to(torch.int32), 0, out=cu_k[1:])
+            max_q, max_k = 1, ctx.max_seqlen_k
+        if self.max_model_len:
+            max_k = self.max_model_len
+        return _ops.verify_attention(q, k_cache, v_cache, ctx.block_tables, cu_q, cu_k, max_q,
+                                     max_k, self.scale, k_scale=self.k_scale,
+                                     v_scale=self.v_scale)

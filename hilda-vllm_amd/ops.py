@@ -138,7 +138,8 @@ def spec_accept(target_logits: torch.Tensor, draft_probs: torch.Tensor | None,
 def sample_rows(logits: torch.Tensor, temperatures: torch.Tensor | None = None,
                 top_ks: torch.Tensor | None = None, top_ps: torch.Tensor | None = None, *,
                 mode="reference", uniforms: torch.Tensor | None = None, want_probs: bool = False,
-                out_kind: int = 0, row_stats: bool = False):
+                out_kind: int = 0, row_stats: bool = False,
+                probs_out: torch.Tensor | None = None, tokens_out: torch.Tensor | None = None):
     """Row sampler (Sampler.forward / draft probabilities).
 
     Returns dict(probs=[rows, V] f32 or None, tokens=[rows] int64 or None,
@@ -161,11 +162,22 @@ def sample_rows(logits: torch.Tensor, temperatures: torch.Tensor | None = None,
         top_ks = top_ks.to(torch.int32).reshape(rows).contiguous()
         top_ps = top_ps.to(torch.float32).reshape(rows).contiguous()
     probs = None
-    if want_probs and m != L.HS_ACCEPT_GREEDY:
+    if probs_out is not None:
+        if probs_out.shape != (rows, V) or probs_out.stride(1) != 1 or \
+                probs_out.dtype != torch.float32:
+            raise ValueError("probs_out must be [rows, V] float32 with contiguous rows")
+        probs = probs_out
+    elif want_probs and m != L.HS_ACCEPT_GREEDY:
         probs = torch.empty((rows, V), dtype=torch.float32, device=dev)
     toks = None
     if m == L.HS_ACCEPT_GREEDY or uniforms is not None:
-        toks = torch.empty(rows, dtype=torch.int64, device=dev)
+        if tokens_out is not None:
+            if tokens_out.numel() != rows or not tokens_out.is_contiguous() or \
+                    tokens_out.dtype != torch.int64:
+                raise ValueError("tokens_out must be a contiguous int64 [rows] tensor")
+            toks = tokens_out
+        else:
+            toks = torch.empty(rows, dtype=torch.int64, device=dev)
     if uniforms is not None:
         uniforms = uniforms.to(torch.float32).reshape(rows).contiguous()
     if m == L.HS_ACCEPT_GREEDY and uniforms is None:
@@ -182,7 +194,7 @@ def sample_rows(logits: torch.Tensor, temperatures: torch.Tensor | None = None,
     rc = lib.hs_sampler(p(lg), _logit_dtype(lg), lstride, rows, V, p(temperatures),
                         p(top_ks) if m == L.HS_ACCEPT_FILTERED else None,
                         p(top_ps) if m == L.HS_ACCEPT_FILTERED else None, m, p(probs),
-                        V if probs is not None else 0, int(out_kind),
+                        probs.stride(0) if probs is not None else 0, int(out_kind),
                         uniforms_ptr if m != L.HS_ACCEPT_GREEDY else None,
                         p(toks), p(stats), ws.data_ptr(), ws.numel(), _stream(dev))
     L.check(rc, "hs_sampler")
@@ -377,3 +389,29 @@ def zero_kv_slots(cache: torch.Tensor, slots: torch.Tensor) -> None:
 def ctypes_ref(st):
     import ctypes
     return ctypes.byref(st)
+
+
+def draft_prepare(state: SpecStateTensors, draft_tokens: torch.Tensor | None, step: int,
+                  out: tuple | None = None, lookback: bool = False):
+    """model_runner.py:294-310 on the device for draft step `step`.
+
+    Returns (input_ids, positions, slot_mapping, cu_q [B+1], cu_k [B+1]) with R rows
+    per sequence (R = 2 for step 0 with lookback, else 1); `out` may pass
+    preallocated tensors of those shapes (graph capture)."""
+    dev = state.context_lens.device
+    B = state.B
+    R = 2 if (step == 0 and lookback) else 1
+    if out is None:
+        out = (torch.empty(B * R, dtype=torch.int64, device=dev),
+               torch.empty(B * R, dtype=torch.int64, device=dev),
+               torch.empty(B * R, dtype=torch.int32, device=dev),
+               torch.empty(B + 1, dtype=torch.int32, device=dev),
+               torch.empty(B + 1, dtype=torch.int32, device=dev))
+    ids, pos, slots, cq, ck = out
+    st = state.struct()
+    stride = draft_tokens.stride(0) if draft_tokens is not None else 0
+    L.check(L.lib().hs_draft_prepare(
+        ctypes_ref(st), None if draft_tokens is None else draft_tokens.data_ptr(), int(stride),
+        int(step), int(R == 2), ids.data_ptr(), pos.data_ptr(), slots.data_ptr(), cq.data_ptr(),
+        ck.data_ptr(), _stream(dev)), "hs_draft_prepare")
+    return out

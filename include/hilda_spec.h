@@ -203,6 +203,18 @@ int hs_verify_prepare(const hs_spec_state* state, const int64_t* draft_tokens, i
                       int64_t* input_ids, int64_t* positions, int32_t* slot_mapping,
                       int32_t* cu_seqlens_q, int32_t* cu_seqlens_k, void* stream);
 
+/* Draft-step staging, mini_vllm/engine/model_runner.py:294-310: step j of   */
+/* the draft loop feeds draft_tokens[b, j-1] (last_token for j = 0) at        */
+/* position len - 1 + j with context length len + j; one query per sequence.  */
+/* lookback = 1 makes step 0 feed the last two tokens (positions len-2 and    */
+/* len-1, two queries per sequence; outputs sized 2*B): after a step that     */
+/* accepted all drafts, the reference's draft cache has no K/V for the last   */
+/* accepted draft (it is never fed, :294-305) and this fills it.              */
+int hs_draft_prepare(const hs_spec_state* state, const int64_t* draft_tokens, int draft_stride,
+                     int step, int lookback, int64_t* input_ids, int64_t* positions,
+                     int32_t* slot_mapping, int32_t* cu_seqlens_q, int32_t* cu_seqlens_k,
+                     void* stream);
+
 /* Commit and rollback after acceptance, mini_vllm/engine/llm_engine.py:     */
 /* 146-195: append out_tokens[b, :out_len[b]] one by one, stopping at EOS    */
 /* (unless ignore_eos) or max_tokens (sequence finished: all blocks released */
