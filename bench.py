@@ -238,7 +238,8 @@ def bench_spec(args, torch, hv):
 def attention_probe(torch, hv, runner, L):
     """Average duration of the verify-attention kernel at the verify shape of this run
     (B=1, gamma+1=4 queries, 32 Q / 8 KV heads, context L) over the target's 36 layer
-    caches, timed with HIP events on the launch stream."""
+    caches: 36 launches captured in a HIP graph, replayed 20 times between two HIP
+    events on the launch stream (per-launch time includes the graph's launch gaps)."""
     dev = runner.device
     g = runner.target.g
     R = runner.gamma + 1
@@ -259,12 +260,23 @@ def attention_probe(torch, hv, runner, L):
 
     launch_all()
     torch.cuda.synchronize()
+    # one verify step's worth of attention launches (36 layers) as a HIP graph, so
+    # the timing is GPU time, as in the graph-replayed verify step
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream(device=dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            launch_all()
+    torch.cuda.current_stream(dev).wait_stream(s)
+    graph.replay()
+    torch.cuda.synchronize()
     stream = torch.cuda.current_stream(dev)
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     e0.record(stream)
     for _ in range(reps):
-        launch_all()
+        graph.replay()
     e1.record(stream)
     torch.cuda.synchronize()
     us = e0.elapsed_time(e1) * 1e3 / (reps * len(layers))

@@ -1,0 +1,216 @@
+// Fused elementwise kernels of the Qwen3 decoder layer around the verify path.
+//
+// The reference fuses these with torch.compile (mini_vllm/layers/
+// layernorm.py:18-36, rotary_embedding.py:8-50, activation.py:8-16); eager
+// PyTorch would launch ~45 tiny kernels per layer for them, which at batch 1
+// costs more than the layer's GEMMs. One launch each here:
+//   hs_rmsnorm       (optional residual add) + RMSNorm, one workgroup per row;
+//   hs_qk_norm_rope  per-head RMSNorm of q and k + neox RoPE, one wave per
+//                    (token, head): lane l owns the rotation pair (l, l + 64);
+//   hs_silu_mul      silu(gate) * up.
+// Numerics follow the reference: the residual sum and the normalisation are
+// fp32, the normalised value is rounded to bf16 before the weight multiply.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/hilda_spec.h"
+
+namespace hs {
+
+__device__ __forceinline__ float bf(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+__device__ __forceinline__ uint16_t to_bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+// bf16 * bf16 rounded to bf16 (the product is exact in fp32)
+__device__ __forceinline__ uint16_t bf_mul(uint16_t a, uint16_t b) { return to_bf(bf(a) * bf(b)); }
+
+constexpr int kNT = 256;
+
+__device__ __forceinline__ void load4(const uint16_t* p, float (&a)[4]) {
+  const uint2 raw = *reinterpret_cast<const uint2*>(p);
+  a[0] = bf((uint16_t)raw.x);
+  a[1] = bf((uint16_t)(raw.x >> 16));
+  a[2] = bf((uint16_t)raw.y);
+  a[3] = bf((uint16_t)(raw.y >> 16));
+}
+
+// x [rows, H] (row stride xs), residual [rows, H] (rs; may be null), w [H].
+// Pass 1 accumulates the sum of squares of the fp32 (x + residual); pass 2
+// re-reads the row (cache-resident), stores the bf16 residual and the output.
+__global__ __launch_bounds__(kNT) void k_rmsnorm(const uint16_t* __restrict__ x, int64_t xs,
+                                                 uint16_t* __restrict__ res, int64_t rs,
+                                                 const uint16_t* __restrict__ w,
+                                                 uint16_t* __restrict__ out, int64_t os, int H,
+                                                 float eps) {
+  __shared__ float s_sum[kNT / 64];
+  const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const uint16_t* xr = x + row * xs;
+  uint16_t* rr = res ? res + row * rs : nullptr;
+  uint16_t* orow = out + row * os;
+  float ss = 0.0f;
+  for (int i = tid * 4; i < H; i += kNT * 4) {
+    float a[4], r[4];
+    load4(xr + i, a);
+    if (rr) {
+      load4(rr + i, r);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) a[k] += r[k];
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) ss += a[k] * a[k];
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+  if (lane == 0) s_sum[wid] = ss;
+  __syncthreads();
+  ss = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kNT / 64; ++k) ss += s_sum[k];
+  const float inv = rsqrtf(ss / (float)H + eps);
+  for (int i = tid * 4; i < H; i += kNT * 4) {
+    float a[4], r[4], wf[4];
+    load4(xr + i, a);
+    if (rr) {
+      load4(rr + i, r);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) a[k] += r[k];
+      uint2 nr;
+      nr.x = (uint32_t)to_bf(a[0]) | ((uint32_t)to_bf(a[1]) << 16);
+      nr.y = (uint32_t)to_bf(a[2]) | ((uint32_t)to_bf(a[3]) << 16);
+      *reinterpret_cast<uint2*>(rr + i) = nr;
+    }
+    load4(w + i, wf);
+    uint16_t o[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) o[k] = to_bf(bf(to_bf(a[k] * inv)) * wf[k]);
+    uint2 ov;
+    ov.x = (uint32_t)o[0] | ((uint32_t)o[1] << 16);
+    ov.y = (uint32_t)o[2] | ((uint32_t)o[3] << 16);
+    *reinterpret_cast<uint2*>(orow + i) = ov;
+  }
+}
+
+// one wave per (token, head); heads [0, Hq) are q, [Hq, Hq+Hkv) are k
+__global__ __launch_bounds__(kNT) void k_qk_norm_rope(const uint16_t* __restrict__ qkv, int64_t ts,
+                                                      int Hq, int Hkv,
+                                                      const uint16_t* __restrict__ qw,
+                                                      const uint16_t* __restrict__ kw,
+                                                      const float* __restrict__ cos_sin,
+                                                      const int64_t* __restrict__ positions,
+                                                      float eps, uint16_t* __restrict__ qo,
+                                                      uint16_t* __restrict__ ko, int N) {
+  const int wave = blockIdx.x * (kNT / 64) + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int H = Hq + Hkv;
+  if (wave >= N * H) return;
+  const int tok = wave / H, h = wave % H;
+  const bool isq = h < Hq;
+  const uint16_t* src = qkv + tok * ts + h * 128;
+  float x1 = bf(src[lane]), x2 = bf(src[lane + 64]);
+  float ss = x1 * x1 + x2 * x2;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+  const float inv = rsqrtf(ss / 128.0f + eps);
+  const uint16_t* w = isq ? qw : kw;
+  // RMSNorm (layernorm.py:18-25): normalise in fp32, round, multiply by weight
+  x1 = bf(bf_mul(to_bf(x1 * inv), w[lane]));
+  x2 = bf(bf_mul(to_bf(x2 * inv), w[lane + 64]));
+  // neox RoPE (rotary_embedding.py:8-16): cos/sin cache [pos, 64 | 64]
+  const int64_t p = positions[tok];
+  const float c = cos_sin[p * 128 + lane], s = cos_sin[p * 128 + 64 + lane];
+  const float y1 = x1 * c - x2 * s;
+  const float y2 = x2 * c + x1 * s;
+  uint16_t* dst = isq ? qo + ((int64_t)tok * Hq + h) * 128 : ko + ((int64_t)tok * Hkv + (h - Hq)) * 128;
+  dst[lane] = to_bf(y1);
+  dst[lane + 64] = to_bf(y2);
+}
+
+__global__ __launch_bounds__(kNT) void k_silu_mul(const uint16_t* __restrict__ gu, int64_t gs,
+                                                  int F, uint16_t* __restrict__ out, int64_t os,
+                                                  int N) {
+  const int64_t total = (int64_t)N * (F / 4);
+  for (int64_t i = blockIdx.x * (int64_t)kNT + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * kNT) {
+    const int64_t row = i / (F / 4);
+    const int c = (int)(i % (F / 4)) * 4;
+    const uint2 g = *reinterpret_cast<const uint2*>(gu + row * gs + c);
+    const uint2 u = *reinterpret_cast<const uint2*>(gu + row * gs + F + c);
+    const uint16_t gv[4] = {(uint16_t)g.x, (uint16_t)(g.x >> 16), (uint16_t)g.y,
+                            (uint16_t)(g.y >> 16)};
+    const uint16_t uv[4] = {(uint16_t)u.x, (uint16_t)(u.x >> 16), (uint16_t)u.y,
+                            (uint16_t)(u.y >> 16)};
+    uint16_t o[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float a = bf(gv[k]);
+      const uint16_t sl = to_bf(a / (1.0f + __expf(-a)));  // F.silu in fp32, rounded
+      o[k] = bf_mul(sl, uv[k]);
+    }
+    uint2 ov;
+    ov.x = (uint32_t)o[0] | ((uint32_t)o[1] << 16);
+    ov.y = (uint32_t)o[2] | ((uint32_t)o[3] << 16);
+    *reinterpret_cast<uint2*>(out + row * os + c) = ov;
+  }
+}
+
+}  // namespace hs
+
+using namespace hs;
+
+extern "C" {
+
+int hs_rmsnorm(const void* x, int64_t x_stride, void* residual, int64_t residual_stride,
+               const void* weight, void* out, int64_t out_stride, int rows, int hidden,
+               float eps, void* stream) {
+  if (rows == 0) return HS_OK;
+  if (!x || !weight || !out || rows < 0 || hidden <= 0) return HS_ERR_INVALID;
+  if (hidden % 4) return HS_ERR_UNSUPPORTED;
+  if ((x_stride | out_stride | (residual ? residual_stride : 0)) & 3) return HS_ERR_UNSUPPORTED;
+  if (((uintptr_t)x | (uintptr_t)out | (uintptr_t)weight | (uintptr_t)residual) & 7)
+    return HS_ERR_UNSUPPORTED;
+  hipLaunchKernelGGL(k_rmsnorm, dim3(rows), dim3(kNT), 0, reinterpret_cast<hipStream_t>(stream),
+                     static_cast<const uint16_t*>(x), x_stride, static_cast<uint16_t*>(residual),
+                     residual_stride, static_cast<const uint16_t*>(weight),
+                     static_cast<uint16_t*>(out), out_stride, hidden, eps);
+  return hipGetLastError() == hipSuccess ? HS_OK : HS_ERR_LAUNCH;
+}
+
+int hs_qk_norm_rope(const void* qkv, int64_t token_stride, int num_q_heads, int num_kv_heads,
+                    int head_dim, const void* q_weight, const void* k_weight,
+                    const float* cos_sin, const int64_t* positions, float eps, void* q_out,
+                    void* k_out, int num_tokens, void* stream) {
+  if (num_tokens == 0) return HS_OK;
+  if (!qkv || !q_weight || !k_weight || !cos_sin || !positions || !q_out || !k_out ||
+      num_tokens < 0 || num_q_heads <= 0 || num_kv_heads <= 0)
+    return HS_ERR_INVALID;
+  if (head_dim != 128) return HS_ERR_UNSUPPORTED;
+  const int64_t waves = (int64_t)num_tokens * (num_q_heads + num_kv_heads);
+  hipLaunchKernelGGL(k_qk_norm_rope, dim3((unsigned)((waves + 3) / 4)), dim3(kNT), 0,
+                     reinterpret_cast<hipStream_t>(stream), static_cast<const uint16_t*>(qkv),
+                     token_stride, num_q_heads, num_kv_heads,
+                     static_cast<const uint16_t*>(q_weight),
+                     static_cast<const uint16_t*>(k_weight), cos_sin, positions, eps,
+                     static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(k_out), num_tokens);
+  return hipGetLastError() == hipSuccess ? HS_OK : HS_ERR_LAUNCH;
+}
+
+int hs_silu_mul(const void* gate_up, int64_t gate_up_stride, int ffn, void* out,
+                int64_t out_stride, int rows, void* stream) {
+  if (rows == 0) return HS_OK;
+  if (!gate_up || !out || rows < 0 || ffn <= 0) return HS_ERR_INVALID;
+  if (ffn % 4 || (gate_up_stride | out_stride) & 3) return HS_ERR_UNSUPPORTED;
+  if (((uintptr_t)gate_up | (uintptr_t)out) & 7) return HS_ERR_UNSUPPORTED;
+  const int64_t total = (int64_t)rows * (ffn / 4);
+  int64_t blocks = (total + kNT - 1) / kNT;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(k_silu_mul, dim3((unsigned)blocks), dim3(kNT), 0,
+                     reinterpret_cast<hipStream_t>(stream),
+                     static_cast<const uint16_t*>(gate_up), gate_up_stride, ffn,
+                     static_cast<uint16_t*>(out), out_stride, rows);
+  return hipGetLastError() == hipSuccess ? HS_OK : HS_ERR_LAUNCH;
+}
+
+}  // extern "C"

@@ -5,7 +5,7 @@
 // paged cache with block_table, causal=True, softmax_scale = D^-0.5), and is
 // also usable for decode (q_len 1) and prefill (q_len > gamma+1).
 //
-// Work decomposition: a workgroup (4 waves) owns one (sequence, kv head,
+// Work decomposition: a workgroup (8 waves) owns one (sequence, kv head,
 // 16-row query tile, key split). The query tile holds the G = Hq/Hkv query
 // heads of up to 16/G consecutive query tokens, so one K/V head is streamed
 // once for all of them (GQA). Each wave walks 32-key windows of the split:
@@ -29,12 +29,14 @@ namespace hs {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kAW = 4;          // waves per workgroup
+constexpr int kAW = 8;          // waves per workgroup
 constexpr int kAT = kAW * 64;   // threads per workgroup
 constexpr int kD = 128;         // head dim
 constexpr int kWin = 32;        // keys per window
 constexpr int kRows = 16;       // query rows per tile
 constexpr int kVtStride = 40;   // LDS row stride (bf16) of the transposed V tile
+constexpr int kMaxSplit = 4096; // keys per split (block-table prefetch capacity)
+constexpr int kBtCap = kMaxSplit / kWin + 2;
 
 struct AttnArgs {
   const uint16_t* q;
@@ -105,9 +107,13 @@ __device__ __forceinline__ bf16x8_t load_kv8(const uint8_t* base, int64_t elem_o
 
 template <bool kFp8>
 __global__ __launch_bounds__(kAT) void k_verify_attn(AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t s_vt[kAW][kD * kVtStride];
+  // per-wave transposed V tiles; after the key loop the same bytes hold the
+  // per-wave partial outputs for the merge
+  constexpr int kVtBytes = kAW * kD * kVtStride * 2;
+  constexpr int kOBytes = kAW * kRows * kD * 4;
+  __shared__ __attribute__((aligned(16))) uint8_t s_raw[kVtBytes > kOBytes ? kVtBytes : kOBytes];
   __shared__ float s_m[kAW][kRows], s_l[kAW][kRows];
-  __shared__ float s_o[kAW][kRows * kD];
+  __shared__ int s_bt[kBtCap];
 
   const int split = blockIdx.x;
   const int kvh = blockIdx.y / a.qtiles;
@@ -134,6 +140,14 @@ __global__ __launch_bounds__(kAT) void k_verify_attn(AttnArgs a) {
     if (lim < hi) hi = lim;
   }
 
+  // block-table entries of the split, fetched once (in parallel with Q)
+  const int bt0 = lo / a.block_size;
+  const int nbt = (hi > lo) ? (hi - 1) / a.block_size - bt0 + 1 : 0;
+  for (int i = tid; i < nbt && i < kBtCap; i += kAT) {
+    const int bi = bt0 + i;
+    s_bt[i] = (bi < a.bt_width) ? a.bt[(int64_t)b * a.bt_stride + bi] : -1;
+  }
+
   // query row of this lane
   const int r = r0 + n;
   const bool r_ok = r < rows;
@@ -155,11 +169,12 @@ __global__ __launch_bounds__(kAT) void k_verify_attn(AttnArgs a) {
   f32x4_t oacc[8];
 #pragma unroll
   for (int db = 0; db < 8; ++db) oacc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  uint16_t* vt = s_vt[wid];
+  uint16_t* vt = reinterpret_cast<uint16_t*>(s_raw) + wid * (kD * kVtStride);
+  __syncthreads();  // s_bt ready
 
   for (int ws = lo + wid * kWin; ws < hi; ws += kAW * kWin) {
     const int blk_idx = ws / a.block_size;
-    const int blk = (blk_idx < a.bt_width) ? a.bt[(int64_t)b * a.bt_stride + blk_idx] : -1;
+    const int blk = s_bt[blk_idx - bt0];
     const bool blk_ok = (blk >= 0 && blk < a.num_blocks);
     const int slot0 = ws - blk_idx * a.block_size;
     const int64_t blk_base = (int64_t)blk * a.c_sb + (int64_t)kvh * a.c_sh;
@@ -263,14 +278,17 @@ __global__ __launch_bounds__(kAT) void k_verify_attn(AttnArgs a) {
     s_m[wid][n] = m;
     s_l[wid][n] = lsum;
   }
+  __syncthreads();  // every wave is done with its V tile
+  float(*s_o)[kRows * kD] = reinterpret_cast<float(*)[kRows * kD]>(s_raw);
   // O^T layout: lane holds O[row n][d = db*16 + 4g + j]
 #pragma unroll
   for (int db = 0; db < 8; ++db)
 #pragma unroll
     for (int j = 0; j < 4; ++j) s_o[wid][n * kD + db * 16 + 4 * g + j] = oacc[db][j];
   __syncthreads();
+  if (tid >= kRows * 16) return;
 
-  // merge the 4 waves: thread handles row tid/16, dims (tid%16)*8 .. +8
+  // merge the waves: thread handles row tid/16, dims (tid%16)*8 .. +8
   const int row = tid >> 4;
   const int d0 = (tid & 15) * 8;
   float M = -INFINITY;
@@ -317,7 +335,7 @@ __global__ __launch_bounds__(kAT) void k_verify_attn(AttnArgs a) {
 }
 
 // merges the key splits of every (sequence, kv head, query tile)
-__global__ __launch_bounds__(kAT) void k_attn_combine(AttnArgs a) {
+__global__ __launch_bounds__(kRows * 16) void k_attn_combine(AttnArgs a) {
   const int kvh = blockIdx.y / a.qtiles;
   const int qt = blockIdx.y % a.qtiles;
   const int b = blockIdx.x;
@@ -366,7 +384,10 @@ static void attn_plan(int B, int Hkv, int qtiles, int max_seqlen_k, int* nsplit,
   if (want < 1) want = 1;
   int64_t len = (max_seqlen_k + want - 1) / want;
   len = (len + 127) / 128 * 128;
-  if (len < 128) len = 128;
+  // a split below 512 keys costs more in the extra combine launch than it
+  // gains in parallelism; splits are also capped by the block-table prefetch
+  if (len < 512) len = 512;
+  if (len > kMaxSplit) len = kMaxSplit;
   *split_len = (int)len;
   *nsplit = (int)((max_seqlen_k + len - 1) / len);
   if (*nsplit < 1) *nsplit = 1;
@@ -464,8 +485,8 @@ int hs_verify_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_he
   else
     hipLaunchKernelGGL(k_verify_attn<false>, grid, dim3(kAT), 0, s, a);
   if (a.nsplit > 1)
-    hipLaunchKernelGGL(k_attn_combine, dim3(num_seqs, num_kv_heads * a.qtiles), dim3(kAT), 0, s,
-                       a);
+    hipLaunchKernelGGL(k_attn_combine, dim3(num_seqs, num_kv_heads * a.qtiles),
+                       dim3(kRows * 16), 0, s, a);
   return hipGetLastError() == hipSuccess ? HS_OK : HS_ERR_LAUNCH;
 }
 

@@ -15,6 +15,7 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
+from .. import ops as _ops
 from ..layers.attention import Attention
 
 
@@ -101,6 +102,25 @@ class Qwen3Layer(nn.Module):
         self.attn = Attention(g.num_heads, D, D ** -0.5, g.num_kv_heads)
 
     def forward(self, positions, h, residual):
+        """qwen3.py:148-161 with the fused gfx950 elementwise kernels."""
+        g = self.g
+        if residual is None:
+            residual = h  # the embedding output; later adds update it in place
+            x = _ops.rmsnorm(h, self.ln1, g.rms_eps)
+        else:
+            x = _ops.rmsnorm(h, self.ln1, g.rms_eps, residual=residual)
+        qkv = F.linear(x, self.qkv)
+        q, k = _ops.qk_norm_rope(qkv, g.num_heads, g.num_kv_heads, self.q_norm, self.k_norm,
+                                 self.rope.cos_sin, positions, g.rms_eps)
+        v = qkv[:, self.q_size + self.kv_size:].view(-1, g.num_kv_heads, g.head_dim)
+        o = self.attn(q, k, v)
+        h = F.linear(o.reshape(o.shape[0], -1), self.o)
+        x = _ops.rmsnorm(h, self.ln2, g.rms_eps, residual=residual)
+        h = F.linear(_ops.silu_mul(F.linear(x, self.gate_up)), self.down)
+        return h, residual
+
+    def forward_reference(self, positions, h, residual):
+        """Eager PyTorch restatement of the same layer (used by tests)."""
         g = self.g
         if residual is None:
             x, residual = rms_norm(h, self.ln1, g.rms_eps), h
@@ -164,13 +184,18 @@ class Qwen3Host(nn.Module):
     def attention_layers(self):
         return [layer.attn for layer in self.layers]
 
-    def forward(self, input_ids, positions):
+    def forward(self, input_ids, positions, reference: bool = False):
         h = F.embedding(input_ids, self.embed)
         residual = None
         for layer in self.layers:
-            h, residual = layer(positions, h, residual)
-        h, _ = add_rms_norm(h, residual, self.norm, self.g.rms_eps)
-        return h
+            if reference:
+                h, residual = layer.forward_reference(positions, h, residual)
+            else:
+                h, residual = layer(positions, h, residual)
+        if reference:
+            h, _ = add_rms_norm(h, residual, self.norm, self.g.rms_eps)
+            return h
+        return _ops.rmsnorm(h, self.norm, self.g.rms_eps, residual=residual)
 
     def compute_logits(self, h):
         return F.linear(h, self.lm_head)

@@ -415,3 +415,44 @@ def draft_prepare(state: SpecStateTensors, draft_tokens: torch.Tensor | None, st
         int(step), int(R == 2), ids.data_ptr(), pos.data_ptr(), slots.data_ptr(), cq.data_ptr(),
         ck.data_ptr(), _stream(dev)), "hs_draft_prepare")
     return out
+
+
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float,
+            residual: torch.Tensor | None = None, out: torch.Tensor | None = None):
+    """RMSNorm (layernorm.py:18-25) or fused add + RMSNorm (:27-36, residual updated
+    in place). x [rows, H] bf16 with contiguous rows."""
+    dev = _need_cuda(x, weight, residual, out)
+    rows, H = x.shape
+    if out is None:
+        out = torch.empty((rows, H), dtype=torch.bfloat16, device=dev)
+    L.check(L.lib().hs_rmsnorm(x.data_ptr(), x.stride(0),
+                               None if residual is None else residual.data_ptr(),
+                               0 if residual is None else residual.stride(0), weight.data_ptr(),
+                               out.data_ptr(), out.stride(0), rows, H, float(eps), _stream(dev)),
+            "hs_rmsnorm")
+    return out
+
+
+def qk_norm_rope(qkv: torch.Tensor, num_q_heads: int, num_kv_heads: int, q_weight, k_weight,
+                 cos_sin: torch.Tensor, positions: torch.Tensor, eps: float):
+    """q/k RMSNorm + RoPE of a fused qkv projection [N, (Hq+2Hkv)*128] -> (q, k)."""
+    dev = _need_cuda(qkv, q_weight, k_weight, cos_sin, positions)
+    N = qkv.shape[0]
+    q = torch.empty((N, num_q_heads, 128), dtype=torch.bfloat16, device=dev)
+    k = torch.empty((N, num_kv_heads, 128), dtype=torch.bfloat16, device=dev)
+    L.check(L.lib().hs_qk_norm_rope(qkv.data_ptr(), qkv.stride(0), num_q_heads, num_kv_heads,
+                                    128, q_weight.data_ptr(), k_weight.data_ptr(),
+                                    cos_sin.data_ptr(), positions.data_ptr(), float(eps),
+                                    q.data_ptr(), k.data_ptr(), N, _stream(dev)),
+            "hs_qk_norm_rope")
+    return q, k
+
+
+def silu_mul(gate_up: torch.Tensor) -> torch.Tensor:
+    """activation.py:8-16: silu(gate) * up of a fused [N, 2F] projection."""
+    dev = _need_cuda(gate_up)
+    N, F2 = gate_up.shape
+    out = torch.empty((N, F2 // 2), dtype=torch.bfloat16, device=dev)
+    L.check(L.lib().hs_silu_mul(gate_up.data_ptr(), gate_up.stride(0), F2 // 2, out.data_ptr(),
+                                out.stride(0), N, _stream(dev)), "hs_silu_mul")
+    return out

@@ -244,6 +244,32 @@ int hs_zero_kv_slots(void* cache, int64_t plane_bytes, int num_planes, int64_t s
                      int64_t row_bytes, int64_t slots_per_plane, const int32_t* slots,
                      int num_slots, void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* Fused elementwise kernels of the decoder layer (bf16 in/out). They stand  */
+/* in for the torch.compile-fused ops of the reference around the verify    */
+/* path: RMSNorm / fused add + RMSNorm (mini_vllm/layers/layernorm.py:18-36),*/
+/* q/k RMSNorm + neox RoPE (qwen3.py:82-85, rotary_embedding.py:8-50) and    */
+/* SiLU-and-mul (activation.py:8-16).                                        */
+/* ------------------------------------------------------------------------ */
+/* out = RMSNorm(x (+ residual)) * weight; with residual != NULL the residual  */
+/* row is replaced by bf16(x + residual) (strides in elements).              */
+int hs_rmsnorm(const void* x, int64_t x_stride, void* residual, int64_t residual_stride,
+               const void* weight, void* out, int64_t out_stride, int rows, int hidden,
+               float eps, void* stream);
+
+/* qkv [tokens, (Hq + 2*Hkv) * 128] (row stride token_stride): q and k heads are */
+/* RMS-normalised with q_weight / k_weight [128], rotated with cos_sin          */
+/* [max_pos, 128] (cos | sin) at positions[tokens], and written to q_out        */
+/* [tokens, Hq, 128] and k_out [tokens, Hkv, 128]. head_dim must be 128.        */
+int hs_qk_norm_rope(const void* qkv, int64_t token_stride, int num_q_heads, int num_kv_heads,
+                    int head_dim, const void* q_weight, const void* k_weight,
+                    const float* cos_sin, const int64_t* positions, float eps, void* q_out,
+                    void* k_out, int num_tokens, void* stream);
+
+/* out[r, :ffn] = silu(gate_up[r, :ffn]) * gate_up[r, ffn:2*ffn]. */
+int hs_silu_mul(const void* gate_up, int64_t gate_up_stride, int ffn, void* out,
+                int64_t out_stride, int rows, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -109,3 +109,32 @@ def test_graph_replay_matches_eager(cuda):
     assert graph.lengths() == eager.lengths()
     for b in range(2):
         assert graph.tokens(b) == eager.tokens(b)
+
+
+def test_fused_layer_matches_eager(cuda):
+    """Fused RMSNorm / qk-norm+RoPE / SiLU-mul kernels vs the eager restatement of
+    qwen3.py:72-185 (same attention kernel on both sides)."""
+    q3, sr = _mods()
+    g = _small(q3, layers=3, hidden=1024, heads=8, kv=4)
+    target = q3.Qwen3Host(g, device=cuda, seed=31)
+    draft = q3.Qwen3Host(g, share_from=target, num_layers=1)
+    runner = sr.SpecRunner(target, draft, batch=1, gamma=2, max_model_len=256, block_size=32,
+                           device=cuda)
+    prompt = list(range(10, 60))
+    runner.load_prompts([prompt])
+    ids = torch.tensor(prompt, device=cuda)
+    pos = torch.arange(len(prompt), device=cuda)
+    slots = torch.tensor([int(runner.state.block_tables[0, i // 32]) * 32 + i % 32
+                          for i in range(len(prompt))], dtype=torch.int32, device=cuda)
+    cu = torch.tensor([0, len(prompt)], dtype=torch.int32, device=cuda)
+    ctx = importlib.import_module("hilda-vllm_amd.utils.context")
+    with torch.inference_mode():
+        ctx.set_context(True, cu, cu, len(prompt), len(prompt), slots, None,
+                        runner.state.block_tables)
+        ref = target(ids, pos, reference=True).float()
+        got = target(ids, pos).float()
+        ctx.reset_context()
+    torch.cuda.synchronize()
+    err = (got - ref).abs()
+    assert err.max() <= 0.05 * ref.abs().max() + 0.02, float(err.max())
+    assert torch.nn.functional.cosine_similarity(got.flatten(), ref.flatten(), dim=0) > 0.999
