@@ -105,8 +105,11 @@ __device__ __forceinline__ bf16x8_t load_kv8(const uint8_t* base, int64_t elem_o
   }
 }
 
-template <bool kFp8>
+// kG: query heads per KV head as a compile-time constant (2, 4 or 8), or 0 to
+// read it from the arguments (any other group size)
+template <bool kFp8, int kG>
 __global__ __launch_bounds__(kAT) void k_verify_attn(AttnArgs a) {
+  const int G = kG ? kG : a.G;
   // per-wave transposed V tiles; after the key loop the same bytes hold the
   // per-wave partial outputs for the merge
   constexpr int kVtBytes = kAW * kD * kVtStride * 2;
@@ -126,7 +129,7 @@ __global__ __launch_bounds__(kAT) void k_verify_attn(AttnArgs a) {
   const int qs = a.cu_q[b];
   const int Lq = a.cu_q[b + 1] - qs;
   const int Lk = a.cu_k[b + 1] - a.cu_k[b];
-  const int rows = Lq * a.G;
+  const int rows = Lq * G;
   const int r0 = qt * kRows;
   if (r0 >= rows || Lk <= 0) return;
   const int nsplit_b = (Lk + a.split_len - 1) / a.split_len;
@@ -136,7 +139,7 @@ __global__ __launch_bounds__(kAT) void k_verify_attn(AttnArgs a) {
   int hi = lo + a.split_len < Lk ? lo + a.split_len : Lk;
   {
     const int last_row = (r0 + kRows - 1 < rows - 1) ? r0 + kRows - 1 : rows - 1;
-    const int lim = Lk - Lq + last_row / a.G + 1;  // keys visible to the tile's last token
+    const int lim = Lk - Lq + last_row / G + 1;  // keys visible to the tile's last token
     if (lim < hi) hi = lim;
   }
 
@@ -151,8 +154,8 @@ __global__ __launch_bounds__(kAT) void k_verify_attn(AttnArgs a) {
   // query row of this lane
   const int r = r0 + n;
   const bool r_ok = r < rows;
-  const int qi = r_ok ? r / a.G : 0;
-  const int qh = kvh * a.G + (r_ok ? r % a.G : 0);
+  const int qi = r_ok ? r / G : 0;
+  const int qh = kvh * G + (r_ok ? r % G : 0);
   const int lim_r = Lk - Lq + qi;  // last visible key of this row
   bf16x8_t qv[4];
 #pragma unroll
@@ -311,7 +314,7 @@ __global__ __launch_bounds__(kAT) void k_verify_attn(AttnArgs a) {
   }
   const int rr = r0 + row;
   if (rr >= rows) return;
-  const int oi = rr / a.G, oh = kvh * a.G + rr % a.G;
+  const int oi = rr / G, oh = kvh * G + rr % G;
   if (nsplit_b == 1) {
     const float inv = (L > 0.0f) ? a.v_scale / L : 0.0f;
     union {
@@ -375,6 +378,16 @@ __global__ __launch_bounds__(kRows * 16) void k_attn_combine(AttnArgs a) {
 #pragma unroll
   for (int t = 0; t < 8; ++t) ob.h[t] = f32_to_bf16_rne(o[t] * inv);
   *reinterpret_cast<uint4*>(a.out + (int64_t)(qs + oi) * a.o_st + (int64_t)oh * a.o_sh + d0) = ob.u;
+}
+
+template <bool kFp8>
+static void launch_attn(int G, dim3 grid, hipStream_t s, const AttnArgs& a) {
+  switch (G) {
+    case 2: hipLaunchKernelGGL((k_verify_attn<kFp8, 2>), grid, dim3(kAT), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((k_verify_attn<kFp8, 4>), grid, dim3(kAT), 0, s, a); break;
+    case 8: hipLaunchKernelGGL((k_verify_attn<kFp8, 8>), grid, dim3(kAT), 0, s, a); break;
+    default: hipLaunchKernelGGL((k_verify_attn<kFp8, 0>), grid, dim3(kAT), 0, s, a); break;
+  }
 }
 
 static void attn_plan(int B, int Hkv, int qtiles, int max_seqlen_k, int* nsplit, int* split_len) {
@@ -481,9 +494,9 @@ int hs_verify_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_he
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   dim3 grid(a.nsplit, num_kv_heads * a.qtiles, num_seqs);
   if (a.fp8)
-    hipLaunchKernelGGL(k_verify_attn<true>, grid, dim3(kAT), 0, s, a);
+    launch_attn<true>(G, grid, s, a);
   else
-    hipLaunchKernelGGL(k_verify_attn<false>, grid, dim3(kAT), 0, s, a);
+    launch_attn<false>(G, grid, s, a);
   if (a.nsplit > 1)
     hipLaunchKernelGGL(k_attn_combine, dim3(num_seqs, num_kv_heads * a.qtiles),
                        dim3(kRows * 16), 0, s, a);
