@@ -34,7 +34,6 @@ constexpr int kAT = kAW * 64;   // threads per workgroup
 constexpr int kD = 128;         // head dim
 constexpr int kWin = 32;        // keys per window
 constexpr int kRows = 16;       // query rows per tile
-constexpr int kVtStride = 40;   // LDS row stride (bf16) of the transposed V tile
 constexpr int kMaxSplit = 4096; // keys per split (block-table prefetch capacity)
 constexpr int kBtCap = kMaxSplit / kWin + 2;
 
@@ -105,16 +104,67 @@ __device__ __forceinline__ bf16x8_t load_kv8(const uint8_t* base, int64_t elem_o
   }
 }
 
+// LDS layout of one window tile: kWin cached head rows, one row per key, with
+// the 16-byte chunks of row kk stored at chunk index (c ^ swz(kk)) so that the
+// MFMA operand reads below are free of bank conflicts.
+//   bf16 rows (256 B, 16 chunks): K reads touch keys 8a+4kb+c (a, c = 0..3)
+//     at one chunk; V transpose reads touch keys 8g+4h+q (q = 0..3) at two
+//     adjacent chunks.
+//   fp8 rows (128 B, 8 chunks): rows of equal parity share a bank half; K
+//     reads touch keys 8a+4kb+{c, c+2}, V transpose reads keys 8g+{0,2,4,6}.
+__device__ __forceinline__ int swz16(int kk) {
+  return ((kk & 3) << 1) | ((kk >> 3) & 1) | (((kk >> 4) & 1) << 3);
+}
+__device__ __forceinline__ int swz8(int kk) {
+  return ((kk >> 1) & 1) | ((((kk >> 2) ^ (kk >> 3)) & 1) << 1) | (((kk >> 4) & 1) << 2);
+}
+
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+typedef int v2i32_t __attribute__((ext_vector_type(2)));
+#define HS_LDS __attribute__((address_space(3)))
+
+// Copies the K and V rows of one 32-key window into the wave's LDS tiles with
+// global->LDS loads (16 bytes per lane, each instruction covering whole rows).
+// Keys at or past `hi` re-read key ws (always valid) so every tile row holds
+// finite cache data; their scores are masked to -inf.
+template <bool kFp8>
+__device__ __forceinline__ void issue_window(const AttnArgs& a, const uint8_t* kbase,
+                                             const uint8_t* vbase, int ws, int hi,
+                                             uint8_t* tile_k, uint8_t* tile_v, int lane) {
+  constexpr int kRowB = kFp8 ? 128 : 256;
+  constexpr int kLanesPerRow = kRowB / 16;
+  constexpr int kRowsPerInst = 64 / kLanesPerRow;
+  const int esz = kFp8 ? 1 : 2;
+#pragma unroll
+  for (int i = 0; i < kWin / kRowsPerInst; ++i) {
+    const int kk = i * kRowsPerInst + lane / kLanesPerRow;
+    const int sl = lane % kLanesPerRow;
+    const int c = sl ^ (kFp8 ? swz8(kk) : swz16(kk));
+    const int key = (ws + kk < hi) ? kk : 0;
+    const int64_t off = ((int64_t)key * a.c_st) * esz + c * 16;
+    __builtin_amdgcn_global_load_lds(kbase + off, (HS_LDS void*)(tile_k + i * 1024), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(vbase + off, (HS_LDS void*)(tile_v + i * 1024), 16, 0, 0);
+  }
+}
+
+// 8 fp8 e4m3fn values held as two dwords -> bf16x8
+__device__ __forceinline__ bf16x8_t fp8x8w_to_bf16(uint32_t lo, uint32_t hi) {
+  return fp8x8_to_bf16(make_uint2(lo, hi));
+}
+
 // kG: query heads per KV head as a compile-time constant (2, 4 or 8), or 0 to
 // read it from the arguments (any other group size)
 template <bool kFp8, int kG>
 __global__ __launch_bounds__(kAT) void k_verify_attn(AttnArgs a) {
   const int G = kG ? kG : a.G;
-  // per-wave transposed V tiles; after the key loop the same bytes hold the
+  constexpr int kRowB = kFp8 ? 128 : 256;
+  constexpr int kTileB = kWin * kRowB;
+  constexpr int kOStride = kD + 8;  // floats per row of a wave's partial output
+  constexpr int kKvBytes = kAW * 2 * kTileB;
+  constexpr int kOBytes = kAW * kRows * kOStride * 4;
+  // per-wave K and V window tiles; after the key loop the same bytes hold the
   // per-wave partial outputs for the merge
-  constexpr int kVtBytes = kAW * kD * kVtStride * 2;
-  constexpr int kOBytes = kAW * kRows * kD * 4;
-  __shared__ __attribute__((aligned(16))) uint8_t s_raw[kVtBytes > kOBytes ? kVtBytes : kOBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t s_raw[kKvBytes > kOBytes ? kKvBytes : kOBytes];
   __shared__ float s_m[kAW][kRows], s_l[kAW][kRows];
   __shared__ int s_bt[kBtCap];
 
@@ -126,6 +176,16 @@ __global__ __launch_bounds__(kAT) void k_verify_attn(AttnArgs a) {
   const int n = lane & 15;  // query row of this lane (B-operand column)
   const int g = lane >> 4;  // k-group of this lane
 
+  // block-table entries this split can touch, fetched before the sequence
+  // lengths are known (they only depend on the split)
+  const int lo = split * a.split_len;
+  const int bt0 = lo / a.block_size;
+  {
+    int nbt = (lo + a.split_len - 1) / a.block_size - bt0 + 1;
+    if (nbt > a.bt_width - bt0) nbt = a.bt_width - bt0;
+    for (int i = tid; i < nbt && i < kBtCap; i += kAT) s_bt[i] = a.bt[(int64_t)b * a.bt_stride + bt0 + i];
+  }
+
   const int qs = a.cu_q[b];
   const int Lq = a.cu_q[b + 1] - qs;
   const int Lk = a.cu_k[b + 1] - a.cu_k[b];
@@ -135,21 +195,13 @@ __global__ __launch_bounds__(kAT) void k_verify_attn(AttnArgs a) {
   const int nsplit_b = (Lk + a.split_len - 1) / a.split_len;
   if (split >= nsplit_b) return;
 
-  const int lo = split * a.split_len;
   int hi = lo + a.split_len < Lk ? lo + a.split_len : Lk;
   {
     const int last_row = (r0 + kRows - 1 < rows - 1) ? r0 + kRows - 1 : rows - 1;
     const int lim = Lk - Lq + last_row / G + 1;  // keys visible to the tile's last token
     if (lim < hi) hi = lim;
   }
-
-  // block-table entries of the split, fetched once (in parallel with Q)
-  const int bt0 = lo / a.block_size;
-  const int nbt = (hi > lo) ? (hi - 1) / a.block_size - bt0 + 1 : 0;
-  for (int i = tid; i < nbt && i < kBtCap; i += kAT) {
-    const int bi = bt0 + i;
-    s_bt[i] = (bi < a.bt_width) ? a.bt[(int64_t)b * a.bt_stride + bi] : -1;
-  }
+  const int nbt_used = (hi > lo) ? (hi - 1) / a.block_size - bt0 + 1 : 0;
 
   // query row of this lane
   const int r = r0 + n;
@@ -172,106 +224,138 @@ __global__ __launch_bounds__(kAT) void k_verify_attn(AttnArgs a) {
   f32x4_t oacc[8];
 #pragma unroll
   for (int db = 0; db < 8; ++db) oacc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  uint16_t* vt = reinterpret_cast<uint16_t*>(s_raw) + wid * (kD * kVtStride);
+  uint8_t* tile_k = s_raw + wid * 2 * kTileB;
+  uint8_t* tile_v = tile_k + kTileB;
+  const int esz = kFp8 ? 1 : 2;
   __syncthreads();  // s_bt ready
 
-  for (int ws = lo + wid * kWin; ws < hi; ws += kAW * kWin) {
+  // window ws of this wave -> cache row bases (bytes) of its K and V head rows;
+  // false when its block is not a valid cache block (the window is skipped)
+  auto window_base = [&](int ws, const uint8_t*& kb, const uint8_t*& vb) -> bool {
     const int blk_idx = ws / a.block_size;
-    const int blk = s_bt[blk_idx - bt0];
-    const bool blk_ok = (blk >= 0 && blk < a.num_blocks);
-    const int slot0 = ws - blk_idx * a.block_size;
-    const int64_t blk_base = (int64_t)blk * a.c_sb + (int64_t)kvh * a.c_sh;
+    const int bi = blk_idx - bt0;
+    const int blk = (bi < nbt_used && bi < kBtCap && bt0 + bi < a.bt_width) ? s_bt[bi] : -1;
+    if (blk < 0 || blk >= a.num_blocks) return false;
+    const int64_t off = ((int64_t)blk * a.c_sb + (int64_t)(ws - blk_idx * a.block_size) * a.c_st +
+                         (int64_t)kvh * a.c_sh) * esz;
+    kb = a.kc + off;
+    vb = a.vc + off;
+    return true;
+  };
 
-    // K as the A operand: row rho = n holds key ws + 8*(n/4) + 4*kb + (n%4)
-    bf16x8_t ka[2][4];
+  int ws = lo + wid * kWin;
+  bool have = false;
+  if (ws < hi) {
+    const uint8_t *kb, *vb;
+    have = window_base(ws, kb, vb);
+    if (have) issue_window<kFp8>(a, kb, vb, ws, hi, tile_k, tile_v, lane);
+  }
+  while (ws < hi) {
+    const int ws_next = ws + kAW * kWin;
+    const bool cur = have;
+    bf16x8_t ka[2][4], va[8];
+    if (cur) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      // K as the A operand: row rho = n holds key ws + 8*(n/4) + 4*kb + (n%4)
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      const int kl = 8 * (n >> 2) + 4 * kb + (n & 3);
-      const bool ok = blk_ok && (ws + kl < hi);
-      const int64_t off = blk_base + (int64_t)(slot0 + kl) * a.c_st + g * 8;
+      for (int kb = 0; kb < 2; ++kb) {
+        const int kk = 8 * (n >> 2) + 4 * kb + (n & 3);
+        const uint8_t* row = tile_k + kk * kRowB;
 #pragma unroll
-      for (int ds = 0; ds < 4; ++ds)
-        ka[kb][ds] = ok ? load_kv8<kFp8>(a.kc, off + ds * 32)
-                        : u4_to_bf16x8(make_uint4(0, 0, 0, 0));
-    }
-    // V rows of the window: load i holds key ws + 4*i + g, dims 8*n .. 8*n+7
-    bf16x8_t vv[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int kl = 4 * i + g;
-      const bool ok = blk_ok && (ws + kl < hi);
-      const int64_t off = blk_base + (int64_t)(slot0 + kl) * a.c_st + n * 8;
-      vv[i] = ok ? load_kv8<kFp8>(a.vc, off) : u4_to_bf16x8(make_uint4(0, 0, 0, 0));
-    }
-
-    // S^T = K Q^T for the two 16-key blocks
-    f32x4_t st[2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ds = 0; ds < 4; ++ds)
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[kb][ds], qv[ds], acc, 0, 0, 0);
-      st[kb] = acc;
-    }
-    // lane holds row n, keys ws + 8g + 4kb + j
-    float sv[8];
-    float mloc = -INFINITY;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int key = ws + 8 * g + 4 * kb + j;
-        float v = st[kb][j] * a.scale_log2;
-        if (!r_ok || key >= hi || key > lim_r) v = -INFINITY;
-        sv[kb * 4 + j] = v;
-        mloc = fmaxf(mloc, v);
+        for (int ds = 0; ds < 4; ++ds) {
+          if constexpr (kFp8) {
+            const int u = g + 4 * ds;  // 8-byte unit of dims 8g + 32ds
+            const int ph = (((u >> 1) ^ swz8(kk)) << 4) | ((u & 1) << 3);
+            const uint2 raw = *reinterpret_cast<const uint2*>(row + ph);
+            ka[kb][ds] = fp8x8w_to_bf16(raw.x, raw.y);
+          } else {
+            const int ph = ((g + 4 * ds) ^ swz16(kk)) << 4;
+            ka[kb][ds] = u4_to_bf16x8(*reinterpret_cast<const uint4*>(row + ph));
+          }
+        }
       }
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-    const float m_new = fmaxf(m, mloc);
-    const float base = (m_new == -INFINITY) ? 0.0f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m - base);
-    m = m_new;
-    float psum = 0.0f;
-    union {
-      uint16_t h[8];
-      bf16x8_t v;
-    } pb;
+      // V^T as the A operand of d-block db: lane (i = n, g) holds V[8g .. 8g+7][16db + i],
+      // gathered from the row-major tile with transposing LDS reads
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      const float p = __builtin_amdgcn_exp2f(sv[t] - base);
-      psum += p;
-      pb.h[t] = f32_to_bf16_rne(p);
+      for (int db = 0; db < 8; ++db) {
+        if constexpr (kFp8) {
+          const int kk = 8 * g + (n >> 1);
+          const int ph = ((db ^ swz8(kk)) << 4) | ((n & 1) << 3);
+          const v2i32_t t = __builtin_amdgcn_ds_read_tr8_b64_v2i32((HS_LDS v2i32_t*)(tile_v + kk * kRowB + ph));
+          va[db] = fp8x8w_to_bf16((uint32_t)t[0], (uint32_t)t[1]);
+        } else {
+          union {
+            v4i16_t h[2];
+            bf16x8_t v;
+          } u;
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int kk = 8 * g + 4 * h + (n >> 2);
+            const int ph = (((2 * db + ((n & 3) >> 1)) ^ swz16(kk)) << 4) | ((n & 1) << 3);
+            u.h[h] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((HS_LDS v4i16_t*)(tile_v + kk * kRowB + ph));
+          }
+          va[db] = u.v;
+        }
+      }
+      // every LDS read of the tiles has returned before the next window overwrites them
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
-    lsum = lsum * alpha + psum;
+    have = false;
+    if (ws_next < hi) {
+      const uint8_t *kb, *vb;
+      have = window_base(ws_next, kb, vb);
+      if (have) issue_window<kFp8>(a, kb, vb, ws_next, hi, tile_k, tile_v, lane);
+    }
+    if (cur) {
+      // S^T = K Q^T for the two 16-key blocks
+      f32x4_t st[2];
 #pragma unroll
-    for (int db = 0; db < 8; ++db) oacc[db] *= alpha;
-
-    // V^T into LDS: vt[d][key]
+      for (int kb = 0; kb < 2; ++kb) {
+        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+        for (int ds = 0; ds < 4; ++ds)
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[kb][ds], qv[ds], acc, 0, 0, 0);
+        st[kb] = acc;
+      }
+      // lane holds row n, keys ws + 8g + 4kb + j
+      float sv[8];
+      float mloc = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int key = ws + 8 * g + 4 * kb + j;
+          float v = st[kb][j] * a.scale_log2;
+          if (!r_ok || key >= hi || key > lim_r) v = -INFINITY;
+          sv[kb * 4 + j] = v;
+          mloc = fmaxf(mloc, v);
+        }
+      mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
+      mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+      const float m_new = fmaxf(m, mloc);
+      const float base = (m_new == -INFINITY) ? 0.0f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f(m - base);
+      m = m_new;
+      float psum = 0.0f;
       union {
-        bf16x8_t v;
         uint16_t h[8];
-      } u;
-      u.v = vv[i];
-      const int kl = 4 * i + g;
+        bf16x8_t v;
+      } pb;
 #pragma unroll
-      for (int t = 0; t < 8; ++t) vt[(n * 8 + t) * kVtStride + kl] = u.h[t];
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // O^T[d][row] += V^T[d][keys 8g..8g+7] * P^T
+      for (int t = 0; t < 8; ++t) {
+        const float p = __builtin_amdgcn_exp2f(sv[t] - base);
+        psum += p;
+        pb.h[t] = f32_to_bf16_rne(p);
+      }
+      lsum = lsum * alpha + psum;
+      // O^T[d][row] = alpha * O^T + V^T[d][keys 8g..8g+7] * P^T
 #pragma unroll
-    for (int db = 0; db < 8; ++db) {
-      const uint4 av = *reinterpret_cast<const uint4*>(&vt[(db * 16 + n) * kVtStride + 8 * g]);
-      oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(u4_to_bf16x8(av), pb.v, oacc[db], 0, 0, 0);
+      for (int db = 0; db < 8; ++db) {
+        oacc[db] *= alpha;
+        oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[db], pb.v, oacc[db], 0, 0, 0);
+      }
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    ws = ws_next;
   }
 
   // per-row totals of this wave
@@ -281,13 +365,13 @@ __global__ __launch_bounds__(kAT) void k_verify_attn(AttnArgs a) {
     s_m[wid][n] = m;
     s_l[wid][n] = lsum;
   }
-  __syncthreads();  // every wave is done with its V tile
-  float(*s_o)[kRows * kD] = reinterpret_cast<float(*)[kRows * kD]>(s_raw);
+  __syncthreads();  // every wave is done with its tiles
+  float* s_o = reinterpret_cast<float*>(s_raw);
   // O^T layout: lane holds O[row n][d = db*16 + 4g + j]
 #pragma unroll
   for (int db = 0; db < 8; ++db)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) s_o[wid][n * kD + db * 16 + 4 * g + j] = oacc[db][j];
+    *reinterpret_cast<float4*>(&s_o[(wid * kRows + n) * kOStride + db * 16 + 4 * g]) =
+        make_float4(oacc[db][0], oacc[db][1], oacc[db][2], oacc[db][3]);
   __syncthreads();
   if (tid >= kRows * 16) return;
 
@@ -304,13 +388,13 @@ __global__ __launch_bounds__(kAT) void k_verify_attn(AttnArgs a) {
     f[w] = __builtin_amdgcn_exp2f(s_m[w][row] - Mb);
     L += s_l[w][row] * f[w];
   }
-  float o[8];
+  float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    float acc = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kAW; ++w) acc += s_o[w][row * kD + d0 + t] * f[w];
-    o[t] = acc;
+  for (int w = 0; w < kAW; ++w) {
+    const float4 x0 = *reinterpret_cast<const float4*>(&s_o[(w * kRows + row) * kOStride + d0]);
+    const float4 x1 = *reinterpret_cast<const float4*>(&s_o[(w * kRows + row) * kOStride + d0 + 4]);
+    o[0] += x0.x * f[w]; o[1] += x0.y * f[w]; o[2] += x0.z * f[w]; o[3] += x0.w * f[w];
+    o[4] += x1.x * f[w]; o[5] += x1.y * f[w]; o[6] += x1.z * f[w]; o[7] += x1.w * f[w];
   }
   const int rr = r0 + row;
   if (rr >= rows) return;
