@@ -110,6 +110,11 @@ def _accept_inputs(torch, hv, dev, args):
     return target, q, small
 
 
+def _accept_tag(args) -> str:
+    tag = f"accept-b{args.batch}-g{args.gamma}-{args.mode}-{args.logits}"
+    return tag + ("-perseq" if args.per_seq else "")
+
+
 def bench_accept(args, torch, hv):
     dev = torch.device("cuda:0")
     B, gamma = args.batch, args.gamma
@@ -167,7 +172,8 @@ def bench_accept(args, torch, hv):
         "wall_s": round(wall, 3),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None, "bytes_per_step": step_bytes,
+                     "traffic": profiled_traffic("hs_spec_accept call", _accept_tag(args)),
+                     "bytes_per_step": step_bytes,
                      "kernels": "one hs_spec_accept call (row statistics, filter when "
                                 "filtered, decision + resample partials, final search)"},
     }
@@ -251,7 +257,9 @@ def bench_attention(args, torch, hv):
         "tflops": round(flops / (us * 1e-6) / 1e12, 3),
         "wall_s": round(wall, 3),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": profiled_traffic(f"k_verify_attn<{'true' if fp8 else 'false'}, 2>",
+                                                 f"attention-{args.kv}"),
                      "bytes_per_launch": per_launch,
                      "kernel": f"k_verify_attn<{'true' if fp8 else 'false'}, 2> (+ k_attn_combine when split)"},
     }
@@ -348,7 +356,7 @@ def bench_spec(args, torch, hv):
     verify_ms = sum(evs[3 * i + 1].elapsed_time(evs[3 * i + 2]) for i in range(args.steps))
     tok_s = emitted / (gpu_ms / 1e3)
     accepted_drafts = emitted - args.steps
-    roof = attention_probe(torch, hv, runner, len1)
+    roof = attention_probe(torch, hv, kv=args.kv)
     res = {
         "metric": METRIC,
         "value": round(tok_s, 2),
@@ -383,43 +391,146 @@ def bench_spec(args, torch, hv):
     return res
 
 
-def attention_probe(torch, hv, runner, L):
-    """Average duration of the verify-attention kernel at the verify shape of this run
-    (B=1, gamma+1=4 queries, 32 Q / 8 KV heads, context L) over the target's 36 layer
-    caches: 36 launches captured in a HIP graph, replayed 20 times between two HIP
-    events on the launch stream (per-launch time includes the graph's launch gaps)."""
-    dev = runner.device
-    g = runner.target.g
-    R = runner.gamma + 1
-    reps = 20
-    q = torch.randn((R, g.num_heads, g.head_dim), device=dev).to(torch.bfloat16)
+PROBE_CONTEXT = 320  # config-3 end state: 64 prompt tokens + 256 generated tokens
+
+
+def attention_probe(torch, hv, kv: str = "auto", L: int = PROBE_CONTEXT, layers: int = 36,
+                    reps: int = 20):
+    """The verify-attention kernel at the batch-1 verify shape of the 8B target
+    (B=1, gamma+1=4 queries, 32 Q / 8 KV heads, D=128, context L, 256-token blocks):
+    one launch per layer over `layers` separate random caches (as in one verify
+    step), captured in a HIP graph and replayed `reps` times between two HIP events
+    on the launch stream. avg_launch_us includes the graph's per-node dispatch gap."""
+    dev = torch.device("cuda:0")
+    R, Hq, Hkv, D, bs = 4, 32, 8, 128, 256
+    nb = (L + bs - 1) // bs
+    gen = torch.Generator(device=dev).manual_seed(1)
+    fp8 = kv == "fp8"
+    caches = []
+    for _ in range(layers):
+        k = torch.randn((nb, bs, Hkv, D), generator=gen, device=dev)
+        v = torch.randn((nb, bs, Hkv, D), generator=gen, device=dev)
+        dt = torch.float8_e4m3fn if fp8 else torch.bfloat16
+        caches.append((k.to(dt), v.to(dt)))
+    q = torch.randn((R, Hq, D), generator=gen, device=dev).to(torch.bfloat16)
     cu_q = torch.tensor([0, R], dtype=torch.int32, device=dev)
     cu_k = torch.tensor([0, L], dtype=torch.int32, device=dev)
-    bt = runner.state.block_tables
-    layers = runner.target.attention_layers()
-    kmax = layers[0].max_model_len
-    ksc = layers[0].k_scale
-    vsc = layers[0].v_scale
+    bt = torch.randperm(nb, generator=torch.Generator().manual_seed(2)).to(torch.int32)
+    bt = bt.view(1, nb).to(dev)
+    outs = [torch.empty((R, Hq, D), dtype=torch.bfloat16, device=dev) for _ in range(layers)]
 
     def launch_all():
-        for a in layers:
-            hv.ops.verify_attention(q, a.k_cache, a.v_cache, bt, cu_q, cu_k, R, kmax,
-                                    g.head_dim ** -0.5, k_scale=ksc, v_scale=vsc)
+        for i, (k, v) in enumerate(caches):
+            hv.ops.verify_attention(q, k, v, bt, cu_q, cu_k, R, L, D ** -0.5, out=outs[i])
 
-    # one verify step's worth of attention launches (36 layers) as a HIP graph, so
-    # the timing is GPU time, as in the graph-replayed verify step
-    us = graph_time_us(torch, dev, launch_all, reps) / len(layers)
-    kv_bytes = L * g.num_kv_heads * g.head_dim * 2 * runner.kv.element_size()
-    qo_bytes = 2 * R * g.num_heads * g.head_dim * 2
-    per_launch = kv_bytes + qo_bytes
+    us = graph_time_us(torch, dev, launch_all, reps) / layers
+    per_launch = L * Hkv * D * 2 * (1 if fp8 else 2) + 2 * R * Hq * D * 2
     achieved = per_launch / (us * 1e-6) / 1e9
+    kernel = f"k_verify_attn<{'true' if fp8 else 'false'}, 4>"
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": None,
-            "kernel": f"k_verify_attn<{'true' if runner.kv.element_size() == 1 else 'false'}, "
-                      f"{g.num_heads // g.num_kv_heads}> (+ k_attn_combine when split)",
-            "bytes_per_launch": per_launch, "avg_launch_us": round(us, 3),
-            "shape": f"B=1 q={R} Hq={g.num_heads} Hkv={g.num_kv_heads} D={g.head_dim} L={L}",
-            "launches": reps * len(layers)}
+            "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": profiled_traffic(kernel, "attention-b1"),
+            "kernel": kernel, "bytes_per_launch": per_launch, "avg_launch_us": round(us, 3),
+            "shape": f"B=1 q={R} Hq={Hq} Hkv={Hkv} D={D} L={L} block {bs}",
+            "launches": reps * layers}
+
+
+def profiled_traffic(kernel: str, workload: str):
+    """HBM bytes per launch of `kernel` in `workload` from the committed rocprofv3
+    counter summary profiles/traffic.md (FETCH_SIZE and WRITE_SIZE in KiB per
+    dispatch, each scaled by the factor a plain 256 MiB copy gives), or None."""
+    path = ROOT / "profiles" / "traffic.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) >= 5 and cells[0] == workload and cells[1] == kernel:
+            try:
+                return int(float(cells[4]))
+            except ValueError:
+                return None
+    return None
+
+
+def bench_attention_b1(args, torch, hv):
+    roof = attention_probe(torch, hv, kv=args.kv, reps=max(1, args.steps // 36))
+    return {"metric": METRIC, "value": roof["avg_launch_us"], "unit": "us/launch (verify attention)",
+            "n_gpus": 1, "steps": roof["launches"], "warmup": 36, "ms_per_step": roof["avg_launch_us"] / 1e3,
+            "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+            "dtype": "fp8-e4m3 KV, bf16 MFMA" if args.kv == "fp8" else "bf16",
+            "data": "synthetic (seeded N(0,1) q/k/v, random block permutation)",
+            "config": {"workload": "verify attention at the config-3 batch-1 verify shape, 36 layers",
+                       "kv_cache": args.kv, "context": PROBE_CONTEXT},
+            "roofline": roof}
+
+
+def bench_copy(args, torch, hv):
+    """Plain device-to-device copy of 256 MiB (the calibration kernel for the HBM
+    byte counters): GB/s counts the bytes read plus the bytes written."""
+    dev = torch.device("cuda:0")
+    n = 256 << 20
+    src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    us = graph_time_us(torch, dev, lambda: dst.copy_(src), max(1, args.steps))
+    gbs = 2 * n / (us * 1e-6) / 1e9
+    return {"metric": "device copy bandwidth (calibration)", "value": round(gbs, 1), "unit": "GB/s",
+            "n_gpus": 1, "steps": max(1, args.steps), "warmup": 1, "ms_per_step": round(us / 1e3, 4),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u8",
+            "data": "synthetic", "config": {"workload": "copy 256 MiB", "bytes_read": n,
+                                            "bytes_written": n}}
+
+
+def _csv_rows(path):
+    import csv
+    with open(path, newline="") as f:
+        return list(csv.DictReader(f))
+
+
+def rocprof_summary(directory: str, kernel_filter: str | None = None) -> str:
+    """Text summary of a rocprofv3 CSV output directory (--output-format csv):
+    per-kernel dispatch statistics (kernel_stats.csv), per-grid statistics of the
+    kernels matching `kernel_filter` (kernel_trace.csv) and per-kernel averages
+    of collected counters (counter_collection.csv)."""
+    import glob
+    out = []
+    stats = sorted(glob.glob(os.path.join(directory, "**", "*kernel_stats.csv"), recursive=True))
+    if stats:
+        rows = _csv_rows(stats[0])
+        total = sum(float(r["TotalDurationNs"]) for r in rows)
+        out.append(f"kernel dispatch statistics ({os.path.basename(stats[0])}), "
+                   f"total {total / 1e3:.1f} us")
+        out.append(f"{'calls':>7} {'avg_us':>9} {'min_us':>9} {'max_us':>9} {'share':>6}  kernel")
+        for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"]))[:25]:
+            out.append(f"{int(r['Calls']):>7} {float(r['AverageNs']) / 1e3:>9.2f} "
+                       f"{float(r['MinNs']) / 1e3:>9.2f} {float(r['MaxNs']) / 1e3:>9.2f} "
+                       f"{100 * float(r['TotalDurationNs']) / total:>5.1f}%  {r['Name'][:110]}")
+    trace = sorted(glob.glob(os.path.join(directory, "**", "*kernel_trace.csv"), recursive=True))
+    if trace and kernel_filter:
+        groups = {}
+        for r in _csv_rows(trace[0]):
+            if kernel_filter not in r["Kernel_Name"]:
+                continue
+            key = (r["Kernel_Name"][:80], r["Grid_Size_X"], r["Grid_Size_Y"], r["Grid_Size_Z"])
+            groups.setdefault(key, []).append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+        out.append("")
+        out.append(f"per-grid statistics of kernels matching '{kernel_filter}' (grid in work-items)")
+        for (name, gx, gy, gz), d in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+            out.append(f"{len(d):>7} {sum(d) / len(d) / 1e3:>9.2f} {min(d) / 1e3:>9.2f} "
+                       f"{max(d) / 1e3:>9.2f}  grid=({gx},{gy},{gz}) {name}")
+    cc = sorted(glob.glob(os.path.join(directory, "**", "*counter_collection.csv"), recursive=True))
+    if cc:
+        agg = {}
+        for r in _csv_rows(cc[0]):
+            if kernel_filter and kernel_filter not in r["Kernel_Name"]:
+                continue
+            key = (r["Kernel_Name"][:100], r["Counter_Name"])
+            agg.setdefault(key, []).append(float(r["Counter_Value"]))
+        out.append("")
+        out.append("counter averages per dispatch")
+        out.append(f"{'dispatches':>10} {'average':>14} {'min':>14} {'max':>14}  counter  kernel")
+        for (name, cname), v in sorted(agg.items(), key=lambda kv: -sum(kv[1]))[:25]:
+            out.append(f"{len(v):>10} {sum(v) / len(v):>14.2f} {min(v):>14.2f} {max(v):>14.2f}  "
+                       f"{cname}  {name}")
+    return "\n".join(out)
 
 
 def main(argv=None):
@@ -427,7 +538,11 @@ def main(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default="spec", choices=["spec", "accept", "attention"])
+    ap.add_argument("--workload", default="spec",
+                    choices=["spec", "accept", "attention", "attention-b1", "copy"])
+    ap.add_argument("--rocprof-summary", metavar="DIR", default=None,
+                    help="print a text summary of a rocprofv3 CSV output directory and exit")
+    ap.add_argument("--kernel", default=None, help="kernel-name filter for --rocprof-summary")
     ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--gamma", type=int, default=3)
     ap.add_argument("--mode", default="reference", choices=["reference", "filtered", "greedy"])
@@ -442,13 +557,16 @@ def main(argv=None):
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     args = ap.parse_args(argv)
+    if args.rocprof_summary:
+        print(rocprof_summary(args.rocprof_summary, args.kernel))
+        return 0
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; the verify path shards "
                           "by sequence / KV head across GPUs by design but no multi-GPU run "
                           "is part of it", "n_gpus": args.gpus}))
         return 2
     if args.steps is None:
-        args.steps = 96 if args.workload == "spec" else 200
+        args.steps = {"spec": 96, "attention-b1": 720}.get(args.workload, 200)
     if args.warmup is None:
         args.warmup = 8 if args.workload == "spec" else 20
     import torch
@@ -457,6 +575,10 @@ def main(argv=None):
         res = bench_spec(args, torch, hv)
     elif args.workload == "attention":
         res = bench_attention(args, torch, hv)
+    elif args.workload == "copy":
+        res = bench_copy(args, torch, hv)
+    elif args.workload == "attention-b1":
+        res = bench_attention_b1(args, torch, hv)
     else:
         res = bench_accept(args, torch, hv)
     print(json.dumps(res))
