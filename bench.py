@@ -391,6 +391,71 @@ def bench_spec(args, torch, hv):
     return res
 
 
+def bench_adaptive(args, torch, hv):
+    """Config 4: adaptive-gamma batched speculative decoding, B sequences (default 32),
+    prompts ~ U[32, 128], every sequence decoding to --max-context tokens (default
+    8192) in an FP8-e4m3 target cache of 256-token blocks whose pool holds 3/4 of
+    what all sequences need at the end (block pressure: sequences wait for blocks
+    until others finish). Random-init 8B target / 0.6B draft, T=0.6, reference
+    acceptance, gamma from 3 adapted in [1, 8] (llm_engine.py:197-208)."""
+    import importlib as _il
+    import numpy as np
+    q3 = _il.import_module("hilda-vllm_amd.engine.qwen3_host")
+    sr = _il.import_module("hilda-vllm_amd.engine.spec_runner")
+    dev = torch.device("cuda:0")
+    B, bs = args.batch if args.batch > 1 else 32, 256
+    rng = np.random.default_rng(0)
+    plens = rng.integers(32, 129, size=B)
+    prompts = [rng.integers(0, 10000, size=n).tolist() for n in plens]
+    ctx = args.max_context
+    need = sum(-(-(ctx + 9) // bs) for _ in range(B))
+    num_blocks = max(int(0.75 * need), sum(-(-int(n) // bs) for n in plens) + B)
+    target = q3.Qwen3Host(q3.QWEN3_8B, device=dev, seed=1)
+    draft = q3.Qwen3Host(q3.QWEN3_0_6B, device=dev, seed=2)
+    runner = sr.SpecRunner(target, draft, batch=B, gamma=3, max_model_len=ctx + 16, block_size=bs,
+                           kv_cache_dtype="fp8", num_blocks=num_blocks, temperature=0.6,
+                           mode="reference", adaptive=True, device=dev)
+    runner.load_prompts(prompts)
+    runner.state.max_tokens.copy_(torch.tensor([ctx - int(n) for n in plens], dtype=torch.int32))
+    runner.prefill()
+    len0 = sum(runner.lengths())
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    waited = 0
+    t0 = time.perf_counter()
+    e0.record(stream)
+    steps = 0
+    while steps < args.steps:
+        if bool(runner.state.finished.all()):
+            break
+        runner.step_graph()
+        G = runner._per_gamma[runner.history[-1][0]]
+        waited += int(((G.elig == 0) & (runner.state.finished == 0)).sum())
+        steps += 1
+        if steps % 200 == 0:
+            print(f"[adaptive] step {steps} tokens {sum(runner.lengths()) - len0} "
+                  f"gamma {runner.gamma}", file=sys.stderr, flush=True)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_ms = e0.elapsed_time(e1)
+    emitted = sum(runner.lengths()) - len0
+    gam = [h[0] for h in runner.history]
+    acc = sum(h[1] for h in runner.history)
+    prop = sum(h[2] for h in runner.history)
+    return {"metric": "adaptive-gamma batched spec decode tokens/s (config 4)",
+            "value": round(emitted / (gpu_ms / 1e3), 2), "unit": "tok/s (all sequences)",
+            "n_gpus": 1, "steps": steps, "warmup": 0, "ms_per_step": round(gpu_ms / max(steps, 1), 3),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16, fp8-e4m3 KV",
+            "data": "synthetic (random-init weights, uniform-random prompt ids)",
+            "config": {"workload": "config 4: adaptive gamma, FP8 KV, block pressure", "batch": B,
+                       "max_context": ctx, "num_blocks": num_blocks, "blocks_needed_at_end": need},
+            "tokens_emitted": emitted, "all_finished": bool(runner.state.finished.all()),
+            "gamma_histogram": {str(k): gam.count(k) for k in sorted(set(gam))},
+            "acceptance_rate": round(acc / max(prop, 1), 4), "sequence_steps_waiting_for_blocks": waited,
+            "wall_s": round(wall, 2)}
+
+
 PROBE_CONTEXT = 320  # config-3 end state: 64 prompt tokens + 256 generated tokens
 
 
@@ -539,7 +604,8 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="spec",
-                    choices=["spec", "accept", "attention", "attention-b1", "copy"])
+                    choices=["spec", "accept", "attention", "attention-b1", "copy", "adaptive"])
+    ap.add_argument("--max-context", type=int, default=8192)
     ap.add_argument("--rocprof-summary", metavar="DIR", default=None,
                     help="print a text summary of a rocprofv3 CSV output directory and exit")
     ap.add_argument("--kernel", default=None, help="kernel-name filter for --rocprof-summary")
@@ -566,7 +632,7 @@ def main(argv=None):
                           "is part of it", "n_gpus": args.gpus}))
         return 2
     if args.steps is None:
-        args.steps = {"spec": 96, "attention-b1": 720}.get(args.workload, 200)
+        args.steps = {"spec": 96, "attention-b1": 720, "adaptive": 1 << 30}.get(args.workload, 200)
     if args.warmup is None:
         args.warmup = 8 if args.workload == "spec" else 20
     import torch
@@ -579,6 +645,8 @@ def main(argv=None):
         res = bench_copy(args, torch, hv)
     elif args.workload == "attention-b1":
         res = bench_attention_b1(args, torch, hv)
+    elif args.workload == "adaptive":
+        res = bench_adaptive(args, torch, hv)
     else:
         res = bench_accept(args, torch, hv)
     print(json.dumps(res))

@@ -223,8 +223,8 @@ struct CommitWs {
 
 __global__ __launch_bounds__(kCT) void k_commit(hs_spec_state s, int gamma, const int32_t* nacc,
                                                 const int64_t* out_tokens, const int32_t* out_len,
-                                                int32_t* appended, int32_t* dirty, int dirty_mode,
-                                                CommitWs w) {
+                                                const int32_t* eligible, int32_t* appended,
+                                                int32_t* dirty, int dirty_mode, CommitWs w) {
   __shared__ int s_w[kCW];
   __shared__ int s_tot[2];
   const int tid = threadIdx.x;
@@ -241,7 +241,7 @@ __global__ __launch_bounds__(kCT) void k_commit(hs_spec_state s, int gamma, cons
     const int len0 = s.context_lens[b];
     const int nblk = s.num_seq_blocks[b];
     int len = len0, fin = s.finished[b], app = 0;
-    const int n = fin ? 0 : out_len[b];
+    const int n = (fin || (eligible && !eligible[b])) ? 0 : out_len[b];
     for (int j = 0; j < n && !fin; ++j) {
       const int64_t tok = out_tokens[(int64_t)b * R + j];
       if (len < s.T) s.tokens[(int64_t)b * s.T + len] = tok;
@@ -431,8 +431,8 @@ size_t hs_spec_commit_workspace_size(int batch, int table_width, int num_blocks)
 }
 
 int hs_spec_commit(const hs_spec_state* state, int gamma, const int32_t* num_accepted,
-                   const int64_t* out_tokens, const int32_t* out_len, int32_t* appended,
-                   int32_t* dirty_slots, int dirty_mode, void* workspace,
+                   const int64_t* out_tokens, const int32_t* out_len, const int32_t* eligible,
+                   int32_t* appended, int32_t* dirty_slots, int dirty_mode, void* workspace,
                    size_t workspace_bytes, void* stream) {
   if (!state_ok(state) || gamma < 0 || !out_tokens || !out_len || !workspace)
     return HS_ERR_INVALID;
@@ -447,8 +447,8 @@ int hs_spec_commit(const hs_spec_state* state, int gamma, const int32_t* num_acc
   w.ev_free = w.ev_blk + (size_t)state->B * state->W;
   w.seq = w.ev_free + (size_t)state->B * state->W;
   hipLaunchKernelGGL(k_commit, dim3(1), dim3(kCT), 0, reinterpret_cast<hipStream_t>(stream),
-                     *state, gamma, num_accepted, out_tokens, out_len, appended, dirty_slots,
-                     dirty_mode, w);
+                     *state, gamma, num_accepted, out_tokens, out_len, eligible, appended,
+                     dirty_slots, dirty_mode, w);
   return hipGetLastError() == hipSuccess ? HS_OK : HS_ERR_LAUNCH;
 }
 

@@ -12,7 +12,10 @@ around the gfx950 kernels:
   * verify runs the target over gamma+1 tokens, the LM head over all rows and
     the fused acceptance (hs_spec_accept) with explicit uniforms;
   * the draft phase and the verify phase can each be captured once into a HIP
-    graph and replayed.
+    graph and replayed (one pair of graphs per gamma);
+  * with adaptive=True gamma follows the acceptance-rate controller of
+    llm_engine.py:197-208 (AdaptiveGamma); the step's accepted/proposed
+    totals are read back after every step, as the reference does on the host.
 Uniforms are drawn on the device from torch's generator (graph-safe).
 """
 from __future__ import annotations
@@ -21,9 +24,12 @@ import math
 
 import torch
 
+from types import SimpleNamespace
+
 from .. import ops
 from ..layers.sampler import Sampler
 from ..utils.context import reset_context, set_context
+from .adaptive_gamma import AdaptiveGamma
 
 
 class SpecRunner:
@@ -32,12 +38,14 @@ class SpecRunner:
                  block_size: int = 256, kv_cache_dtype: str = "auto", num_blocks: int | None = None,
                  temperature: float = 1.0, top_k: int = 0, top_p: float = 1.0,
                  mode: str = "reference", eos: int = -1, k_scale: float = 1.0,
-                 v_scale: float = 1.0, device="cuda"):
+                 v_scale: float = 1.0, device="cuda", adaptive: bool = False,
+                 max_gamma: int | None = None):
         self.target, self.draft = target, draft
         self.B, self.gamma = batch, gamma
+        self.max_gamma = max(gamma, max_gamma or (8 if adaptive else gamma))
         self.bs = block_size
         self.max_model_len = max_model_len
-        self.W = math.ceil((max_model_len + gamma + 2) / block_size)
+        self.W = math.ceil((max_model_len + self.max_gamma + 2) / block_size)
         self.num_blocks = num_blocks or batch * self.W + 2
         self.mode = mode
         self.device = torch.device(device)
@@ -49,7 +57,7 @@ class SpecRunner:
                                tg.num_kv_heads, tg.head_dim), dtype=kv_dtype, device=dev)
         self.dkv = torch.zeros((2, len(draft.layers), self.num_blocks, block_size,
                                 dg.num_kv_heads, dg.head_dim), dtype=torch.bfloat16, device=dev)
-        kmax = max_model_len + gamma + 2
+        kmax = max_model_len + self.max_gamma + 2
         for i, a in enumerate(target.attention_layers()):
             a.k_cache, a.v_cache = self.kv[0, i], self.kv[1, i]
             a.kv_cache_dtype = kv_cache_dtype
@@ -65,17 +73,46 @@ class SpecRunner:
         self.temps = torch.full((batch,), float(temperature), **f32)
         self.top_ks = torch.full((batch,), int(top_k), dtype=torch.int32, device=dev)
         self.top_ps = torch.full((batch,), float(top_p), **f32)
-        self.draft_tokens = torch.zeros((batch, gamma), dtype=torch.int64, device=dev)
-        self.draft_probs = torch.zeros((batch, gamma, self.V), **f32)
         self.tok_scratch = torch.zeros(batch, dtype=torch.int64, device=dev)
-        self.u_draft = torch.zeros((gamma, batch), **f32)
-        self.u_acc = torch.zeros((batch, gamma), **f32)
         self.u_res = torch.zeros(batch, **f32)
         self.d_stage = self._stage_bufs(batch)
         self.d_stage0 = self._stage_bufs(2 * batch)
         self.sampler = Sampler()
-        self.graphs = None
+        self._per_gamma: dict[int, SimpleNamespace] = {}
+        self.controller = AdaptiveGamma(gamma, max_gamma=self.max_gamma) if adaptive else None
+        self.history: list[tuple[int, int, int]] = []  # (gamma, accepted, proposed) per step
         self.last = None
+
+    def _g(self, gamma: int | None = None) -> SimpleNamespace:
+        """Buffers (and graphs) of one gamma: draft tokens [B, g], draft probabilities
+        [B, g, V], uniforms, eligibility and the last acceptance outputs."""
+        g = self.gamma if gamma is None else gamma
+        G = self._per_gamma.get(g)
+        if G is None:
+            dev, B = self.device, self.B
+            G = SimpleNamespace(
+                gamma=g,
+                draft_tokens=torch.zeros((B, g), dtype=torch.int64, device=dev),
+                draft_probs=torch.zeros((B, g, self.V), dtype=torch.float32, device=dev),
+                u_draft=torch.zeros((g, B), dtype=torch.float32, device=dev),
+                u_acc=torch.zeros((B, g), dtype=torch.float32, device=dev),
+                elig=torch.zeros(B, dtype=torch.int32, device=dev),
+                graphs=None, last=None)
+            self._per_gamma[g] = G
+        return G
+
+    # buffers of the current gamma (the fixed-gamma interface)
+    @property
+    def draft_tokens(self):
+        return self._g().draft_tokens
+
+    @property
+    def draft_probs(self):
+        return self._g().draft_probs
+
+    @property
+    def graphs(self):
+        return self._g().graphs
 
     def _stage_bufs(self, rows):
         dev = self.device
@@ -154,10 +191,11 @@ class SpecRunner:
         """Pre-allocation (llm_engine.py:111-128) and gamma draft steps
         (model_runner.py:294-318)."""
         st = self.state
-        ops.spec_prealloc(st, self.gamma)
-        self.u_draft.uniform_()
+        G = self._g()
+        ops.spec_prealloc(st, G.gamma, out=G.elig)
+        G.u_draft.uniform_()
         mode = "filtered" if self.mode == "filtered" else "reference"
-        for j in range(self.gamma):
+        for j in range(G.gamma):
             if j == 0:
                 # two queries: the previous token (fills the draft K/V the last step
                 # left out when it accepted every draft) and the last token
@@ -166,7 +204,7 @@ class SpecRunner:
                 set_context(True, cq, ck, 2, 0, slots, None, st.block_tables)
                 h = self.draft(ids, pos)[1::2]
             else:
-                ids, pos, slots, cq, ck = ops.draft_prepare(st, self.draft_tokens, j,
+                ids, pos, slots, cq, ck = ops.draft_prepare(st, G.draft_tokens, j,
                                                             out=self.d_stage)
                 set_context(False, cq, ck, 1, 0, slots, None, st.block_tables)
                 h = self.draft(ids, pos)
@@ -175,38 +213,69 @@ class SpecRunner:
                 ops.sample_rows(logits, mode="greedy", tokens_out=self.tok_scratch)
             else:
                 ops.sample_rows(logits, self.temps, self.top_ks, self.top_ps, mode=mode,
-                                uniforms=self.u_draft[j], probs_out=self.draft_probs[:, j],
+                                uniforms=G.u_draft[j], probs_out=G.draft_probs[:, j],
                                 tokens_out=self.tok_scratch)
-            self.draft_tokens[:, j].copy_(self.tok_scratch)
+            G.draft_tokens[:, j].copy_(self.tok_scratch)
         reset_context()
 
     def verify_phase(self):
         """Verify forward + LM head over all gamma+1 rows + fused acceptance
         (model_runner.py:329-428) + commit/rollback (llm_engine.py:146-181)."""
-        st, g = self.state, self.gamma
-        ids, pos, slots, cq, ck = ops.verify_prepare(st, self.draft_tokens, g)
+        st = self.state
+        G = self._g()
+        g = G.gamma
+        ids, pos, slots, cq, ck = ops.verify_prepare(st, G.draft_tokens, g)
         set_context(True, cq, ck, g + 1, 0, slots, None, st.block_tables)
         h = self.target(ids, pos)
         reset_context()
         logits = self.target.compute_logits(h).view(self.B, g + 1, self.V)
-        self.u_acc.uniform_()
+        G.u_acc.uniform_()
         self.u_res.uniform_()
-        nacc, out, olen = ops.spec_accept(logits, self.draft_probs, self.draft_tokens, self.temps,
-                                          self.u_acc, self.u_res, mode=self.mode,
+        nacc, out, olen = ops.spec_accept(logits, G.draft_probs, G.draft_tokens, self.temps,
+                                          G.u_acc, self.u_res, mode=self.mode,
                                           top_ks=self.top_ks, top_ps=self.top_ps)
-        ops.spec_commit(st, g, out, olen)
-        self.last = (nacc, out, olen)
+        ops.spec_commit(st, g, out, olen, eligible=G.elig)
+        G.last = (nacc, out, olen)
+        self.last = G.last
 
     def step(self):
+        """One eager speculative step (then the gamma update when adaptive)."""
         self.draft_phase()
         self.verify_phase()
+        self._after_step()
+
+    def step_graph(self):
+        """One step through the HIP graphs of the current gamma; the first step at
+        a new gamma runs eagerly and then captures that gamma's graphs."""
+        G = self._g()
+        if G.graphs is None:
+            self.draft_phase()
+            self.verify_phase()
+            self.capture()
+        else:
+            G.graphs[0].replay()
+            G.graphs[1].replay()
+        self._after_step()
+
+    def _after_step(self):
+        if self.controller is None:
+            return
+        G = self._g()
+        nacc = G.last[0]
+        # accepted drafts and proposals of the sequences that took part (llm_engine.py:150-151)
+        tot = torch.stack([(nacc * G.elig).sum(), G.elig.sum()]).cpu().tolist()
+        accepted, proposed = int(tot[0]), int(tot[1]) * G.gamma
+        self.history.append((G.gamma, accepted, proposed))
+        self.gamma = self.controller.update(accepted, proposed)
 
     # ------------------------------------------------------------------ graphs
     def capture(self):
-        """Records the draft phase and the verify phase into two HIP graphs.
-        The caller must have run at least one eager step (workspaces exist)."""
+        """Records the draft phase and the verify phase of the current gamma into
+        two HIP graphs (a memory pool of their own). The caller must have run at
+        least one eager step at this gamma (workspaces and library handles exist)."""
         torch.cuda.synchronize()
         snap = self._snapshot()
+        G = self._g()
         gd, gv = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
         s = torch.cuda.Stream(device=self.device)
         s.wait_stream(torch.cuda.current_stream(self.device))
@@ -218,10 +287,10 @@ class SpecRunner:
         torch.cuda.current_stream(self.device).wait_stream(s)
         torch.cuda.synchronize()
         self._restore(snap)  # capture executed nothing, but keep the state exact
-        self.graphs = (gd, gv)
+        G.graphs = (gd, gv)
 
     def replay(self):
-        gd, gv = self.graphs
+        gd, gv = self._g().graphs
         gd.replay()
         gv.replay()
 

@@ -15,12 +15,17 @@ from . import _lib as L
 _MODES = {"reference": L.HS_ACCEPT_REFERENCE, "filtered": L.HS_ACCEPT_FILTERED,
           "greedy": L.HS_ACCEPT_GREEDY}
 _WS: dict = {}
+_RETIRED: list = []
 
 
 def workspace(device: torch.device, nbytes: int, kind: str) -> torch.Tensor:
+    """Workspace of one kind on one device, grown on demand. A superseded buffer is
+    kept alive (never freed) because HIP graphs captured earlier still point at it."""
     key = (device.index, kind)
     ws = _WS.get(key)
     if ws is None or ws.numel() < nbytes:
+        if ws is not None:
+            _RETIRED.append(ws)
         ws = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device)
         _WS[key] = ws
     return ws
@@ -322,10 +327,13 @@ class SpecStateTensors:
         return st
 
 
-def spec_prealloc(state: SpecStateTensors, gamma: int) -> torch.Tensor:
-    """llm_engine.py:111-128 on the device; returns eligible int32 [B]."""
+def spec_prealloc(state: SpecStateTensors, gamma: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """llm_engine.py:111-128 on the device; returns eligible int32 [B] (into `out`
+    when given)."""
     dev = state.context_lens.device
-    elig = torch.empty(state.B, dtype=torch.int32, device=dev)
+    elig = out if out is not None else torch.empty(state.B, dtype=torch.int32, device=dev)
+    if elig.dtype != torch.int32 or elig.numel() != state.B or not elig.is_contiguous():
+        raise ValueError("out must be a contiguous int32 [B] tensor")
     st = state.struct()
     L.check(L.lib().hs_spec_prealloc(ctypes_ref(st), int(gamma), elig.data_ptr(), None,
                                      _stream(dev)), "hs_spec_prealloc")
@@ -353,8 +361,10 @@ def verify_prepare(state: SpecStateTensors, draft_tokens: torch.Tensor, gamma: i
 
 
 def spec_commit(state: SpecStateTensors, gamma: int, out_tokens: torch.Tensor,
-                out_len: torch.Tensor, *, dirty_mode: int | None = None):
-    """llm_engine.py:146-195 on the device. Returns (appended, dirty_slots or None)."""
+                out_len: torch.Tensor, *, dirty_mode: int | None = None,
+                eligible: torch.Tensor | None = None):
+    """llm_engine.py:146-195 on the device. Rows whose `eligible` entry is 0 (the
+    status of spec_prealloc) take no tokens. Returns (appended, dirty_slots or None)."""
     dev = state.context_lens.device
     app = torch.empty(state.B, dtype=torch.int32, device=dev)
     dirty = None
@@ -362,9 +372,15 @@ def spec_commit(state: SpecStateTensors, gamma: int, out_tokens: torch.Tensor,
         dirty = torch.empty((state.B, gamma + 1), dtype=torch.int32, device=dev)
     ot = out_tokens.to(torch.int64).contiguous()
     ol = out_len.to(torch.int32).contiguous()
+    el = None
+    if eligible is not None:
+        if eligible.dtype != torch.int32 or eligible.numel() != state.B:
+            raise ValueError("eligible must be an int32 [B] tensor")
+        el = eligible.contiguous()
     st = state.struct()
     L.check(L.lib().hs_spec_commit(ctypes_ref(st), int(gamma), None, ot.data_ptr(),
-                                   ol.data_ptr(), app.data_ptr(),
+                                   ol.data_ptr(), None if el is None else el.data_ptr(),
+                                   app.data_ptr(),
                                    None if dirty is None else dirty.data_ptr(),
                                    int(dirty_mode or 0), state.commit_ws.data_ptr(),
                                    state.commit_ws.numel(), _stream(dev)), "hs_spec_commit")

@@ -227,12 +227,15 @@ int hs_draft_prepare(const hs_spec_state* state, const int64_t* draft_tokens, in
 /* (model_runner.py:439-464): dirty_mode 0 uses the reference range          */
 /* [len, old_len + gamma + 1), dirty_mode 1 the exact range                  */
 /* [len - 1, old_len + gamma). num_accepted is not needed (may be NULL).     */
+/* eligible (optional, [B] int32, the status of hs_spec_prealloc): rows with */
+/* 0 sat out the step (llm_engine.py:120-121) and take no tokens; NULL means */
+/* every row took part.                                                      */
 /* The workspace must be zero-filled before its first use; every call leaves */
 /* it zero-filled.                                                           */
 size_t hs_spec_commit_workspace_size(int batch, int table_width, int num_blocks);
 int hs_spec_commit(const hs_spec_state* state, int gamma, const int32_t* num_accepted,
-                   const int64_t* out_tokens, const int32_t* out_len, int32_t* appended,
-                   int32_t* dirty_slots, int dirty_mode, void* workspace,
+                   const int64_t* out_tokens, const int32_t* out_len, const int32_t* eligible,
+                   int32_t* appended, int32_t* dirty_slots, int dirty_mode, void* workspace,
                    size_t workspace_bytes, void* stream);
 
 /* Zeroes row_bytes at every slot of slots[] (entries < 0 skipped) in each of */

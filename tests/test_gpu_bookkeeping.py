@@ -116,7 +116,8 @@ def test_random_spec_steps_match_oracle(hv, cuda, seed):
         olen = np.zeros(len(seqs), np.int32)
         acc = []
         for i, s in enumerate(seqs):
-            n = int(rng.integers(1, R + 1)) if elig_ref[i] else 0
+            # ineligible rows offer tokens too: the commit must skip them by `eligible`
+            n = int(rng.integers(1, R + 1)) if elig_ref[i] else int(rng.integers(0, R + 1))
             toks = list(rng.integers(0, 9, size=n))
             out[i, :n] = toks
             olen[i] = n
@@ -126,7 +127,8 @@ def test_random_spec_steps_match_oracle(hv, cuda, seed):
         mode = step % 2
         app_ref, dirty_ref = bm.commit(batch, batch_acc, gamma, dirty_mode=mode)
         app, dirty = hv.ops.spec_commit(st, gamma, torch.from_numpy(out).to(cuda),
-                                        torch.from_numpy(olen).to(cuda), dirty_mode=mode)
+                                        torch.from_numpy(olen).to(cuda), dirty_mode=mode,
+                                        eligible=elig)
         torch.cuda.synchronize()
         app_c = app.cpu().numpy()
         dirty_c = dirty.cpu().numpy()

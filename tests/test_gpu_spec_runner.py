@@ -138,3 +138,76 @@ def test_fused_layer_matches_eager(cuda):
     err = (got - ref).abs()
     assert err.max() <= 0.05 * ref.abs().max() + 0.02, float(err.max())
     assert torch.nn.functional.cosine_similarity(got.flatten(), ref.flatten(), dim=0) > 0.999
+
+
+@pytest.mark.parametrize("draft_kind", ["self", "random"])
+def test_adaptive_gamma_fp8_block_pressure(cuda, draft_kind):
+    """Config 4 at test scale: adaptive gamma, FP8 target cache, a block pool too
+    small for every sequence at once (some sequences must wait), sequences of
+    different max_tokens finishing and releasing their blocks."""
+    q3, sr = _mods()
+    AG = importlib.import_module("hilda-vllm_amd.engine.adaptive_gamma").AdaptiveGamma
+    g = _small(q3, layers=2)
+    target = q3.Qwen3Host(g, device=cuda, seed=61)
+    if draft_kind == "self":
+        draft = q3.Qwen3Host(g, share_from=target)
+        mode, temp, g0 = "greedy", 0.0, 3
+    else:
+        draft = q3.Qwen3Host(_small(q3, layers=1), device=cuda, seed=62)
+        mode, temp, g0 = "reference", 0.9, 5
+    B, bs = 6, 32
+    # five short sequences that never outgrow their two prompt blocks (even with the
+    # lookahead of gamma 8) and one long sequence whose prompt fills its three blocks:
+    # with no spare block it needs a fourth at once and waits until the short ones
+    # finish and release theirs
+    prompts = [list(range(10 + i, 10 + i + n)) for i, n in enumerate([33, 34, 35, 36, 37, 95])]
+    max_tokens = [12, 14, 10, 16, 8, 200]
+    num_blocks = 13  # exactly the prompt blocks
+    runner = sr.SpecRunner(target, draft, batch=B, gamma=g0, max_model_len=400, block_size=bs,
+                           kv_cache_dtype="fp8", num_blocks=num_blocks, temperature=temp,
+                           mode=mode, adaptive=True, device=cuda)
+    runner.load_prompts(prompts)
+    st = runner.state
+    st.max_tokens.copy_(torch.tensor(max_tokens, dtype=torch.int32))
+    runner.prefill()
+    waited = 0
+    for step in range(400):
+        fin = st.finished.cpu()
+        if bool(fin.all()):
+            break
+        runner.step_graph()
+        G = runner._per_gamma[runner.history[-1][0]]
+        elig = G.elig.cpu()
+        waited += int(((elig == 0) & (fin == 0)).sum())
+        _check_blocks(runner)
+    torch.cuda.synchronize()
+    assert bool(st.finished.cpu().all()), "sequences did not finish"
+    lens = runner.lengths()
+    assert lens == [len(p) + m for p, m in zip(prompts, max_tokens)]
+    assert int(st.free_hdr[1]) == num_blocks  # every block released
+    assert waited > 0, "the block pool never ran short"
+    # the gamma trajectory is the controller's on the recorded totals
+    ctl = AG(g0, max_gamma=8)
+    for k, (gk, acc, prop) in enumerate(runner.history):
+        assert gk == ctl.gamma, (k, runner.history[:k + 1])
+        assert 0 <= acc <= prop
+        ctl.update(acc, prop)
+    gammas = [h[0] for h in runner.history]
+    print("gamma trajectory", gammas, flush=True)
+    if draft_kind == "self":
+        assert max(gammas) > g0, gammas  # high acceptance raises gamma
+    else:
+        assert min(gammas) < g0, gammas  # low acceptance lowers it
+
+
+def _check_blocks(runner):
+    st = runner.state
+    nb = st.num_seq_blocks.cpu()
+    lens = st.context_lens.cpu()
+    fin = st.finished.cpu()
+    for b in range(runner.B):
+        if fin[b]:
+            assert int(nb[b]) == 0
+        else:
+            assert int(nb[b]) == (int(lens[b]) + runner.bs - 1) // runner.bs
+    assert int(st.free_hdr[1]) + int(nb.sum()) == runner.num_blocks
