@@ -10,6 +10,7 @@ constexpr int kFilterThreads = 512;
 constexpr int kCand = 4096;       // LDS candidate capacity of the filter kernel
 constexpr int kMaxRows = 65535;   // units per call (grid.y of k_sample_part)
 constexpr int kChunkThreads = 256;  // one workgroup streams one 2048-element chunk
+constexpr int kCB = 256;          // buckets of the top-p coarse and fine histograms
 
 enum : int { kFinRow = 0, kFinDecide = 1, kFinPlain = 2 };
 enum : int { kKindNone = 0, kKindResidual = 1, kKindBonus = 2, kKindPlain = 3 };
@@ -50,10 +51,23 @@ struct SampPart {
   uint64_t p;  // probability weight sum of the chunk
 };
 
+// Per-row state of the filter passes (k_filter_plan* write it, the passes and
+// k_row_filter read it).
 struct FilterScratch {
   int32_t kept;
   int32_t path;
-  int32_t pad[2];
+  int32_t ncand;   // candidates appended by the filter passes
+  int32_t b1;      // coarse boundary bucket (-1: the row never reaches p)
+  int32_t b2;      // fine boundary bucket (-1: not refined)
+  int32_t pad;
+  float m;         // row max and normaliser (x = logit / T)
+  float s;
+  uint32_t tau;    // top-k gather threshold (order key)
+  uint32_t pad2;
+  uint64_t theta;  // top-p mass threshold (fixed point)
+  uint64_t ac;     // count, mass and e-mass of the elements before the boundary bucket
+  uint64_t am;
+  uint64_t ae;
 };
 
 struct Problem {
@@ -67,6 +81,7 @@ struct Problem {
   const float* temps;     // per unit
   const int32_t* top_ks;  // per unit
   const float* top_ps;    // per unit
+  int filtered;           // the chunk pass clears the filter scratch
 };
 
 struct AcceptArgs {
@@ -86,6 +101,13 @@ struct Work {
   SeqState* st;
   SampPart* spart;
   FilterScratch* filt;
+  uint64_t* cand;  // [rows, kCand] candidates (key << 32 | ~index)
+  uint64_t* h1m;   // [rows, kCB] coarse top-p histogram: masses, e-masses, counts
+  uint64_t* h1e;
+  uint32_t* h1c;
+  uint64_t* h2m;   // [rows, kCB] fine histogram inside the coarse boundary bucket
+  uint64_t* h2e;
+  uint32_t* h2c;
 };
 
 struct SampleOut {
@@ -99,7 +121,7 @@ struct SampleOut {
 };
 
 struct Layout {
-  size_t part, desc, st, spart, filt, total;
+  size_t part, desc, st, spart, filt, cand, h1m, h1e, h1c, h2m, h2e, h2c, total;
 };
 
 template <typename T>

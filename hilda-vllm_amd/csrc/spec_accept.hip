@@ -79,6 +79,17 @@ __global__ __launch_bounds__(kT) void k_chunk_stats(Problem P, Work W) {
       cs.e = s_e[0] + s_e[1] + s_e[2] + s_e[3];
       W.part[it] = cs;
     }
+    if (P.filtered && c == 0) {
+      // the filter passes accumulate into these (kernel order: this launch first)
+      const int64_t hb = (int64_t)row * kCB + tid;
+      W.h1m[hb] = 0ull;
+      W.h1e[hb] = 0ull;
+      W.h1c[hb] = 0u;
+      W.h2m[hb] = 0ull;
+      W.h2e[hb] = 0ull;
+      W.h2c[hb] = 0u;
+      if (tid == 0) W.filt[row].ncand = 0;
+    }
   }
 }
 
@@ -440,6 +451,13 @@ Layout make_layout(int units, int rows, int nchunk) {
   L.st = off; off = align_up(off + (size_t)units * sizeof(SeqState), 256);
   L.spart = off; off = align_up(off + (size_t)units * nchunk * sizeof(SampPart), 256);
   L.filt = off; off = align_up(off + (size_t)rows * sizeof(FilterScratch), 256);
+  L.cand = off; off = align_up(off + (size_t)rows * kCand * sizeof(uint64_t), 256);
+  L.h1m = off; off = align_up(off + (size_t)rows * kCB * sizeof(uint64_t), 256);
+  L.h1e = off; off = align_up(off + (size_t)rows * kCB * sizeof(uint64_t), 256);
+  L.h1c = off; off = align_up(off + (size_t)rows * kCB * sizeof(uint32_t), 256);
+  L.h2m = off; off = align_up(off + (size_t)rows * kCB * sizeof(uint64_t), 256);
+  L.h2e = off; off = align_up(off + (size_t)rows * kCB * sizeof(uint64_t), 256);
+  L.h2c = off; off = align_up(off + (size_t)rows * kCB * sizeof(uint32_t), 256);
   L.total = off;
   return L;
 }
@@ -452,6 +470,13 @@ Work bind_work(void* ws, const Layout& L) {
   W.st = reinterpret_cast<SeqState*>(b + L.st);
   W.spart = reinterpret_cast<SampPart*>(b + L.spart);
   W.filt = reinterpret_cast<FilterScratch*>(b + L.filt);
+  W.cand = reinterpret_cast<uint64_t*>(b + L.cand);
+  W.h1m = reinterpret_cast<uint64_t*>(b + L.h1m);
+  W.h1e = reinterpret_cast<uint64_t*>(b + L.h1e);
+  W.h1c = reinterpret_cast<uint32_t*>(b + L.h1c);
+  W.h2m = reinterpret_cast<uint64_t*>(b + L.h2m);
+  W.h2e = reinterpret_cast<uint64_t*>(b + L.h2e);
+  W.h2c = reinterpret_cast<uint32_t*>(b + L.h2c);
   return W;
 }
 
@@ -564,6 +589,7 @@ int hs_spec_accept(const void* target_logits, int logits_dtype, int64_t logits_r
   P.temps = temperatures;
   P.top_ks = top_ks;
   P.top_ps = top_ps;
+  P.filtered = (mode == HS_ACCEPT_FILTERED);
   AcceptArgs A;
   A.q = draft_probs;
   A.q_stride = draft_row_stride;
@@ -628,6 +654,7 @@ int hs_sampler(const void* logits, int logits_dtype, int64_t logits_row_stride, 
   P.temps = temperatures;
   P.top_ks = top_ks;
   P.top_ps = top_ps;
+  P.filtered = (mode == HS_ACCEPT_FILTERED);
   AcceptArgs A;
   memset(&A, 0, sizeof(A));
   SampleOut O;

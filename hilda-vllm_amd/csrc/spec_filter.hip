@@ -11,14 +11,24 @@
 // The cumulative sum is the exact fixed-point sum of floor(2^44 * p_r),
 // rounded to float, so the kept set does not depend on summation order.
 //
-// One 512-thread workgroup owns one row (re-reads hit L2/MALL):
-//   1. top-k: 8-bit radix passes over the order key, histogramming counts in
-//      LDS; as soon as the candidates above the current bucket fit in LDS
-//      (<= 4096) they are gathered and bitonic-sorted, which finishes the
-//      selection in LDS (typically after one pass).
-//   2. top-p: the same scheme with exact mass histograms (u64 LDS atomics);
-//      ties at the final key are resolved in closed form (equal keys have
-//      equal mass) plus one index-ordered pass when a tie is split.
+// Work split:
+//   1. top-k with k <= number of 2048-element chunks: the k-th largest chunk
+//      maximum is a lower bound of the k-th largest element, so a
+//      chunk-parallel pass appends every element at or above it to the row's
+//      candidate list (a few dozen for ordinary logits); one workgroup per row
+//      sorts them in LDS and applies top-k and top-p (which only looks at the k
+//      survivors);
+//   2. top-p alone: chunk-parallel passes build an exact mass histogram over
+//      256 buckets of (M - x) * 8 (bucket 255 collects the zero masses), find
+//      the bucket where the cumulative mass reaches p and append its elements
+//      (or, when it holds more than 4096, refine it into 256 sub-buckets and
+//      append the boundary sub-bucket); the row workgroup sorts them and scans
+//      their masses from the histogram's prefix;
+//   3. otherwise (k above the chunk count, or more than 4096 candidates): the
+//      row workgroup runs 8-bit radix passes over the order key with count /
+//      mass histograms, finishing in LDS as soon as the candidates fit; ties
+//      at the final key are resolved in closed form (equal keys have equal
+//      mass) plus one index-ordered pass when a tie is split.
 // The acceptance test runs afterwards in k_sample_part (spec_accept.hip).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -35,13 +45,18 @@ constexpr int kFW = kFT / kWave;  // waves per workgroup
 
 struct FilterSmem {
   uint64_t cand[kCand];
-  uint64_t scanm[kCand];
-  uint64_t scane[kCand];
+  union {
+    struct {
+      uint64_t scanm[kCand];
+      uint64_t scane[kCand];
+    } sc;
+  } u;
   uint32_t hc[256];
   uint64_t hm[256];
   uint64_t he[256];
   uint64_t wsum[kFW];
   uint64_t wsum2[kFW];
+  uint64_t wsum3[kFW];
   uint64_t u64v[8];
   int32_t i32v[8];
 };
@@ -71,16 +86,17 @@ __device__ __forceinline__ uint64_t block_sum(uint64_t v, uint64_t* wsum) {
 
 // Smallest X with round_to_float(X) >= p * 2^44 (so that "cumsum < p" is
 // "exact fixed-point cumsum < X").
-__device__ uint64_t mass_threshold(float p) {
-  const float target = p * kTwo44;
-  if (!(target > 0.0f)) return 0ull;
-  uint64_t lo = 0, hi = (1ull << 62);
-  while (lo < hi) {
-    uint64_t mid = lo + ((hi - lo) >> 1);
-    if (hs_f32_of_u64(mid) >= target) hi = mid;
-    else lo = mid + 1;
-  }
-  return lo;
+__device__ __forceinline__ uint64_t mass_threshold(float p) {
+  const float t = p * kTwo44;  // exact
+  if (!(t > 0.0f)) return 0ull;
+  // integers below the midpoint of t and the float just below it round below t,
+  // integers above it round to t or more; the midpoint itself (a tie) rounds to
+  // t only when t's significand is even
+  const float tm = u2f(f2u(t) - 1u);
+  const double mid = 0.5 * ((double)t + (double)tm);
+  uint64_t x0 = (uint64_t)ceil(mid);
+  if ((double)x0 == mid && (f2u(t) & 1u)) x0 += 1;
+  return x0;
 }
 
 template <typename T>
@@ -89,20 +105,48 @@ struct RowCtx {
   bool vec_ok;
   int V;
   float Tt;
+  float rt;   // 1 / Tt, correctly rounded
+  bool fast;  // hs_div_rcp applies to Tt
   float M;
   // membership in the kept set A of an earlier stage
   bool a_all;
   uint32_t a_key;
   int64_t a_idx;
+  // x = logit / T with IEEE division semantics
+  __device__ float div(float v) const { return hs_div_temp(v, Tt, rt, fast); }
   __device__ bool inA(uint32_t key, int64_t i) const {
     return a_all || key > a_key || (key == a_key && i <= a_idx);
   }
 };
 
+// Visits every element (raw value, index) of the row. Each thread takes groups
+// of 8 consecutive elements kFT * 8 apart and loads kAhead groups before
+// handling them, so one workgroup keeps several loads per lane in flight.
+template <typename T, typename F>
+__device__ __forceinline__ void stream_row(const RowCtx<T>& C, F&& f) {
+  constexpr int kAhead = 4;
+  const int64_t step = (int64_t)kFT * 8;
+  for (int64_t b0 = (int64_t)threadIdx.x * 8; b0 < C.V; b0 += step * kAhead) {
+    float v[kAhead][8];
+#pragma unroll
+    for (int u = 0; u < kAhead; ++u) {
+      const int64_t base = b0 + u * step;
+      if (base < C.V) load8<T>(C.rp, base, C.V, C.vec_ok, v[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < kAhead; ++u) {
+      const int64_t base = b0 + u * step;
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        if (base + k < C.V) f(v[u][k], base + k);
+    }
+  }
+}
+
 // Histogram pass: counts (and masses when `mass`) of elements in A whose key
 // prefix above `shift + 8` bits equals `prefix`, bucketed by the next 8 bits.
 template <typename T, bool kMass>
-__device__ void hist_pass(const RowCtx<T>& C, FilterSmem& sm, int lvl, uint32_t prefix,
+__device__ void hist_pass(RowCtx<T> C, FilterSmem& sm, int lvl, uint32_t prefix,
                           float sA) {
   const int tid = threadIdx.x;
   for (int b = tid; b < 256; b += kFT) {
@@ -112,28 +156,23 @@ __device__ void hist_pass(const RowCtx<T>& C, FilterSmem& sm, int lvl, uint32_t 
   }
   __syncthreads();
   const int shift = 24 - 8 * lvl;
-  for (int64_t base = (int64_t)tid * 8; base < C.V; base += (int64_t)kFT * 8) {
-    float v[8];
-    load8<T>(C.rp, base, C.V, C.vec_ok, v);
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const int64_t i = base + k;
-      if (i >= C.V) continue;
-      const float x = hs_div_t(v[k], C.Tt);
-      const uint32_t key = hs_key(x);
-      if (lvl > 0 && (key >> (shift + 8)) != prefix) continue;
-      if (!C.inA(key, i)) continue;
-      const uint32_t b = (key >> shift) & 255u;
-      atomicAdd(&sm.hc[b], 1u);
-      if (kMass) {
-        const float e = hs_exp(x - C.M);
-        const uint64_t em = hs_fx44(e);
-        const uint64_t mm = hs_fx44(e / sA);
-        if (mm) atomicAdd((unsigned long long*)&sm.hm[b], (unsigned long long)mm);
-        if (em) atomicAdd((unsigned long long*)&sm.he[b], (unsigned long long)em);
-      }
+  const float rsA = 1.0f / sA;
+  const bool fastA = hs_rcp_ok(sA);
+  stream_row(C, [&](float raw, int64_t i) {
+    const float x = C.div(raw);
+    const uint32_t key = hs_key(x);
+    if (lvl > 0 && (key >> (shift + 8)) != prefix) return;
+    if (!C.inA(key, i)) return;
+    const uint32_t b = (key >> shift) & 255u;
+    atomicAdd(&sm.hc[b], 1u);
+    if (kMass) {
+      const float e = hs_exp(x - C.M);
+      const uint64_t em = hs_fx44(e);
+      const uint64_t mm = hs_fx44(hs_div_temp(e, sA, rsA, fastA));
+      if (mm) atomicAdd((unsigned long long*)&sm.hm[b], (unsigned long long)mm);
+      if (em) atomicAdd((unsigned long long*)&sm.he[b], (unsigned long long)em);
     }
-  }
+  });
   __syncthreads();
 }
 
@@ -141,7 +180,7 @@ __device__ void hist_pass(const RowCtx<T>& C, FilterSmem& sm, int lvl, uint32_t 
 // (key << 32) | (0xffffffff - index) and sorts them descending (rank order).
 // Returns the padded power-of-two size; sm.i32v[0] holds the count.
 template <typename T>
-__device__ int gather_sort(const RowCtx<T>& C, FilterSmem& sm, uint32_t lo_key, int expect) {
+__device__ int gather_sort(RowCtx<T> C, FilterSmem& sm, uint32_t lo_key, int expect) {
   const int tid = threadIdx.x;
   int n2 = 1;
   while (n2 < expect) n2 <<= 1;
@@ -149,20 +188,13 @@ __device__ int gather_sort(const RowCtx<T>& C, FilterSmem& sm, uint32_t lo_key, 
   for (int i = tid; i < n2; i += kFT) sm.cand[i] = 0ull;
   if (tid == 0) sm.i32v[0] = 0;
   __syncthreads();
-  for (int64_t base = (int64_t)tid * 8; base < C.V; base += (int64_t)kFT * 8) {
-    float v[8];
-    load8<T>(C.rp, base, C.V, C.vec_ok, v);
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const int64_t i = base + k;
-      if (i >= C.V) continue;
-      const uint32_t key = hs_key(hs_div_t(v[k], C.Tt));
-      if (key < lo_key || !C.inA(key, i)) continue;
-      const int slot = atomicAdd(&sm.i32v[0], 1);
-      if (slot < kCand)
-        sm.cand[slot] = ((uint64_t)key << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
-    }
-  }
+  stream_row(C, [&](float raw, int64_t i) {
+    const uint32_t key = hs_key(C.div(raw));
+    if (key < lo_key || !C.inA(key, i)) return;
+    const int slot = atomicAdd(&sm.i32v[0], 1);
+    if (slot < kCand)
+      sm.cand[slot] = ((uint64_t)key << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
+  });
   __syncthreads();
   // bitonic sort, descending
   for (int k = 2; k <= n2; k <<= 1) {
@@ -191,7 +223,7 @@ __device__ __forceinline__ int64_t cand_idx(uint64_t c) {
 
 // Index of the n-th (1-based) element in index order with key == key0 and in A.
 template <typename T>
-__device__ int64_t nth_tie(const RowCtx<T>& C, FilterSmem& sm, uint32_t key0, uint64_t n) {
+__device__ int64_t nth_tie(RowCtx<T> C, FilterSmem& sm, uint32_t key0, uint64_t n) {
   const int tid = threadIdx.x;
   uint64_t running = 0;
   if (tid == 0) sm.u64v[0] = ~0ull;
@@ -207,7 +239,7 @@ __device__ int64_t nth_tie(const RowCtx<T>& C, FilterSmem& sm, uint32_t key0, ui
       const int64_t i = base + k;
       hit[k] = false;
       if (i < C.V) {
-        const uint32_t key = hs_key(hs_div_t(v[k], C.Tt));
+        const uint32_t key = hs_key(C.div(v[k]));
         hit[k] = (key == key0) && C.inA(key, i);
       }
       cnt += hit[k] ? 1u : 0u;
@@ -237,15 +269,16 @@ __device__ int64_t nth_tie(const RowCtx<T>& C, FilterSmem& sm, uint32_t key0, ui
 
 // Top-p over sorted candidates sm.cand[0, n) (rank order from rank 0).
 // Writes kept count, boundary and S_B (e-units) to shared scalars.
-__device__ void lds_top_p(FilterSmem& sm, int n, float M, float sA, bool p_on, uint64_t theta,
+__device__ __forceinline__ void lds_top_p(FilterSmem& sm, int n, float M, float sA, bool p_on, uint64_t theta,
                           int n2) {
   const int tid = threadIdx.x;
-  // per-thread block of 8 consecutive ranks
-  uint64_t me[8], mm[8];
+  // per-thread block of kRpt consecutive ranks
+  constexpr int kRpt = kCand / kFT;
+  uint64_t me[kRpt], mm[kRpt];
   uint64_t se = 0, smm = 0;
-  const int r0 = tid * 8;
+  const int r0 = tid * kRpt;
 #pragma unroll
-  for (int k = 0; k < 8; ++k) {
+  for (int k = 0; k < kRpt; ++k) {
     const int r = r0 + k;
     me[k] = 0;
     mm[k] = 0;
@@ -265,13 +298,13 @@ __device__ void lds_top_p(FilterSmem& sm, int n, float M, float sA, bool p_on, u
   {
     uint64_t ae = exe, am = exm;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
+    for (int k = 0; k < kRpt; ++k) {
       const int r = r0 + k;
       ae += me[k];
       am += mm[k];
       if (r < kCand) {
-        sm.scane[r] = ae;
-        sm.scanm[r] = am;
+        sm.u.sc.scane[r] = ae;
+        sm.u.sc.scanm[r] = am;
       }
     }
   }
@@ -279,9 +312,9 @@ __device__ void lds_top_p(FilterSmem& sm, int n, float M, float sA, bool p_on, u
   __syncthreads();
   if (p_on) {
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
+    for (int k = 0; k < kRpt; ++k) {
       const int r = r0 + k;
-      if (r < n && sm.scanm[r] >= theta) {
+      if (r < n && sm.u.sc.scanm[r] >= theta) {
         atomicMin(&sm.i32v[1], r);
         break;
       }
@@ -292,10 +325,633 @@ __device__ void lds_top_p(FilterSmem& sm, int n, float M, float sA, bool p_on, u
     int K = sm.i32v[1];
     if (K < 1) K = 1;
     sm.i32v[2] = K;
-    sm.u64v[1] = sm.scane[K - 1];  // S_B
+    sm.u64v[1] = sm.u.sc.scane[K - 1];  // S_B
     sm.u64v[2] = sm.cand[K - 1];   // boundary
   }
   __syncthreads();
+}
+
+// Bitonic sort of sm.cand[0, n2) descending (n2 a power of two).
+__device__ __forceinline__ void sort_desc(FilterSmem& sm, int n2) {
+  const int tid = threadIdx.x;
+  for (int k = 2; k <= n2; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = tid; i < n2; i += kFT) {
+        const int ixj = i ^ j;
+        if (ixj > i) {
+          uint64_t a = sm.cand[i], b = sm.cand[ixj];
+          const bool desc = ((i & k) == 0);
+          if (desc ? (a < b) : (a > b)) {
+            sm.cand[i] = b;
+            sm.cand[ixj] = a;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// Bitonic sort of n2 = 64 * E entries of sm.cand (descending) by wave 0 in
+// registers: element i = lane * E + e.
+template <int E>
+__device__ __forceinline__ void wave_sort_desc(FilterSmem& sm) {
+  const int lane = threadIdx.x;
+  constexpr int n2 = 64 * E;
+  uint64_t v[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) v[e] = sm.cand[lane * E + e];
+#pragma unroll
+  for (int k = 2; k <= n2; k <<= 1) {
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      if (j < E) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          const int pe = e ^ j;
+          if (pe > e) {
+            const bool desc = (((lane * E + e) & k) == 0);
+            const uint64_t a = v[e], b = v[pe];
+            if (desc ? (a < b) : (a > b)) {
+              v[e] = b;
+              v[pe] = a;
+            }
+          }
+        }
+      } else {
+        const int lm = j / E;  // partner lane distance
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          const uint64_t o = __shfl_xor((unsigned long long)v[e], lm, kWave);
+          const bool desc = (((lane * E + e) & k) == 0);
+          const bool keep_max = (desc == ((lane & lm) == 0));
+          v[e] = keep_max ? (v[e] > o ? v[e] : o) : (v[e] < o ? v[e] : o);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < E; ++e) sm.cand[lane * E + e] = v[e];
+}
+
+// Sorts sm.cand[0, n) descending, padding with zeros (which sort last) up to a
+// power of two; wave 0 alone sorts up to 256 entries in registers.
+__device__ __forceinline__ int pad_sort(FilterSmem& sm, int n) {
+  int n2 = 64;
+  while (n2 < n) n2 <<= 1;
+  for (int i = n + threadIdx.x; i < n2; i += kFT) sm.cand[i] = 0ull;
+  __syncthreads();
+  if (n2 <= 256) {
+    if (threadIdx.x < kWave) {
+      if (n2 == 64) wave_sort_desc<1>(sm);
+      else if (n2 == 128) wave_sort_desc<2>(sm);
+      else wave_sort_desc<4>(sm);
+    }
+    __syncthreads();
+  } else {
+    sort_desc(sm, n2);
+  }
+  return n2;
+}
+
+// Wave 0 over sorted candidates sm.cand[0, n), n <= 256 (4 ranks per lane):
+//   esum_k = sum of floor(2^44 exp(x_r - M)) over the first k ranks (k <= n);
+//   first  = first rank r < n whose base_m + sum_{r' <= r} floor(2^44 e_r' / sA)
+//            reaches theta (n if none), with e_first = e-mass sum of ranks
+//            < first (ranks 0 .. first-1).
+// Results in sm.i32v[1] (first) and sm.u64v[1] (e_first), sm.u64v[3] (esum_k).
+__device__ __forceinline__ void wave_scan_cands(FilterSmem& sm, int n, float M, float sA,
+                                                uint64_t base_m, uint64_t theta, int k) {
+  const int lane = threadIdx.x;
+  if (lane < kWave) {
+    uint64_t me[4], mm[4];
+    uint64_t le = 0, lm = 0, lk = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int r = lane * 4 + q;
+      me[q] = 0;
+      mm[q] = 0;
+      if (r < n) {
+        const float e = hs_exp(hs_unkey(cand_key(sm.cand[r])) - M);
+        me[q] = hs_fx44(e);
+        mm[q] = hs_fx44(e / sA);
+      }
+      le += me[q];
+      lm += mm[q];
+      if (r < k) lk += me[q];
+    }
+    const uint64_t ie = wave_incl_scan_u64(le, lane);
+    const uint64_t im = wave_incl_scan_u64(lm, lane);
+    const uint64_t esk = wave_sum_u64(lk);
+    uint64_t ae = ie - le, am = base_m + im - lm;
+    int first = n;
+    uint64_t efirst = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int r = lane * 4 + q;
+      if (r < n && first == n && am + mm[q] >= theta) {
+        first = r;
+        efirst = ae;
+      }
+      ae += me[q];
+      am += mm[q];
+    }
+    const uint64_t hit = __ballot(first < n);
+    if (hit) {
+      const int src = __ffsll((long long)hit) - 1;
+      first = __shfl(first, src, kWave);
+      efirst = __shfl((unsigned long long)efirst, src, kWave);
+    } else {
+      first = n;
+      efirst = wave_sum_u64(le);
+    }
+    if (lane == 0) {
+      sm.i32v[1] = first;
+      sm.u64v[1] = efirst;
+      sm.u64v[3] = esk;
+    }
+  }
+  __syncthreads();
+}
+
+// Inclusive scans of the masses of the sorted candidates sm.cand[0, n):
+// sm.i32v[1] = first rank whose scan reaches theta_rel (n if none), with the
+// inclusive e-mass scan in sm.u.sc.scane.
+__device__ __forceinline__ void scan_bucket(FilterSmem& sm, int n, float M, float sA, uint64_t theta_rel) {
+  const int tid = threadIdx.x;
+  constexpr int kRpt = kCand / kFT;
+  uint64_t me[kRpt], mm[kRpt];
+  uint64_t se = 0, smm = 0;
+  const int r0 = tid * kRpt;
+#pragma unroll
+  for (int k = 0; k < kRpt; ++k) {
+    const int r = r0 + k;
+    me[k] = 0;
+    mm[k] = 0;
+    if (r < n) {
+      const float e = hs_exp(hs_unkey(cand_key(sm.cand[r])) - M);
+      me[k] = hs_fx44(e);
+      mm[k] = hs_fx44(e / sA);
+    }
+    se += me[k];
+    smm += mm[k];
+  }
+  uint64_t te, tm;
+  uint64_t ae = block_excl_scan(se, sm.wsum, &te);
+  uint64_t am = block_excl_scan(smm, sm.wsum2, &tm);
+  if (tid == 0) sm.i32v[1] = n;
+  __syncthreads();
+  bool found = false;
+#pragma unroll
+  for (int k = 0; k < kRpt; ++k) {
+    const int r = r0 + k;
+    ae += me[k];
+    am += mm[k];
+    if (r < n) {
+      sm.u.sc.scane[r] = ae;
+      if (!found && am >= theta_rel) {
+        atomicMin(&sm.i32v[1], r);
+        found = true;
+      }
+    }
+  }
+  __syncthreads();
+}
+
+// ---------------------------------------------------------------------------
+// Chunk-parallel filter passes (one 256-thread workgroup per 2048-element
+// chunk of a row, the geometry of k_chunk_stats).
+//   mode 1 (top-k with k <= chunks): pass 1 appends every element at or above
+//           the k-th largest chunk maximum to the row's candidate list;
+//   mode 2 (top-p alone): pass 1 accumulates exact masses into a 256-bucket
+//           histogram of (M - x) * 8 (bucket 255 collects the zero masses);
+//           pass 2 finds the coarse bucket where the cumulative mass reaches p
+//           and appends its elements (at most kCand of them), or else
+//           histograms them into 256 fine sub-buckets; pass 3 appends the
+//           elements of the fine boundary bucket.
+// k_row_filter then finishes each row in LDS from its candidates.
+// ---------------------------------------------------------------------------
+constexpr int kPT = kChunkThreads;
+static_assert(kPT == kCB, "one histogram bucket per thread");
+// a coarse boundary bucket with more elements than this is refined into fine
+// sub-buckets first (small candidate sets sort in one wave)
+constexpr uint32_t kDirect = 256;
+
+__device__ __forceinline__ int filter_mode(const Problem& P, int unit) {
+  const int kk = P.top_ks[unit];
+  const float pp = P.top_ps[unit];
+  const bool k_on = (kk > 0 && kk < P.V);
+  if (k_on && kk <= P.nchunk) return 1;
+  if (!k_on && pp < 1.0f) return 2;
+  return 0;
+}
+
+// coarse bucket of (M - x) * 8; monotone in x
+__device__ __forceinline__ int coarse_bucket(float x, float M) {
+  const float d = (M - x) * 8.0f;
+  return (d < (float)(kCB - 1)) ? (int)d : kCB - 1;
+}
+// fine bucket inside coarse bucket b1 (x must lie in b1); monotone in x
+__device__ __forceinline__ int fine_bucket(float x, float M, int b1) {
+  const float f = ((M - x) * 8.0f - (float)b1) * 256.0f;  // exact: Sterbenz, powers of two
+  const int b = (int)f;
+  return b < 0 ? 0 : (b > kCB - 1 ? kCB - 1 : b);
+}
+
+// exclusive scan over the kNT threads of a workgroup (kNT / 64 waves)
+template <int kNT>
+__device__ __forceinline__ uint64_t blk_scan(uint64_t v, uint64_t* wsum, uint64_t* total) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const uint64_t incl = wave_incl_scan_u64(v, lane);
+  if (lane == 63) wsum[wid] = incl;
+  __syncthreads();
+  uint64_t off = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < kNT / 64; ++w) {
+    const uint64_t x = wsum[w];
+    if (w < wid) off += x;
+    tot += x;
+  }
+  __syncthreads();
+  *total = tot;
+  return off + incl - v;
+}
+
+// First bucket of a kCB-bucket histogram (thread t holds bucket t, t < kCB) whose
+// inclusive cumulative mass, starting from base_m, reaches theta. Returns it (or
+// -1) and the count / mass / e-mass of the buckets before it (plus the bases).
+struct Crossing {
+  int b;
+  uint64_t c, m, e;
+};
+template <int kNT>
+__device__ __forceinline__ Crossing find_crossing(uint64_t hc, uint64_t hm, uint64_t he, uint64_t base_m,
+                                  uint64_t theta, uint64_t* wsum, int* s_b, uint64_t* s_v) {
+  const int t = threadIdx.x;
+  uint64_t tot;
+  const uint64_t xm = blk_scan<kNT>(hm, wsum, &tot) + base_m;
+  const uint64_t xe = blk_scan<kNT>(he, wsum, &tot);
+  const uint64_t xc = blk_scan<kNT>(hc, wsum, &tot);
+  if (t == 0) *s_b = -1;
+  __syncthreads();
+  if (t < kCB && xm < theta && xm + hm >= theta) {
+    *s_b = t;  // unique: the cumulative mass is monotone
+    s_v[0] = xc;
+    s_v[1] = xm;
+    s_v[2] = xe;
+  }
+  __syncthreads();
+  Crossing r;
+  r.b = *s_b;
+  r.c = s_v[0];
+  r.m = s_v[1];
+  r.e = s_v[2];
+  __syncthreads();
+  return r;
+}
+
+// Appends the (up to 8) flagged elements of every thread of the workgroup to the
+// row's candidate list with one global atomic per workgroup.
+__device__ __forceinline__ void append_cands(const Work& W, int row, const uint32_t (&key)[8],
+                                             uint32_t flags, int64_t i0, int* s_cnt, int* s_base) {
+  const int tid = threadIdx.x;
+  if (tid == 0) *s_cnt = 0;
+  __syncthreads();
+  const int n = __popc(flags);
+  const int off = n ? atomicAdd(s_cnt, n) : 0;
+  __syncthreads();
+  if (tid == 0) *s_base = *s_cnt ? atomicAdd(&W.filt[row].ncand, *s_cnt) : 0;
+  __syncthreads();
+  int slot = *s_base + off;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    if (flags & (1u << k)) {
+      if (slot < kCand)
+        W.cand[(int64_t)row * kCand + slot] =
+            ((uint64_t)key[k] << 32) | (uint64_t)(0xffffffffu - (uint32_t)(i0 + k));
+      ++slot;
+    }
+  }
+}
+
+struct PassShared {
+  uint32_t keys[kCB];
+  uint64_t wsum[kPT / 64];
+  uint64_t hm[kCB], he[kCB];
+  uint32_t hc[kCB];
+  uint64_t v[3];
+  int b, cnt, base;
+};
+
+// Per row (one 256-thread workgroup): row max M and normaliser S (the fold of
+// the chunk statistics), the top-k gather threshold (mode 1: key of the keff-th
+// largest chunk maximum; its rank = greater keys + equal keys of lower chunk
+// index, unique) and the top-p mass threshold (mode 2).
+__global__ __launch_bounds__(kPT) void k_filter_plan1(Problem P, Work W) {
+  __shared__ PassShared ps;
+  const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int unit = row / P.rows_per_unit;
+  const int mode = filter_mode(P, unit);
+  FilterScratch& f = W.filt[row];
+  if (wid == 0) {
+    const RowDesc d = fold_row_desc(P, W, row, lane);
+    if (lane == 0) {
+      f.m = d.m;
+      f.s = d.s;
+      f.b1 = -1;
+      f.b2 = -1;
+      f.ac = f.am = f.ae = 0ull;
+      f.theta = (mode == 2) ? mass_threshold(P.top_ps[unit]) : 0ull;
+    }
+  }
+  if (mode != 1) return;
+  const int keff = P.top_ks[unit];
+  const ChunkStat* cp = W.part + (int64_t)row * P.nchunk;
+  for (int base = 0; base < P.nchunk; base += kCB) {
+    // chunk maxima [base, base + kCB) ranked against all chunk maxima
+    const int c = base + tid;
+    const uint32_t kc = (c < P.nchunk) ? hs_key(cp[c].m) : 0u;
+    int rank = 0;
+    for (int b2 = 0; b2 < P.nchunk; b2 += kCB) {
+      __syncthreads();
+      ps.keys[tid] = (b2 + tid < P.nchunk) ? hs_key(cp[b2 + tid].m) : 0u;
+      __syncthreads();
+      const int ne = (P.nchunk - b2 < kCB) ? P.nchunk - b2 : kCB;
+      for (int e = 0; e < ne; ++e) {
+        const uint32_t ke = ps.keys[e];
+        rank += (ke > kc || (ke == kc && b2 + e < c)) ? 1 : 0;
+      }
+    }
+    if (c < P.nchunk && rank == keff - 1) f.tau = kc;
+  }
+}
+
+// Per mode-2 row: the coarse bucket where the cumulative mass reaches p, whether
+// it is refined, and the sums before it.
+__global__ __launch_bounds__(kPT) void k_filter_plan2(Problem P, Work W) {
+  __shared__ PassShared ps;
+  const int row = blockIdx.x, t = threadIdx.x;
+  if (filter_mode(P, row / P.rows_per_unit) != 2) return;
+  FilterScratch& f = W.filt[row];
+  const int64_t hb = (int64_t)row * kCB + t;
+  const Crossing cr = find_crossing<kPT>(W.h1c[hb], W.h1m[hb], W.h1e[hb], 0ull, f.theta, ps.wsum,
+                                         &ps.b, ps.v);
+  if (t == 0) {
+    f.b1 = cr.b;
+    f.b2 = -1;
+    f.ac = cr.c;
+    f.am = cr.m;
+    f.ae = cr.e;
+  }
+}
+
+// Per refined mode-2 row: the fine sub-bucket where the cumulative mass reaches p.
+__global__ __launch_bounds__(kPT) void k_filter_plan3(Problem P, Work W) {
+  __shared__ PassShared ps;
+  const int row = blockIdx.x, t = threadIdx.x;
+  if (filter_mode(P, row / P.rows_per_unit) != 2) return;
+  FilterScratch& f = W.filt[row];
+  const int b1 = f.b1;
+  if (b1 < 0 || W.h1c[(int64_t)row * kCB + b1] <= kDirect) return;
+  const int64_t hb = (int64_t)row * kCB + t;
+  const uint64_t am = f.am, ac = f.ac, ae = f.ae;
+  const Crossing cf = find_crossing<kPT>(W.h2c[hb], W.h2m[hb], W.h2e[hb], am, f.theta, ps.wsum,
+                                         &ps.b, ps.v);
+  if (t == 0) {
+    f.b2 = cf.b;
+    if (cf.b >= 0) {
+      f.ac = ac + cf.c;
+      f.am = cf.m;  // includes the base
+      f.ae = ae + cf.e;
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kPT) void k_filter_pass1(Problem P, Work W) {
+  __shared__ PassShared ps;
+  const int tid = threadIdx.x;
+  const int64_t items = (int64_t)P.units * P.rows_per_unit * P.nchunk;
+  for (int64_t it = blockIdx.x; it < items; it += gridDim.x) {
+    const int row = (int)(it / P.nchunk);
+    const int c = (int)(it % P.nchunk);
+    const int unit = row / P.rows_per_unit;
+    const int mode = filter_mode(P, unit);
+    if (mode == 0) continue;
+    const float Tt = P.temps[unit];
+    const float rT = 1.0f / Tt;
+    const bool fast = hs_rcp_ok(Tt);
+    const T* rp = reinterpret_cast<const T*>(P.logits) + (int64_t)row * P.row_stride;
+    const bool vec_ok = ((reinterpret_cast<uintptr_t>(rp) & 15u) == 0);
+    const int64_t i0 = chunk_elem(c, tid, 0);
+    float x[8];
+    load8<T>(rp, i0, P.V, vec_ok, x);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) x[k] = hs_div_temp(x[k], Tt, rT, fast);
+    const FilterScratch& f = W.filt[row];
+    if (mode == 1) {
+      const uint32_t tau = f.tau;
+      uint32_t key[8], flags = 0;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        key[k] = hs_key(x[k]);
+        if (i0 + k < P.V && key[k] >= tau) flags |= 1u << k;
+      }
+      append_cands(W, row, key, flags, i0, &ps.cnt, &ps.base);
+    } else {
+      ps.hm[tid] = 0ull;
+      ps.he[tid] = 0ull;
+      ps.hc[tid] = 0u;
+      __syncthreads();
+      const float M = f.m, S = f.s;
+      const float rS = 1.0f / S;
+      const bool fastS = hs_rcp_ok(S);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        if (i0 + k >= P.V) continue;
+        const int b = coarse_bucket(x[k], M);
+        atomicAdd(&ps.hc[b], 1u);
+        if (b < kCB - 1) {  // the last bucket holds only zero masses
+          const float e = hs_exp(x[k] - M);
+          const uint64_t em = hs_fx44(e);
+          const uint64_t mm = hs_fx44(hs_div_temp(e, S, rS, fastS));
+          if (mm) atomicAdd((unsigned long long*)&ps.hm[b], (unsigned long long)mm);
+          if (em) atomicAdd((unsigned long long*)&ps.he[b], (unsigned long long)em);
+        }
+      }
+      __syncthreads();
+      const int64_t hb = (int64_t)row * kCB + tid;
+      if (ps.hc[tid]) {
+        atomicAdd(&W.h1c[hb], ps.hc[tid]);
+        if (ps.hm[tid]) atomicAdd((unsigned long long*)&W.h1m[hb], (unsigned long long)ps.hm[tid]);
+        if (ps.he[tid]) atomicAdd((unsigned long long*)&W.h1e[hb], (unsigned long long)ps.he[tid]);
+      }
+    }
+    __syncthreads();
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kPT) void k_filter_pass2(Problem P, Work W) {
+  __shared__ PassShared ps;
+  const int tid = threadIdx.x;
+  const int64_t items = (int64_t)P.units * P.rows_per_unit * P.nchunk;
+  for (int64_t it = blockIdx.x; it < items; it += gridDim.x) {
+    const int row = (int)(it / P.nchunk);
+    const int c = (int)(it % P.nchunk);
+    const int unit = row / P.rows_per_unit;
+    if (filter_mode(P, unit) != 2) continue;
+    const FilterScratch& f = W.filt[row];
+    const int b1 = f.b1;
+    if (b1 < 0) continue;
+    const bool fine = W.h1c[(int64_t)row * kCB + b1] > kDirect;
+    if (fine) {
+      ps.hm[tid] = 0ull;
+      ps.he[tid] = 0ull;
+      ps.hc[tid] = 0u;
+      __syncthreads();
+    }
+    const float M = f.m, S = f.s;
+    const float Tt = P.temps[unit];
+    const float rT = 1.0f / Tt;
+    const bool fast = hs_rcp_ok(Tt);
+    const T* rp = reinterpret_cast<const T*>(P.logits) + (int64_t)row * P.row_stride;
+    const bool vec_ok = ((reinterpret_cast<uintptr_t>(rp) & 15u) == 0);
+    const int64_t i0 = chunk_elem(c, tid, 0);
+    float x[8];
+    load8<T>(rp, i0, P.V, vec_ok, x);
+    const float rS = 1.0f / S;
+    const bool fastS = hs_rcp_ok(S);
+    uint32_t key[8], flags = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      key[k] = 0;
+      if (i0 + k >= P.V) continue;
+      const float xv = hs_div_temp(x[k], Tt, rT, fast);
+      if (coarse_bucket(xv, M) != b1) continue;
+      if (!fine) {
+        key[k] = hs_key(xv);
+        flags |= 1u << k;
+      } else {
+        const int b = fine_bucket(xv, M, b1);
+        const float e = hs_exp(xv - M);
+        atomicAdd(&ps.hc[b], 1u);
+        const uint64_t mm = hs_fx44(hs_div_temp(e, S, rS, fastS));
+        const uint64_t em = hs_fx44(e);
+        if (mm) atomicAdd((unsigned long long*)&ps.hm[b], (unsigned long long)mm);
+        if (em) atomicAdd((unsigned long long*)&ps.he[b], (unsigned long long)em);
+      }
+    }
+    if (!fine) append_cands(W, row, key, flags, i0, &ps.cnt, &ps.base);
+    if (fine) {
+      __syncthreads();
+      const int64_t hb = (int64_t)row * kCB + tid;
+      if (ps.hc[tid]) {
+        atomicAdd(&W.h2c[hb], ps.hc[tid]);
+        if (ps.hm[tid]) atomicAdd((unsigned long long*)&W.h2m[hb], (unsigned long long)ps.hm[tid]);
+        if (ps.he[tid]) atomicAdd((unsigned long long*)&W.h2e[hb], (unsigned long long)ps.he[tid]);
+      }
+    }
+    __syncthreads();
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kPT) void k_filter_pass3(Problem P, Work W) {
+  __shared__ PassShared ps;
+  const int tid = threadIdx.x;
+  const int64_t items = (int64_t)P.units * P.rows_per_unit * P.nchunk;
+  for (int64_t it = blockIdx.x; it < items; it += gridDim.x) {
+    const int row = (int)(it / P.nchunk);
+    const int c = (int)(it % P.nchunk);
+    const int unit = row / P.rows_per_unit;
+    if (filter_mode(P, unit) != 2) continue;
+    const FilterScratch& f = W.filt[row];
+    const int b1 = f.b1, b2 = f.b2;
+    if (b1 < 0 || b2 < 0) continue;
+    const float M = f.m;
+    const float Tt = P.temps[unit];
+    const float rT = 1.0f / Tt;
+    const bool fast = hs_rcp_ok(Tt);
+    const T* rp = reinterpret_cast<const T*>(P.logits) + (int64_t)row * P.row_stride;
+    const bool vec_ok = ((reinterpret_cast<uintptr_t>(rp) & 15u) == 0);
+    const int64_t i0 = chunk_elem(c, tid, 0);
+    float x[8];
+    load8<T>(rp, i0, P.V, vec_ok, x);
+    uint32_t key[8], flags = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      key[k] = 0;
+      if (i0 + k >= P.V) continue;
+      const float xv = hs_div_temp(x[k], Tt, rT, fast);
+      if (coarse_bucket(xv, M) == b1 && fine_bucket(xv, M, b1) == b2) {
+        key[k] = hs_key(xv);
+        flags |= 1u << k;
+      }
+    }
+    append_cands(W, row, key, flags, i0, &ps.cnt, &ps.base);
+    __syncthreads();
+  }
+}
+
+// Copies the row's n candidates from the workspace into sm.cand.
+__device__ __forceinline__ void load_cands(const Work& W, int row, int n, FilterSmem& sm) {
+  const uint64_t* src = W.cand + (int64_t)row * kCand;
+  for (int i = threadIdx.x; i < n; i += kFT) sm.cand[i] = src[i];
+  __syncthreads();
+}
+
+// Top-p boundary of a mode-2 row from its histograms and candidates (kFT
+// threads). Returns false when the candidates overflowed (radix fallback).
+struct TopP {
+  bool all;
+  int64_t kept;
+  uint32_t bkey;
+  int64_t bidx;
+  uint64_t sb_fx;
+};
+__device__ __forceinline__ bool top_p_from_hist(const Work& W, int row, FilterSmem& sm, float M, float sA,
+                                uint64_t theta, TopP& out) {
+  (void)theta;
+  const FilterScratch& f = W.filt[row];
+  const int b1 = f.b1;
+  if (b1 < 0) {
+    out.all = true;
+    return true;
+  }
+  if (W.h1c[(int64_t)row * kCB + b1] > kDirect && f.b2 < 0) return false;
+  const uint64_t ac = f.ac, am = f.am, ae = f.ae;
+  const int n = W.filt[row].ncand;
+  if (n > kCand || n <= 0) return false;
+  load_cands(W, row, n, sm);
+  (void)pad_sort(sm, n);
+  int j;
+  uint64_t ej;  // e-mass of the bucket's ranks before j
+  if (n <= 256) {
+    wave_scan_cands(sm, n, M, sA, am, theta, 0);
+    j = sm.i32v[1];
+    ej = sm.u64v[1];
+  } else {
+    scan_bucket(sm, n, M, sA, theta - am);
+    j = sm.i32v[1];
+    ej = j > 0 ? sm.u.sc.scane[j - 1] : 0ull;
+  }
+  if (ac == 0 && j == 0) {  // rank 0 is always kept
+    j = 1;
+    ej = hs_fx44(hs_exp(hs_unkey(cand_key(sm.cand[0])) - M));
+  }
+  out.all = false;
+  out.kept = (int64_t)(ac + j);
+  out.sb_fx = ae + ej;
+  if (j > 0) {
+    out.bkey = cand_key(sm.cand[j - 1]);
+    out.bidx = cand_idx(sm.cand[j - 1]);
+  } else {
+    out.bkey = cand_key(sm.cand[0]);  // keep exactly the keys above the bucket
+    out.bidx = -1;
+  }
+  __syncthreads();
+  return true;
 }
 
 template <typename T>
@@ -313,9 +969,18 @@ __global__ __launch_bounds__(kFT) void k_row_filter(Problem P, Work W, float* ro
   const bool k_on = keff < V;
   const bool p_on = pp < 1.0f;
 
-  if (wid == 0) {
-    const RowDesc d = fold_row_desc(P, W, row, lane);
-    if (lane == 0) s_fold = d;
+  if (tid == 0) {
+    // the row fold of k_filter_plan1
+    RowDesc d;
+    d.m = W.filt[row].m;
+    d.s = W.filt[row].s;
+    d.tkey = 0u;
+    d.tidx = 0x7fffffff;
+    d.all = 1;
+    d.token = -1;
+    d.s_full = d.s;
+    d.pad = 0;
+    s_fold = d;
   }
   __syncthreads();
   if (!(k_on || p_on) && tid == 0) {
@@ -332,6 +997,8 @@ __global__ __launch_bounds__(kFT) void k_row_filter(Problem P, Work W, float* ro
     C.vec_ok = ((reinterpret_cast<uintptr_t>(C.rp) & 15u) == 0);
     C.V = V;
     C.Tt = P.temps[unit];
+    C.rt = 1.0f / C.Tt;
+    C.fast = hs_rcp_ok(C.Tt);
     C.M = D.m;
     C.a_all = true;
     C.a_key = 0u;
@@ -341,7 +1008,23 @@ __global__ __launch_bounds__(kFT) void k_row_filter(Problem P, Work W, float* ro
     bool cand_ready = false;  // sm.cand holds the sorted A (first nA entries)
     int64_t nA = V;
     int n2 = 0;
-    if (k_on) {
+    int path = 0;
+    const int mode = filter_mode(P, unit);
+    if (mode == 1) {
+      // candidates at or above the keff-th largest chunk maximum (k_filter_pass1)
+      const int n = W.filt[row].ncand;
+      if (n <= kCand) {
+        load_cands(W, row, n, sm);
+        n2 = pad_sort(sm, n);
+        const uint64_t bnd = sm.cand[keff - 1];
+        C.a_all = false;
+        C.a_key = cand_key(bnd);
+        C.a_idx = cand_idx(bnd);
+        cand_ready = true;
+        path = 1;
+      }
+    }
+    if (k_on && !cand_ready) {
       uint32_t prefix = 0;
       uint64_t above = 0, cnt_b = 0;
       bool done = false;
@@ -420,7 +1103,13 @@ __global__ __launch_bounds__(kFT) void k_row_filter(Problem P, Work W, float* ro
     // ---- normaliser over A --------------------------------------------------
     float sA = D.s_full;
     uint64_t sA_fx = 0;
-    if (k_on && cand_ready) {
+    const bool wave_k = k_on && cand_ready && keff <= 256;
+    if (wave_k) {
+      // from the sorted candidates (first keff), one wave
+      wave_scan_cands(sm, (int)keff, C.M, 1.0f, 0ull, ~0ull, (int)keff);
+      sA_fx = sm.u64v[3];
+      sA = hs_f32_rz_of_u64(sA_fx) * kTwoM44;
+    } else if (k_on && cand_ready) {
       // from the sorted candidates (first keff)
       uint64_t s = 0;
       for (int r = tid; r < (int)keff; r += kFT)
@@ -429,17 +1118,10 @@ __global__ __launch_bounds__(kFT) void k_row_filter(Problem P, Work W, float* ro
       sA = hs_f32_rz_of_u64(sA_fx) * kTwoM44;
     } else if (k_on) {
       uint64_t s = 0;
-      for (int64_t base = (int64_t)tid * 8; base < V; base += (int64_t)kFT * 8) {
-        float v[8];
-        load8<T>(C.rp, base, V, C.vec_ok, v);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          const int64_t i = base + k;
-          if (i >= V) continue;
-          const float x = hs_div_t(v[k], C.Tt);
-          if (C.inA(hs_key(x), i)) s += hs_fx44(hs_exp(x - C.M));
-        }
-      }
+      stream_row(C, [&](float raw, int64_t i) {
+        const float x = C.div(raw);
+        if (C.inA(hs_key(x), i)) s += hs_fx44(hs_exp(x - C.M));
+      });
       sA_fx = block_sum(s, sm.wsum);
       sA = hs_f32_rz_of_u64(sA_fx) * kTwoM44;
     }
@@ -454,7 +1136,20 @@ __global__ __launch_bounds__(kFT) void k_row_filter(Problem P, Work W, float* ro
       if (tid == 0) sm.u64v[4] = mass_threshold(pp);
       __syncthreads();
       const uint64_t theta = sm.u64v[4];
-      if (cand_ready) {
+      if (wave_k) {
+        wave_scan_cands(sm, (int)keff, C.M, sA, 0ull, theta, 0);
+        int K = sm.i32v[1];  // first rank whose cumulative sum reaches p: not kept
+        uint64_t eK = sm.u64v[1];
+        if (K == 0) {  // rank 0 is always kept
+          K = 1;
+          eK = hs_fx44(hs_exp(hs_unkey(cand_key(sm.cand[0])) - C.M));
+        }
+        kept = K;
+        sB = (K == keff) ? sA : hs_f32_rz_of_u64(eK) * kTwoM44;
+        ball = false;
+        bkey = cand_key(sm.cand[K - 1]);
+        bidx = cand_idx(sm.cand[K - 1]);
+      } else if (cand_ready) {
         lds_top_p(sm, (int)nA, C.M, sA, true, theta, n2);
         kept = sm.i32v[2];
         sB = hs_f32_rz_of_u64(sm.u64v[1]) * kTwoM44;
@@ -462,9 +1157,28 @@ __global__ __launch_bounds__(kFT) void k_row_filter(Problem P, Work W, float* ro
         bkey = cand_key(sm.u64v[2]);
         bidx = cand_idx(sm.u64v[2]);
       } else {
+        bool done = false;
+        if (mode == 2) {
+          // top-p alone: boundary from the chunk-parallel histograms + candidates
+          TopP tp;
+          if (top_p_from_hist(W, row, sm, C.M, sA, theta, tp)) {
+            if (tp.all) {
+              ball = true;
+              kept = V;
+              sB = sA;
+            } else {
+              kept = tp.kept;
+              bkey = tp.bkey;
+              bidx = tp.bidx;
+              ball = (kept == V);
+              sB = ball ? sA : hs_f32_rz_of_u64(tp.sb_fx) * kTwoM44;
+            }
+            done = true;
+            path = 2;
+          }
+        }
         uint32_t prefix = 0;
         uint64_t above_m = 0, above_e = 0, above_c = 0;
-        bool done = false;
         for (int lvl = 0; lvl < 4 && !done; ++lvl) {
           hist_pass<T, true>(C, sm, lvl, prefix, sA);
           if (wid == 0) {
@@ -567,11 +1281,8 @@ __global__ __launch_bounds__(kFT) void k_row_filter(Problem P, Work W, float* ro
       d.tidx = (int32_t)bidx;
       d.s = sB;
       W.desc[row] = d;
-      FilterScratch fs;
-      fs.kept = (int32_t)kept;
-      fs.path = cand_ready ? 1 : 0;
-      fs.pad[0] = fs.pad[1] = 0;
-      W.filt[row] = fs;
+      W.filt[row].kept = (int32_t)kept;
+      W.filt[row].path = path;
       if (row_stats) {
         row_stats[2 * (int64_t)row] = d.m;
         row_stats[2 * (int64_t)row + 1] = sB;
@@ -583,6 +1294,14 @@ __global__ __launch_bounds__(kFT) void k_row_filter(Problem P, Work W, float* ro
 template <typename T>
 int launch_filter(const Problem& P, const Work& W, float* row_stats, hipStream_t stream) {
   const int rows = P.units * P.rows_per_unit;
+  const int64_t items = (int64_t)rows * P.nchunk;
+  const int grid = (int)(items < 4096 ? items : 4096);
+  hipLaunchKernelGGL(k_filter_plan1, dim3(rows), dim3(kPT), 0, stream, P, W);
+  hipLaunchKernelGGL(k_filter_pass1<T>, dim3(grid), dim3(kPT), 0, stream, P, W);
+  hipLaunchKernelGGL(k_filter_plan2, dim3(rows), dim3(kPT), 0, stream, P, W);
+  hipLaunchKernelGGL(k_filter_pass2<T>, dim3(grid), dim3(kPT), 0, stream, P, W);
+  hipLaunchKernelGGL(k_filter_plan3, dim3(rows), dim3(kPT), 0, stream, P, W);
+  hipLaunchKernelGGL(k_filter_pass3<T>, dim3(grid), dim3(kPT), 0, stream, P, W);
   hipLaunchKernelGGL(k_row_filter<T>, dim3(rows), dim3(kFT), 0, stream, P, W, row_stats);
   return hipGetLastError() == hipSuccess ? HS_OK : HS_ERR_LAUNCH;
 }

@@ -217,3 +217,59 @@ def test_shape_changes_share_workspace(hv, orc, cuda):
         w = hv.synthetic.accept_workload(B, g, vocab=V, seed=400 + i)
         got, ref = _run_both(hv, orc, w, cuda, "reference")
         _assert_same(got, ref)
+
+
+def _degenerate_rows(V, rng):
+    rows = [np.zeros(V, np.float32),                                    # all tied
+            rng.integers(0, 2, size=V).astype(np.float32),              # two values
+            np.where(rng.random(V) < 0.5, -np.inf, rng.standard_normal(V) * 3).astype(np.float32),
+            np.concatenate([[40.0], np.full(V - 1, -5.0)]).astype(np.float32),  # one spike
+            (rng.standard_normal(V) * 0.05).astype(np.float32)]        # nearly flat
+    return np.stack(rows)
+
+
+@pytest.mark.parametrize("k,p", [(0, 0.9), (0, 0.5), (20, 1.0), (50, 0.9), (100, 0.8), (0, 0.999)])
+def test_filter_paths_on_degenerate_rows(hv, orc, cuda, k, p):
+    """Rows that overflow the LDS candidate capacity (ties, flat logits) take the
+    radix fallback; -inf entries and spikes exercise the bucket edges."""
+    rng = np.random.default_rng(31 + k)
+    V = 151936
+    x = _degenerate_rows(V, rng)
+    R = x.shape[0]
+    T = np.full(R, 0.8, np.float32)
+    tk = np.full(R, k, np.int32)
+    tp = np.full(R, p, np.float32)
+    u = rng.random(R).astype(np.float32)
+    print(f"degenerate rows k={k} p={p}", flush=True)
+    r = hv.ops.sample_rows(torch.from_numpy(x).to(cuda), torch.from_numpy(T).to(cuda),
+                           torch.from_numpy(tk).to(cuda), torch.from_numpy(tp).to(cuda),
+                           mode="filtered", uniforms=torch.from_numpy(u).to(cuda),
+                           want_probs=True, row_stats=True)
+    ref = orc.sampler(x, T, tk, tp, mode="filtered", uniforms=u)
+    np.testing.assert_array_equal(r["probs"].cpu().numpy(), ref["probs"])
+    np.testing.assert_array_equal(r["tokens"].cpu().numpy(), ref["tokens"])
+    np.testing.assert_array_equal(r["row_stats"].cpu().numpy(), ref["row_stats"])
+
+
+@pytest.mark.parametrize("k,p", [(20, 0.9), (50, 0.5), (0, 0.95), (0, 0.8), (75, 0.99)])
+def test_filter_fast_paths_random_rows(hv, orc, cuda, k, p):
+    """Chunk-maximum gather (k <= chunks) and (M - x) bucket (top-p alone) paths
+    on N(0, 2^2) bf16 rows at several temperatures."""
+    rng = np.random.default_rng(51 + k)
+    V = 151936
+    R = 6
+    x = rng.standard_normal((R, V), dtype=np.float32) * 2
+    bits = hv.synthetic.f32_to_bf16_bits(x)
+    xf = hv.synthetic.bf16_bits_to_f32(bits)
+    lg = torch.from_numpy(bits.view(np.int16)).to(cuda).view(torch.bfloat16)
+    T = np.array([0.5, 0.7, 0.9, 1.0, 1.2, 2.0], np.float32)
+    tk = np.full(R, k, np.int32)
+    tp = np.full(R, p, np.float32)
+    u = rng.random(R).astype(np.float32)
+    r = hv.ops.sample_rows(lg, torch.from_numpy(T).to(cuda), torch.from_numpy(tk).to(cuda),
+                           torch.from_numpy(tp).to(cuda), mode="filtered",
+                           uniforms=torch.from_numpy(u).to(cuda), want_probs=True, row_stats=True)
+    ref = orc.sampler(xf, T, tk, tp, mode="filtered", uniforms=u)
+    np.testing.assert_array_equal(r["probs"].cpu().numpy(), ref["probs"])
+    np.testing.assert_array_equal(r["tokens"].cpu().numpy(), ref["tokens"])
+    np.testing.assert_array_equal(r["row_stats"].cpu().numpy(), ref["row_stats"])
