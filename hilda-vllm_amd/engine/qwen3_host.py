@@ -2,9 +2,9 @@
 
 The target (Qwen3-8B geometry) and draft (Qwen3-0.6B geometry) models of the
 batch-1 speculative benchmark, restated after mini_vllm/models/qwen3.py:15-218
-with eager PyTorch for the dense parts (embedding, projections, RMSNorm, RoPE,
-SwiGLU: hipBLASLt GEMMs through torch) and the gfx950 Attention layer for the
-paged attention. Weights are N(0, 0.02^2) in bf16 (no checkpoint is loaded).
+with the gfx950 kernels for the projections of decode / verify rows (hs_linear,
+SwiGLU fused into the gate_up projection), RMSNorm, q/k-norm + RoPE and the
+paged attention; prefill-sized projections are hipBLASLt GEMMs through torch. Weights are N(0, 0.02^2) in bf16 (no checkpoint is loaded).
 """
 from __future__ import annotations
 
@@ -109,14 +109,14 @@ class Qwen3Layer(nn.Module):
             x = _ops.rmsnorm(h, self.ln1, g.rms_eps)
         else:
             x = _ops.rmsnorm(h, self.ln1, g.rms_eps, residual=residual)
-        qkv = F.linear(x, self.qkv)
+        qkv = _ops.linear(x, self.qkv)
         q, k = _ops.qk_norm_rope(qkv, g.num_heads, g.num_kv_heads, self.q_norm, self.k_norm,
                                  self.rope.cos_sin, positions, g.rms_eps)
         v = qkv[:, self.q_size + self.kv_size:].view(-1, g.num_kv_heads, g.head_dim)
         o = self.attn(q, k, v)
-        h = F.linear(o.reshape(o.shape[0], -1), self.o)
+        h = _ops.linear(o.reshape(o.shape[0], -1), self.o)
         x = _ops.rmsnorm(h, self.ln2, g.rms_eps, residual=residual)
-        h = F.linear(_ops.silu_mul(F.linear(x, self.gate_up)), self.down)
+        h = _ops.linear(_ops.linear(x, self.gate_up, swiglu=True), self.down)
         return h, residual
 
     def forward_reference(self, positions, h, residual):
@@ -198,4 +198,4 @@ class Qwen3Host(nn.Module):
         return _ops.rmsnorm(h, self.norm, self.g.rms_eps, residual=residual)
 
     def compute_logits(self, h):
-        return F.linear(h, self.lm_head)
+        return _ops.linear(h, self.lm_head)

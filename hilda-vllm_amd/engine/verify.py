@@ -32,7 +32,6 @@ from time import perf_counter
 
 import numpy as np
 import torch
-import torch.nn.functional as F
 
 from .. import ops as _ops
 from ..utils.context import reset_context, set_context
@@ -153,7 +152,7 @@ class VerifyRunner:
 
         t0 = perf_counter()
         # logits for every verify token (model_runner.py:380-383)
-        logits = F.linear(hidden, self._lm_head())
+        logits = _ops.linear(hidden, self._lm_head())
         self._sync()
         lmh = perf_counter() - t0
         self.last_logits = logits

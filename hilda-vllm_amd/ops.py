@@ -472,3 +472,32 @@ def silu_mul(gate_up: torch.Tensor) -> torch.Tensor:
     L.check(L.lib().hs_silu_mul(gate_up.data_ptr(), gate_up.stride(0), F2 // 2, out.data_ptr(),
                                 out.stride(0), N, _stream(dev)), "hs_silu_mul")
     return out
+
+
+def linear(x: torch.Tensor, weight: torch.Tensor, *, swiglu: bool = False,
+           out: torch.Tensor | None = None) -> torch.Tensor:
+    """F.linear(x, weight) for decode / verify rows (bf16). Rows <= 8 with
+    in_features % 512 == 0 run the skinny HIP kernel (hs_linear); larger row
+    counts are plain library GEMMs (hipBLASLt through torch). With swiglu=True
+    the weight is [2F, K] (gate | up) and the result is silu(gate) * up [rows, F]."""
+    if x.dim() != 2 or x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise ValueError("linear expects a 2-D bf16 input and a bf16 weight")
+    M, K = x.shape
+    N = weight.shape[0] // 2 if swiglu else weight.shape[0]
+    if weight.shape[1] != K:
+        raise ValueError("in_features mismatch")
+    fast = (M <= 8 and K % 512 == 0 and N % 4 == 0 and x.stride(1) == 1 and
+            x.stride(0) % 8 == 0 and weight.is_contiguous() and x.data_ptr() % 16 == 0 and
+            weight.data_ptr() % 16 == 0)
+    if not fast:
+        y = torch.nn.functional.linear(x, weight)
+        return silu_mul(y) if swiglu else y
+    dev = _need_cuda(x, weight, out)
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    elif out.shape != (M, N) or out.stride(1) != 1 or out.dtype != torch.bfloat16:
+        raise ValueError("out must be [rows, out_features] bf16 with contiguous rows")
+    L.check(L.lib().hs_linear(x.data_ptr(), x.stride(0), weight.data_ptr(), M, K, N,
+                              1 if swiglu else 0, out.data_ptr(), out.stride(0), _stream(dev)),
+            "hs_linear")
+    return out

@@ -254,6 +254,19 @@ int hs_zero_kv_slots(void* cache, int64_t plane_bytes, int num_planes, int64_t s
 /* q/k RMSNorm + neox RoPE (qwen3.py:82-85, rotary_embedding.py:8-50) and    */
 /* SiLU-and-mul (activation.py:8-16).                                        */
 /* ------------------------------------------------------------------------ */
+/* Skinny projection for decode / verify rows: out[r, n] = sum_k x[r, k] *    */
+/* weight[n, k] (bf16 in, fp32 accumulation, bf16 out), nn.Linear's          */
+/* F.linear(x, weight) of the model's qkv / o / gate_up / down / lm_head       */
+/* layers (mini_vllm/layers/linear.py) at rows <= 8. HS_LINEAR_SWIGLU takes a */
+/* [2 * out_features, in_features] gate|up weight and writes                   */
+/* silu(gate) * up (activation.py:8-16) with the rounding of the unfused ops.  */
+/* in_features must be a multiple of 512, out_features of 4; strides in        */
+/* elements. Larger row counts are plain library GEMMs.                        */
+#define HS_LINEAR_PLAIN 0
+#define HS_LINEAR_SWIGLU 1
+int hs_linear(const void* x, int64_t x_stride, const void* weight, int rows, int in_features,
+              int out_features, int epilogue, void* out, int64_t out_stride, void* stream);
+
 /* out = RMSNorm(x (+ residual)) * weight; with residual != NULL the residual  */
 /* row is replaced by bf16(x + residual) (strides in elements).              */
 int hs_rmsnorm(const void* x, int64_t x_stride, void* residual, int64_t residual_stride,
