@@ -481,9 +481,10 @@ static void attn_plan(int B, int Hkv, int qtiles, int max_seqlen_k, int* nsplit,
   if (want < 1) want = 1;
   int64_t len = (max_seqlen_k + want - 1) / want;
   len = (len + 127) / 128 * 128;
-  // a split below 512 keys costs more in the extra combine launch than it
-  // gains in parallelism; splits are also capped by the block-table prefetch
-  if (len < 512) len = 512;
+  // a split below 1024 keys costs more in the extra combine launch (~3.5 us)
+  // than it gains in parallelism (each wave already prefetches its next
+  // window); splits are also capped by the block-table prefetch
+  if (len < 1024) len = 1024;
   if (len > kMaxSplit) len = kMaxSplit;
   *split_len = (int)len;
   *nsplit = (int)((max_seqlen_k + len - 1) / len);
