@@ -30,7 +30,8 @@ COMMON_FLAGS = [
     "-fPIC",
     "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-fno-gpu-rdc",
-    # packed fp32 instructions stay off (see the pool notes in DESIGN.md)
+    # packed fp32 instructions stay off: some of their forms have given silent
+    # wrong results on the MI355X machines this library is tested on
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-result",
     f"-I{INCLUDE}",

@@ -7,6 +7,10 @@
 //   hs_rmsnorm       (optional residual add) + RMSNorm, one workgroup per row;
 //   hs_qk_norm_rope  per-head RMSNorm of q and k + neox RoPE, one wave per
 //                    (token, head): lane l owns the rotation pair (l, l + 64);
+//   hs_qk_norm_rope_store  the same, with k written straight into its paged
+//                    cache slot and v copied there (bf16, or FP8 e4m3fn with a
+//                    per-tensor scale), replacing the separate store_kvcache
+//                    launch (attention.py:59-90, :145);
 //   hs_silu_mul      silu(gate) * up.
 // Numerics follow the reference: the residual sum and the normalisation are
 // fp32, the normalised value is rounded to bf16 before the weight multiply.
@@ -14,15 +18,14 @@
 #include <stdint.h>
 
 #include "../../include/hilda_spec.h"
+#include "hs_fp8.h"
 
 namespace hs {
 
 __device__ __forceinline__ float bf(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+// f32 -> bf16, round to nearest even
 __device__ __forceinline__ uint16_t to_bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));  // v_cvt_pk_bf16_f32 (RNE)
 }
 // bf16 * bf16 rounded to bf16 (the product is exact in fp32)
 __device__ __forceinline__ uint16_t bf_mul(uint16_t a, uint16_t b) { return to_bf(bf(a) * bf(b)); }
@@ -93,6 +96,25 @@ __global__ __launch_bounds__(kNT) void k_rmsnorm(const uint16_t* __restrict__ x,
   }
 }
 
+// RMSNorm (layernorm.py:18-25: normalise in fp32, round, multiply by the
+// weight) and neox RoPE (rotary_embedding.py:8-16, cos/sin cache [pos, 64 | 64])
+// of one 128-wide head held as the pair (l, l + 64) by lane l; returns the
+// rotated pair rounded to bf16
+__device__ __forceinline__ void norm_rope_pair(const uint16_t* src, const uint16_t* w,
+                                               const float* cs, float eps, int lane,
+                                               uint16_t& o1, uint16_t& o2) {
+  float x1 = bf(src[lane]), x2 = bf(src[lane + 64]);
+  float ss = x1 * x1 + x2 * x2;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+  const float inv = rsqrtf(ss / 128.0f + eps);
+  x1 = bf(bf_mul(to_bf(x1 * inv), w[lane]));
+  x2 = bf(bf_mul(to_bf(x2 * inv), w[lane + 64]));
+  const float c = cs[lane], s = cs[64 + lane];
+  o1 = to_bf(x1 * c - x2 * s);
+  o2 = to_bf(x2 * c + x1 * s);
+}
+
 // one wave per (token, head); heads [0, Hq) are q, [Hq, Hq+Hkv) are k
 __global__ __launch_bounds__(kNT) void k_qk_norm_rope(const uint16_t* __restrict__ qkv, int64_t ts,
                                                       int Hq, int Hkv,
@@ -108,24 +130,79 @@ __global__ __launch_bounds__(kNT) void k_qk_norm_rope(const uint16_t* __restrict
   if (wave >= N * H) return;
   const int tok = wave / H, h = wave % H;
   const bool isq = h < Hq;
-  const uint16_t* src = qkv + tok * ts + h * 128;
-  float x1 = bf(src[lane]), x2 = bf(src[lane + 64]);
-  float ss = x1 * x1 + x2 * x2;
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-  const float inv = rsqrtf(ss / 128.0f + eps);
-  const uint16_t* w = isq ? qw : kw;
-  // RMSNorm (layernorm.py:18-25): normalise in fp32, round, multiply by weight
-  x1 = bf(bf_mul(to_bf(x1 * inv), w[lane]));
-  x2 = bf(bf_mul(to_bf(x2 * inv), w[lane + 64]));
-  // neox RoPE (rotary_embedding.py:8-16): cos/sin cache [pos, 64 | 64]
-  const int64_t p = positions[tok];
-  const float c = cos_sin[p * 128 + lane], s = cos_sin[p * 128 + 64 + lane];
-  const float y1 = x1 * c - x2 * s;
-  const float y2 = x2 * c + x1 * s;
+  uint16_t y1, y2;
+  norm_rope_pair(qkv + tok * ts + h * 128, isq ? qw : kw, cos_sin + positions[tok] * 128, eps,
+                 lane, y1, y2);
   uint16_t* dst = isq ? qo + ((int64_t)tok * Hq + h) * 128 : ko + ((int64_t)tok * Hkv + (h - Hq)) * 128;
-  dst[lane] = to_bf(y1);
-  dst[lane + 64] = to_bf(y2);
+  dst[lane] = y1;
+  dst[lane + 64] = y2;
+}
+
+struct NormRopeStoreArgs {
+  const uint16_t* qkv;
+  int64_t ts;
+  int Hq, Hkv;
+  const uint16_t* qw;
+  const uint16_t* kw;
+  const float* cos_sin;
+  const int64_t* positions;
+  float eps;
+  uint16_t* qo;
+  uint8_t* kc;
+  uint8_t* vc;
+  int64_t c_sb, c_st, c_sh;  // cache strides in elements
+  float k_scale, v_scale;
+  const int32_t* slots;
+  int block_size, num_blocks, N;
+};
+
+template <bool kFp8>
+__device__ __forceinline__ void store_pair(uint8_t* base, int64_t elem, int lane, uint16_t a,
+                                           uint16_t b, float scale) {
+  if constexpr (kFp8) {
+    base[elem + lane] = f32_to_e4m3fn_sat(bf(a) / scale);
+    base[elem + lane + 64] = f32_to_e4m3fn_sat(bf(b) / scale);
+  } else {
+    uint16_t* p = reinterpret_cast<uint16_t*>(base) + elem;
+    p[lane] = a;
+    p[lane + 64] = b;
+  }
+}
+
+// one wave per (token, head) over the q, k and v heads of the fused qkv row:
+// q heads are normalised, rotated and written to qo; k heads are normalised,
+// rotated and stored at the token's cache slot; v heads are stored unchanged.
+// Slots < 0 (and blocks beyond num_blocks) store nothing, as store_kvcache.
+template <bool kFp8>
+__global__ __launch_bounds__(kNT) void k_qk_norm_rope_store(NormRopeStoreArgs a) {
+  const int wave = blockIdx.x * (kNT / 64) + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int H = a.Hq + 2 * a.Hkv;
+  if (wave >= a.N * H) return;
+  const int tok = wave / H, h = wave % H;
+  const uint16_t* src = a.qkv + tok * a.ts + h * 128;
+  if (h < a.Hq) {
+    uint16_t y1, y2;
+    norm_rope_pair(src, a.qw, a.cos_sin + a.positions[tok] * 128, a.eps, lane, y1, y2);
+    uint16_t* dst = a.qo + ((int64_t)tok * a.Hq + h) * 128;
+    dst[lane] = y1;
+    dst[lane + 64] = y2;
+    return;
+  }
+  const int slot = a.slots[tok];
+  if (slot < 0) return;
+  const int blk = slot / a.block_size, off = slot % a.block_size;
+  if (blk >= a.num_blocks) return;
+  const bool isk = h < a.Hq + a.Hkv;
+  const int kvh = isk ? h - a.Hq : h - a.Hq - a.Hkv;
+  const int64_t elem = (int64_t)blk * a.c_sb + (int64_t)off * a.c_st + (int64_t)kvh * a.c_sh;
+  if (isk) {
+    uint16_t y1, y2;
+    norm_rope_pair(src, a.kw, a.cos_sin + a.positions[tok] * 128, a.eps, lane, y1, y2);
+    store_pair<kFp8>(a.kc, elem, lane, y1, y2, a.k_scale);
+  } else {
+    store_pair<kFp8>(a.vc, elem, lane, src[lane], src[lane + 64], a.v_scale);
+  }
 }
 
 __global__ __launch_bounds__(kNT) void k_silu_mul(const uint16_t* __restrict__ gu, int64_t gs,
@@ -194,6 +271,57 @@ int hs_qk_norm_rope(const void* qkv, int64_t token_stride, int num_q_heads, int 
                      static_cast<const uint16_t*>(q_weight),
                      static_cast<const uint16_t*>(k_weight), cos_sin, positions, eps,
                      static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(k_out), num_tokens);
+  return hipGetLastError() == hipSuccess ? HS_OK : HS_ERR_LAUNCH;
+}
+
+int hs_qk_norm_rope_store(const void* qkv, int64_t token_stride, int num_q_heads,
+                          int num_kv_heads, int head_dim, const void* q_weight,
+                          const void* k_weight, const float* cos_sin, const int64_t* positions,
+                          float eps, void* q_out, void* k_cache, void* v_cache, int kv_dtype,
+                          int64_t cache_stride_block, int64_t cache_stride_tok,
+                          int64_t cache_stride_head, float k_scale, float v_scale,
+                          const int32_t* slot_mapping, int block_size, int num_blocks,
+                          int num_tokens, void* stream) {
+  if (num_tokens == 0) return HS_OK;
+  if (!qkv || !q_weight || !k_weight || !cos_sin || !positions || !q_out || !k_cache ||
+      !v_cache || !slot_mapping || num_tokens < 0 || num_q_heads <= 0 || num_kv_heads <= 0 ||
+      block_size <= 0 || num_blocks <= 0)
+    return HS_ERR_INVALID;
+  if (head_dim != 128) return HS_ERR_UNSUPPORTED;
+  if (kv_dtype != HS_BF16 && kv_dtype != HS_FP8_E4M3) return HS_ERR_INVALID;
+  if (kv_dtype == HS_FP8_E4M3 && !(k_scale > 0.0f && v_scale > 0.0f)) return HS_ERR_INVALID;
+  if (token_stride < (int64_t)(num_q_heads + 2 * num_kv_heads) * 128) return HS_ERR_INVALID;
+  if (((uintptr_t)qkv | (uintptr_t)q_out | (uintptr_t)k_cache | (uintptr_t)v_cache) & 1)
+    return HS_ERR_UNSUPPORTED;
+  NormRopeStoreArgs a;
+  a.qkv = static_cast<const uint16_t*>(qkv);
+  a.ts = token_stride;
+  a.Hq = num_q_heads;
+  a.Hkv = num_kv_heads;
+  a.qw = static_cast<const uint16_t*>(q_weight);
+  a.kw = static_cast<const uint16_t*>(k_weight);
+  a.cos_sin = cos_sin;
+  a.positions = positions;
+  a.eps = eps;
+  a.qo = static_cast<uint16_t*>(q_out);
+  a.kc = static_cast<uint8_t*>(k_cache);
+  a.vc = static_cast<uint8_t*>(v_cache);
+  a.c_sb = cache_stride_block;
+  a.c_st = cache_stride_tok;
+  a.c_sh = cache_stride_head;
+  a.k_scale = k_scale;
+  a.v_scale = v_scale;
+  a.slots = slot_mapping;
+  a.block_size = block_size;
+  a.num_blocks = num_blocks;
+  a.N = num_tokens;
+  const int64_t waves = (int64_t)num_tokens * (num_q_heads + 2 * num_kv_heads);
+  const dim3 grid((unsigned)((waves + 3) / 4));
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (kv_dtype == HS_FP8_E4M3)
+    hipLaunchKernelGGL(k_qk_norm_rope_store<true>, grid, dim3(kNT), 0, s, a);
+  else
+    hipLaunchKernelGGL(k_qk_norm_rope_store<false>, grid, dim3(kNT), 0, s, a);
   return hipGetLastError() == hipSuccess ? HS_OK : HS_ERR_LAUNCH;
 }
 

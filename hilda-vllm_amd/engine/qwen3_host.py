@@ -2,9 +2,12 @@
 
 The target (Qwen3-8B geometry) and draft (Qwen3-0.6B geometry) models of the
 batch-1 speculative benchmark, restated after mini_vllm/models/qwen3.py:15-218
-with the gfx950 kernels for the projections of decode / verify rows (hs_linear,
-SwiGLU fused into the gate_up projection), RMSNorm, q/k-norm + RoPE and the
-paged attention; prefill-sized projections are hipBLASLt GEMMs through torch. Weights are N(0, 0.02^2) in bf16 (no checkpoint is loaded).
+with the gfx950 kernels: skinny projections for decode / verify rows with the
+layer's RMSNorm (and residual add) computed in their prologue and SwiGLU in the
+gate_up epilogue, q/k-norm + RoPE fused with the KV-cache store, and the paged
+attention; prefill-sized projections are hipBLASLt GEMMs through torch behind
+the standalone RMSNorm kernel. Weights are N(0, 0.02^2) in bf16 (no checkpoint
+is loaded).
 """
 from __future__ import annotations
 
@@ -17,6 +20,7 @@ from torch import nn
 
 from .. import ops as _ops
 from ..layers.attention import Attention
+from ..utils.context import get_context
 
 
 @dataclass(frozen=True)
@@ -102,21 +106,23 @@ class Qwen3Layer(nn.Module):
         self.attn = Attention(g.num_heads, D, D ** -0.5, g.num_kv_heads)
 
     def forward(self, positions, h, residual):
-        """qwen3.py:148-161 with the fused gfx950 elementwise kernels."""
+        """qwen3.py:148-161 in four fused launches plus attention: input RMSNorm (+ the
+        residual add) inside the qkv projection, q/k-norm + RoPE + KV store, o projection,
+        post-attention RMSNorm inside the gate_up projection with SwiGLU, down projection."""
         g = self.g
-        if residual is None:
-            residual = h  # the embedding output; later adds update it in place
-            x = _ops.rmsnorm(h, self.ln1, g.rms_eps)
-        else:
-            x = _ops.rmsnorm(h, self.ln1, g.rms_eps, residual=residual)
-        qkv = _ops.linear(x, self.qkv)
-        q, k = _ops.qk_norm_rope(qkv, g.num_heads, g.num_kv_heads, self.q_norm, self.k_norm,
-                                 self.rope.cos_sin, positions, g.rms_eps)
-        v = qkv[:, self.q_size + self.kv_size:].view(-1, g.num_kv_heads, g.head_dim)
-        o = self.attn(q, k, v)
+        qkv, residual = _ops.linear_rmsnorm(h, self.ln1, g.rms_eps, self.qkv, residual=residual)
+        attn = self.attn
+        ctx = get_context()
+        attn._check_bound(ctx)
+        q = _ops.qk_norm_rope_store(qkv, g.num_heads, g.num_kv_heads, self.q_norm, self.k_norm,
+                                    self.rope.cos_sin, positions, g.rms_eps, attn.k_cache,
+                                    attn.v_cache, ctx.slot_mapping, k_scale=attn.k_scale,
+                                    v_scale=attn.v_scale)
+        o = attn.attend(q)
         h = _ops.linear(o.reshape(o.shape[0], -1), self.o)
-        x = _ops.rmsnorm(h, self.ln2, g.rms_eps, residual=residual)
-        h = _ops.linear(_ops.linear(x, self.gate_up, swiglu=True), self.down)
+        x, residual = _ops.linear_rmsnorm(h, self.ln2, g.rms_eps, self.gate_up, residual=residual,
+                                          swiglu=True)
+        h = _ops.linear(x, self.down)
         return h, residual
 
     def forward_reference(self, positions, h, residual):

@@ -54,17 +54,28 @@ class Attention(nn.Module):
         # for graph capture; 0 means "use the context's max_seqlen_k")
         self.max_model_len = 0
 
-    def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
-        ctx = get_context()
-        k_cache, v_cache = self.k_cache, self.v_cache
-        if not (k_cache.numel() and v_cache.numel()):
+    def _check_bound(self, ctx):
+        if not (self.k_cache.numel() and self.v_cache.numel()):
             raise RuntimeError("Attention needs a bound KV cache (k_cache / v_cache)")
         if ctx.block_tables is None:
             raise RuntimeError("Attention needs context.block_tables (paged KV)")
-        q = q.view(-1, self.num_heads, self.head_dim)
+
+    def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+        ctx = get_context()
+        self._check_bound(ctx)
         k = k.view(-1, self.num_kv_heads, self.head_dim)
         v = v.view(-1, self.num_kv_heads, self.head_dim)
-        store_kvcache(k, v, k_cache, v_cache, ctx.slot_mapping, self.k_scale, self.v_scale)
+        store_kvcache(k, v, self.k_cache, self.v_cache, ctx.slot_mapping, self.k_scale,
+                      self.v_scale)
+        return self.attend(q)
+
+    def attend(self, q: torch.Tensor) -> torch.Tensor:
+        """The attention half of forward: q against the cache, whose K/V for the
+        current tokens a fused producer (ops.qk_norm_rope_store) has already stored."""
+        ctx = get_context()
+        self._check_bound(ctx)
+        k_cache, v_cache = self.k_cache, self.v_cache
+        q = q.view(-1, self.num_heads, self.head_dim)
         if ctx.is_prefill:
             cu_q, cu_k = ctx.cu_seqlens_q, ctx.cu_seqlens_k
             max_q, max_k = ctx.max_seqlen_q, ctx.max_seqlen_k

@@ -464,6 +464,43 @@ def qk_norm_rope(qkv: torch.Tensor, num_q_heads: int, num_kv_heads: int, q_weigh
     return q, k
 
 
+def qk_norm_rope_store(qkv: torch.Tensor, num_q_heads: int, num_kv_heads: int, q_weight,
+                       k_weight, cos_sin: torch.Tensor, positions: torch.Tensor, eps: float,
+                       k_cache: torch.Tensor, v_cache: torch.Tensor, slot_mapping: torch.Tensor,
+                       *, k_scale: float = 1.0, v_scale: float = 1.0) -> torch.Tensor:
+    """qk_norm_rope plus the KV store of the same tokens in one launch: the normalised,
+    rotated k heads and the v heads of qkv [N, (Hq+2Hkv)*128] go to their slot_mapping
+    slots (store_kvcache semantics, slots < 0 skipped); returns q [N, Hq, 128]."""
+    dev = _need_cuda(qkv, q_weight, k_weight, cos_sin, positions, k_cache, v_cache, slot_mapping)
+    N = qkv.shape[0]
+    if qkv.dtype != torch.bfloat16 or qkv.dim() != 2 or qkv.stride(1) != 1:
+        raise ValueError("qkv must be [tokens, (Hq + 2 Hkv) * 128] bf16 with contiguous rows")
+    if qkv.shape[1] != (num_q_heads + 2 * num_kv_heads) * 128:
+        raise ValueError("qkv width does not match the head counts")
+    if slot_mapping.numel() != N or positions.numel() != N:
+        raise ValueError("slot_mapping and positions need one entry per token")
+    if k_cache.shape != v_cache.shape or k_cache.dtype != v_cache.dtype:
+        raise ValueError("k_cache and v_cache must match")
+    if k_cache.stride() != v_cache.stride() or k_cache.stride(3) != 1:
+        raise ValueError("k_cache and v_cache need identical strides with contiguous head_dim")
+    nb, bs, Hc, Dc = k_cache.shape
+    if (Hc, Dc) != (num_kv_heads, 128):
+        raise ValueError("cache geometry mismatch")
+    if cos_sin.dtype != torch.float32 or not cos_sin.is_contiguous() or cos_sin.shape[1] != 128:
+        raise ValueError("cos_sin must be a contiguous f32 [max_position, 128] table")
+    pos = positions if positions.dtype == torch.int64 else positions.to(torch.int64)
+    sm = slot_mapping if slot_mapping.dtype == torch.int32 else slot_mapping.to(torch.int32)
+    pos, sm = pos.contiguous(), sm.contiguous()
+    q = torch.empty((N, num_q_heads, 128), dtype=torch.bfloat16, device=dev)
+    L.check(L.lib().hs_qk_norm_rope_store(
+        qkv.data_ptr(), qkv.stride(0), num_q_heads, num_kv_heads, 128, q_weight.data_ptr(),
+        k_weight.data_ptr(), cos_sin.data_ptr(), pos.data_ptr(), float(eps), q.data_ptr(),
+        k_cache.data_ptr(), v_cache.data_ptr(), _kv_code(k_cache), k_cache.stride(0),
+        k_cache.stride(1), k_cache.stride(2), float(k_scale), float(v_scale), sm.data_ptr(), bs,
+        nb, N, _stream(dev)), "hs_qk_norm_rope_store")
+    return q
+
+
 def silu_mul(gate_up: torch.Tensor) -> torch.Tensor:
     """activation.py:8-16: silu(gate) * up of a fused [N, 2F] projection."""
     dev = _need_cuda(gate_up)
@@ -486,9 +523,7 @@ def linear(x: torch.Tensor, weight: torch.Tensor, *, swiglu: bool = False,
     N = weight.shape[0] // 2 if swiglu else weight.shape[0]
     if weight.shape[1] != K:
         raise ValueError("in_features mismatch")
-    fast = (M <= 8 and K % 512 == 0 and N % 4 == 0 and x.stride(1) == 1 and
-            x.stride(0) % 8 == 0 and weight.is_contiguous() and x.data_ptr() % 16 == 0 and
-            weight.data_ptr() % 16 == 0)
+    fast = _skinny_ok(x, weight, N)
     if not fast:
         y = torch.nn.functional.linear(x, weight)
         return silu_mul(y) if swiglu else y
@@ -501,3 +536,42 @@ def linear(x: torch.Tensor, weight: torch.Tensor, *, swiglu: bool = False,
                               1 if swiglu else 0, out.data_ptr(), out.stride(0), _stream(dev)),
             "hs_linear")
     return out
+
+
+def _skinny_ok(x: torch.Tensor, weight: torch.Tensor, N: int) -> bool:
+    M, K = x.shape
+    return (M <= 8 and K % 512 == 0 and N % 4 == 0 and x.stride(1) == 1 and
+            x.stride(0) % 8 == 0 and weight.is_contiguous() and x.data_ptr() % 16 == 0 and
+            weight.data_ptr() % 16 == 0)
+
+
+def linear_rmsnorm(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, weight: torch.Tensor,
+                   *, residual: torch.Tensor | None = None, swiglu: bool = False):
+    """linear(RMSNorm(x (+ residual)) * norm_weight, weight) for decode / verify rows, the
+    norm computed inside the projection (hs_linear_rmsnorm). Returns (y, new_residual) with
+    new_residual = bf16(x + residual) (layernorm.py:27-36), or x itself without a residual.
+    Rows > 8 run hs_rmsnorm and a library GEMM; the residual is then updated in place."""
+    if x.dim() != 2 or x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise ValueError("linear_rmsnorm expects a 2-D bf16 input and a bf16 weight")
+    M, K = x.shape
+    N = weight.shape[0] // 2 if swiglu else weight.shape[0]
+    if weight.shape[1] != K or norm_weight.numel() != K:
+        raise ValueError("in_features mismatch")
+    fast = _skinny_ok(x, weight, N) and norm_weight.is_contiguous() and \
+        norm_weight.data_ptr() % 16 == 0
+    if residual is not None:
+        fast = fast and residual.shape == x.shape and residual.stride(1) == 1 and \
+            residual.stride(0) % 8 == 0 and residual.data_ptr() % 16 == 0
+    if not fast:
+        xn = rmsnorm(x, norm_weight, eps, residual=residual)
+        return linear(xn, weight, swiglu=swiglu), (x if residual is None else residual)
+    dev = _need_cuda(x, weight, norm_weight, residual)
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    res_out = None if residual is None else torch.empty((M, K), dtype=torch.bfloat16, device=dev)
+    L.check(L.lib().hs_linear_rmsnorm(
+        x.data_ptr(), x.stride(0), None if residual is None else residual.data_ptr(),
+        0 if residual is None else residual.stride(0),
+        None if res_out is None else res_out.data_ptr(), 0 if res_out is None else K,
+        norm_weight.data_ptr(), float(eps), weight.data_ptr(), M, K, N, 1 if swiglu else 0,
+        out.data_ptr(), N, _stream(dev)), "hs_linear_rmsnorm")
+    return out, (x if residual is None else res_out)

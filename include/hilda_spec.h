@@ -267,6 +267,20 @@ int hs_zero_kv_slots(void* cache, int64_t plane_bytes, int num_planes, int64_t s
 int hs_linear(const void* x, int64_t x_stride, const void* weight, int rows, int in_features,
               int out_features, int epilogue, void* out, int64_t out_stride, void* stream);
 
+/* hs_linear whose input is the decoder's RMSNorm (the input_layernorm /     */
+/* post_attention_layernorm in front of qkv_proj / gate_up_proj,             */
+/* qwen3.py:148-161, layernorm.py:18-36): row r of the projection input is    */
+/* bf16(bf16(h * rsqrt(mean(h^2) + eps)) * norm_weight) with the fp32 sum      */
+/* h = x[r] (+ residual_in[r]). residual_in may be NULL (plain RMSNorm). When  */
+/* residual_out != NULL it receives bf16(h) (the add_rms_norm residual); it   */
+/* must not overlap x or residual_in (HS_ERR_INVALID). Same shape limits as   */
+/* hs_linear; residual strides multiples of 8 elements.                       */
+int hs_linear_rmsnorm(const void* x, int64_t x_stride, const void* residual_in,
+                      int64_t residual_in_stride, void* residual_out, int64_t residual_out_stride,
+                      const void* norm_weight, float eps, const void* weight, int rows,
+                      int in_features, int out_features, int epilogue, void* out,
+                      int64_t out_stride, void* stream);
+
 /* out = RMSNorm(x (+ residual)) * weight; with residual != NULL the residual  */
 /* row is replaced by bf16(x + residual) (strides in elements).              */
 int hs_rmsnorm(const void* x, int64_t x_stride, void* residual, int64_t residual_stride,
@@ -281,6 +295,21 @@ int hs_qk_norm_rope(const void* qkv, int64_t token_stride, int num_q_heads, int 
                     int head_dim, const void* q_weight, const void* k_weight,
                     const float* cos_sin, const int64_t* positions, float eps, void* q_out,
                     void* k_out, int num_tokens, void* stream);
+
+/* hs_qk_norm_rope fused with the KV store of the same tokens (the           */
+/* store_kvcache call at the top of Attention.forward, attention.py:59-90 and */
+/* :145): q heads go to q_out [tokens, Hq, 128]; the normalised, rotated k    */
+/* heads and the v heads (columns (Hq + Hkv) * 128 .. of qkv) are written to   */
+/* their slot_mapping slots of k_cache / v_cache with the layout, dtype and    */
+/* scales of hs_store_kvcache (slots < 0 skipped).                            */
+int hs_qk_norm_rope_store(const void* qkv, int64_t token_stride, int num_q_heads,
+                          int num_kv_heads, int head_dim, const void* q_weight,
+                          const void* k_weight, const float* cos_sin, const int64_t* positions,
+                          float eps, void* q_out, void* k_cache, void* v_cache, int kv_dtype,
+                          int64_t cache_stride_block, int64_t cache_stride_tok,
+                          int64_t cache_stride_head, float k_scale, float v_scale,
+                          const int32_t* slot_mapping, int block_size, int num_blocks,
+                          int num_tokens, void* stream);
 
 /* out[r, :ffn] = silu(gate_up[r, :ffn]) * gate_up[r, ffn:2*ffn]. */
 int hs_silu_mul(const void* gate_up, int64_t gate_up_stride, int ffn, void* out,

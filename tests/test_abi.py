@@ -90,3 +90,43 @@ def test_no_cpu_fallback_symbol(hv, fn):
     lib = hv._lib.lib()
     assert not hasattr(lib, "or_spec_accept")
     assert hasattr(lib, fn)
+
+
+def test_linear_rmsnorm_rejects_overlapping_residual_on_host(hv):
+    """Workgroup 0 writes residual_out while the other workgroups still read x and
+    residual_in, so any overlap is refused before a launch."""
+    lib = hv._lib.lib()
+    buf = ctypes.create_string_buffer(1 << 16)
+    base = (ctypes.cast(buf, ctypes.c_void_p).value + 255) // 256 * 256
+    x, res, w, nw, out = base, base + 8192, base + 16384, base + 24576, base + 32768
+    K, N = 512, 4
+
+    def call(r_out, r_in=res, rows=2):
+        return lib.hs_linear_rmsnorm(x, K, r_in, K, r_out, K, nw, 1e-6, w, rows, K, N, 0, out, N,
+                                     None)
+    assert call(res) == -1          # residual_out == residual_in
+    assert call(x) == -1            # residual_out == x
+    assert call(res + 2 * K) == -1  # overlaps the second residual row
+    assert call(x, r_in=None) == -1
+    # shape limits: 9 rows, K not a multiple of 512
+    assert lib.hs_linear_rmsnorm(x, K, None, 0, None, 0, nw, 1e-6, w, 9, K, N, 0, out, N,
+                                 None) == -4
+    assert lib.hs_linear_rmsnorm(x, K, None, 0, None, 0, nw, 1e-6, w, 1, 500, N, 0, out, N,
+                                 None) == -4
+    assert lib.hs_linear_rmsnorm(x, K, None, 0, None, 0, None, 1e-6, w, 1, K, N, 0, out, N,
+                                 None) == -1
+
+
+def test_qk_norm_rope_store_rejects_bad_arguments_on_host(hv):
+    lib = hv._lib.lib()
+    buf = ctypes.create_string_buffer(256)
+    p = (ctypes.cast(buf, ctypes.c_void_p).value + 15) // 16 * 16
+
+    def call(hd=128, dtype=1, ks=1.0, ts=(4 + 2 * 2) * 128, bs=16):
+        return lib.hs_qk_norm_rope_store(p, ts, 4, 2, hd, p, p, p, p, 1e-6, p, p, p, dtype, 0, 0, 0,
+                                         ks, 1.0, p, bs, 8, 3, None)
+    assert call(hd=64) == -4
+    assert call(dtype=7) == -1
+    assert call(dtype=2, ks=0.0) == -1
+    assert call(ts=100) == -1
+    assert call(bs=0) == -1

@@ -1,0 +1,127 @@
+"""Fused decoder-layer kernels vs the unfused kernels they replace.
+
+* hs_linear_rmsnorm (RMSNorm / add + RMSNorm inside the projection) against
+  hs_rmsnorm followed by hs_linear and against an fp32 PyTorch restatement of
+  layernorm.py:18-36 + F.linear. The new residual bf16(x + residual) is one
+  fp32 add and one rounding on both sides: bit-exact. The outputs may differ
+  where the fused kernel's sum of squares (summed in another order) moves a
+  normalised value across a bf16 rounding boundary: |err| <= 1e-2 * scale, the
+  bound of the plain projection test.
+* hs_qk_norm_rope_store against hs_qk_norm_rope + hs_store_kvcache: the same
+  per-lane arithmetic, so q and both caches (bf16 and FP8) are bit-exact,
+  including tokens whose slot is -1 (nothing stored).
+"""
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _norm_ref(x, res, w, eps):
+    """layernorm.py:18-36 in fp32 with the reference's two roundings."""
+    xf = x.float() if res is None else x.float() + res.float()
+    inv = torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    return ((xf * inv).to(torch.bfloat16).float() * w.float()).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("M", [1, 2, 4, 5, 8])
+@pytest.mark.parametrize("K,N,swiglu", [(4096, 6144, False), (1024, 4096, False),
+                                        (4096, 12288, True), (1024, 3072, True),
+                                        (4096, 151936, False)])
+@pytest.mark.parametrize("with_residual", [False, True])
+def test_linear_rmsnorm_matches_unfused(hv, cuda, M, K, N, swiglu, with_residual):
+    ops = hv.ops
+    g = torch.Generator(device=cuda).manual_seed(M * 7 + K + N + with_residual)
+    x = (torch.randn((M, K), generator=g, device=cuda) * 3).to(torch.bfloat16)
+    res = (torch.randn((M, K), generator=g, device=cuda) * 5).to(torch.bfloat16) \
+        if with_residual else None
+    nw = (1 + 0.1 * torch.randn(K, generator=g, device=cuda)).to(torch.bfloat16)
+    rows = 2 * N if swiglu else N
+    w = (torch.randn((rows, K), generator=g, device=cuda) * 0.02).to(torch.bfloat16)
+    eps = 1e-6
+    print(f"linear_rmsnorm M={M} K={K} N={N} swiglu={swiglu} res={with_residual}", flush=True)
+    res_before = None if res is None else res.clone()
+    y, new_res = ops.linear_rmsnorm(x, nw, eps, w, residual=res, swiglu=swiglu)
+    # unfused chain: rmsnorm kernel (residual updated in place) + skinny projection
+    res_u = None if res is None else res.clone()
+    xn = ops.rmsnorm(x, nw, eps, residual=res_u)
+    y_u = ops.linear(xn, w, swiglu=swiglu)
+    torch.cuda.synchronize()
+    if res is None:
+        assert new_res is x
+    else:
+        assert torch.equal(res, res_before), "the input residual must not be modified"
+        assert torch.equal(new_res, res_u)
+        assert torch.equal(new_res, (x.float() + res_before.float()).to(torch.bfloat16))
+    # fp32 reference of the whole chain
+    xr = _norm_ref(x, res_before, nw, eps).float()
+    ref = xr @ w.float().t()
+    if swiglu:
+        ref = torch.nn.functional.silu(ref[:, :N]) * ref[:, N:]
+    scale = ref.abs().max().item()
+    assert (y.float() - ref).abs().max().item() <= 1e-2 * scale
+    assert (y.float() - y_u.float()).abs().max().item() <= 1e-2 * scale
+
+
+def test_linear_rmsnorm_fallback_rows(hv, cuda):
+    """More than 8 rows: hs_rmsnorm + library GEMM, residual updated in place."""
+    ops = hv.ops
+    g = torch.Generator(device=cuda).manual_seed(5)
+    x = torch.randn((16, 1024), generator=g, device=cuda).to(torch.bfloat16)
+    res = torch.randn((16, 1024), generator=g, device=cuda).to(torch.bfloat16)
+    nw = torch.ones(1024, device=cuda, dtype=torch.bfloat16)
+    w = (torch.randn((512, 1024), generator=g, device=cuda) * 0.02).to(torch.bfloat16)
+    expect_res = (x.float() + res.float()).to(torch.bfloat16)
+    xr = _norm_ref(x, res, nw, 1e-6).float()
+    y, new_res = ops.linear_rmsnorm(x, nw, 1e-6, w, residual=res)
+    torch.cuda.synchronize()
+    assert torch.equal(new_res, expect_res)
+    ref = xr @ w.float().t()
+    assert (y.float() - ref).abs().max().item() <= 1e-2 * ref.abs().max().item()
+
+
+def _rope_table(max_pos, device):
+    inv = 1.0 / (1e6 ** (torch.arange(0, 128, 2, dtype=torch.float32, device=device) / 128))
+    f = torch.outer(torch.arange(max_pos, dtype=torch.float32, device=device), inv)
+    return torch.cat([f.cos(), f.sin()], -1).contiguous()
+
+
+@pytest.mark.parametrize("kv", ["bf16", "fp8"])
+@pytest.mark.parametrize("N,Hq,Hkv", [(4, 32, 8), (1, 16, 8), (37, 8, 4)])
+def test_qk_norm_rope_store_matches_separate(hv, cuda, kv, N, Hq, Hkv):
+    ops = hv.ops
+    g = torch.Generator(device=cuda).manual_seed(N * 100 + Hq + Hkv)
+    qkv = (torch.randn((N, (Hq + 2 * Hkv) * 128), generator=g, device=cuda) * 2).to(
+        torch.bfloat16)
+    qw = (1 + 0.1 * torch.randn(128, generator=g, device=cuda)).to(torch.bfloat16)
+    kw = (1 + 0.1 * torch.randn(128, generator=g, device=cuda)).to(torch.bfloat16)
+    cs = _rope_table(4096, cuda)
+    pos = torch.randint(0, 4096, (N,), generator=g, device=cuda)
+    nb, bs = 6, 16
+    slots = torch.randperm(nb * bs, generator=g, device=cuda)[:N].to(torch.int32)
+    slots[::3] = -1  # tokens without a slot store nothing
+    dt = torch.bfloat16 if kv == "bf16" else torch.float8_e4m3fn
+    ksc, vsc = (1.0, 1.0) if kv == "bf16" else (0.05, 0.03)
+    print(f"qk_norm_rope_store kv={kv} N={N} Hq={Hq} Hkv={Hkv}", flush=True)
+
+    def caches():
+        fill = torch.randint(0, 255, (2, nb, bs, Hkv, 128), generator=g, device=cuda,
+                             dtype=torch.uint8)
+        if dt == torch.bfloat16:
+            fill = fill.to(torch.int16).view(torch.bfloat16)
+            return fill[0].clone(), fill[1].clone()
+        fill = fill & 0x77  # finite e4m3 codes
+        return fill[0].clone().view(dt), fill[1].clone().view(dt)
+
+    kc1, vc1 = caches()
+    kc2, vc2 = kc1.clone(), vc1.clone()
+    q1, k1 = ops.qk_norm_rope(qkv, Hq, Hkv, qw, kw, cs, pos, 1e-6)
+    v = qkv[:, (Hq + Hkv) * 128:].reshape(N, Hkv, 128)
+    ops.store_kvcache(k1, v, kc1, vc1, slots, k_scale=ksc, v_scale=vsc)
+    q2 = ops.qk_norm_rope_store(qkv, Hq, Hkv, qw, kw, cs, pos, 1e-6, kc2, vc2, slots,
+                                k_scale=ksc, v_scale=vsc)
+    torch.cuda.synchronize()
+    assert torch.equal(q1.view(torch.int16), q2.view(torch.int16))
+    u8 = lambda t: t.view(torch.uint8)  # noqa: E731
+    assert torch.equal(u8(kc1), u8(kc2))
+    assert torch.equal(u8(vc1), u8(vc2))

@@ -112,8 +112,9 @@ def test_graph_replay_matches_eager(cuda):
 
 
 def test_fused_layer_matches_eager(cuda):
-    """Fused RMSNorm / qk-norm+RoPE / SiLU-mul kernels vs the eager restatement of
-    qwen3.py:72-185 (same attention kernel on both sides)."""
+    """Fused kernels (RMSNorm inside the projections, qk-norm + RoPE + KV store,
+    SwiGLU epilogue) vs the eager restatement of qwen3.py:72-185 (same attention
+    kernel on both sides), at prefill size and at a 4-row verify pass."""
     q3, sr = _mods()
     g = _small(q3, layers=3, hidden=1024, heads=8, kv=4)
     target = q3.Qwen3Host(g, device=cuda, seed=31)
@@ -138,6 +139,25 @@ def test_fused_layer_matches_eager(cuda):
     err = (got - ref).abs()
     assert err.max() <= 0.05 * ref.abs().max() + 0.02, float(err.max())
     assert torch.nn.functional.cosine_similarity(got.flatten(), ref.flatten(), dim=0) > 0.999
+    # a 4-row verify pass (positions 50..53) runs the skinny projections with the
+    # RMSNorm prologue; the reference pass stores its own K/V first, the fused pass
+    # then overwrites those slots with its own
+    n0 = len(prompt)
+    ids4 = torch.tensor([5, 6, 7, 8], device=cuda)
+    pos4 = torch.arange(n0, n0 + 4, device=cuda)
+    slots4 = torch.tensor([int(runner.state.block_tables[0, i // 32]) * 32 + i % 32
+                           for i in range(n0, n0 + 4)], dtype=torch.int32, device=cuda)
+    cq = torch.tensor([0, 4], dtype=torch.int32, device=cuda)
+    ck = torch.tensor([0, n0 + 4], dtype=torch.int32, device=cuda)
+    with torch.inference_mode():
+        ctx.set_context(True, cq, ck, 4, n0 + 4, slots4, None, runner.state.block_tables)
+        ref4 = target(ids4, pos4, reference=True).float()
+        got4 = target(ids4, pos4).float()
+        ctx.reset_context()
+    torch.cuda.synchronize()
+    err4 = (got4 - ref4).abs()
+    assert err4.max() <= 0.05 * ref4.abs().max() + 0.02, float(err4.max())
+    assert torch.nn.functional.cosine_similarity(got4.flatten(), ref4.flatten(), dim=0) > 0.999
 
 
 @pytest.mark.parametrize("draft_kind", ["self", "random"])
