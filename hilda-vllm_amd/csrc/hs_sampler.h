@@ -95,7 +95,19 @@ struct AcceptArgs {
   int32_t* len_out;
 };
 
+// Launch epoch of the single-launch acceptance (spec_accept_small.hip), at the
+// start of the workspace: `start` must be zero before the first call and every
+// completed call leaves its count half zero; `err` is set if a wait for
+// another workgroup's data ever ran out (the outputs of that call are invalid).
+struct SmallSync {
+  uint64_t start;  // epoch << 32 | workgroups of the current launch that started
+  uint32_t err;
+  uint32_t pad[61];
+};
+
 struct Work {
+  SmallSync* sync;
+  uint64_t* tags;  // epoch-tagged partials of the single-launch acceptance
   ChunkStat* part;
   RowDesc* desc;
   SeqState* st;
@@ -121,10 +133,17 @@ struct SampleOut {
 };
 
 struct Layout {
-  size_t part, desc, st, spart, filt, cand, h1m, h1e, h1c, h2m, h2e, h2c, total;
+  size_t sync, tags, part, desc, st, spart, filt, cand, h1m, h1e, h1c, h2m, h2e, h2c, total;
 };
 
 template <typename T>
 int launch_filter(const Problem& P, const Work& W, float* row_stats, hipStream_t stream);
+
+// single-launch acceptance (reference mode) for grids that fit one workgroup
+// per CU (spec_accept_small.hip)
+int small_accept_ok(const Problem& P, const AcceptArgs& A, int mode, int esz);
+template <typename T>
+int launch_accept_small(const Problem& P, const AcceptArgs& A, const Work& W, const SampleOut& O,
+                        hipStream_t stream);
 
 }  // namespace hs

@@ -17,8 +17,10 @@
 // weight vectors (non-temporal loads: each weight is read once per call),
 // keeps kR x M fp32 partial sums, reduces them across the wave with
 // recursive-halving shuffles and across the P waves through LDS (two buffers,
-// one barrier per tile). The next tile's weight loads are issued before the
-// current tile's reduction, so HBM stays busy while the sums are combined.
+// one barrier per tile). Weight tiles are double-buffered in registers: a
+// workgroup issues its first two tiles before the activation prologue, and
+// refills a buffer with the tile two ahead as soon as its products are done,
+// so two tiles per wave are in flight while the sums are combined.
 // Epilogue 1 (SwiGLU, activation.py:8-16): the tile holds the gate rows n and
 // the up rows F + n of a [2F, K] weight and writes
 // bf16(bf16(silu(bf16(g))) * bf16(u)), the rounding of the unfused
@@ -177,31 +179,46 @@ __device__ __forceinline__ void load_tile(uint4 (&wv)[S][RR], const SkinnyArgs& 
   }
 }
 
-// Activation slice of the wave: xv[s][m] = 8 bf16 of row m at k0 + s * kStep,
-// normalised (NORM) with the workgroup-wide sum of squares.
+// Activation slice of the wave, raw: xr[s][m] = 8 bf16 of row m at k0 + s * kStep
+// (and the residual rows rr with RES, the norm weights nr with NORM). Issued
+// before the weight loads and fenced from them, so the prologue that consumes
+// them waits for these loads only while the weights are still in flight.
 template <int M, int S, bool NORM, bool RES>
-__device__ __forceinline__ void load_activations(uint4 (&xv)[S][M], const SkinnyArgs& a, int k0,
-                                                 int lane, int wid, int nw) {
+__device__ __forceinline__ void issue_activations(uint4 (&xr)[S][M], uint4 (&rr)[S][M],
+                                                  uint4 (&nr)[S], const SkinnyArgs& a, int k0) {
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const int64_t k = k0 + s * kStep;
+      xr[s][m] = *reinterpret_cast<const uint4*>(a.X + (int64_t)m * a.xs + k);
+      if (RES) rr[s][m] = *reinterpret_cast<const uint4*>(a.Rin + (int64_t)m * a.rs_in + k);
+    }
+    if (NORM) nr[s] = *reinterpret_cast<const uint4*>(a.NW + k0 + s * kStep);
+  }
+  // keeps the compiler from interleaving these loads with the weight loads
+  // issued next (loads complete in order, so a wait for the last activation
+  // load would otherwise also wait for the weights issued before it)
+  asm volatile("" ::: "memory");
+}
+
+// Projection input of the wave from the raw slices: the slices themselves, or
+// (NORM) their RMSNorm with the workgroup-wide sum of squares.
+template <int M, int S, bool NORM, bool RES>
+__device__ __forceinline__ void finish_activations(uint4 (&xv)[S][M], const uint4 (&xr)[S][M],
+                                                   const uint4 (&rr)[S][M], const uint4 (&nr)[S],
+                                                   const SkinnyArgs& a,
+                                                   int k0, int lane, int wid, int nw) {
   if constexpr (!NORM) {
 #pragma unroll
     for (int s = 0; s < S; ++s)
 #pragma unroll
-      for (int m = 0; m < M; ++m)
-        xv[s][m] = *reinterpret_cast<const uint4*>(a.X + (int64_t)m * a.xs + k0 + s * kStep);
+      for (int m = 0; m < M; ++m) xv[s][m] = xr[s][m];
   } else {
     __shared__ float s_ss[kMaxWaves][M];
-    uint4 xr[S][M], rr[S][M];
     float ss[M];
 #pragma unroll
     for (int m = 0; m < M; ++m) ss[m] = 0.0f;
-#pragma unroll
-    for (int s = 0; s < S; ++s)
-#pragma unroll
-      for (int m = 0; m < M; ++m) {
-        const int64_t k = k0 + s * kStep;
-        xr[s][m] = *reinterpret_cast<const uint4*>(a.X + (int64_t)m * a.xs + k);
-        if (RES) rr[s][m] = *reinterpret_cast<const uint4*>(a.Rin + (int64_t)m * a.rs_in + k);
-      }
 #pragma unroll
     for (int s = 0; s < S; ++s)
 #pragma unroll
@@ -227,7 +244,7 @@ __device__ __forceinline__ void load_activations(uint4 (&xv)[S][M], const Skinny
 #pragma unroll
     for (int s = 0; s < S; ++s) {
       float nwf[8];
-      unpack8(*reinterpret_cast<const uint4*>(a.NW + k0 + s * kStep), nwf);
+      unpack8(nr[s], nwf);
 #pragma unroll
       for (int m = 0; m < M; ++m) {
         float t = 0.0f;
@@ -250,6 +267,56 @@ __device__ __forceinline__ void load_activations(uint4 (&xv)[S][M], const Skinny
   }
 }
 
+// One tile: products of the wave's weight slice wv with the activations, the
+// weight loads of tile `prefetch` issued into wv as soon as it is consumed
+// (PF 1: always, PF 2: if that tile exists, PF 0: none), then the wave /
+// workgroup reduction and the tile's outputs.
+template <int M, int S, int EPI, int PF>
+__device__ __forceinline__ void tile_step(uint4 (&wv)[S][EPI ? 2 * kR : kR],
+                                          const uint4 (&xv)[S][M], const SkinnyArgs& a, int tile,
+                                          int prefetch, int k0, int lane, int wid, int nw,
+                                          float (*s_part)[EPI ? 2 * kR * M : kR * M]) {
+  constexpr int RR = EPI ? 2 * kR : kR;
+  float acc[RR * M];
+#pragma unroll
+  for (int i = 0; i < RR * M; ++i) acc[i] = 0.0f;
+#pragma unroll
+  for (int s = 0; s < S; ++s)
+#pragma unroll
+    for (int r = 0; r < RR; ++r)
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        float c = acc[r * M + m];
+        c = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(wv[s][r].x), as_bf2(xv[s][m].x), c, false);
+        c = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(wv[s][r].y), as_bf2(xv[s][m].y), c, false);
+        c = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(wv[s][r].z), as_bf2(xv[s][m].z), c, false);
+        c = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(wv[s][r].w), as_bf2(xv[s][m].w), c, false);
+        acc[r * M + m] = c;
+      }
+  if (PF == 1 || (PF == 2 && prefetch < a.ntiles)) load_tile<S, RR>(wv, a, prefetch, k0);
+  wave_sums_to<RR * M>(acc, lane, s_part[wid]);
+  // one barrier per tile: the LDS buffer written here is read back after it,
+  // and written again only two tiles later, after the next tile's barrier
+  __syncthreads();
+  const int t = threadIdx.x;
+  if (t < kR * M) {
+    const int r = t / M, m = t % M;
+    float y = 0.0f;
+    for (int w = 0; w < nw; ++w) y += s_part[w][r * M + m];
+    uint16_t out;
+    if (EPI) {
+      float u = 0.0f;
+      for (int w = 0; w < nw; ++w) u += s_part[w][(kR + r) * M + m];
+      const float g = bfv(to_bf16(y));
+      const uint16_t sl = to_bf16(g / (1.0f + __expf(-g)));
+      out = to_bf16(bfv(sl) * bfv(to_bf16(u)));
+    } else {
+      out = to_bf16(y);
+    }
+    a.Y[(int64_t)m * a.ys + tile * kR + r] = out;
+  }
+}
+
 template <int M, int S, int EPI, bool NORM, bool RES>
 __global__ __launch_bounds__(kMaxWaves * 64) void k_skinny(SkinnyArgs a) {
   constexpr int RR = EPI ? 2 * kR : kR;  // weight rows of a tile
@@ -259,54 +326,56 @@ __global__ __launch_bounds__(kMaxWaves * 64) void k_skinny(SkinnyArgs a) {
   const int k0 = wid * S * kStep + 8 * lane;
   int tile = blockIdx.x;
   if (tile >= a.ntiles) return;  // the host launches at most ntiles workgroups
+  const int step = gridDim.x;
 
-  uint4 wv[S][RR];
-  load_tile<S, RR>(wv, a, tile, k0);
+  uint4 xr[S][M], rr[S][M], nr[S];
+  issue_activations<M, S, NORM, RES>(xr, rr, nr, a, k0);
+  uint4 wa[S][RR];
+  load_tile<S, RR>(wa, a, tile, k0);
   uint4 xv[S][M];
-  load_activations<M, S, NORM, RES>(xv, a, k0, lane, wid, nw);
-
-  for (int buf = 0;; buf ^= 1) {
-    float acc[RR * M];
-#pragma unroll
-    for (int i = 0; i < RR * M; ++i) acc[i] = 0.0f;
-#pragma unroll
-    for (int s = 0; s < S; ++s)
-#pragma unroll
-      for (int r = 0; r < RR; ++r)
-#pragma unroll
-        for (int m = 0; m < M; ++m) {
-          float c = acc[r * M + m];
-          c = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(wv[s][r].x), as_bf2(xv[s][m].x), c, false);
-          c = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(wv[s][r].y), as_bf2(xv[s][m].y), c, false);
-          c = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(wv[s][r].z), as_bf2(xv[s][m].z), c, false);
-          c = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(wv[s][r].w), as_bf2(xv[s][m].w), c, false);
-          acc[r * M + m] = c;
-        }
-    const int next = tile + gridDim.x;
-    if (next < a.ntiles) load_tile<S, RR>(wv, a, next, k0);  // in flight during the reduction
-    wave_sums_to<RR * M>(acc, lane, s_part[buf][wid]);
-    // one barrier per tile: the buffer written here is read back after it, and
-    // written again only two tiles later, after the next tile's barrier
-    __syncthreads();
-    const int t = threadIdx.x;
-    if (t < kR * M) {
-      const int r = t / M, m = t % M;
-      float y = 0.0f;
-      for (int w = 0; w < nw; ++w) y += s_part[buf][w][r * M + m];
-      uint16_t out;
-      if (EPI) {
-        float u = 0.0f;
-        for (int w = 0; w < nw; ++w) u += s_part[buf][w][(kR + r) * M + m];
-        const float g = bfv(to_bf16(y));
-        const uint16_t sl = to_bf16(g / (1.0f + __expf(-g)));
-        out = to_bf16(bfv(sl) * bfv(to_bf16(u)));
-      } else {
-        out = to_bf16(y);
-      }
-      a.Y[(int64_t)m * a.ys + tile * kR + r] = out;
+  // two register buffers of weights unless a tile is large (SwiGLU tiles over
+  // more than one K step), where the second buffer would spill
+  constexpr bool kDouble = RR * S <= 12;
+  if constexpr (!kDouble) {
+    // one buffer: the next tile's loads overlap the current tile's reduction
+    finish_activations<M, S, NORM, RES>(xv, xr, rr, nr, a, k0, lane, wid, nw);
+    for (int buf = 0;; buf ^= 1) {
+      tile_step<M, S, EPI, 2>(wa, xv, a, tile, tile + step, k0, lane, wid, nw, s_part[buf]);
+      tile += step;
+      if (tile >= a.ntiles) break;
     }
-    tile = next;
-    if (tile >= a.ntiles) break;
+  } else {
+    // Two weight tiles in flight from the start: the activations first (the
+    // prologue waits for them only), then the workgroup's first two tiles.
+    // Tiles alternate between the buffers wa / wb, and a buffer is refilled
+    // with the tile two ahead as soon as its products are done. Every load up
+    // to the last two tiles is unconditional, so each wait before a tile's
+    // products covers that tile's loads only (after a conditional load the
+    // compiler has to wait for every outstanding load). A workgroup with a
+    // single tile (the host sizes the grid to avoid it on large matrices)
+    // loads that tile twice.
+    const int T = (a.ntiles - tile + step - 1) / step;  // tiles of this workgroup
+    uint4 wb[S][RR];
+    load_tile<S, RR>(wb, a, T > 1 ? tile + step : tile, k0);
+    finish_activations<M, S, NORM, RES>(xv, xr, rr, nr, a, k0, lane, wid, nw);
+    if (T == 1) {
+      tile_step<M, S, EPI, 0>(wa, xv, a, tile, 0, k0, lane, wid, nw, s_part[0]);
+      return;
+    }
+    int j = 0;
+    for (; j + 3 < T; j += 2, tile += 2 * step) {
+      tile_step<M, S, EPI, 1>(wa, xv, a, tile, tile + 2 * step, k0, lane, wid, nw, s_part[0]);
+      tile_step<M, S, EPI, 1>(wb, xv, a, tile + step, tile + 3 * step, k0, lane, wid, nw,
+                              s_part[1]);
+    }
+    if (T - j == 3) {
+      tile_step<M, S, EPI, 1>(wa, xv, a, tile, tile + 2 * step, k0, lane, wid, nw, s_part[0]);
+      tile_step<M, S, EPI, 0>(wb, xv, a, tile + step, 0, k0, lane, wid, nw, s_part[1]);
+      tile_step<M, S, EPI, 0>(wa, xv, a, tile + 2 * step, 0, k0, lane, wid, nw, s_part[0]);
+    } else {
+      tile_step<M, S, EPI, 0>(wa, xv, a, tile, 0, k0, lane, wid, nw, s_part[0]);
+      tile_step<M, S, EPI, 0>(wb, xv, a, tile + step, 0, k0, lane, wid, nw, s_part[1]);
+    }
   }
 }
 
@@ -336,7 +405,12 @@ void launch_skinny(const SkinnyArgs& a, int waves, hipStream_t stream) {
       n = 1;
     occ[waves] = n;
   }
-  int64_t grid = (int64_t)num_cus() * occ[waves];
+  const int64_t cus = num_cus();
+  int64_t grid = cus * occ[waves];
+  // double-buffered kernels: at least two tiles per workgroup once the matrix
+  // has enough tiles to keep every CU busy with half as many workgroups
+  constexpr bool kDouble = (EPI ? 2 * kR : kR) * S <= 12;
+  if (kDouble && a.ntiles >= 2 * cus && grid > a.ntiles / 2) grid = a.ntiles / 2;
   if (grid > a.ntiles) grid = a.ntiles;
   hipLaunchKernelGGL((k_skinny<M, S, EPI, NORM, RES>), dim3((unsigned)grid), dim3(64 * waves), 0,
                      stream, a);

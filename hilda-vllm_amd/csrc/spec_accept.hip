@@ -21,6 +21,8 @@
 //   4. k_sample_final  one workgroup per sequence: locates the chunk holding
 //      the inverse-CDF point and rescans that one chunk to find the token.
 // Greedy mode: k_chunk_argmax then k_greedy_final.
+// Reference-mode calls small enough for one workgroup per CU run instead as
+// one launch, k_accept_small (spec_accept_small.hip), with the same arithmetic.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <string.h>
@@ -446,6 +448,9 @@ static inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; 
 Layout make_layout(int units, int rows, int nchunk) {
   Layout L;
   size_t off = 0;
+  L.sync = off; off = align_up(off + sizeof(SmallSync), 256);
+  // single-launch acceptance: 3 tagged words per (row, chunk) and 4 per (unit, chunk)
+  L.tags = off; off = align_up(off + ((size_t)rows * 3 + (size_t)units * 4) * nchunk * 8, 256);
   L.part = off; off = align_up(off + (size_t)rows * nchunk * sizeof(ChunkStat), 256);
   L.desc = off; off = align_up(off + (size_t)rows * sizeof(RowDesc), 256);
   L.st = off; off = align_up(off + (size_t)units * sizeof(SeqState), 256);
@@ -465,6 +470,8 @@ Layout make_layout(int units, int rows, int nchunk) {
 Work bind_work(void* ws, const Layout& L) {
   char* b = static_cast<char*>(ws);
   Work W;
+  W.sync = reinterpret_cast<SmallSync*>(b + L.sync);
+  W.tags = reinterpret_cast<uint64_t*>(b + L.tags);
   W.part = reinterpret_cast<ChunkStat*>(b + L.part);
   W.desc = reinterpret_cast<RowDesc*>(b + L.desc);
   W.st = reinterpret_cast<SeqState*>(b + L.st);
@@ -609,6 +616,10 @@ int hs_spec_accept(const void* target_logits, int logits_dtype, int64_t logits_r
   O.row_stats = row_stats;
   Work W = bind_work(workspace, L);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (small_accept_ok(P, A, mode, logits_dtype == HS_F32 ? 4 : 2)) {
+    if (logits_dtype == HS_F32) return launch_accept_small<float>(P, A, W, O, s);
+    return launch_accept_small<uint16_t>(P, A, W, O, s);
+  }
   if (logits_dtype == HS_F32) return run_sampler_chain<float>(P, A, W, mode, O, s);
   return run_sampler_chain<uint16_t>(P, A, W, mode, O, s);
 }

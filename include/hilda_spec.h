@@ -69,6 +69,13 @@ int hs_version(void);
 /*                 int64 (-1 after the last emitted token), out_len [batch]. */
 /* row_stats     : optional [batch*(gamma+1), 2] f32: per target row the     */
 /*                 softmax max and normaliser over the kept set.            */
+/* workspace     : hs_spec_accept_workspace_size bytes, zero-filled before   */
+/*                 its first use; calls leave it ready for the next one, of  */
+/*                 any shape. Calls that share a workspace must not overlap. */
+/*                 Small reference-mode batches (batch x ceil(vocab/2048)    */
+/*                 workgroups fit one per CU, gamma <= 7, aligned rows, vocab */
+/*                 a multiple of 8) run as a single launch; if one of its    */
+/*                 bounded waits ever ran out, num_accepted is -1.           */
 /* ------------------------------------------------------------------------ */
 size_t hs_spec_accept_workspace_size(int batch, int gamma, int vocab);
 

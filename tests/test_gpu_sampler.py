@@ -99,6 +99,31 @@ def test_all_reject_positions_with_small_vocab(hv, orc, cuda):
     assert len(set(ref["num_accepted"].tolist())) >= 3
 
 
+@pytest.mark.parametrize("B,g,dtype", [(1, 1, "f32"), (1, 3, "bf16"), (1, 7, "f32"),
+                                       (2, 5, "bf16"), (3, 2, "f32")])
+def test_small_batch_single_launch_every_reject_position(hv, orc, cuda, B, g, dtype):
+    """Batches whose grid fits one workgroup per CU (B <= 3 at V = 151936) run the
+    single-launch kernel with grid barriers between its phases. The acceptance
+    uniforms force every first-reject position 0..gamma in turn (u = 0 accepts any
+    draft with nonzero target probability, u = 1 rejects), so both the residual and
+    the bonus draw run on it; every call reuses the same barrier state."""
+    V = 151936 if B == 1 else 50000
+    base = hv.synthetic.accept_workload(B, g, vocab=V, seed=500 + 10 * B + g, dtype=dtype,
+                                        per_seq_settings=(B > 1))
+    for r in range(g + 1):
+        w = dict(base)
+        u = np.zeros((B, g), np.float32)
+        if r < g:
+            u[:, r] = 1.0
+        w["u_accept"] = u
+        w["u_resample"] = ((np.arange(B, dtype=np.float32) + 0.5 + r) / (B + g + 1)).astype(
+            np.float32)
+        print(f"single-launch B={B} gamma={g} {dtype} reject at {r}", flush=True)
+        got, ref = _run_both(hv, orc, w, cuda, "reference")
+        _assert_same(got, ref)
+        assert (ref["num_accepted"] == r).all()
+
+
 def test_draft_equal_to_target_accepts_everything(hv, orc, cuda):
     B, g, V = 4, 3, 5000
     w = hv.synthetic.accept_workload(B, g, vocab=V, seed=8)
