@@ -165,9 +165,13 @@ __global__ __launch_bounds__(kAT) void k_verify_attn(AttnArgs a) {
   __shared__ float s_m[kAW][kRows], s_l[kAW][kRows];
   __shared__ int s_bt[kBtCap];
 
-  const int split = blockIdx.x;
-  const int kvh = blockIdx.y / a.qtiles;
-  const int qt = blockIdx.y % a.qtiles;
+  // grid (kv head x query tile, split, sequence): consecutive workgroups go to
+  // the 8 XCDs in turn, so the fastest dimension must not be the split (the
+  // later splits of short sequences are empty, and would all land on the same
+  // XCDs); with 8 KV heads every XCD gets one head of every sequence and split
+  const int kvh = blockIdx.x / a.qtiles;
+  const int qt = blockIdx.x % a.qtiles;
+  const int split = blockIdx.y;
   const int b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int n = lane & 15;  // query row of this lane (B-operand column)
@@ -545,7 +549,8 @@ int hs_verify_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_he
   a.qtiles = (max_seqlen_q * G + kRows - 1) / kRows;
   attn_plan(num_seqs, num_kv_heads, a.qtiles, max_seqlen_k, &a.nsplit, &a.split_len);
   if (a.nsplit > 1 && (!workspace || workspace_bytes < need)) return HS_ERR_WORKSPACE;
-  if ((int64_t)num_kv_heads * a.qtiles > 65535 || num_seqs > 65535) return HS_ERR_UNSUPPORTED;
+  if ((int64_t)num_kv_heads * a.qtiles > 65535 || a.nsplit > 65535 || num_seqs > 65535)
+    return HS_ERR_UNSUPPORTED;
   a.q = static_cast<const uint16_t*>(q);
   a.q_st = q_stride_tok;
   a.q_sh = q_stride_head;
@@ -574,7 +579,7 @@ int hs_verify_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_he
   a.part_o = static_cast<float*>(workspace);
   a.part_ml = workspace ? static_cast<float*>(workspace) + parts * kD : nullptr;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  dim3 grid(a.nsplit, num_kv_heads * a.qtiles, num_seqs);
+  dim3 grid(num_kv_heads * a.qtiles, a.nsplit, num_seqs);
   if (a.fp8)
     launch_attn<true>(G, grid, s, a);
   else
