@@ -79,6 +79,56 @@ __device__ __forceinline__ int64_t chunk_elem(int c, int tid, int k) {
   return (int64_t)c * kChunk + (int64_t)tid * kGroupElems + k;
 }
 
+// One wave per chunk: lane `lane` holds elements c0 + 512 s + 8 lane + k
+// (group s = 0..3, k = 0..7), each group one coalesced 1 KB (bf16) or 2 KB
+// (f32) wave load, kept as raw 16-byte words until used. For 16-byte aligned
+// rows with V % 8 == 0 a group is wholly inside the row or wholly past its
+// end; past the end, and for every group when `use` is false, the lane reads
+// the row's first 16 bytes (one cache line for the wave) and the values are
+// not used. No branch, so all of a chunk's loads are in flight together.
+constexpr int kLaneChunkGroups = kChunk / (kWave * kGroupElems);  // 4
+
+template <typename T>
+struct LaneChunk {
+  static constexpr int kWords = kLaneChunkGroups * kGroupElems * (int)sizeof(T) / 16;
+  uint4 w[kWords];
+};
+
+__device__ __forceinline__ int64_t lane_chunk_idx(int64_t c0, int s, int lane, int k) {
+  return c0 + (int64_t)s * (kWave * kGroupElems) + lane * kGroupElems + k;
+}
+
+template <typename T>
+__device__ __forceinline__ void lane_chunk_load(const T* __restrict__ rp, int64_t c0, int V,
+                                                int lane, bool use, LaneChunk<T>& r) {
+#pragma unroll
+  for (int s = 0; s < kLaneChunkGroups; ++s) {
+    const int64_t i = lane_chunk_idx(c0, s, lane, 0);
+    const T* p = rp + ((use && i < V) ? i : 0);
+    if constexpr (sizeof(T) == 2) {
+      r.w[s] = *reinterpret_cast<const uint4*>(p);
+    } else {
+      r.w[2 * s] = *reinterpret_cast<const uint4*>(p);
+      r.w[2 * s + 1] = *reinterpret_cast<const uint4*>(p + 4);
+    }
+  }
+}
+
+__device__ __forceinline__ uint32_t u4_word(const uint4& u, int i) {
+  return i == 0 ? u.x : i == 1 ? u.y : i == 2 ? u.z : u.w;
+}
+
+// element (s, k) of a lane's chunk as float (s, k compile-time after unrolling)
+template <typename T>
+__device__ __forceinline__ float lane_chunk_val(const LaneChunk<T>& r, int s, int k) {
+  if constexpr (sizeof(T) == 2) {
+    const uint32_t w = u4_word(r.w[s], k >> 1);
+    return (k & 1) ? u2f(w & 0xffff0000u) : u2f(w << 16);
+  } else {
+    return u2f(u4_word(r.w[2 * s + (k >> 2)], k & 3));
+  }
+}
+
 // Folds the chunk partials of one row into its max M and normaliser
 //   S = f32rz(sum_c floor(2^40 * f32rz(E_c) 2^-44 * exp(m_c - M))) 2^-40
 // (one wave; every lane returns the same descriptor, kept set = whole row).

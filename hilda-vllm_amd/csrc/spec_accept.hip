@@ -10,7 +10,9 @@
 // invalidate per workgroup; kernel boundaries are cheaper):
 //   1. k_chunk_stats   one 256-thread workgroup per 2048-element chunk of a
 //      target row: chunk max m_c and E_c = sum floor(2^44 exp(x_i - m_c)).
-//      Target logits are read from HBM exactly once here.
+//      Target logits are read from HBM exactly once here. For 16-byte
+//      aligned rows with V % 8 == 0, k_chunk_stats_w does the same with one
+//      wave per chunk and the wave's next chunk in flight.
 //   2. (filtered mode) k_row_filter, spec_filter.hip: top-k / top-p kept set
 //      and normaliser per row.
 //   3. k_sample_part   grid (splits, B). Every workgroup first recomputes the
@@ -92,6 +94,90 @@ __global__ __launch_bounds__(kT) void k_chunk_stats(Problem P, Work W) {
       W.h2c[hb] = 0u;
       if (tid == 0) W.filt[row].ncand = 0;
     }
+  }
+}
+
+// The same statistics with one wave per chunk (aligned rows, V % 8 == 0):
+// no barrier, and each wave's next chunk is in flight while it reduces the
+// current one (waves stride over the items; buffers alternate).
+template <typename T>
+__device__ __forceinline__ void chunk_stats_wave(const Problem& P, const Work& W, int64_t it,
+                                                 const LaneChunk<T>& r, int lane) {
+  const int row = (int)(it / P.nchunk);
+  const int c = (int)(it % P.nchunk);
+  const int unit = row / P.rows_per_unit;
+  const float Tt = P.temps[unit];
+  const float rT = 1.0f / Tt;
+  const bool fast = hs_rcp_ok(Tt);
+  const int64_t c0 = (int64_t)c * kChunk;
+  float x[kLaneChunkGroups][kGroupElems];
+  float m = -INFINITY;
+#pragma unroll
+  for (int s = 0; s < kLaneChunkGroups; ++s) {
+    const bool in = lane_chunk_idx(c0, s, lane, 0) < P.V;
+#pragma unroll
+    for (int k = 0; k < kGroupElems; ++k) {
+      x[s][k] = hs_div_temp(lane_chunk_val<T>(r, s, k), Tt, rT, fast);
+      if (in) m = fmaxf(m, x[s][k]);
+    }
+  }
+  m = wave_max_f32(m);
+  uint32_t hi = 0, lo = 0;
+#pragma unroll
+  for (int s = 0; s < kLaneChunkGroups; ++s) {
+    const bool in = lane_chunk_idx(c0, s, lane, 0) < P.V;
+#pragma unroll
+    for (int k = 0; k < kGroupElems; ++k)
+      if (in) hs_fx44_split(hs_exp(x[s][k] - m), hi, lo);
+  }
+  const uint64_t e = wave_sum_u64(hs_join44(hi, lo));
+  if (lane == 0) {
+    ChunkStat cs;
+    cs.m = m;
+    cs.pad = 0;
+    cs.e = e;
+    W.part[it] = cs;
+  }
+  if (P.filtered && c == 0) {
+    // the filter passes accumulate into these (kernel order: this launch first)
+    for (int i = lane; i < kCB; i += kWave) {
+      const int64_t hb = (int64_t)row * kCB + i;
+      W.h1m[hb] = 0ull;
+      W.h1e[hb] = 0ull;
+      W.h1c[hb] = 0u;
+      W.h2m[hb] = 0ull;
+      W.h2e[hb] = 0ull;
+      W.h2c[hb] = 0u;
+    }
+    if (lane == 0) W.filt[row].ncand = 0;
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kT) void k_chunk_stats_w(Problem P, Work W) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int64_t items = (int64_t)P.units * P.rows_per_unit * P.nchunk;
+  const int64_t stride = (int64_t)gridDim.x * (kT / kWave);
+  int64_t it = (int64_t)blockIdx.x * (kT / kWave) + wid;
+  if (it >= items) return;
+  const T* base = reinterpret_cast<const T*>(P.logits);
+  auto load = [&](int64_t item, LaneChunk<T>& r) {
+    const bool use = item < items;
+    const int64_t row = use ? item / P.nchunk : 0;
+    const int64_t c0 = use ? (item % P.nchunk) * (int64_t)kChunk : 0;
+    lane_chunk_load<T>(base + row * P.row_stride, c0, P.V, lane, use, r);
+  };
+  LaneChunk<T> a, b;
+  load(it, a);
+  for (;;) {
+    load(it + stride, b);
+    chunk_stats_wave<T>(P, W, it, a, lane);
+    it += stride;
+    if (it >= items) break;
+    load(it + stride, a);
+    chunk_stats_wave<T>(P, W, it, b, lane);
+    it += stride;
+    if (it >= items) break;
   }
 }
 
@@ -204,20 +290,18 @@ __device__ void decide_from(const Problem& P, const AcceptArgs& A, const RowDesc
   }
 }
 
+// Start of k_sample_part: the unit's row
+// descriptors (from the filter kernel, or folded here from the chunk
+// statistics), the decision, and the unit's bookkeeping writes by split 0.
+// Every workgroup of the unit computes the same values.
 template <typename T>
-__global__ __launch_bounds__(kT) void k_sample_part(Problem P, AcceptArgs A, Work W, SampleOut O,
-                                                    int mode, int desc_ready) {
-  __shared__ RowDesc s_desc[kMaxGamma + 1];
-  __shared__ SeqState s_st;
-  __shared__ uint64_t s_w[kT / kWave], s_p[kT / kWave];
-  const int unit = blockIdx.y;
-  const int split = blockIdx.x;
+__device__ __forceinline__ SeqState part_prologue(const Problem& P, const AcceptArgs& A,
+                                                  const Work& W, const SampleOut& O,
+                                                  int desc_ready, int unit, int split,
+                                                  RowDesc* s_desc, SeqState* s_st) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int R = P.rows_per_unit;
   const bool spec = (A.tok_out != nullptr);
-  (void)mode;
-
-  // descriptors of the unit's rows: from the filter kernel or folded here
   if (desc_ready) {
     for (int j = tid; j < R; j += kT) s_desc[j] = W.desc[(int64_t)unit * R + j];
   } else {
@@ -229,16 +313,16 @@ __global__ __launch_bounds__(kT) void k_sample_part(Problem P, AcceptArgs A, Wor
   __syncthreads();
   if (wid == 0) {
     if (spec) {
-      decide_from<T>(P, A, s_desc, unit, lane, &s_st);
+      decide_from<T>(P, A, s_desc, unit, lane, s_st);
     } else if (lane == 0) {
-      s_st.kind = kKindPlain;
-      s_st.row = unit;
-      s_st.qrow = -1;
-      s_st.nacc = 0;
+      s_st->kind = kKindPlain;
+      s_st->row = unit;
+      s_st->qrow = -1;
+      s_st->nacc = 0;
     }
   }
   __syncthreads();
-  const SeqState st = s_st;
+  const SeqState st = *s_st;
   if (split == 0 && tid == 0) W.st[unit] = st;
   if (split == 0 && O.row_stats && tid < R) {
     const int64_t row = (int64_t)unit * R + tid;
@@ -246,6 +330,21 @@ __global__ __launch_bounds__(kT) void k_sample_part(Problem P, AcceptArgs A, Wor
     O.row_stats[2 * row + 1] = s_desc[tid].s;
   }
   if (split == 0 && !desc_ready && tid < R) W.desc[(int64_t)unit * R + tid] = s_desc[tid];
+  return st;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kT) void k_sample_part(Problem P, AcceptArgs A, Work W, SampleOut O,
+                                                    int mode, int desc_ready) {
+  __shared__ RowDesc s_desc[kMaxGamma + 1];
+  __shared__ SeqState s_st;
+  __shared__ uint64_t s_w[kT / kWave], s_p[kT / kWave];
+  const int unit = blockIdx.y;
+  const int split = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int R = P.rows_per_unit;
+  (void)mode;
+  const SeqState st = part_prologue<T>(P, A, W, O, desc_ready, unit, split, s_desc, &s_st);
 
   const int row = st.row;
   const bool residual = (st.kind == kKindResidual);
@@ -504,6 +603,16 @@ static int pick_split(int units, int nchunk) {
 
 static inline int launch_ok() { return hipGetLastError() == hipSuccess ? HS_OK : HS_ERR_LAUNCH; }
 
+// the wave-per-chunk kernels need 16-byte aligned rows and V % 8 == 0
+template <typename T>
+static bool wave_chunks_ok(const Problem& P, const AcceptArgs& A) {
+  if (P.V % kGroupElems) return false;
+  if ((reinterpret_cast<uintptr_t>(P.logits) & 15u) || ((P.row_stride * (int64_t)sizeof(T)) % 16))
+    return false;
+  if (A.q && ((reinterpret_cast<uintptr_t>(A.q) & 15u) || ((A.q_stride * 4) % 16))) return false;
+  return true;
+}
+
 template <typename T>
 int run_sampler_chain(const Problem& P0, const AcceptArgs& A, const Work& W, int mode,
                       SampleOut O, hipStream_t stream) {
@@ -515,7 +624,16 @@ int run_sampler_chain(const Problem& P0, const AcceptArgs& A, const Work& W, int
     hipLaunchKernelGGL(k_greedy_final, dim3(P.units), dim3(kWave), 0, stream, P, A, W, O.tokens);
     return launch_ok();
   }
-  hipLaunchKernelGGL(k_chunk_stats<T>, dim3(grid_items(items)), dim3(kT), 0, stream, P, W);
+  const bool wave = wave_chunks_ok<T>(P, A);
+  if (wave) {
+    // one chunk per wave, at most the 6 workgroups (24 waves) per CU that fit
+    // at once on 256 CUs
+    const int64_t wgs = (items + kT / kWave - 1) / (kT / kWave);
+    hipLaunchKernelGGL(k_chunk_stats_w<T>, dim3((int)(wgs < 1536 ? wgs : 1536)), dim3(kT), 0,
+                       stream, P, W);
+  } else {
+    hipLaunchKernelGGL(k_chunk_stats<T>, dim3(grid_items(items)), dim3(kT), 0, stream, P, W);
+  }
   const bool filtered = (mode == HS_ACCEPT_FILTERED);
   if (filtered) {
     int rc = launch_filter<T>(P, W, O.row_stats, stream);

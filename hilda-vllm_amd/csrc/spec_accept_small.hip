@@ -225,8 +225,10 @@ __global__ __launch_bounds__(SmallShape<G>::kThreads) void k_accept_small(Proble
 #pragma unroll
   for (int s = 0; s < RPG; ++s) {
     const int j = grp + NG * s;
-    load8_row<T>(lrow + (j < R ? j : R - 1) * P.row_stride, i0, in, x[s]);
-    load8_row<float>(qrow + (j < G ? j : G - 1) * A.q_stride, i0, in, q[s]);
+    // a slot past the last row (and the bonus row's absent draft row) reads
+    // only its clamped row's first 8 elements, not a second copy of that row
+    load8_row<T>(lrow + (j < R ? j : R - 1) * P.row_stride, i0, in && j < R, x[s]);
+    load8_row<float>(qrow + (j < G ? j : G - 1) * A.q_stride, i0, in && j < G, q[s]);
   }
   // keeps the scheduler from hoisting uses of the small inputs (and their
   // waits) above the row loads

@@ -19,6 +19,14 @@
 // FP8 (e4m3fn) caches are decoded exactly to bf16 in registers; the per-tensor
 // k/v scales are folded into the softmax scale and the output.
 // Splits of one query tile are merged by k_attn_combine.
+//
+// Large launches (enough 32-key windows for every CU) run instead as the
+// balanced launch k_verify_attn_sk: one workgroup per CU, each streaming an
+// equal share of all windows (the hardware dispatcher left a third of the
+// CUs idle between workgroups of the grid above), with 8 kv heads as one
+// head per wave over the same windows so each window reads whole cached
+// token rows; pieces of tiles shared by two workgroups are merged by
+// k_attn_combine_sk.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -55,8 +63,10 @@ struct AttnArgs {
   float scale_log2;          // softmax_scale * k_scale * log2(e)
   uint16_t* out;
   int64_t o_st, o_sh;
-  float* part_o;             // [B, Hkv, qtiles, nsplit, 16, 128]
-  float* part_ml;            // [B, Hkv, qtiles, nsplit, 16, 2]
+  float* part_o;             // [slots, 16, 128]: key splits, or two per balanced workgroup
+  float* part_ml;            // [slots, 16, 2]
+  int* sk_pre;               // balanced launch: window prefix over the tiles [tiles + 1]
+  int sk_nwg;                // balanced launch: workgroups
 };
 
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
@@ -149,59 +159,73 @@ __device__ __forceinline__ bf16x8_t fp8x8w_to_bf16(uint32_t lo, uint32_t hi) {
   return fp8x8_to_bf16(make_uint2(lo, hi));
 }
 
-// kG: query heads per KV head as a compile-time constant (2, 4 or 8), or 0 to
-// read it from the arguments (any other group size)
-template <bool kFp8, int kG>
-__global__ __launch_bounds__(kAT) void k_verify_attn(AttnArgs a) {
-  const int G = kG ? kG : a.G;
-  constexpr int kRowB = kFp8 ? 128 : 256;
-  constexpr int kTileB = kWin * kRowB;
-  constexpr int kOStride = kD + 8;  // floats per row of a wave's partial output
-  constexpr int kKvBytes = kAW * 2 * kTileB;
-  constexpr int kOBytes = kAW * kRows * kOStride * 4;
-  // per-wave K and V window tiles; after the key loop the same bytes hold the
-  // per-wave partial outputs for the merge
-  __shared__ __attribute__((aligned(16))) uint8_t s_raw[kKvBytes > kOBytes ? kKvBytes : kOBytes];
-  __shared__ float s_m[kAW][kRows], s_l[kAW][kRows];
-  __shared__ int s_bt[kBtCap];
+// One query tile: sequence b, kv head kvh, query tile qt (rows qt*16 ..
+// qt*16 + 15 of the sequence's Lq * G (token, head) rows), with the
+// sequence's query start qs and lengths.
+struct TileRef {
+  int b, kvh, qt, qs, Lq, Lk, rows;
+};
 
-  // grid (kv head x query tile, split, sequence): consecutive workgroups go to
-  // the 8 XCDs in turn, so the fastest dimension must not be the split (the
-  // later splits of short sequences are empty, and would all land on the same
-  // XCDs); with 8 KV heads every XCD gets one head of every sequence and split
-  const int kvh = blockIdx.x / a.qtiles;
-  const int qt = blockIdx.x % a.qtiles;
-  const int split = blockIdx.y;
-  const int b = blockIdx.z;
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+__device__ __forceinline__ TileRef tile_ref(const AttnArgs& a, int b, int kvh, int qt, int G) {
+  TileRef t;
+  t.b = b;
+  t.kvh = kvh;
+  t.qt = qt;
+  t.qs = a.cu_q[b];
+  t.Lq = a.cu_q[b + 1] - t.qs;
+  t.Lk = a.cu_k[b + 1] - a.cu_k[b];
+  t.rows = t.Lq * G;
+  return t;
+}
+
+// keys of the sequence visible to the tile's last row (0 for an empty tile)
+__device__ __forceinline__ int tile_keys(const TileRef& t, int G) {
+  const int r0 = t.qt * kRows;
+  if (r0 >= t.rows || t.Lk <= 0) return 0;
+  const int last_row = (r0 + kRows - 1 < t.rows - 1) ? r0 + kRows - 1 : t.rows - 1;
+  const int lim = t.Lk - t.Lq + last_row / G + 1;
+  const int hi = lim < t.Lk ? lim : t.Lk;
+  return hi > 0 ? hi : 0;
+}
+
+constexpr int kOStride = kD + 8;  // floats per row of a wave's partial output
+template <bool kFp8>
+struct AttnLds {
+  static constexpr int kRowB = kFp8 ? 128 : 256;
+  static constexpr int kTileB = kWin * kRowB;
+  static constexpr int kKvBytes = kAW * 2 * kTileB;
+  static constexpr int kOBytes = kAW * kRows * kOStride * 4;
+  static constexpr int kRawBytes = kKvBytes > kOBytes ? kKvBytes : kOBytes;
+};
+
+// Running softmax state of one wave: per query row (lane column n) the max
+// (log2 domain) and the sum of the lane's exp2 terms, and O^T in the MFMA
+// accumulator layout (lane holds O[row n][d = db*16 + 4g + j]).
+struct WaveAcc {
+  float m, lsum;
+  f32x4_t oacc[8];
+};
+
+// Walks keys [lo, hi) of query tile t (hi clipped to the keys the tile's
+// last row sees) against kv head kvh in this wave: 32-key windows ws0,
+// ws0 + step, ... below hi, the next window's K/V rows in flight while the
+// current one is multiplied. Loads the wave's query rows, then waits at a
+// workgroup barrier for s_bt: the block-table entries of the sequence from
+// block lo / block_size on, up to bt_cap of them, filled by the caller.
+// kG: query heads per KV head as a compile-time constant (2, 4 or 8), or 0 to
+// read it from the arguments (any other group size).
+template <bool kFp8, int kG>
+__device__ __forceinline__ void wave_walk(const AttnArgs& a, const TileRef& t, int kvh, int lo,
+                                          int hi, int ws0, int step, const int* s_bt, int bt_cap,
+                                          uint8_t* tile_k, uint8_t* tile_v, WaveAcc& acc) {
+  const int G = kG ? kG : a.G;
+  constexpr int kRowB = AttnLds<kFp8>::kRowB;
+  const int qs = t.qs, Lq = t.Lq, Lk = t.Lk, rows = t.rows;
+  const int lane = threadIdx.x & 63;
   const int n = lane & 15;  // query row of this lane (B-operand column)
   const int g = lane >> 4;  // k-group of this lane
-
-  // block-table entries this split can touch, fetched before the sequence
-  // lengths are known (they only depend on the split)
-  const int lo = split * a.split_len;
+  const int r0 = t.qt * kRows;
   const int bt0 = lo / a.block_size;
-  {
-    int nbt = (lo + a.split_len - 1) / a.block_size - bt0 + 1;
-    if (nbt > a.bt_width - bt0) nbt = a.bt_width - bt0;
-    for (int i = tid; i < nbt && i < kBtCap; i += kAT) s_bt[i] = a.bt[(int64_t)b * a.bt_stride + bt0 + i];
-  }
-
-  const int qs = a.cu_q[b];
-  const int Lq = a.cu_q[b + 1] - qs;
-  const int Lk = a.cu_k[b + 1] - a.cu_k[b];
-  const int rows = Lq * G;
-  const int r0 = qt * kRows;
-  if (r0 >= rows || Lk <= 0) return;
-  const int nsplit_b = (Lk + a.split_len - 1) / a.split_len;
-  if (split >= nsplit_b) return;
-
-  int hi = lo + a.split_len < Lk ? lo + a.split_len : Lk;
-  {
-    const int last_row = (r0 + kRows - 1 < rows - 1) ? r0 + kRows - 1 : rows - 1;
-    const int lim = Lk - Lq + last_row / G + 1;  // keys visible to the tile's last token
-    if (lim < hi) hi = lim;
-  }
   const int nbt_used = (hi > lo) ? (hi - 1) / a.block_size - bt0 + 1 : 0;
 
   // query row of this lane
@@ -225,8 +249,6 @@ __global__ __launch_bounds__(kAT) void k_verify_attn(AttnArgs a) {
   f32x4_t oacc[8];
 #pragma unroll
   for (int db = 0; db < 8; ++db) oacc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  uint8_t* tile_k = s_raw + wid * 2 * kTileB;
-  uint8_t* tile_v = tile_k + kTileB;
   const int esz = kFp8 ? 1 : 2;
   __syncthreads();  // s_bt ready
 
@@ -235,7 +257,7 @@ __global__ __launch_bounds__(kAT) void k_verify_attn(AttnArgs a) {
   auto window_base = [&](int ws, const uint8_t*& kb, const uint8_t*& vb) -> bool {
     const int blk_idx = ws / a.block_size;
     const int bi = blk_idx - bt0;
-    const int blk = (bi < nbt_used && bi < kBtCap && bt0 + bi < a.bt_width) ? s_bt[bi] : -1;
+    const int blk = (bi < nbt_used && bi < bt_cap && bt0 + bi < a.bt_width) ? s_bt[bi] : -1;
     if (blk < 0 || blk >= a.num_blocks) return false;
     const int64_t off = ((int64_t)blk * a.c_sb + (int64_t)(ws - blk_idx * a.block_size) * a.c_st +
                          (int64_t)kvh * a.c_sh) * esz;
@@ -244,7 +266,7 @@ __global__ __launch_bounds__(kAT) void k_verify_attn(AttnArgs a) {
     return true;
   };
 
-  int ws = lo + wid * kWin;
+  int ws = ws0;
   bool have = false;
   if (ws < hi) {
     const uint8_t *kb, *vb;
@@ -252,7 +274,7 @@ __global__ __launch_bounds__(kAT) void k_verify_attn(AttnArgs a) {
     if (have) issue_window<kFp8>(a, kb, vb, ws, hi, tile_k, tile_v, lane);
   }
   while (ws < hi) {
-    const int ws_next = ws + kAW * kWin;
+    const int ws_next = ws + step;
     const bool cur = have;
     bf16x8_t ka[2][4], va[8];
     if (cur) {
@@ -358,26 +380,51 @@ __global__ __launch_bounds__(kAT) void k_verify_attn(AttnArgs a) {
     }
     ws = ws_next;
   }
-
   // per-row totals of this wave
   lsum += __shfl_xor(lsum, 16, 64);
   lsum += __shfl_xor(lsum, 32, 64);
+  acc.m = m;
+  acc.lsum = lsum;
+#pragma unroll
+  for (int db = 0; db < 8; ++db) acc.oacc[db] = oacc[db];
+}
+
+// Attends query tile t over keys [klo, khi) with the 8 waves of the workgroup
+// (wave w takes windows w, w + 8, ...), merges the waves and writes the
+// normalised output (pslot < 0) or the unnormalised partial (o, running max,
+// sum) at partial slot pslot. s_bt as for wave_walk. s_raw holds the per-wave
+// K and V window tiles and, after the key loop, the per-wave partial outputs.
+template <bool kFp8, int kG>
+__device__ __forceinline__ void attend_keys(const AttnArgs& a, const TileRef& t, int klo, int khi,
+                                            int64_t pslot, uint8_t* s_raw, float (*s_m)[kRows],
+                                            float (*s_l)[kRows], const int* s_bt, int bt_cap) {
+  const int G = kG ? kG : a.G;
+  constexpr int kTileB = AttnLds<kFp8>::kTileB;
+  const int kvh = t.kvh, qs = t.qs, rows = t.rows;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const int r0 = t.qt * kRows;
+  uint8_t* tile_k = s_raw + wid * 2 * kTileB;
+  uint8_t* tile_v = tile_k + kTileB;
+  WaveAcc acc;
+  wave_walk<kFp8, kG>(a, t, kvh, klo, khi, klo + wid * kWin, kAW * kWin, s_bt, bt_cap, tile_k,
+                      tile_v, acc);
   if (g == 0) {
-    s_m[wid][n] = m;
-    s_l[wid][n] = lsum;
+    s_m[wid][n] = acc.m;
+    s_l[wid][n] = acc.lsum;
   }
   __syncthreads();  // every wave is done with its tiles
   float* s_o = reinterpret_cast<float*>(s_raw);
-  // O^T layout: lane holds O[row n][d = db*16 + 4g + j]
 #pragma unroll
   for (int db = 0; db < 8; ++db)
     *reinterpret_cast<float4*>(&s_o[(wid * kRows + n) * kOStride + db * 16 + 4 * g]) =
-        make_float4(oacc[db][0], oacc[db][1], oacc[db][2], oacc[db][3]);
+        make_float4(acc.oacc[db][0], acc.oacc[db][1], acc.oacc[db][2], acc.oacc[db][3]);
   __syncthreads();
-  if (tid >= kRows * 16) return;
-
-  // merge the waves: thread handles row tid/16, dims (tid%16)*8 .. +8
+  // merge the waves: thread handles row tid/16, dims (tid%16)*8 .. +8 (the
+  // other threads have no row; there is no barrier below)
   const int row = tid >> 4;
+  const int rr = r0 + row;
+  if (tid >= kRows * 16 || rr >= rows) return;
   const int d0 = (tid & 15) * 8;
   float M = -INFINITY;
 #pragma unroll
@@ -397,10 +444,8 @@ __global__ __launch_bounds__(kAT) void k_verify_attn(AttnArgs a) {
     o[0] += x0.x * f[w]; o[1] += x0.y * f[w]; o[2] += x0.z * f[w]; o[3] += x0.w * f[w];
     o[4] += x1.x * f[w]; o[5] += x1.y * f[w]; o[6] += x1.z * f[w]; o[7] += x1.w * f[w];
   }
-  const int rr = r0 + row;
-  if (rr >= rows) return;
   const int oi = rr / G, oh = kvh * G + rr % G;
-  if (nsplit_b == 1) {
+  if (pslot < 0) {
     const float inv = (L > 0.0f) ? a.v_scale / L : 0.0f;
     union {
       uint16_t h[8];
@@ -410,8 +455,7 @@ __global__ __launch_bounds__(kAT) void k_verify_attn(AttnArgs a) {
     for (int t = 0; t < 8; ++t) ob.h[t] = f32_to_bf16_rne(o[t] * inv);
     *reinterpret_cast<uint4*>(a.out + (int64_t)(qs + oi) * a.o_st + (int64_t)oh * a.o_sh + d0) = ob.u;
   } else {
-    const int64_t pidx =
-        ((((int64_t)b * a.Hkv + kvh) * a.qtiles + qt) * a.nsplit + split) * kRows + row;
+    const int64_t pidx = pslot * kRows + row;
     float* po = a.part_o + pidx * kD + d0;
     *reinterpret_cast<float4*>(po) = make_float4(o[0], o[1], o[2], o[3]);
     *reinterpret_cast<float4*>(po + 4) = make_float4(o[4], o[5], o[6], o[7]);
@@ -420,6 +464,269 @@ __global__ __launch_bounds__(kAT) void k_verify_attn(AttnArgs a) {
       a.part_ml[pidx * 2 + 1] = L;
     }
   }
+}
+
+// One launch = one workgroup per (kv head x query tile, split, sequence).
+// The grid's fastest dimension is not the split: consecutive workgroups go to
+// the 8 XCDs in turn and the later splits of short sequences are empty, so
+// split-fastest would leave the same XCDs idle; with 8 KV heads every XCD
+// gets one head of every sequence and split.
+template <bool kFp8, int kG>
+__global__ __launch_bounds__(kAT) void k_verify_attn(AttnArgs a) {
+  const int G = kG ? kG : a.G;
+  __shared__ __attribute__((aligned(16))) uint8_t s_raw[AttnLds<kFp8>::kRawBytes];
+  __shared__ float s_m[kAW][kRows], s_l[kAW][kRows];
+  __shared__ int s_bt[kBtCap];
+  const int kvh = blockIdx.x / a.qtiles;
+  const int qt = blockIdx.x % a.qtiles;
+  const int split = blockIdx.y;
+  const int b = blockIdx.z;
+  const int tid = threadIdx.x;
+
+  // block-table entries this split can touch, fetched before the sequence
+  // lengths are known (they only depend on the split)
+  const int lo = split * a.split_len;
+  const int bt0 = lo / a.block_size;
+  {
+    int nbt = (lo + a.split_len - 1) / a.block_size - bt0 + 1;
+    if (nbt > a.bt_width - bt0) nbt = a.bt_width - bt0;
+    for (int i = tid; i < nbt && i < kBtCap; i += kAT) s_bt[i] = a.bt[(int64_t)b * a.bt_stride + bt0 + i];
+  }
+  const TileRef t = tile_ref(a, b, kvh, qt, G);
+  if (qt * kRows >= t.rows || t.Lk <= 0) return;
+  const int nsplit_b = (t.Lk + a.split_len - 1) / a.split_len;
+  if (split >= nsplit_b) return;
+  int hi = lo + a.split_len;
+  const int vis = tile_keys(t, G);
+  if (vis < hi) hi = vis;
+  const int64_t pslot =
+      nsplit_b == 1 ? -1 : (((int64_t)b * a.Hkv + kvh) * a.qtiles + qt) * a.nsplit + split;
+  attend_keys<kFp8, kG>(a, t, lo, hi, pslot, s_raw, s_m, s_l, s_bt, kBtCap);
+}
+
+// Balanced launch: one workgroup per CU. The 32-key windows of all tiles
+// form one list; workgroup k of N takes windows [W*k/N, W*(k+1)/N) of the W
+// in all, so every workgroup streams the same number of windows whatever the
+// sequence lengths, and no workgroup waits on the hardware dispatcher after
+// the start. Its range covers whole tiles (written as final outputs) and at
+// most two pieces of tiles shared with its neighbours: its first piece goes
+// to partial slot 2k, its last to 2k + 1, merged by k_attn_combine_sk.
+// Two tile kinds:
+//   kHeads = false: tile = (kv head, sequence, query tile), kv-head-major;
+//     the 8 waves take alternate windows of one kv head and merge in LDS.
+//     Workgroups k, k + N/Hkv, ... walk the same sequences at the same
+//     offsets for different heads, so the heads' 256-byte pieces of each
+//     cached token row are read close together in time.
+//   kHeads = true (8 kv heads): tile = (sequence, query tile); wave w takes
+//     kv head w over the same windows, so each window reads whole cached
+//     token rows (all heads) at once, and the waves need no merge. A slot
+//     then holds the pieces of all 8 heads.
+constexpr int kSkMaxTiles = 4096;
+constexpr int kSkBtCap = 1024 + 2;
+
+// tile j of the balanced launch's list
+template <bool kHeads>
+__device__ __forceinline__ void sk_tile(const AttnArgs& a, int j, int& b, int& kvh, int& qt) {
+  if constexpr (kHeads) {
+    kvh = 0;
+    b = j / a.qtiles;
+    qt = j % a.qtiles;
+  } else {
+    const int per_head = a.B * a.qtiles;
+    kvh = j / per_head;
+    const int rem = j % per_head;
+    b = rem / a.qtiles;
+    qt = rem % a.qtiles;
+  }
+}
+
+template <bool kHeads>
+__device__ __forceinline__ int sk_tiles(const AttnArgs& a) {
+  return kHeads ? a.B * a.qtiles : a.B * a.Hkv * a.qtiles;
+}
+
+// Attends query tile t over keys [klo, khi) with wave w on kv head w (all
+// waves walk the same windows) and writes each wave's rows: normalised
+// output (pslot < 0) or the unnormalised partial at partial slot pslot.
+template <bool kFp8, int kG>
+__device__ __forceinline__ void attend_heads(const AttnArgs& a, const TileRef& t, int klo, int khi,
+                                             int64_t pslot, uint8_t* s_raw, const int* s_bt,
+                                             int bt_cap) {
+  const int G = kG ? kG : a.G;
+  constexpr int kTileB = AttnLds<kFp8>::kTileB;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const int kvh = wid;
+  uint8_t* tile_k = s_raw + wid * 2 * kTileB;
+  uint8_t* tile_v = tile_k + kTileB;
+  WaveAcc acc;
+  wave_walk<kFp8, kG>(a, t, kvh, klo, khi, klo, kWin, s_bt, bt_cap, tile_k, tile_v, acc);
+  const int r = t.qt * kRows + n;
+  if (r >= t.rows) return;
+  const int qi = r / G, qh = kvh * G + r % G;
+  if (pslot < 0) {
+    const float inv = (acc.lsum > 0.0f) ? a.v_scale / acc.lsum : 0.0f;
+    uint16_t* op = a.out + (int64_t)(t.qs + qi) * a.o_st + (int64_t)qh * a.o_sh + 4 * g;
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+      const uint32_t w0 = (uint32_t)f32_to_bf16_rne(acc.oacc[db][0] * inv) |
+                          ((uint32_t)f32_to_bf16_rne(acc.oacc[db][1] * inv) << 16);
+      const uint32_t w1 = (uint32_t)f32_to_bf16_rne(acc.oacc[db][2] * inv) |
+                          ((uint32_t)f32_to_bf16_rne(acc.oacc[db][3] * inv) << 16);
+      *reinterpret_cast<uint2*>(op + db * 16) = make_uint2(w0, w1);
+    }
+  } else {
+    const int64_t pidx = (pslot * a.Hkv + kvh) * kRows + n;
+    float* po = a.part_o + pidx * kD + 4 * g;
+#pragma unroll
+    for (int db = 0; db < 8; ++db)
+      *reinterpret_cast<float4*>(po + db * 16) =
+          make_float4(acc.oacc[db][0], acc.oacc[db][1], acc.oacc[db][2], acc.oacc[db][3]);
+    if (g == 0) {
+      a.part_ml[pidx * 2] = acc.m;
+      a.part_ml[pidx * 2 + 1] = acc.lsum;
+    }
+  }
+}
+
+template <bool kFp8, int kG, bool kHeads>
+__global__ __launch_bounds__(kAT) void k_verify_attn_sk(AttnArgs a) {
+  const int G = kG ? kG : a.G;
+  constexpr int kRaw = kHeads ? AttnLds<kFp8>::kKvBytes : AttnLds<kFp8>::kRawBytes;
+  __shared__ __attribute__((aligned(16))) uint8_t s_raw[kRaw];
+  __shared__ float s_m[kHeads ? 1 : kAW][kRows], s_l[kHeads ? 1 : kAW][kRows];
+  __shared__ int s_bt[kSkBtCap];
+  __shared__ int s_pre[kSkMaxTiles + 1];
+  __shared__ int s_wsum[kAW];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int ntiles = sk_tiles<kHeads>(a);
+
+  // window count of every tile, then their prefix sums (s_pre[j] = windows
+  // before tile j); thread tid owns tiles [tid * per, tid * per + per)
+  const int per = (ntiles + kAT - 1) / kAT;
+  int tsum = 0;
+  for (int i = 0; i < per; ++i) {
+    const int j = tid * per + i;
+    if (j >= ntiles) break;
+    int b, kvh, qt;
+    sk_tile<kHeads>(a, j, b, kvh, qt);
+    const TileRef t = tile_ref(a, b, kvh, qt, G);
+    const int nw = (tile_keys(t, G) + kWin - 1) / kWin;
+    s_pre[j + 1] = nw;
+    tsum += nw;
+  }
+  int incl = tsum;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int v = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += v;
+  }
+  if (lane == 63) s_wsum[wid] = incl;
+  __syncthreads();
+  int run = incl - tsum;
+  for (int w = 0; w < wid; ++w) run += s_wsum[w];
+  for (int i = 0; i < per; ++i) {
+    const int j = tid * per + i;
+    if (j >= ntiles) break;
+    run += s_pre[j + 1];
+    s_pre[j + 1] = run;
+  }
+  if (tid == 0) s_pre[0] = 0;
+  __syncthreads();
+
+  const int64_t W = s_pre[ntiles];
+  const int64_t N = gridDim.x, k = blockIdx.x;
+  if (k == 0)
+    for (int j = tid; j <= ntiles; j += kAT) a.sk_pre[j] = s_pre[j];
+  const int w_begin = (int)(W * k / N), w_end = (int)(W * (k + 1) / N);
+  if (w_begin >= w_end) return;
+  // tile holding window w_begin: the last j with s_pre[j] <= w_begin
+  int jl = 0, jh = ntiles - 1;
+  while (jl < jh) {
+    const int mid = (jl + jh + 1) >> 1;
+    if (s_pre[mid] <= w_begin) jl = mid; else jh = mid - 1;
+  }
+  int j = jl, w = w_begin, seg = 0;
+  while (w < w_end) {
+    while (s_pre[j + 1] <= w) ++j;  // tiles without windows
+    const int s0 = s_pre[j], s1 = s_pre[j + 1];
+    const int seg_end = s1 < w_end ? s1 : w_end;
+    int b, kvh, qt;
+    sk_tile<kHeads>(a, j, b, kvh, qt);
+    const TileRef t = tile_ref(a, b, kvh, qt, G);
+    const int klo = (w - s0) * kWin;
+    int khi = (seg_end - s0) * kWin;
+    const int vis = tile_keys(t, G);
+    if (vis < khi) khi = vis;
+    const int64_t pslot = (w == s0 && seg_end == s1) ? -1 : 2 * k + (seg > 0 ? 1 : 0);
+    __syncthreads();  // the previous piece's readers of s_bt and the tiles are done
+    const int bt0 = klo / a.block_size;
+    const int nbt = (khi - 1) / a.block_size - bt0 + 1;
+    for (int i = tid; i < nbt && i < kSkBtCap && bt0 + i < a.bt_width; i += kAT)
+      s_bt[i] = a.bt[(int64_t)b * a.bt_stride + bt0 + i];
+    if constexpr (kHeads)
+      attend_heads<kFp8, kG>(a, t, klo, khi, pslot, s_raw, s_bt, kSkBtCap);
+    else
+      attend_keys<kFp8, kG>(a, t, klo, khi, pslot, s_raw, s_m, s_l, s_bt, kSkBtCap);
+    w = seg_end;
+    ++seg;
+  }
+}
+
+// merges the pieces of the tiles that the balanced launch split between
+// workgroups: one workgroup per (tile, kv head of the tile); whole tiles
+// return at once
+template <bool kHeads>
+__global__ __launch_bounds__(kRows * 16) void k_attn_combine_sk(AttnArgs a) {
+  const int j = blockIdx.x;
+  const int ntiles = sk_tiles<kHeads>(a);
+  const int64_t W = a.sk_pre[ntiles], N = a.sk_nwg;
+  const int64_t s0 = a.sk_pre[j], s1 = a.sk_pre[j + 1];
+  if (s0 == s1) return;
+  // first and last workgroups whose window range [W*k/N, W*(k+1)/N) meets [s0, s1)
+  const int64_t kf = (N * (s0 + 1) + W - 1) / W - 1;
+  const int64_t kl = (N * s1 + W - 1) / W - 1;
+  if (kf == kl) return;
+  int b, kvh, qt;
+  sk_tile<kHeads>(a, j, b, kvh, qt);
+  if (kHeads) kvh = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int qs = a.cu_q[b];
+  const int rows = (a.cu_q[b + 1] - qs) * a.G;
+  const int row = tid >> 4;
+  const int d0 = (tid & 15) * 8;
+  const int rr = qt * kRows + row;
+  if (rr >= rows) return;
+  auto piece = [&](int64_t k) -> int64_t {  // partial row index of workgroup k's piece
+    const int64_t slot = 2 * k + ((k == kf && W * k / N < s0) ? 1 : 0);
+    return (kHeads ? slot * a.Hkv + kvh : slot) * kRows + row;
+  };
+  float M = -INFINITY;
+  for (int64_t k = kf; k <= kl; ++k) {
+    if (W * k / N == W * (k + 1) / N) continue;  // empty range
+    M = fmaxf(M, a.part_ml[piece(k) * 2]);
+  }
+  const float Mb = (M == -INFINITY) ? 0.0f : M;
+  float L = 0.0f, o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int64_t k = kf; k <= kl; ++k) {
+    if (W * k / N == W * (k + 1) / N) continue;
+    const int64_t pidx = piece(k);
+    const float f = __builtin_amdgcn_exp2f(a.part_ml[pidx * 2] - Mb);
+    L += a.part_ml[pidx * 2 + 1] * f;
+    const float4 x0 = *reinterpret_cast<const float4*>(a.part_o + pidx * kD + d0);
+    const float4 x1 = *reinterpret_cast<const float4*>(a.part_o + pidx * kD + d0 + 4);
+    o[0] += x0.x * f; o[1] += x0.y * f; o[2] += x0.z * f; o[3] += x0.w * f;
+    o[4] += x1.x * f; o[5] += x1.y * f; o[6] += x1.z * f; o[7] += x1.w * f;
+  }
+  const float inv = (L > 0.0f) ? a.v_scale / L : 0.0f;
+  const int oi = rr / a.G, oh = kvh * a.G + rr % a.G;
+  union {
+    uint16_t h[8];
+    uint4 u;
+  } ob;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) ob.h[t] = f32_to_bf16_rne(o[t] * inv);
+  *reinterpret_cast<uint4*>(a.out + (int64_t)(qs + oi) * a.o_st + (int64_t)oh * a.o_sh + d0) = ob.u;
 }
 
 // merges the key splits of every (sequence, kv head, query tile)
@@ -475,6 +782,54 @@ static void launch_attn(int G, dim3 grid, hipStream_t s, const AttnArgs& a) {
   }
 }
 
+template <bool kFp8, bool kHeads>
+static void launch_attn_sk(int G, int nwg, hipStream_t s, const AttnArgs& a) {
+  switch (G) {
+    case 2: hipLaunchKernelGGL((k_verify_attn_sk<kFp8, 2, kHeads>), dim3(nwg), dim3(kAT), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((k_verify_attn_sk<kFp8, 4, kHeads>), dim3(nwg), dim3(kAT), 0, s, a); break;
+    case 8: hipLaunchKernelGGL((k_verify_attn_sk<kFp8, 8, kHeads>), dim3(nwg), dim3(kAT), 0, s, a); break;
+    default: hipLaunchKernelGGL((k_verify_attn_sk<kFp8, 0, kHeads>), dim3(nwg), dim3(kAT), 0, s, a); break;
+  }
+}
+
+static int g_attn_cus[64];  // CUs per device, filled on first use
+
+static int attn_num_cus() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!g_attn_cus[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    g_attn_cus[dev] = n;
+  }
+  return g_attn_cus[dev];
+}
+
+// Balanced launch (one workgroup per CU) when the tiles fit its prefix table
+// and the longest length gives enough windows per workgroup (below that the
+// classic grid is one short wave of workgroups anyway): with 8 kv heads the
+// heads-in-waves kind (tiles without the head, each wave one head: at least
+// 4 windows per workgroup), otherwise the kv-head-major kind (at least 16
+// windows per workgroup, 2 per wave). Returns the workgroup count, or 0 for
+// the classic grid; *heads tells the kind.
+static int attn_sk_plan(int B, int Hkv, int qtiles, int max_seqlen_k, bool* heads) {
+  const int cus = attn_num_cus();
+  const int64_t wins = (max_seqlen_k + kWin - 1) / kWin;
+  *heads = (Hkv == kAW);
+  const int64_t tiles = (int64_t)B * qtiles * (*heads ? 1 : Hkv);
+  if (tiles > kSkMaxTiles) return 0;
+  if (tiles * wins < (*heads ? 4LL : 16LL) * cus) return 0;
+  return cus;
+}
+
+static size_t attn_sk_workspace(int B, int Hkv, int qtiles, int nwg, bool heads) {
+  const size_t slots = 2 * (size_t)nwg * kRows * (heads ? Hkv : 1);
+  const size_t tiles = (size_t)B * qtiles * (heads ? 1 : Hkv);
+  return slots * kD * sizeof(float) + slots * 2 * sizeof(float) + (tiles + 1) * sizeof(int) + 256;
+}
+
 static void attn_plan(int B, int Hkv, int qtiles, int max_seqlen_k, int* nsplit, int* split_len) {
   const int64_t tiles = (int64_t)B * Hkv * qtiles;
   const int64_t target = 1024;  // workgroups in flight across 256 CUs
@@ -508,7 +863,11 @@ size_t hs_verify_attention_workspace_size(int num_seqs, int num_q_heads, int num
   int nsplit, split_len;
   attn_plan(num_seqs, num_kv_heads, qtiles, max_seqlen_k, &nsplit, &split_len);
   const size_t parts = (size_t)num_seqs * num_kv_heads * qtiles * nsplit * kRows;
-  return parts * kD * sizeof(float) + parts * 2 * sizeof(float) + 256;
+  const size_t classic = parts * kD * sizeof(float) + parts * 2 * sizeof(float) + 256;
+  bool heads = false;
+  const int nwg = attn_sk_plan(num_seqs, num_kv_heads, qtiles, max_seqlen_k, &heads);
+  const size_t sk = nwg ? attn_sk_workspace(num_seqs, num_kv_heads, qtiles, nwg, heads) : 0;
+  return classic > sk ? classic : sk;
 }
 
 int hs_verify_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
@@ -575,10 +934,38 @@ int hs_verify_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_he
   a.out = static_cast<uint16_t*>(out);
   a.o_st = out_stride_tok;
   a.o_sh = out_stride_head;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  bool heads = false;
+  const int nwg = attn_sk_plan(num_seqs, num_kv_heads, a.qtiles, max_seqlen_k, &heads);
+  if (nwg && workspace && workspace_bytes >= need &&
+      (max_seqlen_k + block_size - 1) / block_size + 1 <= kSkBtCap) {
+    const size_t slots = 2 * (size_t)nwg * kRows * (heads ? num_kv_heads : 1);
+    a.part_o = static_cast<float*>(workspace);
+    a.part_ml = a.part_o + slots * kD;
+    a.sk_pre = reinterpret_cast<int*>(a.part_ml + slots * 2);
+    a.sk_nwg = nwg;
+    const int ntiles = num_seqs * a.qtiles * (heads ? 1 : num_kv_heads);
+    if (heads) {
+      if (a.fp8)
+        launch_attn_sk<true, true>(G, nwg, s, a);
+      else
+        launch_attn_sk<false, true>(G, nwg, s, a);
+      hipLaunchKernelGGL(k_attn_combine_sk<true>, dim3(ntiles, num_kv_heads), dim3(kRows * 16), 0,
+                         s, a);
+    } else {
+      if (a.fp8)
+        launch_attn_sk<true, false>(G, nwg, s, a);
+      else
+        launch_attn_sk<false, false>(G, nwg, s, a);
+      hipLaunchKernelGGL(k_attn_combine_sk<false>, dim3(ntiles), dim3(kRows * 16), 0, s, a);
+    }
+    return hipGetLastError() == hipSuccess ? HS_OK : HS_ERR_LAUNCH;
+  }
   const size_t parts = (size_t)num_seqs * num_kv_heads * a.qtiles * a.nsplit * kRows;
   a.part_o = static_cast<float*>(workspace);
   a.part_ml = workspace ? static_cast<float*>(workspace) + parts * kD : nullptr;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  a.sk_pre = nullptr;
+  a.sk_nwg = 0;
   dim3 grid(num_kv_heads * a.qtiles, a.nsplit, num_seqs);
   if (a.fp8)
     launch_attn<true>(G, grid, s, a);

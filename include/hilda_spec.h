@@ -131,7 +131,10 @@ int hs_sampler(const void* logits, int logits_dtype, int64_t logits_row_stride,
 /*               entries outside [0, num_blocks) are treated as empty.       */
 /* cu_seqlens_q/k: int32 [num_seqs + 1] prefix sums of query/key lengths.    */
 /* The workspace (size from hs_verify_attention_workspace_size) holds the    */
-/* partial results of key splits; it needs no initialisation.                */
+/* partial results of key splits (or of the pieces of the one-workgroup-per- */
+/* CU launch used for large calls); it needs no initialisation. With none,  */
+/* or a smaller one, the call uses the per-tile grid and returns             */
+/* HS_ERR_WORKSPACE if that grid splits the keys.                            */
 /* ------------------------------------------------------------------------ */
 size_t hs_verify_attention_workspace_size(int num_seqs, int num_q_heads, int num_kv_heads,
                                           int max_seqlen_q, int max_seqlen_k);

@@ -110,6 +110,45 @@ def test_small_blocks_and_short_contexts(hv, attn, cuda, kv):
     _run(hv, attn, w, cuda, kv=kv)
 
 
+def test_balanced_launch_short_actual_contexts(hv, attn, cuda):
+    """max_seqlen_k selects the one-workgroup-per-CU launch while the actual contexts are
+    1..70 keys: most workgroups get an empty window range and tiles are cut between
+    neighbouring workgroups after a window or two."""
+    print("balanced launch, short contexts", flush=True)
+    lens = np.random.default_rng(7).integers(1, 71, size=64)
+    w = hv.synthetic.attention_workload(batch=64, q_len=4, lens=lens, seed=7)
+    w["max_seqlen_k"] = 2048
+    _run(hv, attn, w, cuda)
+
+
+@pytest.mark.parametrize("kv", ["bf16", "fp8"])
+def test_balanced_launch_odd_group_and_small_blocks(hv, attn, cuda, kv):
+    """24 Q / 8 KV heads (group of 3, the generic group path), 32-token blocks, 3 queries."""
+    print(f"balanced launch, G=3, block 32, {kv}", flush=True)
+    w = hv.synthetic.attention_workload(batch=24, q_len=3, num_q_heads=24, num_kv_heads=8,
+                                        block_size=32, min_len=3, max_len=1500, seed=8)
+    _run(hv, attn, w, cuda, kv=kv)
+
+
+@pytest.mark.parametrize("hq,hkv", [(16, 4), (8, 2)])
+def test_balanced_launch_kv_head_major(hv, attn, cuda, hq, hkv):
+    """Fewer than 8 kv heads: the balanced launch's kv-head-major tiles (waves take
+    alternate windows of one head and merge in LDS)."""
+    print(f"balanced launch, kv-head-major, {hq}/{hkv} heads", flush=True)
+    w = hv.synthetic.attention_workload(batch=48, q_len=4, num_q_heads=hq, num_kv_heads=hkv,
+                                        min_len=4, max_len=1500, seed=9)
+    _run(hv, attn, w, cuda)
+
+
+def test_balanced_launch_prefill_tiles(hv, attn, cuda):
+    """64 queries x 4 heads per kv head = 16 query tiles per sequence, each seeing a
+    different causal key range, in the heads-in-waves balanced launch."""
+    print("balanced launch, prefill tiles", flush=True)
+    w = hv.synthetic.attention_workload(batch=8, q_len=64, num_q_heads=32, num_kv_heads=8,
+                                        min_len=64, max_len=1024, seed=10)
+    _run(hv, attn, w, cuda)
+
+
 def test_batch1_verify_shape_of_8b_target(hv, attn, cuda):
     """B=1, gamma+1=4 queries, 32 Q / 8 KV heads: the verify shape of config 3."""
     w = hv.synthetic.attention_workload(batch=1, q_len=4, num_q_heads=32, num_kv_heads=8,
