@@ -174,8 +174,10 @@ def bench_accept(args, torch, hv):
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": profiled_traffic("hs_spec_accept call", _accept_tag(args)),
                      "bytes_per_step": step_bytes,
-                     "kernels": "one hs_spec_accept call (row statistics, filter when "
-                                "filtered, decision + resample partials, final search)"},
+                     "kernels": "one hs_spec_accept call: k_accept_small for reference-mode "
+                                "calls that fit one workgroup per CU, else the chain (row "
+                                "statistics, filter when filtered, decision + resample "
+                                "partials, final search)"},
     }
     if not args.no_cpu_baseline:
         w = hv.synthetic.accept_workload(1, 3, seed=0, dtype="bf16", temperature=0.6)
@@ -238,6 +240,8 @@ def bench_attention(args, torch, hv):
     per_launch = kv_read + 2 * (B * R * Hq * D * 2)
     achieved = per_launch / (us * 1e-6) / 1e9
     flops = 4 * int(lens.sum()) * R * Hq * D
+    # a call this size runs as the balanced launch (one workgroup per CU, one kv head per wave)
+    main_kernel = f"k_verify_attn_sk<{'true' if fp8 else 'false'}, 2, true>"
     return {
         "metric": METRIC,
         "value": round(us, 3),
@@ -258,10 +262,10 @@ def bench_attention(args, torch, hv):
         "wall_s": round(wall, 3),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": profiled_traffic(f"k_verify_attn<{'true' if fp8 else 'false'}, 2>",
-                                                 f"attention-{args.kv}"),
+                     "traffic": call_traffic([main_kernel, "k_attn_combine_sk<true>"],
+                                             f"attention-{args.kv}"),
                      "bytes_per_launch": per_launch,
-                     "kernel": f"k_verify_attn<{'true' if fp8 else 'false'}, 2> (+ k_attn_combine when split)"},
+                     "kernel": f"{main_kernel} + k_attn_combine_sk<true> (one call, timed together)"},
     }
 
 
@@ -519,6 +523,12 @@ def profiled_traffic(kernel: str, workload: str):
             except ValueError:
                 return None
     return None
+
+
+def call_traffic(kernels, workload: str):
+    """HBM bytes of one call made of `kernels` (the sum of their profiled rows), or None."""
+    rows = [profiled_traffic(k, workload) for k in kernels]
+    return None if any(r is None for r in rows) else sum(rows)
 
 
 def bench_attention_b1(args, torch, hv):

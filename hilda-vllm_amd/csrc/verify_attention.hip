@@ -66,6 +66,7 @@ struct AttnArgs {
   float* part_o;             // [slots, 16, 128]: key splits, or two per balanced workgroup
   float* part_ml;            // [slots, 16, 2]
   int* sk_pre;               // balanced launch: window prefix over the tiles [tiles + 1]
+  int* sk_w0;                // balanced launch: first window of each workgroup [nwg + 1]
   int sk_nwg;                // balanced launch: workgroups
 };
 
@@ -639,6 +640,10 @@ __global__ __launch_bounds__(kAT) void k_verify_attn_sk(AttnArgs a) {
   if (k == 0)
     for (int j = tid; j <= ntiles; j += kAT) a.sk_pre[j] = s_pre[j];
   const int w_begin = (int)(W * k / N), w_end = (int)(W * (k + 1) / N);
+  if (tid == 0) {
+    a.sk_w0[k] = w_begin;
+    if (k == N - 1) a.sk_w0[N] = w_end;
+  }
   if (w_begin >= w_end) return;
   // tile holding window w_begin: the last j with s_pre[j] <= w_begin
   int jl = 0, jh = ntiles - 1;
@@ -675,17 +680,18 @@ __global__ __launch_bounds__(kAT) void k_verify_attn_sk(AttnArgs a) {
 
 // merges the pieces of the tiles that the balanced launch split between
 // workgroups: one workgroup per (tile, kv head of the tile); whole tiles
-// return at once
+// return at once. The pieces' loads go out 8 at a time and merge online.
 template <bool kHeads>
 __global__ __launch_bounds__(kRows * 16) void k_attn_combine_sk(AttnArgs a) {
+  constexpr int kU = 8;
   const int j = blockIdx.x;
   const int ntiles = sk_tiles<kHeads>(a);
   const int64_t W = a.sk_pre[ntiles], N = a.sk_nwg;
-  const int64_t s0 = a.sk_pre[j], s1 = a.sk_pre[j + 1];
+  const int s0 = a.sk_pre[j], s1 = a.sk_pre[j + 1];
   if (s0 == s1) return;
   // first and last workgroups whose window range [W*k/N, W*(k+1)/N) meets [s0, s1)
-  const int64_t kf = (N * (s0 + 1) + W - 1) / W - 1;
-  const int64_t kl = (N * s1 + W - 1) / W - 1;
+  const int kf = (int)((N * (s0 + 1) + W - 1) / W - 1);
+  const int kl = (int)((N * s1 + W - 1) / W - 1);
   if (kf == kl) return;
   int b, kvh, qt;
   sk_tile<kHeads>(a, j, b, kvh, qt);
@@ -697,26 +703,41 @@ __global__ __launch_bounds__(kRows * 16) void k_attn_combine_sk(AttnArgs a) {
   const int d0 = (tid & 15) * 8;
   const int rr = qt * kRows + row;
   if (rr >= rows) return;
-  auto piece = [&](int64_t k) -> int64_t {  // partial row index of workgroup k's piece
-    const int64_t slot = 2 * k + ((k == kf && W * k / N < s0) ? 1 : 0);
-    return (kHeads ? slot * a.Hkv + kvh : slot) * kRows + row;
-  };
-  float M = -INFINITY;
-  for (int64_t k = kf; k <= kl; ++k) {
-    if (W * k / N == W * (k + 1) / N) continue;  // empty range
-    M = fmaxf(M, a.part_ml[piece(k) * 2]);
-  }
-  const float Mb = (M == -INFINITY) ? 0.0f : M;
-  float L = 0.0f, o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  for (int64_t k = kf; k <= kl; ++k) {
-    if (W * k / N == W * (k + 1) / N) continue;
-    const int64_t pidx = piece(k);
-    const float f = __builtin_amdgcn_exp2f(a.part_ml[pidx * 2] - Mb);
-    L += a.part_ml[pidx * 2 + 1] * f;
-    const float4 x0 = *reinterpret_cast<const float4*>(a.part_o + pidx * kD + d0);
-    const float4 x1 = *reinterpret_cast<const float4*>(a.part_o + pidx * kD + d0 + 4);
-    o[0] += x0.x * f; o[1] += x0.y * f; o[2] += x0.z * f; o[3] += x0.w * f;
-    o[4] += x1.x * f; o[5] += x1.y * f; o[6] += x1.z * f; o[7] += x1.w * f;
+  float M = -INFINITY, L = 0.0f, o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int kb = kf; kb <= kl; kb += kU) {
+    float mp[kU], lp[kU];
+    float4 x0[kU], x1[kU];
+    bool use[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int k = kb + u <= kl ? kb + u : kl;
+      const int wk = a.sk_w0[k];
+      use[u] = (kb + u <= kl) && wk != a.sk_w0[k + 1];  // empty ranges hold no piece
+      const int64_t slot = 2 * (int64_t)k + ((k == kf && wk < s0) ? 1 : 0);
+      const int64_t pidx = (kHeads ? slot * a.Hkv + kvh : slot) * kRows + row;
+      mp[u] = a.part_ml[pidx * 2];
+      lp[u] = a.part_ml[pidx * 2 + 1];
+      x0[u] = *reinterpret_cast<const float4*>(a.part_o + pidx * kD + d0);
+      x1[u] = *reinterpret_cast<const float4*>(a.part_o + pidx * kD + d0 + 4);
+    }
+    float Mg = M;
+#pragma unroll
+    for (int u = 0; u < kU; ++u)
+      if (use[u]) Mg = fmaxf(Mg, mp[u]);
+    const float Mb = (Mg == -INFINITY) ? 0.0f : Mg;
+    const float sc = __builtin_amdgcn_exp2f(M - Mb);
+    L *= sc;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) o[t] *= sc;
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      if (!use[u]) continue;  // (its loads read a stale slot; none of it is used)
+      const float f = __builtin_amdgcn_exp2f(mp[u] - Mb);
+      L += lp[u] * f;
+      o[0] += x0[u].x * f; o[1] += x0[u].y * f; o[2] += x0[u].z * f; o[3] += x0[u].w * f;
+      o[4] += x1[u].x * f; o[5] += x1[u].y * f; o[6] += x1[u].z * f; o[7] += x1[u].w * f;
+    }
+    M = Mg;
   }
   const float inv = (L > 0.0f) ? a.v_scale / L : 0.0f;
   const int oi = rr / a.G, oh = kvh * a.G + rr % a.G;
@@ -827,7 +848,8 @@ static int attn_sk_plan(int B, int Hkv, int qtiles, int max_seqlen_k, bool* head
 static size_t attn_sk_workspace(int B, int Hkv, int qtiles, int nwg, bool heads) {
   const size_t slots = 2 * (size_t)nwg * kRows * (heads ? Hkv : 1);
   const size_t tiles = (size_t)B * qtiles * (heads ? 1 : Hkv);
-  return slots * kD * sizeof(float) + slots * 2 * sizeof(float) + (tiles + 1) * sizeof(int) + 256;
+  return slots * kD * sizeof(float) + slots * 2 * sizeof(float) +
+         (tiles + 1 + nwg + 1) * sizeof(int) + 256;
 }
 
 static void attn_plan(int B, int Hkv, int qtiles, int max_seqlen_k, int* nsplit, int* split_len) {
@@ -942,9 +964,10 @@ int hs_verify_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_he
     const size_t slots = 2 * (size_t)nwg * kRows * (heads ? num_kv_heads : 1);
     a.part_o = static_cast<float*>(workspace);
     a.part_ml = a.part_o + slots * kD;
-    a.sk_pre = reinterpret_cast<int*>(a.part_ml + slots * 2);
-    a.sk_nwg = nwg;
     const int ntiles = num_seqs * a.qtiles * (heads ? 1 : num_kv_heads);
+    a.sk_pre = reinterpret_cast<int*>(a.part_ml + slots * 2);
+    a.sk_w0 = a.sk_pre + ntiles + 1;
+    a.sk_nwg = nwg;
     if (heads) {
       if (a.fp8)
         launch_attn_sk<true, true>(G, nwg, s, a);
@@ -965,6 +988,7 @@ int hs_verify_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_he
   a.part_o = static_cast<float*>(workspace);
   a.part_ml = workspace ? static_cast<float*>(workspace) + parts * kD : nullptr;
   a.sk_pre = nullptr;
+  a.sk_w0 = nullptr;
   a.sk_nwg = 0;
   dim3 grid(num_kv_heads * a.qtiles, a.nsplit, num_seqs);
   if (a.fp8)
