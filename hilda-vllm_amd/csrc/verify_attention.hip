@@ -127,6 +127,23 @@ __device__ __forceinline__ int swz8(int kk) {
   return ((kk >> 1) & 1) | ((((kk >> 2) ^ (kk >> 3)) & 1) << 1) | (((kk >> 4) & 1) << 2);
 }
 
+// Max / sum over the four lanes n, n+16, n+32, n+48 of a row with the gfx950
+// lane-swap moves (v_permlane16_swap / v_permlane32_swap: each returns the
+// register with one 16- or 32-lane half exchanged, so the pair holds both
+// partners' values) instead of LDS-routed shuffles.
+__device__ __forceinline__ float row4_max(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float row4_sum(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 typedef short v4i16_t __attribute__((ext_vector_type(4)));
 typedef int v2i32_t __attribute__((ext_vector_type(2)));
 #define HS_LDS __attribute__((address_space(3)))
@@ -354,8 +371,7 @@ __device__ __forceinline__ void wave_walk(const AttnArgs& a, const TileRef& t, i
           sv[kb * 4 + j] = v;
           mloc = fmaxf(mloc, v);
         }
-      mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
-      mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+      mloc = row4_max(mloc);
       const float m_new = fmaxf(m, mloc);
       const float base = (m_new == -INFINITY) ? 0.0f : m_new;
       const float alpha = __builtin_amdgcn_exp2f(m - base);
@@ -382,8 +398,7 @@ __device__ __forceinline__ void wave_walk(const AttnArgs& a, const TileRef& t, i
     ws = ws_next;
   }
   // per-row totals of this wave
-  lsum += __shfl_xor(lsum, 16, 64);
-  lsum += __shfl_xor(lsum, 32, 64);
+  lsum = row4_sum(lsum);
   acc.m = m;
   acc.lsum = lsum;
 #pragma unroll
