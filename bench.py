@@ -242,7 +242,7 @@ def bench_attention(args, torch, hv):
     flops = 4 * int(lens.sum()) * R * Hq * D
     # a call this size runs as the balanced launch (one workgroup per CU, one kv head per wave)
     main_kernel = f"k_verify_attn_sk<{'true' if fp8 else 'false'}, 2, true>"
-    return {
+    res = {
         "metric": METRIC,
         "value": round(us, 3),
         "unit": "us/launch (verify attention)",
@@ -267,6 +267,10 @@ def bench_attention(args, torch, hv):
                      "bytes_per_launch": per_launch,
                      "kernel": f"{main_kernel} + k_attn_combine_sk<true> (one call, timed together)"},
     }
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline_attention(torch, lens, bs, R, Hq, Hkv, D,
+                                                     args.cpu_seconds)
+    return res
 
 
 def cpu_baseline_accept(torch, w, seconds: float):
@@ -295,6 +299,51 @@ def cpu_baseline_accept(torch, w, seconds: float):
             "cores": torch.get_num_threads(), "kind": "port",
             "sample": f"{n} acceptance steps at B=1 gamma=3 V=151936 over {el:.1f} s "
                       "(torch-CPU restatement of model_runner.py:391-428)"}
+
+
+def cpu_baseline_attention(torch, lens, block_size: int, R: int, Hq: int, Hkv: int, D: int,
+                           seconds: float, sample_seqs: int = 8):
+    """The config-2 paged verify attention restated in torch-CPU fp32
+    (oracle/torch_port.paged_attention), timed on a bounded sample: the first
+    `sample_seqs` sequences of the workload, scaled to the whole batch by their
+    share of the key count."""
+    from oracle import torch_port
+    cores = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(cores)
+    sl = [int(x) for x in lens[:sample_seqs]]
+    nblk = [(x + block_size - 1) // block_size for x in sl]
+    nb = sum(nblk)
+    gen = torch.Generator().manual_seed(0)
+    kc = torch.randn((nb, block_size, Hkv, D), generator=gen)
+    vc = torch.randn((nb, block_size, Hkv, D), generator=gen)
+    bt = torch.full((len(sl), max(nblk)), -1, dtype=torch.int32)
+    off = 0
+    for b, n in enumerate(nblk):
+        bt[b, :n] = torch.arange(off, off + n, dtype=torch.int32)
+        off += n
+    q = torch.randn((len(sl) * R, Hq, D), generator=gen)
+    cu_q = [R * b for b in range(len(sl) + 1)]
+    cu_k = [0]
+    for x in sl:
+        cu_k.append(cu_k[-1] + x)
+    scale = D ** -0.5
+    for _ in range(2):
+        torch_port.paged_attention(q, kc, vc, bt, cu_q, cu_k, scale)
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        torch_port.paged_attention(q, kc, vc, bt, cu_q, cu_k, scale)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds and n >= 3:
+            break
+    per_sample = el / n
+    share = sum(sl) / float(sum(int(x) for x in lens))
+    return {"value": round(per_sample / share * 1e6, 1), "unit": "us/launch (verify attention)",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"{n} passes over {len(sl)} of the {len(lens)} sequences ({sum(sl)} of "
+                      f"{int(sum(int(x) for x in lens))} keys, fp32) in {el:.1f} s, scaled by "
+                      "the key share (torch-CPU restatement of attention.py:147-160)"}
 
 
 def bench_spec(args, torch, hv):

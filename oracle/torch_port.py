@@ -56,3 +56,32 @@ def run_verify_accept(logits: torch.Tensor, draft_probs: torch.Tensor,
             accepted.append(_draw(adjusted, float(u_resample[i])))
         results.append((accepted, n_acc))
     return results
+
+
+def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                    block_tables: torch.Tensor, cu_seqlens_q, cu_seqlens_k,
+                    softmax_scale: float) -> torch.Tensor:
+    """torch-CPU fp32 restatement of the verify branch of Attention.forward
+    (mini_vllm/layers/attention.py:147-160: flash_attn_varlen_func over the paged
+    cache with block_table, causal=True): per sequence, gather its pages, expand
+    the KV heads to their query heads and take softmax(Q K^T * scale) V with
+    bottom-right causal alignment (query i of Lq sees keys 0 .. Lk - Lq + i).
+    q [N, Hq, D]; caches [num_blocks, block_size, Hkv, D]; returns [N, Hq, D]."""
+    out = torch.empty_like(q)
+    Hq, Hkv = q.shape[1], k_cache.shape[2]
+    G = Hq // Hkv
+    bs = k_cache.shape[1]
+    for b in range(len(cu_seqlens_q) - 1):
+        qs, qe = int(cu_seqlens_q[b]), int(cu_seqlens_q[b + 1])
+        Lk = int(cu_seqlens_k[b + 1]) - int(cu_seqlens_k[b])
+        Lq = qe - qs
+        nblk = (Lk + bs - 1) // bs
+        blocks = block_tables[b, :nblk].long()
+        k = k_cache[blocks].reshape(-1, Hkv, k_cache.shape[3])[:Lk].repeat_interleave(G, dim=1)
+        v = v_cache[blocks].reshape(-1, Hkv, v_cache.shape[3])[:Lk].repeat_interleave(G, dim=1)
+        s = torch.matmul(q[qs:qe].transpose(0, 1), k.permute(1, 2, 0).contiguous()) * softmax_scale
+        keep = (torch.arange(Lk)[None, :] <= (Lk - Lq + torch.arange(Lq))[:, None])
+        s = s.masked_fill(~keep[None], float("-inf"))
+        p = torch.softmax(s, dim=-1)
+        out[qs:qe] = torch.matmul(p, v.transpose(0, 1).contiguous()).transpose(0, 1)
+    return out

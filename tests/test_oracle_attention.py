@@ -115,3 +115,18 @@ def test_e4m3fn_saturates(attn):
     got = attn.e4m3fn_quantize(x, 1.0)
     assert got.tolist() == [0x7e, 0x7e, 0x7e, 0xfe, 0x7e, 0xfe]
     assert attn.e4m3fn_quantize(np.array([np.nan], np.float32), 1.0)[0] == 0x7f
+
+
+def test_cpu_baseline_port_matches_oracle(hv, attn):
+    """The torch-CPU fp32 restatement timed as bench.py's attention cpu_baseline computes the
+    oracle's result (the NaN-filled slots past each length must stay unread)."""
+    from oracle import torch_port
+    w = _small_case(hv, seed=5, num_q_heads=16, num_kv_heads=8)
+    ref = attn.paged_attention(w["q"], w["k_cache"], w["v_cache"], w["block_tables"],
+                               w["cu_seqlens_q"], w["cu_seqlens_k"], w["softmax_scale"])
+    got = torch_port.paged_attention(
+        torch.from_numpy(w["q"]), torch.from_numpy(w["k_cache"]), torch.from_numpy(w["v_cache"]),
+        torch.from_numpy(w["block_tables"]), w["cu_seqlens_q"], w["cu_seqlens_k"],
+        w["softmax_scale"]).numpy()
+    assert np.isfinite(got).all()
+    np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-5)
