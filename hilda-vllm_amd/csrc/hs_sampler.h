@@ -132,6 +132,14 @@ struct SampleOut {
   float* row_stats;
 };
 
+// Bytes reserved for the single-launch acceptance's tagged words, right after
+// the SmallSync word, in every layout: the same fixed region whatever the
+// call's shape, so the chain kernels of calls of other shapes sharing the
+// workspace never write there (their chunk sums, read as tagged words, could
+// carry a later epoch in their high half). Eligible calls need at most
+// (rows*3 + units*4) * nchunk * 8 <= 28 * 8 * 256 = 57344 bytes.
+constexpr size_t kSmallTagBytes = 65536;
+
 struct Layout {
   size_t sync, tags, part, desc, st, spart, filt, cand, h1m, h1e, h1c, h2m, h2e, h2c, total;
 };

@@ -548,8 +548,10 @@ Layout make_layout(int units, int rows, int nchunk) {
   Layout L;
   size_t off = 0;
   L.sync = off; off = align_up(off + sizeof(SmallSync), 256);
-  // single-launch acceptance: 3 tagged words per (row, chunk) and 4 per (unit, chunk)
-  L.tags = off; off = align_up(off + ((size_t)rows * 3 + (size_t)units * 4) * nchunk * 8, 256);
+  // single-launch acceptance: 3 tagged words per (row, chunk) and 4 per (unit, chunk),
+  // in a region of fixed size and place for every shape
+  (void)units;
+  L.tags = off; off = align_up(off + kSmallTagBytes, 256);
   L.part = off; off = align_up(off + (size_t)rows * nchunk * sizeof(ChunkStat), 256);
   L.desc = off; off = align_up(off + (size_t)rows * sizeof(RowDesc), 256);
   L.st = off; off = align_up(off + (size_t)units * sizeof(SeqState), 256);

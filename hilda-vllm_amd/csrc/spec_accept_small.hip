@@ -24,7 +24,9 @@
 // XCD's L2), and a reader re-reads a word until it carries the current epoch.
 // The epoch comes from a counter every workgroup increments on entry; the
 // last one to enter advances it for the next launch, so epochs never repeat
-// (2^32 launches) whatever the shapes of earlier calls on the same workspace.
+// (2^32 launches) whatever the shapes of earlier calls on the same workspace,
+// and the tagged words live in a region of the workspace (kSmallTagBytes at a
+// fixed offset) that no other kernel writes.
 // The host launches at most one workgroup per CU, so every workgroup is
 // resident while others wait for its data; the waits are still bounded (an
 // error flag is set and the outputs are marked invalid if one runs out).
@@ -499,8 +501,12 @@ int small_accept_ok(const Problem& P, const AcceptArgs& A, int mode, int esz) {
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     return 0;
   // every workgroup must be resident at once: at most one per CU (the folds
-  // read at most four chunks per lane: nchunk <= 256)
-  return (P.nchunk <= 4 * kWave && (int64_t)P.nchunk * P.units <= cus) ? 1 : 0;
+  // read at most four chunks per lane: nchunk <= 256); the tagged words must
+  // fit the region reserved for them
+  const size_t tag_bytes =
+      ((size_t)P.units * (A.gamma + 1) * 3 + (size_t)P.units * 4) * (size_t)P.nchunk * 8;
+  return (P.nchunk <= 4 * kWave && (int64_t)P.nchunk * P.units <= cus &&
+          tag_bytes <= kSmallTagBytes) ? 1 : 0;
 }
 
 template <typename T>

@@ -124,6 +124,35 @@ def test_small_batch_single_launch_every_reject_position(hv, orc, cuda, B, g, dt
         assert (ref["num_accepted"] == r).all()
 
 
+def test_single_launch_ignores_matching_stale_words_elsewhere(hv, orc, cuda):
+    """The single-launch kernel's epoch-tagged words live in a fixed region after the
+    sync word (64 KiB at offset 256), written by no other kernel. Every other word of
+    the shared workspace is filled with a value whose high half is the next launch's
+    epoch, as stale chain data of another shape could eventually be; the call must
+    still match the oracle and report no timed-out wait."""
+    V = 151936
+    w = hv.synthetic.accept_workload(1, 3, seed=77, dtype="bf16")
+    got, ref = _run_both(hv, orc, w, cuda, "reference")  # sets up the shared workspace
+    _assert_same(got, ref)
+    nbytes = hv._lib.lib().hs_spec_accept_workspace_size(1, 3, V)
+    ws = hv.ops.workspace(cuda, nbytes, "spec_accept")
+    rng = np.random.default_rng(5)
+    for step in range(2):
+        torch.cuda.synchronize()
+        sync = ws[:16].cpu().numpy().view(np.uint64)
+        assert int(sync[1]) & 0xffffffff == 0  # no wait ran out so far
+        nxt = (int(sync[0]) >> 32) + 1
+        words = ws[256 + 65536:].view(torch.int64)
+        low = torch.from_numpy(rng.integers(0, 2**32, size=words.numel(), dtype=np.int64))
+        words.copy_(((nxt << 32) | low).to(cuda))
+        w2 = hv.synthetic.accept_workload(1, 3, seed=78 + step, dtype="bf16")
+        print(f"stale words carry epoch {nxt}", flush=True)
+        got, ref = _run_both(hv, orc, w2, cuda, "reference")
+        _assert_same(got, ref)
+    torch.cuda.synchronize()
+    assert int(ws[:16].cpu().numpy().view(np.uint64)[1]) & 0xffffffff == 0
+
+
 def test_draft_equal_to_target_accepts_everything(hv, orc, cuda):
     B, g, V = 4, 3, 5000
     w = hv.synthetic.accept_workload(B, g, vocab=V, seed=8)
