@@ -120,6 +120,7 @@ struct Work {
   uint64_t* h2m;   // [rows, kCB] fine histogram inside the coarse boundary bucket
   uint64_t* h2e;
   uint32_t* h2c;
+  int32_t* flist;  // filtered mode: [2] row counts, then [rows] top-k rows, [rows] top-p rows
 };
 
 struct SampleOut {
@@ -141,11 +142,12 @@ struct SampleOut {
 constexpr size_t kSmallTagBytes = 65536;
 
 struct Layout {
-  size_t sync, tags, part, desc, st, spart, filt, cand, h1m, h1e, h1c, h2m, h2e, h2c, total;
+  size_t sync, tags, part, desc, st, spart, filt, cand, h1m, h1e, h1c, h2m, h2e, h2c, flist, total;
 };
 
 template <typename T>
-int launch_filter(const Problem& P, const Work& W, float* row_stats, hipStream_t stream);
+int launch_filter(const Problem& P, const Work& W, float* row_stats, bool wave,
+                  hipStream_t stream);
 
 // single-launch acceptance (reference mode) for grids that fit one workgroup
 // per CU (spec_accept_small.hip)

@@ -93,6 +93,7 @@ __global__ __launch_bounds__(kT) void k_chunk_stats(Problem P, Work W) {
       W.h2e[hb] = 0ull;
       W.h2c[hb] = 0u;
       if (tid == 0) W.filt[row].ncand = 0;
+      if (tid == 0 && row == 0) W.flist[0] = W.flist[1] = 0;
     }
   }
 }
@@ -150,6 +151,7 @@ __device__ __forceinline__ void chunk_stats_wave(const Problem& P, const Work& W
       W.h2c[hb] = 0u;
     }
     if (lane == 0) W.filt[row].ncand = 0;
+    if (lane == 0 && row == 0) W.flist[0] = W.flist[1] = 0;
   }
 }
 
@@ -564,6 +566,7 @@ Layout make_layout(int units, int rows, int nchunk) {
   L.h2m = off; off = align_up(off + (size_t)rows * kCB * sizeof(uint64_t), 256);
   L.h2e = off; off = align_up(off + (size_t)rows * kCB * sizeof(uint64_t), 256);
   L.h2c = off; off = align_up(off + (size_t)rows * kCB * sizeof(uint32_t), 256);
+  L.flist = off; off = align_up(off + (2 + 2 * (size_t)rows) * sizeof(int32_t), 256);
   L.total = off;
   return L;
 }
@@ -585,6 +588,7 @@ Work bind_work(void* ws, const Layout& L) {
   W.h2m = reinterpret_cast<uint64_t*>(b + L.h2m);
   W.h2e = reinterpret_cast<uint64_t*>(b + L.h2e);
   W.h2c = reinterpret_cast<uint32_t*>(b + L.h2c);
+  W.flist = reinterpret_cast<int32_t*>(b + L.flist);
   return W;
 }
 
@@ -638,7 +642,7 @@ int run_sampler_chain(const Problem& P0, const AcceptArgs& A, const Work& W, int
   }
   const bool filtered = (mode == HS_ACCEPT_FILTERED);
   if (filtered) {
-    int rc = launch_filter<T>(P, W, O.row_stats, stream);
+    int rc = launch_filter<T>(P, W, O.row_stats, wave, stream);
     if (rc != HS_OK) return rc;
   }
   if (!O.probs && !O.sample) {

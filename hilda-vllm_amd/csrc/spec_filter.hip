@@ -653,6 +653,13 @@ __global__ __launch_bounds__(kPT) void k_filter_plan1(Problem P, Work W) {
   const int unit = row / P.rows_per_unit;
   const int mode = filter_mode(P, unit);
   FilterScratch& f = W.filt[row];
+  if (tid == kPT - kWave && mode) {
+    // the passes below walk only the rows of their mode (counters cleared by
+    // the chunk-statistics launch); the last wave appends while wave 0 folds
+    const int rows = P.units * P.rows_per_unit;
+    if (mode == 1) W.flist[2 + atomicAdd(&W.flist[0], 1)] = row;
+    else W.flist[2 + rows + atomicAdd(&W.flist[1], 1)] = row;
+  }
   if (wid == 0) {
     const RowDesc d = fold_row_desc(P, W, row, lane);
     if (lane == 0) {
@@ -727,13 +734,15 @@ __global__ __launch_bounds__(kPT) void k_filter_plan3(Problem P, Work W) {
   }
 }
 
+// only2: walk the top-p rows only (k_filter_gather_k takes the top-k rows)
 template <typename T>
-__global__ __launch_bounds__(kPT) void k_filter_pass1(Problem P, Work W) {
+__global__ __launch_bounds__(kPT) void k_filter_pass1(Problem P, Work W, int only2) {
   __shared__ PassShared ps;
   const int tid = threadIdx.x;
-  const int64_t items = (int64_t)P.units * P.rows_per_unit * P.nchunk;
+  const int rows = P.units * P.rows_per_unit;
+  const int64_t items = (int64_t)(only2 ? W.flist[1] : rows) * P.nchunk;
   for (int64_t it = blockIdx.x; it < items; it += gridDim.x) {
-    const int row = (int)(it / P.nchunk);
+    const int row = only2 ? W.flist[2 + rows + (int)(it / P.nchunk)] : (int)(it / P.nchunk);
     const int c = (int)(it % P.nchunk);
     const int unit = row / P.rows_per_unit;
     const int mode = filter_mode(P, unit);
@@ -791,13 +800,75 @@ __global__ __launch_bounds__(kPT) void k_filter_pass1(Problem P, Work W) {
   }
 }
 
+// Top-k rows (mode 1) with 16-byte aligned rows and V % 8 == 0, one wave per
+// (row, chunk): a chunk whose maximum lies below the gather threshold holds no
+// candidate and is not read; the others append every element at or above it
+// (the same candidates as k_filter_pass1), placed by a wave scan of the
+// lanes' counts and one atomic per wave, with no barrier.
+template <typename T>
+__global__ __launch_bounds__(kPT) void k_filter_gather_k(Problem P, Work W) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int64_t items = (int64_t)W.flist[0] * P.nchunk;
+  const int64_t stride = (int64_t)gridDim.x * (kPT / kWave);
+  const T* base = reinterpret_cast<const T*>(P.logits);
+  for (int64_t it = (int64_t)blockIdx.x * (kPT / kWave) + wid; it < items; it += stride) {
+    const int row = W.flist[2 + (int)(it / P.nchunk)];
+    const int c = (int)(it % P.nchunk);
+    const uint32_t tau = W.filt[row].tau;
+    if (hs_key(W.part[(int64_t)row * P.nchunk + c].m) < tau) continue;
+    const int unit = row / P.rows_per_unit;
+    const float Tt = P.temps[unit];
+    const float rT = 1.0f / Tt;
+    const bool fast = hs_rcp_ok(Tt);
+    const int64_t c0 = (int64_t)c * kChunk;
+    LaneChunk<T> r;
+    lane_chunk_load<T>(base + (int64_t)row * P.row_stride, c0, P.V, lane, true, r);
+    uint32_t flags = 0;
+#pragma unroll
+    for (int s = 0; s < kLaneChunkGroups; ++s) {
+      const bool in = lane_chunk_idx(c0, s, lane, 0) < P.V;
+#pragma unroll
+      for (int k = 0; k < kGroupElems; ++k) {
+        const float x = hs_div_temp(lane_chunk_val<T>(r, s, k), Tt, rT, fast);
+        if (in && hs_key(x) >= tau) flags |= 1u << (s * kGroupElems + k);
+      }
+    }
+    const int n = __popc(flags);
+    int incl = n;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const int v = __shfl_up(incl, d, kWave);
+      if (lane >= d) incl += v;
+    }
+    const int total = __shfl(incl, kWave - 1, kWave);
+    if (total == 0) continue;
+    int slot0 = 0;
+    if (lane == 0) slot0 = atomicAdd(&W.filt[row].ncand, total);
+    int slot = __shfl(slot0, 0, kWave) + incl - n;
+    uint64_t* cand = W.cand + (int64_t)row * kCand;
+#pragma unroll
+    for (int s = 0; s < kLaneChunkGroups; ++s) {
+#pragma unroll
+      for (int k = 0; k < kGroupElems; ++k) {
+        if (flags & (1u << (s * kGroupElems + k))) {
+          const float x = hs_div_temp(lane_chunk_val<T>(r, s, k), Tt, rT, fast);
+          const uint32_t i = (uint32_t)lane_chunk_idx(c0, s, lane, k);
+          if (slot < kCand) cand[slot] = ((uint64_t)hs_key(x) << 32) | (uint64_t)(0xffffffffu - i);
+          ++slot;
+        }
+      }
+    }
+  }
+}
+
 template <typename T>
 __global__ __launch_bounds__(kPT) void k_filter_pass2(Problem P, Work W) {
   __shared__ PassShared ps;
   const int tid = threadIdx.x;
-  const int64_t items = (int64_t)P.units * P.rows_per_unit * P.nchunk;
+  const int rows = P.units * P.rows_per_unit;
+  const int64_t items = (int64_t)W.flist[1] * P.nchunk;  // top-p rows only
   for (int64_t it = blockIdx.x; it < items; it += gridDim.x) {
-    const int row = (int)(it / P.nchunk);
+    const int row = W.flist[2 + rows + (int)(it / P.nchunk)];
     const int c = (int)(it % P.nchunk);
     const int unit = row / P.rows_per_unit;
     if (filter_mode(P, unit) != 2) continue;
@@ -860,9 +931,10 @@ template <typename T>
 __global__ __launch_bounds__(kPT) void k_filter_pass3(Problem P, Work W) {
   __shared__ PassShared ps;
   const int tid = threadIdx.x;
-  const int64_t items = (int64_t)P.units * P.rows_per_unit * P.nchunk;
+  const int rows = P.units * P.rows_per_unit;
+  const int64_t items = (int64_t)W.flist[1] * P.nchunk;  // top-p rows only
   for (int64_t it = blockIdx.x; it < items; it += gridDim.x) {
-    const int row = (int)(it / P.nchunk);
+    const int row = W.flist[2 + rows + (int)(it / P.nchunk)];
     const int c = (int)(it % P.nchunk);
     const int unit = row / P.rows_per_unit;
     if (filter_mode(P, unit) != 2) continue;
@@ -1292,12 +1364,23 @@ __global__ __launch_bounds__(kFT) void k_row_filter(Problem P, Work W, float* ro
 }
 
 template <typename T>
-int launch_filter(const Problem& P, const Work& W, float* row_stats, hipStream_t stream) {
+int launch_filter(const Problem& P, const Work& W, float* row_stats, bool wave,
+                  hipStream_t stream) {
   const int rows = P.units * P.rows_per_unit;
   const int64_t items = (int64_t)rows * P.nchunk;
   const int grid = (int)(items < 4096 ? items : 4096);
   hipLaunchKernelGGL(k_filter_plan1, dim3(rows), dim3(kPT), 0, stream, P, W);
-  hipLaunchKernelGGL(k_filter_pass1<T>, dim3(grid), dim3(kPT), 0, stream, P, W);
+  if (wave && rows >= 32) {
+    // top-k rows by the wave-per-chunk gather (at most the 6 workgroups per CU
+    // that fit at once on 256 CUs), top-p rows by the histogram pass; below 32
+    // rows one launch with a workgroup per chunk is shorter
+    const int64_t wgs = (items + kPT / kWave - 1) / (kPT / kWave);
+    hipLaunchKernelGGL(k_filter_gather_k<T>, dim3((int)(wgs < 1536 ? wgs : 1536)), dim3(kPT), 0,
+                       stream, P, W);
+    hipLaunchKernelGGL(k_filter_pass1<T>, dim3(grid), dim3(kPT), 0, stream, P, W, 1);
+  } else {
+    hipLaunchKernelGGL(k_filter_pass1<T>, dim3(grid), dim3(kPT), 0, stream, P, W, 0);
+  }
   hipLaunchKernelGGL(k_filter_plan2, dim3(rows), dim3(kPT), 0, stream, P, W);
   hipLaunchKernelGGL(k_filter_pass2<T>, dim3(grid), dim3(kPT), 0, stream, P, W);
   hipLaunchKernelGGL(k_filter_plan3, dim3(rows), dim3(kPT), 0, stream, P, W);
@@ -1306,7 +1389,7 @@ int launch_filter(const Problem& P, const Work& W, float* row_stats, hipStream_t
   return hipGetLastError() == hipSuccess ? HS_OK : HS_ERR_LAUNCH;
 }
 
-template int launch_filter<float>(const Problem&, const Work&, float*, hipStream_t);
-template int launch_filter<uint16_t>(const Problem&, const Work&, float*, hipStream_t);
+template int launch_filter<float>(const Problem&, const Work&, float*, bool, hipStream_t);
+template int launch_filter<uint16_t>(const Problem&, const Work&, float*, bool, hipStream_t);
 
 }  // namespace hs
