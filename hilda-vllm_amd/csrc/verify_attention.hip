@@ -68,6 +68,7 @@ struct AttnArgs {
   int* sk_pre;               // balanced launch: window prefix over the tiles [tiles + 1]
   int* sk_w0;                // balanced launch: first window of each workgroup [nwg + 1]
   int sk_nwg;                // balanced launch: workgroups
+  int xcd_pack;              // per-tile grid: only workgroups x % xcd_pack == 0 work
 };
 
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
@@ -487,14 +488,21 @@ __device__ __forceinline__ void attend_keys(const AttnArgs& a, const TileRef& t,
 // the 8 XCDs in turn and the later splits of short sequences are empty, so
 // split-fastest would leave the same XCDs idle; with 8 KV heads every XCD
 // gets one head of every sequence and split.
+// A small grid (at most one XCD's worth of workgroups) is packed onto one
+// XCD: the host launches xcd_pack = 8 times the x dimension and only the
+// workgroups with x % 8 == 0, which the dispatcher places on the same XCD,
+// do the work; otherwise the workgroups of the XCDs dispatched last start up
+// to ~2 us after the first (measured on an idle GPU; ~0.25 us in a graph).
 template <bool kFp8, int kG>
 __global__ __launch_bounds__(kAT) void k_verify_attn(AttnArgs a) {
   const int G = kG ? kG : a.G;
   __shared__ __attribute__((aligned(16))) uint8_t s_raw[AttnLds<kFp8>::kRawBytes];
   __shared__ float s_m[kAW][kRows], s_l[kAW][kRows];
   __shared__ int s_bt[kBtCap];
-  const int kvh = blockIdx.x / a.qtiles;
-  const int qt = blockIdx.x % a.qtiles;
+  if (blockIdx.x % a.xcd_pack) return;
+  const int bx = blockIdx.x / a.xcd_pack;
+  const int kvh = bx / a.qtiles;
+  const int qt = bx % a.qtiles;
   const int split = blockIdx.y;
   const int b = blockIdx.z;
   const int tid = threadIdx.x;
@@ -983,6 +991,7 @@ int hs_verify_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_he
     a.sk_pre = reinterpret_cast<int*>(a.part_ml + slots * 2);
     a.sk_w0 = a.sk_pre + ntiles + 1;
     a.sk_nwg = nwg;
+    a.xcd_pack = 1;
     if (heads) {
       if (a.fp8)
         launch_attn_sk<true, true>(G, nwg, s, a);
@@ -1005,7 +1014,9 @@ int hs_verify_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_he
   a.sk_pre = nullptr;
   a.sk_w0 = nullptr;
   a.sk_nwg = 0;
-  dim3 grid(num_kv_heads * a.qtiles, a.nsplit, num_seqs);
+  const int64_t wgs = (int64_t)num_kv_heads * a.qtiles * a.nsplit * num_seqs;
+  a.xcd_pack = (wgs <= 32) ? 8 : 1;  // 8 XCDs of 32 CUs; workgroup i runs on XCD i % 8
+  dim3 grid(a.xcd_pack * num_kv_heads * a.qtiles, a.nsplit, num_seqs);
   if (a.fp8)
     launch_attn<true>(G, grid, s, a);
   else
