@@ -454,8 +454,10 @@ def bench_adaptive(args, torch, hv):
     prompts ~ U[32, 128], every sequence decoding to --max-context tokens (default
     8192) in an FP8-e4m3 target cache of 256-token blocks whose pool holds 3/4 of
     what all sequences need at the end (block pressure: sequences wait for blocks
-    until others finish). Random-init 8B target / 0.6B draft, T=0.6, reference
-    acceptance, gamma from 3 adapted in [1, 8] (llm_engine.py:197-208)."""
+    until others finish; when none can proceed the longest is preempted and later
+    recomputed by prefill, scheduler.py:231-238,313-320). Random-init 8B target /
+    0.6B draft, T=0.6, reference acceptance, gamma from 3 adapted in [1, 8]
+    (llm_engine.py:197-208)."""
     import importlib as _il
     import numpy as np
     q3 = _il.import_module("hilda-vllm_amd.engine.qwen3_host")
@@ -479,20 +481,30 @@ def bench_adaptive(args, torch, hv):
     len0 = sum(runner.lengths())
     stream = torch.cuda.current_stream(dev)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    waited = 0
+    waited = preemptions = readmitted = 0
     t0 = time.perf_counter()
     e0.record(stream)
     steps = 0
     while steps < args.steps:
-        if bool(runner.state.finished.all()):
+        if runner.preempted:
+            readmitted += runner.readmit()
+        if bool(runner.state.finished.all()) and not runner.preempted:
             break
         runner.step_graph()
         G = runner._per_gamma[runner.history[-1][0]]
-        waited += int(((G.elig == 0) & (runner.state.finished == 0)).sum())
+        fin = runner.state.finished
+        waited += int(((G.elig == 0) & (fin == 0)).sum())
+        if int(G.elig.sum()) == 0 and not bool(fin.all()):
+            # no sequence could get its blocks: preempt the longest (scheduler.py:231-238
+            # preempts at the first miss; here sequences wait until none can proceed)
+            lens = runner.state.context_lens.masked_fill(fin.bool(), -1)
+            runner.preempt(int(torch.argmax(lens)))
+            preemptions += 1
         steps += 1
         if steps % 200 == 0:
             print(f"[adaptive] step {steps} tokens {sum(runner.lengths()) - len0} "
-                  f"gamma {runner.gamma}", file=sys.stderr, flush=True)
+                  f"gamma {runner.gamma} preempted {preemptions} readmitted {readmitted}",
+                  file=sys.stderr, flush=True)
     e1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
@@ -508,7 +520,9 @@ def bench_adaptive(args, torch, hv):
             "data": "synthetic (random-init weights, uniform-random prompt ids)",
             "config": {"workload": "config 4: adaptive gamma, FP8 KV, block pressure", "batch": B,
                        "max_context": ctx, "num_blocks": num_blocks, "blocks_needed_at_end": need},
-            "tokens_emitted": emitted, "all_finished": bool(runner.state.finished.all()),
+            "tokens_emitted": emitted,
+            "all_finished": bool(runner.state.finished.all()) and not runner.preempted,
+            "preemptions": preemptions, "readmissions": readmitted,
             "gamma_histogram": {str(k): gam.count(k) for k in sorted(set(gam))},
             "acceptance_rate": round(acc / max(prop, 1), 4), "sequence_steps_waiting_for_blocks": waited,
             "wall_s": round(wall, 2)}

@@ -81,6 +81,7 @@ class SpecRunner:
         self._per_gamma: dict[int, SimpleNamespace] = {}
         self.controller = AdaptiveGamma(gamma, max_gamma=self.max_gamma) if adaptive else None
         self.history: list[tuple[int, int, int]] = []  # (gamma, accepted, proposed) per step
+        self.preempted: list[int] = []  # sequences out of the batch until readmit(), next first
         self.last = None
 
     def _g(self, gamma: int | None = None) -> SimpleNamespace:
@@ -185,6 +186,83 @@ class SpecRunner:
         out = first.view(self.B, 1)
         ops.spec_commit(self.state, 0, out, torch.ones(self.B, dtype=torch.int32, device=dev))
         torch.cuda.synchronize()
+
+    # ------------------------------------------------------------------ preemption
+    def preempt(self, b: int):
+        """Scheduler.preempt (scheduler.py:313-320) of sequence b between steps: its
+        blocks return to the tail of the free list in reverse table order
+        (block_manager.py:84-92, deallocate) and it leaves the batch (finished = 1,
+        so prealloc and commit skip it) until readmit() has recomputed its KV; its
+        tokens and max_tokens stay. Like waiting.appendleft, the last one preempted
+        comes back first."""
+        st = self.state
+        n = int(st.num_seq_blocks[b])
+        table = st.block_tables[b, :n].cpu().tolist()
+        ref = st.ref_count.cpu()
+        ring = st.free_ring.cpu()
+        head, count = st.free_hdr.cpu().tolist()
+        for blk in reversed(table):
+            ref[blk] -= 1
+            if int(ref[blk]) == 0:
+                ring[(head + count) % self.num_blocks] = blk
+                count += 1
+        st.ref_count.copy_(ref)
+        st.free_ring.copy_(ring)
+        st.free_hdr.copy_(torch.tensor([head, count], dtype=torch.int32))
+        st.block_tables[b].fill_(-1)
+        st.num_seq_blocks[b] = 0
+        st.finished[b] = 1
+        self.preempted.insert(0, b)
+
+    @torch.inference_mode()
+    def readmit(self) -> int:
+        """Brings preempted sequences back while the free list holds the blocks of
+        their whole length (block_manager.py:59-82, allocate: from the front of the
+        free list) and one more block for every running sequence, so that a sequence
+        preempted for lack of blocks returns only once others have released some;
+        the target and draft K/V of every token but the last, which the next step
+        processes, are recomputed by prefill. Returns how many returned."""
+        st = self.state
+        back = 0
+        while self.preempted:
+            b = self.preempted[0]
+            n = int(st.context_lens[b])
+            need = -(-n // self.bs)
+            running = int((st.finished == 0).sum())
+            head, count = st.free_hdr.cpu().tolist()
+            if count < need + running:
+                break
+            ring = st.free_ring.cpu()
+            blocks = [int(ring[(head + i) % self.num_blocks]) for i in range(need)]
+            st.free_hdr.copy_(torch.tensor([(head + need) % self.num_blocks, count - need],
+                                           dtype=torch.int32))
+            idx = torch.tensor(blocks, dtype=torch.int64, device=self.device)
+            st.ref_count.index_fill_(0, idx, 1)
+            st.block_tables[b, :need] = idx.to(torch.int32)
+            st.num_seq_blocks[b] = need
+            self._prefill_rows(b, n - 1)
+            st.finished[b] = 0
+            self.preempted.pop(0)
+            back += 1
+        return back
+
+    def _prefill_rows(self, b: int, n: int):
+        """Target and draft K/V of tokens [0, n) of sequence b into its blocks."""
+        if n <= 0:
+            return
+        dev = self.device
+        st = self.state
+        ids = st.tokens[b, :n].clone()
+        pos = torch.arange(n, dtype=torch.int64, device=dev)
+        bt = st.block_tables[b:b + 1]
+        blk = bt[0, (pos // self.bs)].to(torch.int64)
+        slots = (blk * self.bs + pos % self.bs).to(torch.int32)
+        cu = torch.tensor([0, n], dtype=torch.int32, device=dev)
+        set_context(True, cu, cu, n, n, slots, None, bt)
+        self.target(ids, pos)
+        set_context(True, cu, cu, n, n, slots, None, bt)
+        self.draft(ids, pos)
+        reset_context()
 
     # ------------------------------------------------------------------ phases
     def draft_phase(self):

@@ -231,3 +231,48 @@ def _check_blocks(runner):
         else:
             assert int(nb[b]) == (int(lens[b]) + runner.bs - 1) // runner.bs
     assert int(st.free_hdr[1]) + int(nb.sum()) == runner.num_blocks
+
+
+def test_preemption_frees_blocks_and_recomputes(cuda):
+    """A pool that cannot hold every sequence to its end: when no sequence gets its
+    blocks the longest is preempted (scheduler.py:313-320: blocks back to the free
+    list, the sequence out of the batch) and readmitted once the free list holds its
+    whole length, its K/V recomputed by prefill. Every sequence must still reach its
+    max_tokens with the block accounting exact after every step."""
+    q3, sr = _mods()
+    g = _small(q3, layers=2)
+    target = q3.Qwen3Host(g, device=cuda, seed=71)
+    draft = q3.Qwen3Host(g, share_from=target)
+    B, bs = 4, 32
+    prompts = [list(range(20 + i, 20 + i + n)) for i, n in enumerate([33, 35, 37, 39])]
+    max_tokens = [150, 150, 150, 150]  # 6 blocks each at the end, 24 in all
+    num_blocks = 12                      # the 8 prompt blocks and 4 more
+    runner = sr.SpecRunner(target, draft, batch=B, gamma=3, max_model_len=400, block_size=bs,
+                           kv_cache_dtype="fp8", num_blocks=num_blocks, temperature=0.0,
+                           mode="greedy", adaptive=True, device=cuda)
+    runner.load_prompts(prompts)
+    st = runner.state
+    st.max_tokens.copy_(torch.tensor(max_tokens, dtype=torch.int32))
+    runner.prefill()
+    preempted = readmitted = 0
+    for step in range(600):
+        if runner.preempted:
+            readmitted += runner.readmit()
+            _check_blocks(runner)
+        fin = st.finished.cpu()
+        if bool(fin.all()) and not runner.preempted:
+            break
+        runner.step_graph()
+        G = runner._per_gamma[runner.history[-1][0]]
+        fin = st.finished.cpu()
+        if int(G.elig.sum()) == 0 and not bool(fin.all()):
+            lens = st.context_lens.cpu().masked_fill(fin.bool(), -1)
+            runner.preempt(int(torch.argmax(lens)))
+            preempted += 1
+        _check_blocks(runner)
+    torch.cuda.synchronize()
+    print(f"preempted {preempted} readmitted {readmitted} steps {step}", flush=True)
+    assert bool(st.finished.cpu().all()) and not runner.preempted, "sequences did not finish"
+    assert runner.lengths() == [len(p) + m for p, m in zip(prompts, max_tokens)]
+    assert preempted > 0 and readmitted == preempted
+    assert int(st.free_hdr[1]) == num_blocks
