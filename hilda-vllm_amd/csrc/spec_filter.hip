@@ -17,7 +17,9 @@
 //      chunk-parallel pass appends every element at or above it to the row's
 //      candidate list (a few dozen for ordinary logits); one workgroup per row
 //      sorts them in LDS and applies top-k and top-p (which only looks at the k
-//      survivors);
+//      survivors). From 32 rows up (aligned rows) the pass is k_filter_gather_k,
+//      one wave per chunk, reading only the chunks whose maximum reaches the
+//      bound; k_filter_plan1 lists the rows of each mode for the passes;
 //   2. top-p alone: chunk-parallel passes build an exact mass histogram over
 //      256 buckets of (M - x) * 8 (bucket 255 collects the zero masses), find
 //      the bucket where the cumulative mass reaches p and append its elements
