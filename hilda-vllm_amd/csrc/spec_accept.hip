@@ -12,7 +12,7 @@
 //      target row: chunk max m_c and E_c = sum floor(2^44 exp(x_i - m_c)).
 //      Target logits are read from HBM exactly once here. For 16-byte
 //      aligned rows with V % 8 == 0, k_chunk_stats_w does the same with one
-//      wave per chunk and the wave's next chunk in flight.
+//      wave per chunk.
 //   2. (filtered mode) k_row_filter, spec_filter.hip: top-k / top-p kept set
 //      and normaliser per row.
 //   3. k_sample_part   grid (splits, B). Every workgroup first recomputes the
@@ -99,8 +99,7 @@ __global__ __launch_bounds__(kT) void k_chunk_stats(Problem P, Work W) {
 }
 
 // The same statistics with one wave per chunk (aligned rows, V % 8 == 0):
-// no barrier, and each wave's next chunk is in flight while it reduces the
-// current one (waves stride over the items; buffers alternate).
+// no barrier; waves stride over the items.
 template <typename T>
 __device__ __forceinline__ void chunk_stats_wave(const Problem& P, const Work& W, int64_t it,
                                                  const LaneChunk<T>& r, int lane) {
@@ -169,17 +168,13 @@ __global__ __launch_bounds__(kT) void k_chunk_stats_w(Problem P, Work W) {
     const int64_t c0 = use ? (item % P.nchunk) * (int64_t)kChunk : 0;
     lane_chunk_load<T>(base + row * P.row_stride, c0, P.V, lane, use, r);
   };
-  LaneChunk<T> a, b;
-  load(it, a);
-  for (;;) {
-    load(it + stride, b);
+  // One chunk in registers at a time (60 VGPRs, 8 waves per SIMD): the other
+  // resident waves hide a wave's load latency, which measured faster than
+  // holding the next chunk in flight (80 VGPRs, 6 waves per SIMD).
+  for (; it < items; it += stride) {
+    LaneChunk<T> a;
+    load(it, a);
     chunk_stats_wave<T>(P, W, it, a, lane);
-    it += stride;
-    if (it >= items) break;
-    load(it + stride, a);
-    chunk_stats_wave<T>(P, W, it, b, lane);
-    it += stride;
-    if (it >= items) break;
   }
 }
 
@@ -632,10 +627,10 @@ int run_sampler_chain(const Problem& P0, const AcceptArgs& A, const Work& W, int
   }
   const bool wave = wave_chunks_ok<T>(P, A);
   if (wave) {
-    // one chunk per wave, at most the 6 workgroups (24 waves) per CU that fit
+    // one chunk per wave, at most the 8 workgroups (32 waves) per CU that fit
     // at once on 256 CUs
     const int64_t wgs = (items + kT / kWave - 1) / (kT / kWave);
-    hipLaunchKernelGGL(k_chunk_stats_w<T>, dim3((int)(wgs < 1536 ? wgs : 1536)), dim3(kT), 0,
+    hipLaunchKernelGGL(k_chunk_stats_w<T>, dim3((int)(wgs < 2048 ? wgs : 2048)), dim3(kT), 0,
                        stream, P, W);
   } else {
     hipLaunchKernelGGL(k_chunk_stats<T>, dim3(grid_items(items)), dim3(kT), 0, stream, P, W);
