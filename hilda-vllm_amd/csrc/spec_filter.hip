@@ -806,9 +806,11 @@ __global__ __launch_bounds__(kPT) void k_filter_pass1(Problem P, Work W, int onl
 // (row, chunk): a chunk whose maximum lies below the gather threshold holds no
 // candidate and is not read; the others append every element at or above it
 // (the same candidates as k_filter_pass1), placed by a wave scan of the
-// lanes' counts and one atomic per wave, with no barrier.
+// lanes' counts and one atomic per wave, with no barrier. Capped at 64 VGPRs
+// (8 waves per SIMD, no spills): resident waves hide the load latency.
 template <typename T>
-__global__ __launch_bounds__(kPT) void k_filter_gather_k(Problem P, Work W) {
+__global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_filter_gather_k(
+    Problem P, Work W) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int64_t items = (int64_t)W.flist[0] * P.nchunk;
   const int64_t stride = (int64_t)gridDim.x * (kPT / kWave);
@@ -1373,11 +1375,11 @@ int launch_filter(const Problem& P, const Work& W, float* row_stats, bool wave,
   const int grid = (int)(items < 4096 ? items : 4096);
   hipLaunchKernelGGL(k_filter_plan1, dim3(rows), dim3(kPT), 0, stream, P, W);
   if (wave && rows >= 32) {
-    // top-k rows by the wave-per-chunk gather (at most the 6 workgroups per CU
+    // top-k rows by the wave-per-chunk gather (at most the 8 workgroups per CU
     // that fit at once on 256 CUs), top-p rows by the histogram pass; below 32
     // rows one launch with a workgroup per chunk is shorter
     const int64_t wgs = (items + kPT / kWave - 1) / (kPT / kWave);
-    hipLaunchKernelGGL(k_filter_gather_k<T>, dim3((int)(wgs < 1536 ? wgs : 1536)), dim3(kPT), 0,
+    hipLaunchKernelGGL(k_filter_gather_k<T>, dim3((int)(wgs < 2048 ? wgs : 2048)), dim3(kPT), 0,
                        stream, P, W);
     hipLaunchKernelGGL(k_filter_pass1<T>, dim3(grid), dim3(kPT), 0, stream, P, W, 1);
   } else {
