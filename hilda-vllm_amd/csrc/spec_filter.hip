@@ -23,7 +23,7 @@
 //   2. top-p alone: chunk-parallel passes build an exact mass histogram over
 //      256 buckets of (M - x) * 8 (bucket 255 collects the zero masses), find
 //      the bucket where the cumulative mass reaches p and append its elements
-//      (or, when it holds more than 4096, refine it into 256 sub-buckets and
+//      (or, when it holds more than 256, refine it into 256 sub-buckets and
 //      append the boundary sub-bucket); the row workgroup sorts them and scans
 //      their masses from the histogram's prefix;
 //   3. otherwise (k above the chunk count, or more than 4096 candidates): the
@@ -521,14 +521,15 @@ __device__ __forceinline__ void scan_bucket(FilterSmem& sm, int n, float M, floa
 }
 
 // ---------------------------------------------------------------------------
-// Chunk-parallel filter passes (one 256-thread workgroup per 2048-element
-// chunk of a row, the geometry of k_chunk_stats).
+// Chunk-parallel filter passes (256-thread workgroups, 8 elements per thread
+// per 2048-element chunk, the geometry of k_chunk_stats; each workgroup takes
+// a segment of consecutive chunks of one row, see seg_plan).
 //   mode 1 (top-k with k <= chunks): pass 1 appends every element at or above
 //           the k-th largest chunk maximum to the row's candidate list;
 //   mode 2 (top-p alone): pass 1 accumulates exact masses into a 256-bucket
 //           histogram of (M - x) * 8 (bucket 255 collects the zero masses);
 //           pass 2 finds the coarse bucket where the cumulative mass reaches p
-//           and appends its elements (at most kCand of them), or else
+//           and appends its elements (at most kDirect of them), or else
 //           histograms them into 256 fine sub-buckets; pass 3 appends the
 //           elements of the fine boundary bucket.
 // k_row_filter then finishes each row in LDS from its candidates.
@@ -612,19 +613,20 @@ __device__ __forceinline__ Crossing find_crossing(uint64_t hc, uint64_t hm, uint
   return r;
 }
 
-// Appends the (up to 8) flagged elements of every thread of the workgroup to the
-// row's candidate list with one global atomic per workgroup.
-__device__ __forceinline__ void append_cands(const Work& W, int row, const uint32_t (&key)[8],
-                                             uint32_t flags, int64_t i0, int* s_cnt, int* s_base) {
-  const int tid = threadIdx.x;
-  if (tid == 0) *s_cnt = 0;
-  __syncthreads();
-  const int n = __popc(flags);
-  const int off = n ? atomicAdd(s_cnt, n) : 0;
-  __syncthreads();
-  if (tid == 0) *s_base = *s_cnt ? atomicAdd(&W.filt[row].ncand, *s_cnt) : 0;
-  __syncthreads();
-  int slot = *s_base + off;
+// Appends the (up to 8) flagged elements of every lane of the calling wave to
+// the row's candidate list: slots placed by a wave scan of the lanes' counts
+// and one global atomic per wave, no barrier. Slots past kCand are counted but
+// not written (the row filter then falls back to its radix select).
+__device__ __forceinline__ void wave_append_cands(const Work& W, int row, const uint32_t (&key)[8],
+                                                  uint32_t flags, int64_t i0) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t n = (uint32_t)__popc(flags);
+  const uint32_t incl = wave_incl_scan_u32(n, lane);
+  const uint32_t total = (uint32_t)__shfl((int)incl, kWave - 1, kWave);
+  if (total == 0) return;  // wave-uniform
+  int base = 0;
+  if (lane == 0) base = atomicAdd(&W.filt[row].ncand, (int)total);
+  int slot = __shfl(base, 0, kWave) + (int)(incl - n);
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     if (flags & (1u << k)) {
@@ -636,14 +638,45 @@ __device__ __forceinline__ void append_cands(const Work& W, int row, const uint3
   }
 }
 
-struct PassShared {
-  uint32_t keys[kCB];
+// Segments of consecutive chunks for the pass kernels: a workgroup takes one
+// segment of one row, with as many segments per row as fill the grid, so a
+// row's LDS histogram reaches global memory once per segment.
+// With nr rows in the list, nseg = max(1, grid / nr) segments per row, so
+// items = nr * nseg <= max(grid, rows) and all of the indexing is 32-bit.
+struct SegPlan {
+  int nseg, q, r, items;
+};
+__device__ __forceinline__ SegPlan seg_plan(const Problem& P, int nr) {
+  int nseg = nr > 0 ? (int)gridDim.x / nr : 1;
+  nseg = nseg < 1 ? 1 : (nseg > P.nchunk ? P.nchunk : nseg);
+  SegPlan sp;
+  sp.nseg = nseg;
+  sp.q = P.nchunk / nseg;
+  sp.r = P.nchunk - sp.q * nseg;
+  sp.items = nr * nseg;
+  return sp;
+}
+// chunks [c_lo, c_hi) of segment seg: the first r segments hold q + 1 chunks,
+// the others q
+__device__ __forceinline__ void seg_chunks(const SegPlan& sp, int seg, int& c_lo, int& c_hi) {
+  c_lo = seg * sp.q + (seg < sp.r ? seg : sp.r);
+  c_hi = c_lo + sp.q + (seg < sp.r ? 1 : 0);
+}
+
+struct alignas(16) PassShared {
+  uint32_t keys[kCB];  // first: read as uint4
   uint64_t wsum[kPT / 64];
   uint64_t hm[kCB], he[kCB];
   uint32_t hc[kCB];
   uint64_t v[3];
-  int b, cnt, base;
+  int b;
 };
+
+// 1 when key ke (slot e of ne) ranks above key kc: greater, or equal at a
+// lower chunk index
+__device__ __forceinline__ int rank_vs(uint32_t ke, uint32_t kc, int e, int ne, bool lower) {
+  return (e < ne && (ke > kc || (ke == kc && lower))) ? 1 : 0;
+}
 
 // Per row (one 256-thread workgroup): row max M and normaliser S (the fold of
 // the chunk statistics), the top-k gather threshold (mode 1: key of the keff-th
@@ -686,9 +719,13 @@ __global__ __launch_bounds__(kPT) void k_filter_plan1(Problem P, Work W) {
       ps.keys[tid] = (b2 + tid < P.nchunk) ? hs_key(cp[b2 + tid].m) : 0u;
       __syncthreads();
       const int ne = (P.nchunk - b2 < kCB) ? P.nchunk - b2 : kCB;
-      for (int e = 0; e < ne; ++e) {
-        const uint32_t ke = ps.keys[e];
-        rank += (ke > kc || (ke == kc && b2 + e < c)) ? 1 : 0;
+      // four keys per LDS read (all kCB slots are written), several in flight
+      const uint4* k4 = reinterpret_cast<const uint4*>(ps.keys);
+#pragma unroll 4
+      for (int e = 0; e < ne; e += 4) {
+        const uint4 q = k4[e >> 2];
+        rank += rank_vs(q.x, kc, e, ne, b2 + e < c) + rank_vs(q.y, kc, e + 1, ne, b2 + e + 1 < c) +
+                rank_vs(q.z, kc, e + 2, ne, b2 + e + 2 < c) + rank_vs(q.w, kc, e + 3, ne, b2 + e + 3 < c);
       }
     }
     if (c < P.nchunk && rank == keff - 1) f.tau = kc;
@@ -736,39 +773,45 @@ __global__ __launch_bounds__(kPT) void k_filter_plan3(Problem P, Work W) {
   }
 }
 
-// only2: walk the top-p rows only (k_filter_gather_k takes the top-k rows)
+// only2: walk the top-p rows only (k_filter_gather_k takes the top-k rows).
+// Workgroups take segments of chunks (seg_plan): a top-p row's histogram
+// accumulates in LDS over the segment and reaches global memory once (flushes
+// per chunk made the global atomics a third of the pass).
 template <typename T>
-__global__ __launch_bounds__(kPT) void k_filter_pass1(Problem P, Work W, int only2) {
+__global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_filter_pass1(
+    Problem P, Work W, int only2) {
   __shared__ PassShared ps;
   const int tid = threadIdx.x;
   const int rows = P.units * P.rows_per_unit;
-  const int64_t items = (int64_t)(only2 ? W.flist[1] : rows) * P.nchunk;
-  for (int64_t it = blockIdx.x; it < items; it += gridDim.x) {
-    const int row = only2 ? W.flist[2 + rows + (int)(it / P.nchunk)] : (int)(it / P.nchunk);
-    const int c = (int)(it % P.nchunk);
+  const SegPlan sp = seg_plan(P, only2 ? W.flist[1] : rows);
+  for (int it = blockIdx.x; it < sp.items; it += gridDim.x) {
+    const int ri = it / sp.nseg;
+    const int row = only2 ? W.flist[2 + rows + ri] : ri;
     const int unit = row / P.rows_per_unit;
     const int mode = filter_mode(P, unit);
     if (mode == 0) continue;
+    int c_lo, c_hi;
+    seg_chunks(sp, it - ri * sp.nseg, c_lo, c_hi);
     const float Tt = P.temps[unit];
     const float rT = 1.0f / Tt;
     const bool fast = hs_rcp_ok(Tt);
     const T* rp = reinterpret_cast<const T*>(P.logits) + (int64_t)row * P.row_stride;
     const bool vec_ok = ((reinterpret_cast<uintptr_t>(rp) & 15u) == 0);
-    const int64_t i0 = chunk_elem(c, tid, 0);
-    float x[8];
-    load8<T>(rp, i0, P.V, vec_ok, x);
-#pragma unroll
-    for (int k = 0; k < 8; ++k) x[k] = hs_div_temp(x[k], Tt, rT, fast);
     const FilterScratch& f = W.filt[row];
     if (mode == 1) {
       const uint32_t tau = f.tau;
-      uint32_t key[8], flags = 0;
+      for (int c = c_lo; c < c_hi; ++c) {
+        const int64_t i0 = chunk_elem(c, tid, 0);
+        float x[8];
+        load8<T>(rp, i0, P.V, vec_ok, x);
+        uint32_t key[8], flags = 0;
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        key[k] = hs_key(x[k]);
-        if (i0 + k < P.V && key[k] >= tau) flags |= 1u << k;
+        for (int k = 0; k < 8; ++k) {
+          key[k] = hs_key(hs_div_temp(x[k], Tt, rT, fast));
+          if (i0 + k < P.V && key[k] >= tau) flags |= 1u << k;
+        }
+        wave_append_cands(W, row, key, flags, i0);
       }
-      append_cands(W, row, key, flags, i0, &ps.cnt, &ps.base);
     } else {
       ps.hm[tid] = 0ull;
       ps.he[tid] = 0ull;
@@ -777,17 +820,23 @@ __global__ __launch_bounds__(kPT) void k_filter_pass1(Problem P, Work W, int onl
       const float M = f.m, S = f.s;
       const float rS = 1.0f / S;
       const bool fastS = hs_rcp_ok(S);
+      for (int c = c_lo; c < c_hi; ++c) {
+        const int64_t i0 = chunk_elem(c, tid, 0);
+        float x[8];
+        load8<T>(rp, i0, P.V, vec_ok, x);
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        if (i0 + k >= P.V) continue;
-        const int b = coarse_bucket(x[k], M);
-        atomicAdd(&ps.hc[b], 1u);
-        if (b < kCB - 1) {  // the last bucket holds only zero masses
-          const float e = hs_exp(x[k] - M);
-          const uint64_t em = hs_fx44(e);
-          const uint64_t mm = hs_fx44(hs_div_temp(e, S, rS, fastS));
-          if (mm) atomicAdd((unsigned long long*)&ps.hm[b], (unsigned long long)mm);
-          if (em) atomicAdd((unsigned long long*)&ps.he[b], (unsigned long long)em);
+        for (int k = 0; k < 8; ++k) {
+          if (i0 + k >= P.V) continue;
+          const float xv = hs_div_temp(x[k], Tt, rT, fast);
+          const int b = coarse_bucket(xv, M);
+          atomicAdd(&ps.hc[b], 1u);
+          if (b < kCB - 1) {  // the last bucket holds only zero masses
+            const float e = hs_exp(xv - M);
+            const uint64_t em = hs_fx44(e);
+            const uint64_t mm = hs_fx44(hs_div_temp(e, S, rS, fastS));
+            if (mm) atomicAdd((unsigned long long*)&ps.hm[b], (unsigned long long)mm);
+            if (em) atomicAdd((unsigned long long*)&ps.he[b], (unsigned long long)em);
+          }
         }
       }
       __syncthreads();
@@ -797,8 +846,8 @@ __global__ __launch_bounds__(kPT) void k_filter_pass1(Problem P, Work W, int onl
         if (ps.hm[tid]) atomicAdd((unsigned long long*)&W.h1m[hb], (unsigned long long)ps.hm[tid]);
         if (ps.he[tid]) atomicAdd((unsigned long long*)&W.h1e[hb], (unsigned long long)ps.he[tid]);
       }
+      __syncthreads();
     }
-    __syncthreads();
   }
 }
 
@@ -865,59 +914,68 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
   }
 }
 
+// Top-p rows, segments of chunks: the elements of the coarse boundary bucket
+// b1 are appended to the candidates, or, when b1 holds more than kDirect
+// elements, histogrammed into fine sub-buckets (LDS over the segment, one
+// flush per segment).
 template <typename T>
-__global__ __launch_bounds__(kPT) void k_filter_pass2(Problem P, Work W) {
+__global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_filter_pass2(
+    Problem P, Work W) {
   __shared__ PassShared ps;
   const int tid = threadIdx.x;
   const int rows = P.units * P.rows_per_unit;
-  const int64_t items = (int64_t)W.flist[1] * P.nchunk;  // top-p rows only
-  for (int64_t it = blockIdx.x; it < items; it += gridDim.x) {
-    const int row = W.flist[2 + rows + (int)(it / P.nchunk)];
-    const int c = (int)(it % P.nchunk);
+  const SegPlan sp = seg_plan(P, W.flist[1]);  // top-p rows only
+  for (int it = blockIdx.x; it < sp.items; it += gridDim.x) {
+    const int ri = it / sp.nseg;
+    const int row = W.flist[2 + rows + ri];
     const int unit = row / P.rows_per_unit;
     if (filter_mode(P, unit) != 2) continue;
     const FilterScratch& f = W.filt[row];
     const int b1 = f.b1;
     if (b1 < 0) continue;
-    const bool fine = W.h1c[(int64_t)row * kCB + b1] > kDirect;
+    const bool fine = W.h1c[(int64_t)row * kCB + b1] > kDirect;  // workgroup-uniform
     if (fine) {
       ps.hm[tid] = 0ull;
       ps.he[tid] = 0ull;
       ps.hc[tid] = 0u;
       __syncthreads();
     }
+    int c_lo, c_hi;
+    seg_chunks(sp, it - ri * sp.nseg, c_lo, c_hi);
     const float M = f.m, S = f.s;
     const float Tt = P.temps[unit];
     const float rT = 1.0f / Tt;
     const bool fast = hs_rcp_ok(Tt);
     const T* rp = reinterpret_cast<const T*>(P.logits) + (int64_t)row * P.row_stride;
     const bool vec_ok = ((reinterpret_cast<uintptr_t>(rp) & 15u) == 0);
-    const int64_t i0 = chunk_elem(c, tid, 0);
-    float x[8];
-    load8<T>(rp, i0, P.V, vec_ok, x);
     const float rS = 1.0f / S;
     const bool fastS = hs_rcp_ok(S);
-    uint32_t key[8], flags = 0;
+    for (int c = c_lo; c < c_hi; ++c) {
+      const int64_t i0 = chunk_elem(c, tid, 0);
+      float x[8];
+      load8<T>(rp, i0, P.V, vec_ok, x);
+      uint32_t key[8], flags = 0;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      key[k] = 0;
-      if (i0 + k >= P.V) continue;
-      const float xv = hs_div_temp(x[k], Tt, rT, fast);
-      if (coarse_bucket(xv, M) != b1) continue;
-      if (!fine) {
-        key[k] = hs_key(xv);
-        flags |= 1u << k;
-      } else {
-        const int b = fine_bucket(xv, M, b1);
-        const float e = hs_exp(xv - M);
-        atomicAdd(&ps.hc[b], 1u);
-        const uint64_t mm = hs_fx44(hs_div_temp(e, S, rS, fastS));
-        const uint64_t em = hs_fx44(e);
-        if (mm) atomicAdd((unsigned long long*)&ps.hm[b], (unsigned long long)mm);
-        if (em) atomicAdd((unsigned long long*)&ps.he[b], (unsigned long long)em);
+      for (int k = 0; k < 8; ++k) {
+        key[k] = 0;
+        if (i0 + k >= P.V) continue;
+        const float xv = hs_div_temp(x[k], Tt, rT, fast);
+        if (coarse_bucket(xv, M) != b1) continue;
+        if (!fine) {
+          key[k] = hs_key(xv);
+          flags |= 1u << k;
+        } else {
+          const int b = fine_bucket(xv, M, b1);
+          const float e = hs_exp(xv - M);
+          atomicAdd(&ps.hc[b], 1u);
+          const uint64_t mm = hs_fx44(hs_div_temp(e, S, rS, fastS));
+          const uint64_t em = hs_fx44(e);
+          if (mm) atomicAdd((unsigned long long*)&ps.hm[b], (unsigned long long)mm);
+          if (em) atomicAdd((unsigned long long*)&ps.he[b], (unsigned long long)em);
+        }
       }
+      if (!fine) wave_append_cands(W, row, key, flags, i0);
     }
-    if (!fine) append_cands(W, row, key, flags, i0, &ps.cnt, &ps.base);
     if (fine) {
       __syncthreads();
       const int64_t hb = (int64_t)row * kCB + tid;
@@ -926,47 +984,52 @@ __global__ __launch_bounds__(kPT) void k_filter_pass2(Problem P, Work W) {
         if (ps.hm[tid]) atomicAdd((unsigned long long*)&W.h2m[hb], (unsigned long long)ps.hm[tid]);
         if (ps.he[tid]) atomicAdd((unsigned long long*)&W.h2e[hb], (unsigned long long)ps.he[tid]);
       }
+      __syncthreads();
     }
-    __syncthreads();
   }
 }
 
+// Refined top-p rows, segments of chunks: appends the elements of fine
+// sub-bucket b2 of coarse bucket b1 (no LDS, no barrier).
 template <typename T>
-__global__ __launch_bounds__(kPT) void k_filter_pass3(Problem P, Work W) {
-  __shared__ PassShared ps;
+__global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_filter_pass3(
+    Problem P, Work W) {
   const int tid = threadIdx.x;
   const int rows = P.units * P.rows_per_unit;
-  const int64_t items = (int64_t)W.flist[1] * P.nchunk;  // top-p rows only
-  for (int64_t it = blockIdx.x; it < items; it += gridDim.x) {
-    const int row = W.flist[2 + rows + (int)(it / P.nchunk)];
-    const int c = (int)(it % P.nchunk);
+  const SegPlan sp = seg_plan(P, W.flist[1]);  // top-p rows only
+  for (int it = blockIdx.x; it < sp.items; it += gridDim.x) {
+    const int ri = it / sp.nseg;
+    const int row = W.flist[2 + rows + ri];
     const int unit = row / P.rows_per_unit;
     if (filter_mode(P, unit) != 2) continue;
     const FilterScratch& f = W.filt[row];
     const int b1 = f.b1, b2 = f.b2;
     if (b1 < 0 || b2 < 0) continue;
+    int c_lo, c_hi;
+    seg_chunks(sp, it - ri * sp.nseg, c_lo, c_hi);
     const float M = f.m;
     const float Tt = P.temps[unit];
     const float rT = 1.0f / Tt;
     const bool fast = hs_rcp_ok(Tt);
     const T* rp = reinterpret_cast<const T*>(P.logits) + (int64_t)row * P.row_stride;
     const bool vec_ok = ((reinterpret_cast<uintptr_t>(rp) & 15u) == 0);
-    const int64_t i0 = chunk_elem(c, tid, 0);
-    float x[8];
-    load8<T>(rp, i0, P.V, vec_ok, x);
-    uint32_t key[8], flags = 0;
+    for (int c = c_lo; c < c_hi; ++c) {
+      const int64_t i0 = chunk_elem(c, tid, 0);
+      float x[8];
+      load8<T>(rp, i0, P.V, vec_ok, x);
+      uint32_t key[8], flags = 0;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      key[k] = 0;
-      if (i0 + k >= P.V) continue;
-      const float xv = hs_div_temp(x[k], Tt, rT, fast);
-      if (coarse_bucket(xv, M) == b1 && fine_bucket(xv, M, b1) == b2) {
-        key[k] = hs_key(xv);
-        flags |= 1u << k;
+      for (int k = 0; k < 8; ++k) {
+        key[k] = 0;
+        if (i0 + k >= P.V) continue;
+        const float xv = hs_div_temp(x[k], Tt, rT, fast);
+        if (coarse_bucket(xv, M) == b1 && fine_bucket(xv, M, b1) == b2) {
+          key[k] = hs_key(xv);
+          flags |= 1u << k;
+        }
       }
+      wave_append_cands(W, row, key, flags, i0);
     }
-    append_cands(W, row, key, flags, i0, &ps.cnt, &ps.base);
-    __syncthreads();
   }
 }
 
@@ -1372,7 +1435,9 @@ int launch_filter(const Problem& P, const Work& W, float* row_stats, bool wave,
                   hipStream_t stream) {
   const int rows = P.units * P.rows_per_unit;
   const int64_t items = (int64_t)rows * P.nchunk;
-  const int grid = (int)(items < 4096 ? items : 4096);
+  // passes 1-3: the 8 workgroups per CU that fit at once on 256 CUs, each
+  // taking a segment of chunks of one row
+  const int grid1 = (int)(items < 2048 ? items : 2048);
   hipLaunchKernelGGL(k_filter_plan1, dim3(rows), dim3(kPT), 0, stream, P, W);
   if (wave && rows >= 32) {
     // top-k rows by the wave-per-chunk gather (at most the 8 workgroups per CU
@@ -1381,14 +1446,14 @@ int launch_filter(const Problem& P, const Work& W, float* row_stats, bool wave,
     const int64_t wgs = (items + kPT / kWave - 1) / (kPT / kWave);
     hipLaunchKernelGGL(k_filter_gather_k<T>, dim3((int)(wgs < 2048 ? wgs : 2048)), dim3(kPT), 0,
                        stream, P, W);
-    hipLaunchKernelGGL(k_filter_pass1<T>, dim3(grid), dim3(kPT), 0, stream, P, W, 1);
+    hipLaunchKernelGGL(k_filter_pass1<T>, dim3(grid1), dim3(kPT), 0, stream, P, W, 1);
   } else {
-    hipLaunchKernelGGL(k_filter_pass1<T>, dim3(grid), dim3(kPT), 0, stream, P, W, 0);
+    hipLaunchKernelGGL(k_filter_pass1<T>, dim3(grid1), dim3(kPT), 0, stream, P, W, 0);
   }
   hipLaunchKernelGGL(k_filter_plan2, dim3(rows), dim3(kPT), 0, stream, P, W);
-  hipLaunchKernelGGL(k_filter_pass2<T>, dim3(grid), dim3(kPT), 0, stream, P, W);
+  hipLaunchKernelGGL(k_filter_pass2<T>, dim3(grid1), dim3(kPT), 0, stream, P, W);
   hipLaunchKernelGGL(k_filter_plan3, dim3(rows), dim3(kPT), 0, stream, P, W);
-  hipLaunchKernelGGL(k_filter_pass3<T>, dim3(grid), dim3(kPT), 0, stream, P, W);
+  hipLaunchKernelGGL(k_filter_pass3<T>, dim3(grid1), dim3(kPT), 0, stream, P, W);
   hipLaunchKernelGGL(k_row_filter<T>, dim3(rows), dim3(kFT), 0, stream, P, W, row_stats);
   return hipGetLastError() == hipSuccess ? HS_OK : HS_ERR_LAUNCH;
 }
