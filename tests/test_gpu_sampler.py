@@ -327,3 +327,41 @@ def test_filter_fast_paths_random_rows(hv, orc, cuda, k, p):
     np.testing.assert_array_equal(r["probs"].cpu().numpy(), ref["probs"])
     np.testing.assert_array_equal(r["tokens"].cpu().numpy(), ref["tokens"])
     np.testing.assert_array_equal(r["row_stats"].cpu().numpy(), ref["row_stats"])
+
+
+@pytest.mark.parametrize("dtype,unaligned", [("bf16", False), ("f32", False), ("bf16", True)])
+def test_filter_segmented_passes_many_rows(hv, orc, cuda, dtype, unaligned):
+    """128 rows, 108 of them top-p alone: the filter passes give each workgroup a segment of
+    4-5 consecutive chunks of one row (histograms accumulate over the segment), and the
+    temperatures put the boundary bucket both below and above the refinement threshold.
+    Unaligned rows send the top-k rows through the same segmented pass."""
+    rng = np.random.default_rng(71)
+    V, R = 151936, 128
+    x = rng.standard_normal((R, V), dtype=np.float32) * 2
+    if dtype == "bf16":
+        bits = hv.synthetic.f32_to_bf16_bits(x)
+        xf = hv.synthetic.bf16_bits_to_f32(bits)
+        lg = torch.from_numpy(bits.view(np.int16)).to(cuda).view(torch.bfloat16)
+    else:
+        xf = x
+        lg = torch.from_numpy(x).to(cuda)
+    if unaligned:  # odd row stride, rows 2 bytes past a 16-byte boundary
+        big = torch.zeros((R, V + 3), dtype=lg.dtype, device=cuda)
+        big[:, 1:V + 1] = lg
+        lg = big[:, 1:V + 1]
+    T = rng.choice(np.array([0.6, 0.8, 1.0, 1.3], np.float32), R)
+    tk = np.zeros(R, np.int32)
+    tk[:8] = 20
+    tk[8:12] = 50
+    tp = rng.choice(np.array([0.5, 0.8, 0.9, 0.95], np.float32), R)
+    tp[:12] = 1.0
+    tp[120:] = 1.0
+    u = rng.random(R).astype(np.float32)
+    print(f"segmented filter passes {dtype} unaligned={unaligned}", flush=True)
+    r = hv.ops.sample_rows(lg, torch.from_numpy(T).to(cuda), torch.from_numpy(tk).to(cuda),
+                           torch.from_numpy(tp).to(cuda), mode="filtered",
+                           uniforms=torch.from_numpy(u).to(cuda), want_probs=True, row_stats=True)
+    ref = orc.sampler(xf, T, tk, tp, mode="filtered", uniforms=u)
+    np.testing.assert_array_equal(r["probs"].cpu().numpy(), ref["probs"])
+    np.testing.assert_array_equal(r["tokens"].cpu().numpy(), ref["tokens"])
+    np.testing.assert_array_equal(r["row_stats"].cpu().numpy(), ref["row_stats"])
