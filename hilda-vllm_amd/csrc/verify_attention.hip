@@ -185,16 +185,21 @@ struct TileRef {
   int b, kvh, qt, qs, Lq, Lk, rows;
 };
 
-__device__ __forceinline__ TileRef tile_ref(const AttnArgs& a, int b, int kvh, int qt, int G) {
+// from the sequence's bounds cu_q[b], cu_q[b + 1], cu_k[b], cu_k[b + 1]
+__device__ __forceinline__ TileRef tile_ref_of(int b, int kvh, int qt, int G, int q0, int q1,
+                                               int k0, int k1) {
   TileRef t;
   t.b = b;
   t.kvh = kvh;
   t.qt = qt;
-  t.qs = a.cu_q[b];
-  t.Lq = a.cu_q[b + 1] - t.qs;
-  t.Lk = a.cu_k[b + 1] - a.cu_k[b];
+  t.qs = q0;
+  t.Lq = q1 - q0;
+  t.Lk = k1 - k0;
   t.rows = t.Lq * G;
   return t;
+}
+__device__ __forceinline__ TileRef tile_ref(const AttnArgs& a, int b, int kvh, int qt, int G) {
+  return tile_ref_of(b, kvh, qt, G, a.cu_q[b], a.cu_q[b + 1], a.cu_k[b], a.cu_k[b + 1]);
 }
 
 // keys of the sequence visible to the tile's last row (0 for an empty tile)
@@ -499,6 +504,11 @@ __global__ __launch_bounds__(kAT) void k_verify_attn(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t s_raw[AttnLds<kFp8>::kRawBytes];
   __shared__ float s_m[kAW][kRows], s_l[kAW][kRows];
   __shared__ int s_bt[kBtCap];
+  // Small calls are latency-bound: every memory round trip before the first
+  // K/V window is issued adds to the kernel. The argument block's four 64-byte
+  // lines are requested together (one use of a field in each), not one miss
+  // per line as fields are first needed.
+  asm volatile("" ::"s"(a.q), "s"(a.bt), "s"(a.block_size), "s"(a.xcd_pack));
   if (blockIdx.x % a.xcd_pack) return;
   const int bx = blockIdx.x / a.xcd_pack;
   const int kvh = bx / a.qtiles;
@@ -507,16 +517,25 @@ __global__ __launch_bounds__(kAT) void k_verify_attn(AttnArgs a) {
   const int b = blockIdx.z;
   const int tid = threadIdx.x;
 
-  // block-table entries this split can touch, fetched before the sequence
-  // lengths are known (they only depend on the split)
+  // The sequence bounds and the block-table entries this split can touch
+  // (they only depend on the split) are requested before either is waited on.
+  const int cq0 = a.cu_q[b], cq1 = a.cu_q[b + 1], ck0 = a.cu_k[b], ck1 = a.cu_k[b + 1];
   const int lo = split * a.split_len;
   const int bt0 = lo / a.block_size;
-  {
-    int nbt = (lo + a.split_len - 1) / a.block_size - bt0 + 1;
-    if (nbt > a.bt_width - bt0) nbt = a.bt_width - bt0;
-    for (int i = tid; i < nbt && i < kBtCap; i += kAT) s_bt[i] = a.bt[(int64_t)b * a.bt_stride + bt0 + i];
-  }
-  const TileRef t = tile_ref(a, b, kvh, qt, G);
+  int nbt = (lo + a.split_len - 1) / a.block_size - bt0 + 1;
+  if (nbt > a.bt_width - bt0) nbt = a.bt_width - bt0;
+  if (nbt > kBtCap) nbt = kBtCap;
+  const int32_t* btrow = a.bt + (int64_t)b * a.bt_stride;
+  // branchless (a branch here would wait for the bounds first): entry
+  // bt0 + tid clamped into the row (bt_width >= 1, checked by the host)
+  const int bi = bt0 + tid < a.bt_width ? bt0 + tid : a.bt_width - 1;
+  const int bt_mine = btrow[bi];
+  // one wait for all five loads (otherwise the compiler sinks the table load
+  // into the store below, behind the wait for the bounds)
+  asm volatile("" ::"v"(bt_mine), "v"(cq0), "v"(cq1), "v"(ck0), "v"(ck1));
+  const TileRef t = tile_ref_of(b, kvh, qt, G, cq0, cq1, ck0, ck1);
+  if (tid < nbt) s_bt[tid] = bt_mine;
+  for (int i = tid + kAT; i < nbt; i += kAT) s_bt[i] = btrow[bt0 + i];
   if (qt * kRows >= t.rows || t.Lk <= 0) return;
   const int nsplit_b = (t.Lk + a.split_len - 1) / a.split_len;
   if (split >= nsplit_b) return;
