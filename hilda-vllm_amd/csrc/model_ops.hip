@@ -175,6 +175,9 @@ __device__ __forceinline__ void store_pair(uint8_t* base, int64_t elem, int lane
 // Slots < 0 (and blocks beyond num_blocks) store nothing, as store_kvcache.
 template <bool kFp8>
 __global__ __launch_bounds__(kNT) void k_qk_norm_rope_store(NormRopeStoreArgs a) {
+  // the argument block's three 64-byte lines requested together (latency-bound
+  // at decode sizes)
+  asm volatile("" ::"s"(a.qkv), "s"(a.qo), "s"(a.block_size));
   const int wave = blockIdx.x * (kNT / 64) + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int H = a.Hq + 2 * a.Hkv;

@@ -319,6 +319,10 @@ __device__ __forceinline__ void tile_step(uint4 (&wv)[S][EPI ? 2 * kR : kR],
 
 template <int M, int S, int EPI, bool NORM, bool RES>
 __global__ __launch_bounds__(kMaxWaves * 64) void k_skinny(SkinnyArgs a) {
+  // the argument block's two 64-byte lines (the second also holds the hidden
+  // launch arguments) requested together, not one miss each as fields are
+  // first used: small calls are latency-bound
+  asm volatile("" ::"s"(a.X), "s"(a.rs_in));
   constexpr int RR = EPI ? 2 * kR : kR;  // weight rows of a tile
   __shared__ float s_part[2][kMaxWaves][RR * M];
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
