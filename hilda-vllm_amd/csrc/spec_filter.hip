@@ -23,8 +23,10 @@
 //   2. top-p alone: chunk-parallel passes build an exact mass histogram over
 //      256 buckets of (M - x) * 8 (bucket 255 collects the zero masses), find
 //      the bucket where the cumulative mass reaches p and append its elements
-//      (or, when it holds more than 256, refine it into 256 sub-buckets and
-//      append the boundary sub-bucket); the row workgroup sorts them and scans
+//      (or, when it holds more than 256, refine it into 256 sub-buckets: up to
+//      4096 elements the whole bucket is still appended and the row workgroup
+//      keeps the boundary sub-bucket's, above that a third pass appends them);
+//      the row workgroup sorts them and scans
 //      their masses from the histogram's prefix;
 //   3. otherwise (k above the chunk count, or more than 4096 candidates): the
 //      row workgroup runs 8-bit radix passes over the order key with count /
@@ -530,8 +532,10 @@ __device__ __forceinline__ void scan_bucket(FilterSmem& sm, int n, float M, floa
 //           histogram of (M - x) * 8 (bucket 255 collects the zero masses);
 //           pass 2 finds the coarse bucket where the cumulative mass reaches p
 //           and appends its elements (at most kDirect of them), or else
-//           histograms them into 256 fine sub-buckets; pass 3 appends the
-//           elements of the fine boundary bucket.
+//           histograms them into 256 fine sub-buckets (still appending them
+//           all when they fit the kCand list, for k_row_filter to pick the
+//           fine boundary bucket from); otherwise pass 3 appends the elements
+//           of the fine boundary bucket.
 // k_row_filter then finishes each row in LDS from its candidates.
 // ---------------------------------------------------------------------------
 constexpr int kPT = kChunkThreads;
@@ -915,9 +919,9 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
 }
 
 // Top-p rows, segments of chunks: the elements of the coarse boundary bucket
-// b1 are appended to the candidates, or, when b1 holds more than kDirect
+// b1 are appended to the candidates, and, when b1 holds more than kDirect
 // elements, histogrammed into fine sub-buckets (LDS over the segment, one
-// flush per segment).
+// flush per segment); above kCand elements they are only histogrammed.
 template <typename T>
 __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_filter_pass2(
     Problem P, Work W) {
@@ -933,7 +937,12 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
     const FilterScratch& f = W.filt[row];
     const int b1 = f.b1;
     if (b1 < 0) continue;
-    const bool fine = W.h1c[(int64_t)row * kCB + b1] > kDirect;  // workgroup-uniform
+    const uint32_t c1 = W.h1c[(int64_t)row * kCB + b1];
+    const bool fine = c1 > kDirect;  // workgroup-uniform
+    // a refined bucket that fits the candidate list is also listed whole: the
+    // row filter then picks the fine boundary sub-bucket out of the list and
+    // pass 3 skips the row
+    const bool listed = c1 <= (uint32_t)kCand;
     if (fine) {
       ps.hm[tid] = 0ull;
       ps.he[tid] = 0ull;
@@ -961,10 +970,11 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
         if (i0 + k >= P.V) continue;
         const float xv = hs_div_temp(x[k], Tt, rT, fast);
         if (coarse_bucket(xv, M) != b1) continue;
-        if (!fine) {
+        if (listed) {
           key[k] = hs_key(xv);
           flags |= 1u << k;
-        } else {
+        }
+        if (fine) {
           const int b = fine_bucket(xv, M, b1);
           const float e = hs_exp(xv - M);
           atomicAdd(&ps.hc[b], 1u);
@@ -974,7 +984,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
           if (em) atomicAdd((unsigned long long*)&ps.he[b], (unsigned long long)em);
         }
       }
-      if (!fine) wave_append_cands(W, row, key, flags, i0);
+      if (listed) wave_append_cands(W, row, key, flags, i0);
     }
     if (fine) {
       __syncthreads();
@@ -1005,6 +1015,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
     const FilterScratch& f = W.filt[row];
     const int b1 = f.b1, b2 = f.b2;
     if (b1 < 0 || b2 < 0) continue;
+    if (W.h1c[(int64_t)row * kCB + b1] <= (uint32_t)kCand) continue;  // listed by pass 2
     int c_lo, c_hi;
     seg_chunks(sp, it - ri * sp.nseg, c_lo, c_hi);
     const float M = f.m;
@@ -1040,6 +1051,30 @@ __device__ __forceinline__ void load_cands(const Work& W, int row, int n, Filter
   __syncthreads();
 }
 
+// Keeps the n candidates in LDS whose value lies in fine sub-bucket b2 of
+// coarse bucket b1 (kFT threads; order not kept, the list is sorted next).
+// The key -> value map is exact, so this selects what pass 3 would append.
+__device__ __forceinline__ int keep_fine_bucket(FilterSmem& sm, int n, float M, int b1, int b2) {
+  constexpr int kPer = kCand / kFT;
+  uint64_t c[kPer];
+  uint32_t flags = 0;
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int i = threadIdx.x + k * kFT;
+    c[k] = i < n ? sm.cand[i] : 0ull;
+    if (i < n && fine_bucket(hs_unkey(cand_key(c[k])), M, b1) == b2) flags |= 1u << k;
+  }
+  uint64_t total;
+  const uint64_t off = block_excl_scan((uint64_t)__popc(flags), sm.wsum, &total);
+  __syncthreads();  // every read of the list precedes the writes below
+  int slot = (int)off;
+#pragma unroll
+  for (int k = 0; k < kPer; ++k)
+    if (flags & (1u << k)) sm.cand[slot++] = c[k];
+  __syncthreads();
+  return (int)total;
+}
+
 // Top-p boundary of a mode-2 row from its histograms and candidates (kFT
 // threads). Returns false when the candidates overflowed (radix fallback).
 struct TopP {
@@ -1058,11 +1093,18 @@ __device__ __forceinline__ bool top_p_from_hist(const Work& W, int row, FilterSm
     out.all = true;
     return true;
   }
-  if (W.h1c[(int64_t)row * kCB + b1] > kDirect && f.b2 < 0) return false;
+  const uint32_t c1 = W.h1c[(int64_t)row * kCB + b1];
+  if (c1 > kDirect && f.b2 < 0) return false;
   const uint64_t ac = f.ac, am = f.am, ae = f.ae;
-  const int n = W.filt[row].ncand;
+  int n = W.filt[row].ncand;
   if (n > kCand || n <= 0) return false;
   load_cands(W, row, n, sm);
+  if (c1 > kDirect && c1 <= (uint32_t)kCand) {
+    // pass 2 listed the whole coarse bucket: keep its fine boundary sub-bucket
+    // (the elements pass 3 would have appended)
+    n = keep_fine_bucket(sm, n, f.m, b1, f.b2);
+    if (n <= 0) return false;
+  }
   (void)pad_sort(sm, n);
   int j;
   uint64_t ej;  // e-mass of the bucket's ranks before j
