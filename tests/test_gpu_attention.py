@@ -157,6 +157,18 @@ def test_batch1_verify_shape_of_8b_target(hv, attn, cuda):
 
 
 @pytest.mark.parametrize("kv", ["bf16", "fp8"])
+def test_batch1_decode_shape_of_draft(hv, attn, cuda, kv):
+    """B=1, one query, 16 Q / 8 KV heads: the draft's decode shape in config 3. The block
+    table is exactly two entries wide, so most threads of the prologue read the clamped
+    last entry and discard it."""
+    print(f"draft decode shape {kv}", flush=True)
+    w = hv.synthetic.attention_workload(batch=1, q_len=1, num_q_heads=16, num_kv_heads=8,
+                                        lens=[324], seed=12)
+    assert w["block_tables"].shape == (1, 2)
+    _run(hv, attn, w, cuda, kv=kv)
+
+
+@pytest.mark.parametrize("kv", ["bf16", "fp8"])
 def test_store_kvcache(hv, attn, cuda, kv):
     rng = np.random.default_rng(7)
     nb, bs, H, D = 6, 32, 8, 128
