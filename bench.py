@@ -273,11 +273,46 @@ def bench_attention(args, torch, hv):
     return res
 
 
+def _host_cores():
+    """(os.cpu_count(), nproc): the machine's logical CPUs and those this process
+    may run on (its affinity mask, what `nproc` prints)."""
+    n_os = os.cpu_count() or 1
+    try:
+        n_proc = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n_proc = n_os
+    return n_os, n_proc
+
+
+def _timed_at_threads(torch, fn, threads: int, seconds: float, min_iters: int):
+    torch.set_num_threads(threads)
+    fn()
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds and n >= min_iters:
+            break
+    return el / n, n, el
+
+
+def _cpu_legs(torch, fn, seconds: float, min_iters: int):
+    """Times fn at every usable core (nproc threads), at os.cpu_count() threads when
+    that differs, and at 1 thread; the fastest multi-thread leg is the baseline."""
+    n_os, n_proc = _host_cores()
+    legs = {}
+    for th in sorted({n_proc, n_os} - {1}) or [1]:
+        legs[th] = _timed_at_threads(torch, fn, th, seconds, min_iters)
+    legs[1] = _timed_at_threads(torch, fn, 1, seconds, min_iters)
+    best = min((k for k in legs if k != 1), key=lambda k: legs[k][0], default=1)
+    torch.set_num_threads(n_proc)
+    return legs, best, n_os, n_proc
+
+
 def cpu_baseline_accept(torch, w, seconds: float):
     from oracle import torch_port
-    cores = os.cpu_count() or 1
-    cores = min(cores, 16)
-    torch.set_num_threads(cores)
     lg = torch.from_numpy(w["logits"])  # bf16-rounded values as f32
     lg = lg.to(torch.bfloat16)
     q = torch.from_numpy(w["draft_probs"])
@@ -285,19 +320,18 @@ def cpu_baseline_accept(torch, w, seconds: float):
     T = torch.from_numpy(w["temperatures"])
     ua = torch.from_numpy(w["u_accept"])
     ur = torch.from_numpy(w["u_resample"])
-    for _ in range(3):
+
+    def fn():
         torch_port.run_verify_accept(lg, q, dt, T, ua, ur)
-    n = 0
-    t0 = time.perf_counter()
-    while True:
-        torch_port.run_verify_accept(lg, q, dt, T, ua, ur)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= seconds and n >= 5:
-            break
-    return {"value": round(el / n * 1e6, 1), "unit": "us/step (fused acceptance)",
-            "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"{n} acceptance steps at B=1 gamma=3 V=151936 over {el:.1f} s "
+
+    legs, best, n_os, n_proc = _cpu_legs(torch, fn, seconds, 5)
+    per, n, el = legs[best]
+    return {"value": round(per * 1e6, 1), "unit": "us/step (fused acceptance)",
+            "cores": best, "kind": "port",
+            "single_thread": {"value": round(legs[1][0] * 1e6, 1), "cores": 1},
+            "threads_tried": {str(k): round(v[0] * 1e6, 1) for k, v in sorted(legs.items())},
+            "os_cpu_count": n_os, "nproc": n_proc,
+            "sample": f"{n} acceptance steps at B=1 gamma=3 V=151936 over {el:.1f} s per leg "
                       "(torch-CPU restatement of model_runner.py:391-428)"}
 
 
@@ -308,8 +342,6 @@ def cpu_baseline_attention(torch, lens, block_size: int, R: int, Hq: int, Hkv: i
     `sample_seqs` sequences of the workload, scaled to the whole batch by their
     share of the key count."""
     from oracle import torch_port
-    cores = min(os.cpu_count() or 1, 16)
-    torch.set_num_threads(cores)
     sl = [int(x) for x in lens[:sample_seqs]]
     nblk = [(x + block_size - 1) // block_size for x in sl]
     nb = sum(nblk)
@@ -327,20 +359,19 @@ def cpu_baseline_attention(torch, lens, block_size: int, R: int, Hq: int, Hkv: i
     for x in sl:
         cu_k.append(cu_k[-1] + x)
     scale = D ** -0.5
-    for _ in range(2):
+
+    def fn():
         torch_port.paged_attention(q, kc, vc, bt, cu_q, cu_k, scale)
-    n = 0
-    t0 = time.perf_counter()
-    while True:
-        torch_port.paged_attention(q, kc, vc, bt, cu_q, cu_k, scale)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= seconds and n >= 3:
-            break
-    per_sample = el / n
+
+    legs, best, n_os, n_proc = _cpu_legs(torch, fn, seconds, 3)
+    per_sample, n, el = legs[best]
     share = sum(sl) / float(sum(int(x) for x in lens))
     return {"value": round(per_sample / share * 1e6, 1), "unit": "us/launch (verify attention)",
-            "cores": torch.get_num_threads(), "kind": "port",
+            "cores": best, "kind": "port",
+            "single_thread": {"value": round(legs[1][0] / share * 1e6, 1), "cores": 1},
+            "threads_tried": {str(k): round(v[0] / share * 1e6, 1)
+                              for k, v in sorted(legs.items())},
+            "os_cpu_count": n_os, "nproc": n_proc,
             "sample": f"{n} passes over {len(sl)} of the {len(lens)} sequences ({sum(sl)} of "
                       f"{int(sum(int(x) for x in lens))} keys, fp32) in {el:.1f} s, scaled by "
                       "the key share (torch-CPU restatement of attention.py:147-160)"}
@@ -402,6 +433,7 @@ def bench_spec(args, torch, hv):
     e_end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - w0
+    runner.check()  # no acceptance call of the timed steps produced invalid outputs
     gpu_ms = e_start.elapsed_time(e_end)
     len1 = runner.lengths()[0]
     emitted = len1 - len0
@@ -427,7 +459,9 @@ def bench_spec(args, torch, hv):
                                f"{'Qwen3-0.6B' if args.draft != 'forced' else 'forced (target first 28 layers)'} draft",
                    "batch": 1, "gamma": gamma, "prompt_len": 64, "temperature": 0.6,
                    "acceptance": "reference", "kv_cache": args.kv,
-                   "hip_graphs": graphs},
+                   "hip_graphs": graphs, "output_tokens_timed": emitted,
+                   "context_range_timed": [len0, len1],
+                   "roofline_probe_context": 320},
         "verify_accept_step_us": round(verify_ms / args.steps * 1e3, 1),
         # published reference numbers (RTX 5090, trained Qwen3-8B / 0.6B, 65.5% acceptance,
         # prompt 256): benchmarks/results/20260322T104708Z-spec-decode-batch1.json:40,45-49;
@@ -456,8 +490,8 @@ def bench_adaptive(args, torch, hv):
     what all sequences need at the end (block pressure: sequences wait for blocks
     until others finish; when none can proceed the longest is preempted and later
     recomputed by prefill, scheduler.py:231-238,313-320). Random-init 8B target /
-    0.6B draft, T=0.6, reference acceptance, gamma from 3 adapted in [1, 8]
-    (llm_engine.py:197-208)."""
+    0.6B draft, T=0.6, reference acceptance, gamma from 3 adapted in [1, 7]
+    (llm_engine.py:197-208 with the range of the config)."""
     import importlib as _il
     import numpy as np
     q3 = _il.import_module("hilda-vllm_amd.engine.qwen3_host")
@@ -474,7 +508,7 @@ def bench_adaptive(args, torch, hv):
     draft = q3.Qwen3Host(q3.QWEN3_0_6B, device=dev, seed=2)
     runner = sr.SpecRunner(target, draft, batch=B, gamma=3, max_model_len=ctx + 16, block_size=bs,
                            kv_cache_dtype="fp8", num_blocks=num_blocks, temperature=0.6,
-                           mode="reference", adaptive=True, device=dev)
+                           mode="reference", adaptive=True, max_gamma=7, device=dev)
     runner.load_prompts(prompts)
     runner.state.max_tokens.copy_(torch.tensor([ctx - int(n) for n in plens], dtype=torch.int32))
     runner.prefill()

@@ -254,6 +254,11 @@ __global__ __launch_bounds__(SmallShape<G>::kThreads) void k_accept_small(Proble
                            __HIP_MEMORY_SCOPE_AGENT);
     }
   }
+  // a count already at the grid size means the word was not left by a
+  // completed launch (an uncleared workspace, or one shared with another
+  // call): the epoch may not advance, so this call's outputs are invalid
+  const bool entry_bad = wid == 0 && lane == 0 && (uint32_t)start >= nwg;
+  if (entry_bad) __hip_atomic_store(&sy->err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
   float m[RPG];
 #pragma unroll
@@ -269,7 +274,7 @@ __global__ __launch_bounds__(SmallShape<G>::kThreads) void k_accept_small(Proble
   }
   if (tid == 0) {
     s_tag = (uint32_t)(start >> 32) + 1u;  // tag 0 never matches a zeroed word
-    s_bad = 0;
+    s_bad = entry_bad ? 1 : 0;
   }
   __syncthreads();
   const uint32_t tag = s_tag;

@@ -114,6 +114,13 @@ class Qwen3Layer(nn.Module):
         attn = self.attn
         ctx = get_context()
         attn._check_bound(ctx)
+        if attn.calib is not None:
+            # FP8 calibration pass: amax of the K rows (after q/k-norm and RoPE) and V rows
+            _, kk = _ops.qk_norm_rope(qkv, g.num_heads, g.num_kv_heads, self.q_norm, self.k_norm,
+                                      self.rope.cos_sin, positions, g.rms_eps)
+            vv = qkv[:, self.q_size + self.kv_size:]
+            torch.maximum(attn.calib, torch.stack([kk.abs().amax(), vv.abs().amax()]).float(),
+                          out=attn.calib)
         q = _ops.qk_norm_rope_store(qkv, g.num_heads, g.num_kv_heads, self.q_norm, self.k_norm,
                                     self.rope.cos_sin, positions, g.rms_eps, attn.k_cache,
                                     attn.v_cache, ctx.slot_mapping, k_scale=attn.k_scale,

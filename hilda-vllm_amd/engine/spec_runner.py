@@ -37,9 +37,14 @@ class SpecRunner:
     def __init__(self, target, draft, *, batch: int, gamma: int, max_model_len: int = 4096,
                  block_size: int = 256, kv_cache_dtype: str = "auto", num_blocks: int | None = None,
                  temperature: float = 1.0, top_k: int = 0, top_p: float = 1.0,
-                 mode: str = "reference", eos: int = -1, k_scale: float = 1.0,
-                 v_scale: float = 1.0, device="cuda", adaptive: bool = False,
+                 mode: str = "reference", eos: int = -1, k_scale: float | None = None,
+                 v_scale: float | None = None, device="cuda", adaptive: bool = False,
                  max_gamma: int | None = None):
+        if mode == "reference" and (0 < top_k < target.g.vocab or top_p < 1.0):
+            # the reference draws draft tokens from the filtered Sampler but keeps the
+            # unfiltered softmax as the draft probabilities (model_runner.py:312-313);
+            # hs_sampler has no output kind giving both, so such settings use "filtered"
+            raise ValueError("reference mode takes no top-k / top-p; use mode='filtered'")
         self.target, self.draft = target, draft
         self.B, self.gamma = batch, gamma
         self.max_gamma = max(gamma, max_gamma or (8 if adaptive else gamma))
@@ -58,10 +63,13 @@ class SpecRunner:
         self.dkv = torch.zeros((2, len(draft.layers), self.num_blocks, block_size,
                                 dg.num_kv_heads, dg.head_dim), dtype=torch.bfloat16, device=dev)
         kmax = max_model_len + self.max_gamma + 2
+        # FP8 per-tensor scales: given, or calibrated from the prompt by prefill()
+        self.kv_calibrate = kv_cache_dtype == "fp8" and k_scale is None and v_scale is None
         for i, a in enumerate(target.attention_layers()):
             a.k_cache, a.v_cache = self.kv[0, i], self.kv[1, i]
             a.kv_cache_dtype = kv_cache_dtype
-            a.k_scale, a.v_scale = k_scale, v_scale
+            a.k_scale = 1.0 if k_scale is None else float(k_scale)
+            a.v_scale = 1.0 if v_scale is None else float(v_scale)
             a.max_model_len = kmax
         for i, a in enumerate(draft.attention_layers()):
             a.k_cache, a.v_cache = self.dkv[0, i], self.dkv[1, i]
@@ -175,6 +183,8 @@ class SpecRunner:
                              dtype=torch.int32, device=dev)
         cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0).tolist()), dtype=torch.int32,
                           device=dev)
+        if self.kv_calibrate:
+            self._calibrate_fp8(ids, pos, cu, max(lens), slots)
         set_context(True, cu, cu, max(lens), max(lens), slots, None, self.state.block_tables)
         h = self.target(ids, pos)
         last = h[cu[1:].long() - 1]
@@ -186,6 +196,31 @@ class SpecRunner:
         out = first.view(self.B, 1)
         ops.spec_commit(self.state, 0, out, torch.ones(self.B, dtype=torch.int32, device=dev))
         torch.cuda.synchronize()
+
+    # FP8 scales sit this factor above the prompt's amax, so later tokens have
+    # headroom before they saturate at +-448 * scale
+    FP8_HEADROOM = 2.0
+
+    def _calibrate_fp8(self, ids, pos, cu, maxlen, slots):
+        """Per-layer k/v scales of the FP8 target cache, headroom * amax / 448, from
+        the K (after q/k-norm and RoPE) and V rows of the prompt; one extra target
+        forward whose cache writes the real prefill then overwrites."""
+        layers = self.target.attention_layers()
+        for a in layers:
+            a.calib = torch.zeros(2, dtype=torch.float32, device=self.device)
+        set_context(True, cu, cu, maxlen, maxlen, slots, None, self.state.block_tables)
+        try:
+            self.target(ids, pos)
+        finally:
+            reset_context()
+        amax = torch.stack([a.calib for a in layers]).cpu()
+        for a, (ka, va) in zip(layers, amax.tolist()):
+            a.k_scale = max(ka, 1e-6) * self.FP8_HEADROOM / 448.0
+            a.v_scale = max(va, 1e-6) * self.FP8_HEADROOM / 448.0
+            a.calib = None
+
+    def kv_scales(self) -> list[tuple[float, float]]:
+        return [(a.k_scale, a.v_scale) for a in self.target.attention_layers()]
 
     # ------------------------------------------------------------------ preemption
     def preempt(self, b: int):
@@ -340,11 +375,25 @@ class SpecRunner:
             return
         G = self._g()
         nacc = G.last[0]
-        # accepted drafts and proposals of the sequences that took part (llm_engine.py:150-151)
-        tot = torch.stack([(nacc * G.elig).sum(), G.elig.sum()]).cpu().tolist()
+        # accepted drafts and proposals of the sequences that took part (llm_engine.py:150-151),
+        # and the smallest count: -1 marks outputs the acceptance kernel could not produce
+        tot = torch.stack([(nacc * G.elig).sum(), G.elig.sum(),
+                           torch.where(G.elig != 0, nacc, 0).min()]).cpu().tolist()
+        if int(tot[2]) < 0:
+            raise RuntimeError("spec step: acceptance outputs invalid (a bounded wait inside "
+                               "the single-launch kernel ran out); the step committed nothing "
+                               "for those sequences")
         accepted, proposed = int(tot[0]), int(tot[1]) * G.gamma
         self.history.append((G.gamma, accepted, proposed))
         self.gamma = self.controller.update(accepted, proposed)
+
+    def check(self):
+        """Raises if any acceptance call since the last check produced invalid
+        outputs (fixed-gamma runs read nothing back per step; the flag is sticky).
+        Synchronises with the device."""
+        if ops.accept_error(self.device, clear=True):
+            raise RuntimeError("spec run: an acceptance call produced invalid outputs (a "
+                               "bounded wait inside the single-launch kernel ran out)")
 
     # ------------------------------------------------------------------ graphs
     def capture(self):

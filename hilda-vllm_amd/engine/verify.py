@@ -222,6 +222,9 @@ class VerifyRunner:
             packed[ix, :g + 1] = out
             packed[ix, -1] = nacc.to(torch.int64)
         host = packed.cpu().numpy()  # the one D2H copy (synchronises)
+        # a negative count marks outputs the kernel could not produce (a bounded
+        # wait ran out): committing them would silently drop the step's tokens
+        _ops.check_accepted(torch.from_numpy(host[:, -1]), "run_verify")
         results = []
         for b in range(B):
             row = host[b]

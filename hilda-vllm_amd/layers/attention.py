@@ -10,7 +10,13 @@ attends over the paged cache through context.block_tables:
     (attention.py:147-160, bottom-right causal);
   * decode: one query per sequence with context.context_lens keys
     (attention.py:162-170); cu_seqlens_k is taken from context.cu_seqlens_k
-    when the caller staged it on the device, else built from context_lens.
+    when the caller staged it on the device, else built from context_lens;
+    the launch is sized by max_model_len when the runner set it, else by
+    max_seqlen_k, else (the reference's decode context sets neither) by the
+    block-table width times the block size.
+Prefill without block tables (the reference then attends over the step's own
+k/v, attention.py:147-149) is not supported: the kernel reads the paged cache
+only, so a runner stages block tables for every prefill.
 kv_cache_dtype "fp8" means float8_e4m3fn caches with per-tensor scales
 k_scale / v_scale, used by every phase (the reference keeps a separate BF16
 prefill cache for verify, attention.py:114-131; one FP8 cache keeps the
@@ -53,12 +59,19 @@ class Attention(nn.Module):
         # upper bound of keys per sequence used to size the launch (set by the runner
         # for graph capture; 0 means "use the context's max_seqlen_k")
         self.max_model_len = 0
+        # FP8 scale calibration: when a [2] f32 tensor, the producer of this layer's
+        # K/V raises it to the amax of the K and V rows it stores
+        self.calib = None
 
     def _check_bound(self, ctx):
         if not (self.k_cache.numel() and self.v_cache.numel()):
             raise RuntimeError("Attention needs a bound KV cache (k_cache / v_cache)")
         if ctx.block_tables is None:
-            raise RuntimeError("Attention needs context.block_tables (paged KV)")
+            # the reference attends over the step's own k/v here (attention.py:147-149);
+            # this build's kernel reads the paged cache only, so the runner must stage
+            # block tables for every prefill (as SpecRunner and VerifyRunner do)
+            raise RuntimeError("Attention needs context.block_tables: prefill over the "
+                               "unpaged k/v of the step is not supported")
 
     def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
         ctx = get_context()
@@ -92,6 +105,11 @@ class Attention(nn.Module):
             max_q, max_k = 1, ctx.max_seqlen_k
         if self.max_model_len:
             max_k = self.max_model_len
+        elif not ctx.is_prefill and max_k <= 0:
+            # the reference's decode context carries no max_seqlen_k
+            # (model_runner.py:310 set_context(False, slot_mapping, context_lens,
+            # block_tables)); the table width bounds every context without a sync
+            max_k = ctx.block_tables.shape[1] * k_cache.shape[1]
         return _ops.verify_attention(q, k_cache, v_cache, ctx.block_tables, cu_q, cu_k, max_q,
                                      max_k, self.scale, k_scale=self.k_scale,
                                      v_scale=self.v_scale)

@@ -85,6 +85,12 @@ def spec_accept(target_logits: torch.Tensor, draft_probs: torch.Tensor | None,
     u_resample [B]. Returns (num_accepted int32 [B], out_tokens int64
     [B, gamma+1], out_len int32 [B]) and, with row_stats=True, a 4th tensor
     [B*(gamma+1), 2] with the max and normaliser of every target row.
+
+    The call does not synchronise, so a failure inside the single-launch
+    kernel (a bounded wait for another workgroup's data that ran out) cannot
+    raise here: that sequence's num_accepted is -1 and its out_len 0. The
+    caller must check num_accepted >= 0 at its next synchronisation (or
+    accept_error(device) at any later point: the flag is sticky).
     """
     m = _mode(mode)
     dev = _need_cuda(target_logits, draft_probs, draft_tokens, temperatures, u_accept,
@@ -138,6 +144,30 @@ def spec_accept(target_logits: torch.Tensor, draft_probs: torch.Tensor | None,
     if row_stats:
         return nacc, out, olen, stats
     return nacc, out, olen
+
+
+def accept_error(device, clear: bool = False) -> bool:
+    """True once a spec_accept call on this device's shared acceptance workspace
+    produced invalid outputs (num_accepted -1): the sticky 32-bit word at byte 8
+    of the workspace (include/hilda_spec.h). Synchronises with the device."""
+    ws = _WS.get((torch.device(device).index, "spec_accept"))
+    if ws is None:
+        return False
+    word = ws[8:12]
+    bad = bool(word.cpu().any())
+    if clear and bad:
+        word.zero_()
+    return bad
+
+
+def check_accepted(num_accepted: torch.Tensor, what: str = "spec_accept") -> None:
+    """Raises if any entry of num_accepted (already on the host, or copied here)
+    is negative: the acceptance kernel marked that sequence's outputs invalid."""
+    n = num_accepted.cpu() if num_accepted.is_cuda else num_accepted
+    if n.numel() and int(n.min()) < 0:
+        bad = torch.nonzero(n < 0).flatten().tolist()
+        raise RuntimeError(f"{what}: acceptance outputs invalid for sequences {bad} "
+                           "(a bounded wait inside the single-launch kernel ran out)")
 
 
 def sample_rows(logits: torch.Tensor, temperatures: torch.Tensor | None = None,

@@ -20,8 +20,22 @@ def _rng(seed: int) -> np.random.Generator:
 
 
 def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
-    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
-    return ((u + (((u >> 16) & 1) + 0x7FFF)) >> 16).astype(np.uint16)
+    """Round-to-nearest-even bf16 bit patterns of float32 values (NaN stays NaN).
+    Works in place on a uint32 copy, 4M elements at a time."""
+    u = np.array(x, dtype=np.float32, copy=True, order="C").view(np.uint32).reshape(-1)
+    out = np.empty(u.shape, np.uint16)
+    step = 1 << 22
+    for a in range(0, u.size, step):
+        c = u[a:a + step]
+        nan = (c & 0x7FFFFFFF) > 0x7F800000
+        r = c >> 16
+        r &= 1
+        r += 0x7FFF
+        c += r  # finite values cannot carry past bit 31: |x| <= 0x7F7FFFFF
+        c >>= 16
+        c[nan] = 0x7FC0
+        out[a:a + step] = c
+    return out.reshape(np.shape(x))
 
 
 def bf16_bits_to_f32(b: np.ndarray) -> np.ndarray:
@@ -36,20 +50,38 @@ def softmax64(x: np.ndarray) -> np.ndarray:
 
 
 def filtered_probs64(logits: np.ndarray, temperature: float, top_k: int, top_p: float):
-    """float64 top-k / top-p distribution of one row (draft-side input only)."""
+    """float64 top-k / top-p distribution of one row (draft-side input only).
+
+    Rank order is descending x = logit / T with ties broken by lower index; top-k
+    keeps the first k ranks, top-p the ranks whose cumulative probability (over the
+    top-k set) is below p, and rank 0. Only the candidates above a partition
+    threshold are sorted, grown until they hold the top-p crossing."""
     x = logits.astype(np.float64) / temperature
     V = x.shape[-1]
-    order = np.lexsort((np.arange(V), -x))
     keep = np.ones(V, bool)
     if 0 < top_k < V:
+        thr = np.partition(x, V - top_k)[V - top_k]  # k-th largest value
+        above = np.flatnonzero(x > thr)
+        ties = np.flatnonzero(x == thr)[:top_k - above.size]
         keep[:] = False
-        keep[order[:top_k]] = True
+        keep[above] = True
+        keep[ties] = True
     if top_p < 1.0:
-        xs = np.where(keep[order], x[order], -np.inf)
-        p = np.exp(xs - xs[0])
-        p /= p.sum()
-        c = np.cumsum(p)
-        ks = c < top_p
+        z = np.where(keep, x, -np.inf)
+        e = np.exp(z - z.max())
+        total = e.sum()
+        nkeep = int(keep.sum())
+        n = min(nkeep, 4096)
+        while True:
+            if n >= nkeep:
+                cand = np.flatnonzero(keep)
+            else:
+                cand = np.flatnonzero(z > np.partition(z, V - n)[V - n])
+            order = cand[np.lexsort((cand, -z[cand]))]
+            ks = np.cumsum(e[order]) / total < top_p
+            if not ks.all() or cand.size == nkeep:
+                break
+            n *= 4
         ks[0] = True
         keep[:] = False
         keep[order[ks]] = True

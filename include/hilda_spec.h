@@ -7,11 +7,16 @@
  * them synchronises the stream or allocates device memory.
  *
  * Workspaces: query the size with the matching *_workspace_size() function
- * and pass a buffer at least that large. A workspace only carries partial
- * results from one launch of a call to the next launch of the same call: it
- * needs no initialisation and no clearing between calls (so the calls can be
- * recorded into a HIP graph). Two calls that share one workspace must not
- * overlap in time.
+ * and pass a buffer at least that large. Two calls that share one workspace
+ * must not overlap in time. Two kinds:
+ *  - hs_sampler and hs_verify_attention: the workspace only carries partial
+ *    results from one launch of a call to the next launch of the same call;
+ *    it needs no initialisation and may be shared between these calls.
+ *  - hs_spec_accept and hs_spec_commit: the workspace also carries state from
+ *    one call to the next. It must be zero-filled before its first use, every
+ *    call leaves it ready for the next (so the calls can be recorded into a
+ *    HIP graph without a clearing step), and it must not be passed to any
+ *    other entry point.
  */
 #ifndef HILDA_SPEC_H
 #define HILDA_SPEC_H
@@ -72,10 +77,15 @@ int hs_version(void);
 /* workspace     : hs_spec_accept_workspace_size bytes, zero-filled before   */
 /*                 its first use; calls leave it ready for the next one, of  */
 /*                 any shape. Calls that share a workspace must not overlap. */
-/*                 Small reference-mode batches (batch x ceil(vocab/2048)    */
-/*                 workgroups fit one per CU, gamma <= 7, aligned rows, vocab */
-/*                 a multiple of 8) run as a single launch; if one of its    */
-/*                 bounded waits ever ran out, num_accepted is -1.           */
+/*                 Small batches (batch x ceil(vocab/2048) workgroups fit one */
+/*                 per CU, gamma <= 7, aligned rows, vocab a multiple of 8)  */
+/*                 run as a single launch whose workgroups exchange data     */
+/*                 through the workspace. If one of its bounded waits ever   */
+/*                 ran out, or its launch counter was not left by a completed */
+/*                 call, that sequence's num_accepted is -1 and out_len 0,   */
+/*                 and the 32-bit word at byte offset 8 of the workspace is  */
+/*                 set to 1 (sticky until the caller clears it). Callers     */
+/*                 must check num_accepted >= 0 at their next synchronisation.*/
 /* ------------------------------------------------------------------------ */
 size_t hs_spec_accept_workspace_size(int batch, int gamma, int vocab);
 

@@ -25,25 +25,41 @@ float or_e4m3fn_decode(uint8_t c) {
   return s ? -v : v;
 }
 
-/* nearest code by exhaustive search over the 127 non-negative finite codes */
+/* Nearest code among the 127 non-negative finite codes, whose values increase
+ * with the code: a binary search over the value table brackets |x| between
+ * codes c and c + 1, and the nearer one wins (ties to the even code, i.e. the
+ * even mantissa). */
+static float g_tab[127];
+static int g_tab_ready = 0;
+
+static void tab_init(void) {
+  if (g_tab_ready) return;
+  for (int c = 0; c <= 0x7e; ++c) g_tab[c] = or_e4m3fn_decode((uint8_t)c);
+  g_tab_ready = 1;
+}
+
 uint8_t or_e4m3fn_encode_sat(float x) {
   if (isnan(x)) return 0x7f;
+  tab_init();
   const uint8_t sign = signbit(x) ? 0x80 : 0;
   float a = fabsf(x);
   if (a > 448.0f) a = 448.0f;
-  int best = 0;
-  double bd = INFINITY;
-  for (int c = 0; c <= 0x7e; ++c) {
-    double d = fabs((double)or_e4m3fn_decode((uint8_t)c) - (double)a);
-    /* ties to even code (even mantissa) */
-    if (d < bd || (d == bd && (c & 1) == 0)) {
-      bd = d;
-      best = c;
-    }
+  int lo = 0, hi = 0x7e;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) / 2;
+    if (g_tab[mid] <= a) lo = mid;
+    else hi = mid - 1;
+  }
+  int best = lo;
+  if (lo < 0x7e) {
+    const double d0 = (double)a - (double)g_tab[lo];
+    const double d1 = (double)g_tab[lo + 1] - (double)a;
+    if (d1 < d0 || (d1 == d0 && ((lo + 1) & 1) == 0)) best = lo + 1;
   }
   return sign | (uint8_t)best;
 }
 
 void or_e4m3fn_quantize(const float* x, int64_t n, float scale, uint8_t* out) {
+  tab_init();
   for (int64_t i = 0; i < n; ++i) out[i] = or_e4m3fn_encode_sat(x[i] / scale);
 }

@@ -1,4 +1,7 @@
-"""Per-sequence host state used by the verify drop-in.
+"""Test fixture: the per-sequence host state the verify drop-in reads.
+
+The tests build run_verify inputs from it, as the reference engine builds them
+from its own Sequence objects; the product package does not import it.
 
 Mirror of mini_vllm/engine/sequence.py:14-132 and mini_vllm/sampling_params.py:4-15
 (the fields run_verify and the spec block read: token_ids, last_token,

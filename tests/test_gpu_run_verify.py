@@ -23,7 +23,7 @@ BS = 32
 def _mods():
     q3 = importlib.import_module("hilda-vllm_amd.engine.qwen3_host")
     vr = importlib.import_module("hilda-vllm_amd.engine.verify")
-    sq = importlib.import_module("hilda-vllm_amd.engine.sequence")
+    sq = importlib.import_module("tests.seq_fixture")
     ctx = importlib.import_module("hilda-vllm_amd.utils.context")
     return q3, vr, sq, ctx
 

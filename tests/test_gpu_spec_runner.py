@@ -276,3 +276,73 @@ def test_preemption_frees_blocks_and_recomputes(cuda):
     assert runner.lengths() == [len(p) + m for p, m in zip(prompts, max_tokens)]
     assert preempted > 0 and readmitted == preempted
     assert int(st.free_hdr[1]) == num_blocks
+
+
+def test_config4_shape_adaptive_fp8_to_8192(cuda):
+    """Config 4's shape: B = 32, prompts ~ U[32, 128], every sequence decoding to an
+    8192-token context in an FP8 target cache of 256-token blocks (32-entry block
+    tables) whose pool holds 3/4 of the final need, gamma adapted in [1, 7]. The
+    models keep config 3's head geometry (16 Q / 8 KV heads of 128) at two layers
+    and a 3000-token vocabulary so the run fits a test; the draft is the target's
+    first layer. Invariants after every step: block accounting; at the end:
+    completion, every block released, no invalid acceptance output, and the gamma
+    trajectory equal to the controller's on the recorded totals."""
+    import numpy as np
+    q3, sr = _mods()
+    AG = importlib.import_module("hilda-vllm_amd.engine.adaptive_gamma").AdaptiveGamma
+    g = q3.Qwen3Geometry(num_layers=2, hidden=1024, num_heads=16, num_kv_heads=8, ffn=1024,
+                         vocab=3000, max_position=8704)
+    target = q3.Qwen3Host(g, device=cuda, seed=81)
+    draft = q3.Qwen3Host(g, share_from=target, num_layers=1)
+    B, bs, ctx = 32, 256, 8192
+    rng = np.random.default_rng(82)
+    plens = rng.integers(32, 129, size=B)
+    prompts = [rng.integers(0, 3000, size=n).tolist() for n in plens]
+    need = B * -(-(ctx + 8) // bs)
+    num_blocks = int(0.75 * need)
+    runner = sr.SpecRunner(target, draft, batch=B, gamma=3, max_model_len=ctx + 16,
+                           block_size=bs, kv_cache_dtype="fp8", num_blocks=num_blocks,
+                           temperature=0.6, mode="reference", adaptive=True, max_gamma=7,
+                           device=cuda)
+    assert runner.W >= 32
+    runner.load_prompts(prompts)
+    st = runner.state
+    st.max_tokens.copy_(torch.tensor([ctx - int(n) for n in plens], dtype=torch.int32))
+    runner.prefill()
+    scales = runner.kv_scales()
+    assert all(0 < k < 1 and 0 < v < 1 for k, v in scales), scales  # calibrated amax/448
+    preempted = readmitted = steps = 0
+    while steps < 20000:
+        if runner.preempted:
+            readmitted += runner.readmit()
+            _check_blocks(runner)
+        fin = st.finished.cpu()
+        if bool(fin.all()) and not runner.preempted:
+            break
+        runner.step_graph()
+        G = runner._per_gamma[runner.history[-1][0]]
+        fin = st.finished.cpu()
+        if int(G.elig.sum()) == 0 and not bool(fin.all()):
+            lens = st.context_lens.cpu().masked_fill(fin.bool(), -1)
+            runner.preempt(int(torch.argmax(lens)))
+            preempted += 1
+        _check_blocks(runner)
+        steps += 1
+        if steps % 500 == 0:
+            print(f"config4 shape: step {steps} tokens {sum(runner.lengths())} "
+                  f"gamma {runner.gamma} preempted {preempted}", flush=True)
+    torch.cuda.synchronize()
+    runner.check()
+    print(f"config4 shape: {steps} steps, preempted {preempted}, readmitted {readmitted}",
+          flush=True)
+    assert bool(st.finished.cpu().all()) and not runner.preempted, "sequences did not finish"
+    assert runner.lengths() == [ctx] * B
+    assert int(st.free_hdr[1]) == num_blocks
+    assert preempted > 0 and readmitted == preempted
+    ctl = AG(3, max_gamma=7)
+    for k, (gk, acc, prop) in enumerate(runner.history):
+        assert gk == ctl.gamma, (k, runner.history[max(0, k - 3):k + 1])
+        assert 1 <= gk <= 7 and 0 <= acc <= prop
+        ctl.update(acc, prop)
+    gammas = [h[0] for h in runner.history]
+    print("gamma histogram", {k: gammas.count(k) for k in sorted(set(gammas))}, flush=True)

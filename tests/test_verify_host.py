@@ -18,7 +18,7 @@ def _vr():
 
 
 def _sq():
-    return importlib.import_module("hilda-vllm_amd.engine.sequence")
+    return importlib.import_module("tests.seq_fixture")
 
 
 @pytest.mark.parametrize("seed", range(3))
@@ -84,3 +84,79 @@ def test_sampling_params_validation():
     with pytest.raises(ValueError):
         sq.SamplingParams(top_p=0.0)
     assert sq.SamplingParams(temperature=0.0).temperature == 0.0
+
+
+def _invalid_accept(monkeypatch, ops):
+    """spec_accept as the single-launch kernel leaves it after a bounded wait ran
+    out for sequence 1: num_accepted -1, out_len 0, tokens -1."""
+    import torch
+
+    def fake(lg, q, dt, T, ua, ur, **kw):
+        B, g = dt.shape
+        nacc = torch.tensor([g if b != 1 else -1 for b in range(B)], dtype=torch.int32)
+        out = torch.cat([dt, torch.zeros((B, 1), dtype=torch.int64)], 1)
+        out[1] = -1
+        olen = (nacc + 1).clamp(min=0).to(torch.int32)
+        return nacc, out, olen
+
+    monkeypatch.setattr(ops, "spec_accept", fake)
+
+
+def test_run_verify_raises_on_invalid_acceptance(monkeypatch):
+    """VerifyRunner._accept reads the results back once; a -1 count must raise,
+    not become an empty commit ([], -1)."""
+    import torch
+    vr, sq = _vr(), _sq()
+    ops = importlib.import_module("hilda-vllm_amd.ops")
+    _invalid_accept(monkeypatch, ops)
+    runner = vr.VerifyRunner(None, device="cpu", record_breakdown=False)
+    V, g = 64, 3
+    seqs = [sq.Sequence([1, 2, 3]) for _ in range(3)]
+    drafts = [[4, 5, 6]] * 3
+    logits = torch.zeros((3 * (g + 1), V))
+    probs = torch.full((3, g, V), 1.0 / V)
+    with pytest.raises(RuntimeError, match="sequences \\[1\\]"):
+        runner._accept(seqs, drafts, probs, logits, [g + 1] * 3, None)
+    # the same call with valid outputs returns every sequence's tokens
+    monkeypatch.setattr(ops, "spec_accept", lambda lg, q, dt, *a, **k: (
+        torch.full((3,), g, dtype=torch.int32),
+        torch.cat([dt, torch.full((3, 1), 9, dtype=torch.int64)], 1),
+        torch.full((3,), g + 1, dtype=torch.int32)))
+    res = runner._accept(seqs, drafts, probs, logits, [g + 1] * 3, None)
+    assert res == [([4, 5, 6, 9], 3)] * 3
+
+
+def test_spec_runner_raises_on_invalid_acceptance():
+    """SpecRunner._after_step copies the step's totals to the host for the gamma
+    controller; a -1 count of a sequence that took part must raise there, and a
+    sequence that sat out (eligible 0) must not."""
+    import types
+    import torch
+    srm = importlib.import_module("hilda-vllm_amd.engine.spec_runner")
+    agm = importlib.import_module("hilda-vllm_amd.engine.adaptive_gamma")
+    r = object.__new__(srm.SpecRunner)
+    r.gamma = 3
+    r.controller = agm.AdaptiveGamma(3, max_gamma=7)
+    r.history = []
+    G = types.SimpleNamespace(gamma=3, elig=torch.tensor([1, 1, 0], dtype=torch.int32),
+                              last=(torch.tensor([2, -1, 0], dtype=torch.int32), None, None))
+    r._per_gamma = {3: G}
+    with pytest.raises(RuntimeError, match="invalid"):
+        r._after_step()
+    assert r.history == []
+    G.last = (torch.tensor([2, 1, -1], dtype=torch.int32), None, None)
+    r._after_step()
+    assert r.history == [(3, 3, 6)]
+
+
+def test_accept_error_flag_is_read_and_cleared(monkeypatch):
+    """The sticky word at byte 8 of the acceptance workspace (set by the kernel
+    when a wait ran out) is what SpecRunner.check reads for fixed-gamma runs."""
+    import torch
+    ops = importlib.import_module("hilda-vllm_amd.ops")
+    ws = torch.zeros(256, dtype=torch.uint8)
+    monkeypatch.setitem(ops._WS, (None, "spec_accept"), ws)
+    assert not ops.accept_error("cpu")
+    ws[8] = 1
+    assert ops.accept_error("cpu", clear=True)
+    assert not ops.accept_error("cpu")
