@@ -106,7 +106,7 @@ class SpecRunner:
                 u_draft=torch.zeros((g, B), dtype=torch.float32, device=dev),
                 u_acc=torch.zeros((B, g), dtype=torch.float32, device=dev),
                 elig=torch.zeros(B, dtype=torch.int32, device=dev),
-                graphs=None, last=None)
+                graphs=None, last=None, graph_last=None)
             self._per_gamma[g] = G
         return G
 
@@ -366,8 +366,7 @@ class SpecRunner:
             self.verify_phase()
             self.capture()
         else:
-            G.graphs[0].replay()
-            G.graphs[1].replay()
+            self.replay()
         self._after_step()
 
     def _after_step(self):
@@ -403,6 +402,10 @@ class SpecRunner:
         torch.cuda.synchronize()
         snap = self._snapshot()
         G = self._g()
+        # the captured verify phase rebinds G.last to the graph's output tensors, which
+        # hold nothing until the first replay: keep the eager step's outputs as the
+        # last results and switch to the graph's on replay
+        eager_last = G.last
         gd, gv = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
         s = torch.cuda.Stream(device=self.device)
         s.wait_stream(torch.cuda.current_stream(self.device))
@@ -415,11 +418,15 @@ class SpecRunner:
         torch.cuda.synchronize()
         self._restore(snap)  # capture executed nothing, but keep the state exact
         G.graphs = (gd, gv)
+        G.graph_last = G.last
+        G.last = self.last = eager_last
 
     def replay(self):
-        gd, gv = self._g().graphs
+        G = self._g()
+        gd, gv = G.graphs
         gd.replay()
         gv.replay()
+        G.last = self.last = G.graph_last
 
     def _snapshot(self):
         st = self.state

@@ -311,7 +311,7 @@ def test_config4_shape_adaptive_fp8_to_8192(cuda):
     runner.prefill()
     scales = runner.kv_scales()
     assert all(0 < k < 1 and 0 < v < 1 for k, v in scales), scales  # calibrated amax/448
-    preempted = readmitted = steps = 0
+    preempted = readmitted = steps = checked = 0
     while steps < 20000:
         if runner.preempted:
             readmitted += runner.readmit()
@@ -319,9 +319,19 @@ def test_config4_shape_adaptive_fp8_to_8192(cuda):
         fin = st.finished.cpu()
         if bool(fin.all()) and not runner.preempted:
             break
+        len0 = st.context_lens.cpu()
         runner.step_graph()
         G = runner._per_gamma[runner.history[-1][0]]
-        fin = st.finished.cpu()
+        fin1 = st.finished.cpu()
+        if bool((fin1 == fin).all()):
+            # the controller's totals are this step's: every participating sequence
+            # appended its accepted drafts plus one token (also at the step that
+            # captured a new gamma's graphs)
+            appended = int((st.context_lens.cpu() - len0).sum())
+            assert runner.history[-1][1] == appended - int(G.elig.sum()), (
+                steps, runner.history[-1], appended)
+            checked += 1
+        fin = fin1
         if int(G.elig.sum()) == 0 and not bool(fin.all()):
             lens = st.context_lens.cpu().masked_fill(fin.bool(), -1)
             runner.preempt(int(torch.argmax(lens)))
@@ -333,8 +343,8 @@ def test_config4_shape_adaptive_fp8_to_8192(cuda):
                   f"gamma {runner.gamma} preempted {preempted}", flush=True)
     torch.cuda.synchronize()
     runner.check()
-    print(f"config4 shape: {steps} steps, preempted {preempted}, readmitted {readmitted}",
-          flush=True)
+    print(f"config4 shape: {steps} steps ({checked} with totals checked), preempted "
+          f"{preempted}, readmitted {readmitted}", flush=True)
     assert bool(st.finished.cpu().all()) and not runner.preempted, "sequences did not finish"
     assert runner.lengths() == [ctx] * B
     assert int(st.free_hdr[1]) == num_blocks
