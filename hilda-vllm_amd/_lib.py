@@ -11,6 +11,7 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "libhilda_spec.so"
 
 HS_OK = 0
+HS_ERR_SCRATCH_LIMIT = -5
 HS_F32, HS_BF16, HS_FP8_E4M3 = 0, 1, 2
 HS_ACCEPT_REFERENCE, HS_ACCEPT_FILTERED, HS_ACCEPT_GREEDY = 0, 1, 2
 
@@ -34,6 +35,11 @@ SIGNATURES: dict[str, tuple] = {
     "hs_verify_attention": (_i32, [_vp, _i64, _i64, _vp, _vp, _i32, _i64, _i64, _i64, _f32, _f32,
                                    _vp, _i64, _i32, _i32, _vp, _vp, _i32, _i32, _i32, _i32, _i32,
                                    _i32, _i32, _f32, _vp, _i64, _i64, _vp, _sz, _vp]),
+    "hs_verify_attention_noalloc": (_i32, [_vp, _i64, _i64, _vp, _vp, _i32, _i64, _i64, _i64,
+                                           _f32, _f32, _vp, _i64, _i32, _i32, _vp, _vp, _i32,
+                                           _i32, _i32, _i32, _i32, _i32, _i32, _f32, _vp, _i64,
+                                           _i64, _vp]),
+    "hs_verify_attention_noalloc_scratch_bytes": (_sz, []),
     "hs_store_kvcache": (_i32, [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i32, _i64, _i64,
                                 _i64, _f32, _f32, _vp, _i32, _i32, _i32, _i32, _i32, _vp]),
 }

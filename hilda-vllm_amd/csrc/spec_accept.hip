@@ -668,6 +668,8 @@ const char* hs_status_string(int status) {
     case HS_ERR_WORKSPACE: return "workspace too small";
     case HS_ERR_LAUNCH: return "kernel launch failed";
     case HS_ERR_UNSUPPORTED: return "unsupported configuration";
+    case HS_ERR_SCRATCH_LIMIT:
+      return "call needs more scratch than the allocation-free entry point holds";
     default: return "unknown status";
   }
 }

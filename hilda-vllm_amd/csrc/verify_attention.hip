@@ -30,6 +30,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "../../include/hilda_spec.h"
 
 namespace hs {
@@ -911,6 +913,35 @@ static void attn_plan(int B, int Hkv, int qtiles, int max_seqlen_k, int* nsplit,
   if (*nsplit < 1) *nsplit = 1;
 }
 
+// Scratch of hs_verify_attention_noalloc: the partial results of key splits
+// or of the balanced launch's shared tile pieces, which hs_verify_attention
+// keeps in the caller's workspace. 34 MiB holds the largest layout the
+// balanced launch uses on a 256-CU device (two pieces of 8 heads x 16 rows x
+// 128 floats per workgroup, 32.5 MiB). Every GPU the library runs on holds
+// its own copy until the process ends; host code must never use the array's
+// name as an address (it is a host-side stand-in): the per-device address
+// comes from hipGetSymbolAddress.
+constexpr size_t kNoAllocScratchBytes = (size_t)34 << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static void* g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+// Device address of this device's scratch, looked up once per device with that
+// device current; null on failure.
+static void* scratch_of_current_device() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
+    g_scratch_ptr[dev] = ptr;
+  }
+  return g_scratch_ptr[dev];
+}
+
 }  // namespace hs
 
 using namespace hs;
@@ -1045,5 +1076,32 @@ int hs_verify_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_he
                        dim3(kRows * 16), 0, s, a);
   return hipGetLastError() == hipSuccess ? HS_OK : HS_ERR_LAUNCH;
 }
+
+int hs_verify_attention_noalloc(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                                const void* k_cache, const void* v_cache, int kv_dtype,
+                                int64_t cache_stride_block, int64_t cache_stride_tok,
+                                int64_t cache_stride_head, float k_scale, float v_scale,
+                                const int32_t* block_tables, int64_t block_table_stride,
+                                int block_table_width, int num_blocks,
+                                const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                int num_seqs, int max_seqlen_q, int max_seqlen_k,
+                                int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                                float softmax_scale, void* out, int64_t out_stride_tok,
+                                int64_t out_stride_head, void* stream) {
+  void* ws = scratch_of_current_device();
+  if (!ws) return HS_ERR_LAUNCH;
+  // same kernels and launch choice as hs_verify_attention with a workspace of
+  // the scratch's size: a call whose layout does not fit runs the per-tile
+  // grid when that needs no partials, and is rejected otherwise
+  const int rc = hs_verify_attention(
+      q, q_stride_tok, q_stride_head, k_cache, v_cache, kv_dtype, cache_stride_block,
+      cache_stride_tok, cache_stride_head, k_scale, v_scale, block_tables, block_table_stride,
+      block_table_width, num_blocks, cu_seqlens_q, cu_seqlens_k, num_seqs, max_seqlen_q,
+      max_seqlen_k, num_q_heads, num_kv_heads, head_dim, block_size, softmax_scale, out,
+      out_stride_tok, out_stride_head, ws, kNoAllocScratchBytes, stream);
+  return rc == HS_ERR_WORKSPACE ? HS_ERR_SCRATCH_LIMIT : rc;
+}
+
+size_t hs_verify_attention_noalloc_scratch_bytes(void) { return kNoAllocScratchBytes; }
 
 }  // extern "C"

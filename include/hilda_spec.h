@@ -34,6 +34,7 @@ extern "C" {
 #define HS_ERR_WORKSPACE (-2)   /* workspace too small                        */
 #define HS_ERR_LAUNCH (-3)      /* kernel launch failed (hipGetLastError)     */
 #define HS_ERR_UNSUPPORTED (-4) /* valid request this build does not support */
+#define HS_ERR_SCRATCH_LIMIT (-5) /* beyond the fixed scratch of a *_noalloc call */
 
 /* element types */
 #define HS_F32 0
@@ -160,6 +161,29 @@ int hs_verify_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_he
                         int block_size, float softmax_scale, void* out, int64_t out_stride_tok,
                         int64_t out_stride_head, void* workspace, size_t workspace_bytes,
                         void* stream);
+
+/* Allocation-free variant of hs_verify_attention. No counterpart in the     */
+/* reference: it is for callers that cannot allocate device memory (code     */
+/* under HIP graph capture, tight serving loops, harnesses that forbid       */
+/* hipMalloc). Same arguments, kernels and results as hs_verify_attention    */
+/* minus the workspace: the partial results live in a fixed scratch array of */
+/* the library (hs_verify_attention_noalloc_scratch_bytes(), 34 MiB, one per */
+/* GPU, held until the process ends). A call whose partials would not fit    */
+/* returns HS_ERR_SCRATCH_LIMIT. Every call on one GPU shares that GPU's     */
+/* scratch: calls that overlap in time on one GPU (two streams) race.        */
+/* The scratch needs no clearing: each call writes the partials it reads.    */
+int hs_verify_attention_noalloc(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                                const void* k_cache, const void* v_cache, int kv_dtype,
+                                int64_t cache_stride_block, int64_t cache_stride_tok,
+                                int64_t cache_stride_head, float k_scale, float v_scale,
+                                const int32_t* block_tables, int64_t block_table_stride,
+                                int block_table_width, int num_blocks,
+                                const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                int num_seqs, int max_seqlen_q, int max_seqlen_k,
+                                int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                                float softmax_scale, void* out, int64_t out_stride_tok,
+                                int64_t out_stride_head, void* stream);
+size_t hs_verify_attention_noalloc_scratch_bytes(void);
 
 /* ------------------------------------------------------------------------ */
 /* KV-cache store: store_kvcache, mini_vllm/layers/attention.py:59-90, and   */
