@@ -126,11 +126,15 @@ def bench_accept(args, torch, hv):
     bufs = [(target.clone(), None if q is None else q.clone()) for _ in range(copies)]
     del target, q
 
+    # the caller-side promise that every top-k is in [1, 64] (single launch for small B)
+    topk_le64 = (args.mode == "filtered" and not args.per_seq and 1 <= args.top_k <= 64
+                 and not args.no_topk_hint)
+
     def step(i):
         lg, qq = bufs[i % copies]
         return hv.ops.spec_accept(lg, qq, s["draft_tokens"], s["temperatures"], s["u_accept"],
                                   s["u_resample"], mode=args.mode, top_ks=s["top_ks"],
-                                  top_ps=s["top_ps"])
+                                  top_ps=s["top_ps"], topk_le64=topk_le64)
 
     outs = []
 
@@ -167,7 +171,7 @@ def bench_accept(args, torch, hv):
                    "vocab": V, "mode": args.mode,
                    "sampling": "per-seq T~U[0.5,1.2], top-k {0,20,50}, top-p {1,0.9,0.8}"
                    if args.per_seq else f"T={args.temperature} top-k={args.top_k} top-p={args.top_p}",
-                   "input_copies_rotated": copies},
+                   "input_copies_rotated": copies, "topk_le64": topk_le64},
         "accepted_mean": round(sum(nacc) / len(nacc), 3),
         "wall_s": round(wall, 3),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
@@ -175,13 +179,25 @@ def bench_accept(args, torch, hv):
                      "traffic": profiled_traffic("hs_spec_accept call", _accept_tag(args)),
                      "bytes_per_step": step_bytes,
                      "kernels": "one hs_spec_accept call: k_accept_small for reference-mode "
-                                "calls that fit one workgroup per CU, else the chain (row "
-                                "statistics, filter when filtered, decision + resample "
-                                "partials, final search)"},
+                                "calls that fit one workgroup per CU, k_accept_small_topk "
+                                "for such filtered calls with every top-k in [1, 64], else "
+                                "the chain (row statistics, filter when filtered, decision + "
+                                "resample partials, final search)"},
     }
     if not args.no_cpu_baseline:
-        w = hv.synthetic.accept_workload(1, 3, seed=0, dtype="bf16", temperature=0.6)
-        res["cpu_baseline"] = cpu_baseline_accept(torch, w, args.cpu_seconds)
+        # one sequence of the same settings (the per-sequence settings of a batch
+        # vary; its first sequence's are used)
+        if args.per_seq or args.mode == "greedy":
+            w = hv.synthetic.accept_workload(1, gamma, seed=0, dtype=args.logits,
+                                             temperature=0.6)
+            mode = "reference"
+        else:
+            w = hv.synthetic.accept_workload(1, gamma, seed=0, dtype=args.logits,
+                                             temperature=args.temperature, top_k=args.top_k,
+                                             top_p=args.top_p, mode=args.mode)
+            mode = args.mode
+        res["cpu_baseline"] = cpu_baseline_accept(torch, w, args.cpu_seconds, mode=mode,
+                                                  logits=args.logits)
     return res
 
 
@@ -311,18 +327,22 @@ def _cpu_legs(torch, fn, seconds: float, min_iters: int):
     return legs, best, n_os, n_proc
 
 
-def cpu_baseline_accept(torch, w, seconds: float):
+def cpu_baseline_accept(torch, w, seconds: float, mode: str = "reference",
+                        logits: str = "bf16"):
     from oracle import torch_port
-    lg = torch.from_numpy(w["logits"])  # bf16-rounded values as f32
-    lg = lg.to(torch.bfloat16)
+    lg = torch.from_numpy(w["logits"])  # (bf16-rounded) values as f32
+    if logits == "bf16":
+        lg = lg.to(torch.bfloat16)
     q = torch.from_numpy(w["draft_probs"])
     dt = torch.from_numpy(w["draft_tokens"])
     T = torch.from_numpy(w["temperatures"])
     ua = torch.from_numpy(w["u_accept"])
     ur = torch.from_numpy(w["u_resample"])
+    B, g = dt.shape
 
     def fn():
-        torch_port.run_verify_accept(lg, q, dt, T, ua, ur)
+        torch_port.run_verify_accept(lg, q, dt, T, ua, ur, mode=mode, top_ks=w["top_ks"],
+                                     top_ps=w["top_ps"])
 
     legs, best, n_os, n_proc = _cpu_legs(torch, fn, seconds, 5)
     per, n, el = legs[best]
@@ -331,8 +351,11 @@ def cpu_baseline_accept(torch, w, seconds: float):
             "single_thread": {"value": round(legs[1][0] * 1e6, 1), "cores": 1},
             "threads_tried": {str(k): round(v[0] * 1e6, 1) for k, v in sorted(legs.items())},
             "os_cpu_count": n_os, "nproc": n_proc,
-            "sample": f"{n} acceptance steps at B=1 gamma=3 V=151936 over {el:.1f} s per leg "
-                      "(torch-CPU restatement of model_runner.py:391-428)"}
+            "sample": f"{n} acceptance steps at B={B} gamma={g} V=151936, {mode} mode, "
+                      f"{logits} logits, over {el:.1f} s per leg (torch-CPU restatement of "
+                      "model_runner.py:391-428" +
+                      (" with sampler.py:27-49's top-k / top-p" if mode == "filtered" else "") +
+                      ")"}
 
 
 def cpu_baseline_attention(torch, lens, block_size: int, R: int, Hq: int, Hkv: int, D: int,
@@ -734,6 +757,8 @@ def main(argv=None):
     ap.add_argument("--eager", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-topk-hint", action="store_true",
+                    help="accept workload: do not pass the top-k <= 64 promise (chain path)")
     args = ap.parse_args(argv)
     if args.rocprof_summary:
         print(rocprof_summary(args.rocprof_summary, args.kernel))

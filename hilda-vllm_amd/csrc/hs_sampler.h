@@ -141,6 +141,17 @@ struct SampleOut {
 // (rows*3 + units*4) * nchunk * 8 <= 28 * 8 * 256 = 57344 bytes.
 constexpr size_t kSmallTagBytes = 65536;
 
+// Tagged words of the single-launch top-k acceptance (filtered mode with every
+// top-k in [1, kTopkMax]), in a second fixed region right after the first:
+// per (row, chunk) the chunk's maximum (key, index) pair (2 words) and its
+// candidate count (1 word), then per (row, chunk) kTopkSlots candidates of 3
+// words (key, index, draft probability). Eligible calls have at most
+// kTopkPairs (row, chunk) pairs.
+constexpr int kTopkMax = 64;
+constexpr int kTopkSlots = 64;
+constexpr int kTopkPairs = 2048;
+constexpr size_t kTopkTagBytes = (size_t)kTopkPairs * (3 + 3 * kTopkSlots) * 8;
+
 struct Layout {
   size_t sync, tags, part, desc, st, spart, filt, cand, h1m, h1e, h1c, h2m, h2e, h2c, flist, total;
 };
@@ -155,5 +166,10 @@ int small_accept_ok(const Problem& P, const AcceptArgs& A, int mode, int esz);
 template <typename T>
 int launch_accept_small(const Problem& P, const AcceptArgs& A, const Work& W, const SampleOut& O,
                         hipStream_t stream);
+// the same for filtered mode when every sequence's top-k is in [1, kTopkMax]
+int small_topk_ok(const Problem& P, const AcceptArgs& A, int esz);
+template <typename T>
+int launch_accept_small_topk(const Problem& P, const AcceptArgs& A, const Work& W,
+                             const SampleOut& O, hipStream_t stream);
 
 }  // namespace hs

@@ -548,7 +548,7 @@ Layout make_layout(int units, int rows, int nchunk) {
   // single-launch acceptance: 3 tagged words per (row, chunk) and 4 per (unit, chunk),
   // in a region of fixed size and place for every shape
   (void)units;
-  L.tags = off; off = align_up(off + kSmallTagBytes, 256);
+  L.tags = off; off = align_up(off + kSmallTagBytes + kTopkTagBytes, 256);
   L.part = off; off = align_up(off + (size_t)rows * nchunk * sizeof(ChunkStat), 256);
   L.desc = off; off = align_up(off + (size_t)rows * sizeof(RowDesc), 256);
   L.st = off; off = align_up(off + (size_t)units * sizeof(SeqState), 256);
@@ -691,8 +691,11 @@ int hs_spec_accept(const void* target_logits, int logits_dtype, int64_t logits_r
                    float* row_stats, void* workspace, size_t workspace_bytes, void* stream) {
   if (batch <= 0 || gamma <= 0 || gamma > kMaxGamma || vocab <= 0) return HS_ERR_INVALID;
   if (batch > kMaxRows) return HS_ERR_UNSUPPORTED;
+  const bool topk_le64 = (mode & HS_ACCEPT_TOPK_LE64) != 0;
+  mode &= ~HS_ACCEPT_TOPK_LE64;
   if (mode != HS_ACCEPT_REFERENCE && mode != HS_ACCEPT_FILTERED && mode != HS_ACCEPT_GREEDY)
     return HS_ERR_INVALID;
+  if (topk_le64 && mode != HS_ACCEPT_FILTERED) return HS_ERR_INVALID;
   if (logits_dtype != HS_F32 && logits_dtype != HS_BF16) return HS_ERR_INVALID;
   if (!target_logits || !draft_tokens || !num_accepted || !out_tokens || !out_len || !workspace)
     return HS_ERR_INVALID;
@@ -740,6 +743,10 @@ int hs_spec_accept(const void* target_logits, int logits_dtype, int64_t logits_r
   if (small_accept_ok(P, A, mode, logits_dtype == HS_F32 ? 4 : 2)) {
     if (logits_dtype == HS_F32) return launch_accept_small<float>(P, A, W, O, s);
     return launch_accept_small<uint16_t>(P, A, W, O, s);
+  }
+  if (topk_le64 && small_topk_ok(P, A, logits_dtype == HS_F32 ? 4 : 2)) {
+    if (logits_dtype == HS_F32) return launch_accept_small_topk<float>(P, A, W, O, s);
+    return launch_accept_small_topk<uint16_t>(P, A, W, O, s);
   }
   if (logits_dtype == HS_F32) return run_sampler_chain<float>(P, A, W, mode, O, s);
   return run_sampler_chain<uint16_t>(P, A, W, mode, O, s);

@@ -1,4 +1,6 @@
-// Single-launch acceptance for small batches (reference mode), gfx950.
+// Single-launch acceptance for small batches, gfx950: reference mode
+// (k_accept_small) and filtered mode with every top-k in [1, 64]
+// (k_accept_small_topk, described above its definition).
 //
 // Same computation as the launch chain of spec_accept.hip (k_chunk_stats ->
 // k_sample_part -> k_sample_final) for ModelRunner.run_verify's rejection
@@ -37,6 +39,10 @@
 #include "hs_sampler.h"
 #include "hs_sampler_dev.h"
 #include "../../include/hilda_spec.h"
+
+// sum over the active lanes of the wave (device library; DPP lane moves)
+extern "C" __device__ __attribute__((const)) unsigned long long __ockl_wfred_add_u64(
+    unsigned long long);
 
 namespace hs {
 
@@ -493,6 +499,672 @@ __global__ __launch_bounds__(SmallShape<G>::kThreads) void k_accept_small(Proble
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// Single launch for filtered mode with every top-k in [1, kTopkMax].
+//
+// Top-k bounds the kept set of each target row to at most 64 elements, so the
+// whole decision and draw of a sequence depend on its rows' top-k candidates
+// only, and no third exchange is needed:
+//   A. every workgroup (one per 2048-element chunk of the sequence) publishes
+//      the maximum (key, index) pair of its chunk of every row;
+//   B. every workgroup reads all chunk maxima of its sequence's rows; the k-th
+//      largest, tau, is at or below the k-th largest element of the row (k
+//      distinct chunk maxima are at or above it), so the row's top-k elements
+//      are among those at or above tau. Each workgroup publishes its chunk's
+//      elements at or above tau (key, index, draft probability), at most its
+//      64 largest (a chunk holds at most k of the row's top k);
+//   C. workgroup 0 gathers the candidates (wave j: row j), sorts them, keeps
+//      the top k, applies top-p on them with the exact fixed-point masses of
+//      the chain (sampler.py:27-49), takes the decision and draws the resample
+//      or bonus token over the kept set of at most 64 elements, in index order.
+// The arithmetic (temperature division, exp, fixed-point sums and their
+// roundings, the draw) is the chain's, so decisions and tokens are the same.
+// ---------------------------------------------------------------------------
+
+// rank key of element idx with order key `key`: larger key first, lower index
+// first among equal keys (0 never occurs for a real element: idx < 2^31)
+__device__ __forceinline__ uint64_t rank_pair(uint32_t key, uint32_t idx) {
+  return ((uint64_t)key << 32) | (uint64_t)(0xffffffffu - idx);
+}
+__device__ __forceinline__ uint32_t pair_idx(uint64_t p) {
+  return 0xffffffffu - (uint32_t)p;
+}
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
+  const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, m, 64);
+  const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), m, 64);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// Bitonic sort, descending, of the NPL*64 keys a wave holds as v[s] at
+// position s*64 + lane, carrying one 32-bit payload per key. Equal keys keep
+// their own payloads (both partners of a compare keep theirs on a tie).
+template <int NPL>
+__device__ __forceinline__ void wave_sort_desc(uint64_t (&v)[NPL], uint32_t (&pl)[NPL],
+                                               int lane) {
+  constexpr int N = NPL * kWave;
+#pragma unroll
+  for (int size = 2; size <= N; size <<= 1) {
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      if (stride >= kWave) {
+        const int ts = stride / kWave;
+#pragma unroll
+        for (int s = 0; s < NPL; ++s) {
+          const int s2 = s ^ ts;
+          if (s2 > s) {
+            const bool desc = ((s * kWave + lane) & size) == 0;
+            const bool sw = desc ? (v[s] < v[s2]) : (v[s] > v[s2]);
+            if (sw) {
+              const uint64_t t = v[s];
+              v[s] = v[s2];
+              v[s2] = t;
+              const uint32_t u = pl[s];
+              pl[s] = pl[s2];
+              pl[s2] = u;
+            }
+          }
+        }
+      } else {
+#pragma unroll
+        for (int s = 0; s < NPL; ++s) {
+          const uint64_t w = shfl_xor_u64(v[s], stride);
+          const uint32_t wp = (uint32_t)__shfl_xor((int)pl[s], stride, 64);
+          const bool lower = (lane & stride) == 0;
+          const bool desc = ((s * kWave + lane) & size) == 0;
+          const bool take = (lower == desc) ? (w > v[s]) : (w < v[s]);
+          if (take) {
+            v[s] = w;
+            pl[s] = wp;
+          }
+        }
+      }
+    }
+  }
+}
+
+// Number of entries of v[0, n) (LDS) greater than `mine`; eight reads are issued
+// before their compares, so a step costs one LDS latency, not eight.
+__device__ __forceinline__ int count_greater(const uint64_t* v, int n, uint64_t mine) {
+  int rank = 0, x = 0;
+  for (; x + 8 <= n; x += 8) {
+    uint64_t t[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) t[u] = v[x + u];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) rank += t[u] > mine ? 1 : 0;
+  }
+  for (; x < n; ++x) rank += v[x] > mine ? 1 : 0;
+  return rank;
+}
+
+// One tagged word, re-read until it carries `tag` (bounded as read_tagged).
+__device__ __forceinline__ uint32_t get_tagged(const uint64_t* p, uint32_t tag, SmallSync* sy,
+                                               int* bad) {
+  for (uint32_t spins = 0;; ++spins) {
+    const uint64_t v = get_u64(p);
+    if ((uint32_t)(v >> 32) == tag) return (uint32_t)v;
+    if (spins == kSpinLimit) {
+      *bad = 1;
+      __hip_atomic_store(&sy->err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return 0u;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+// regions of the top-k words (after the reference-mode words)
+struct TopkWords {
+  uint64_t* base;
+  int rows, nchunk;
+  __device__ uint64_t* maxw(int row) const { return base + (int64_t)row * nchunk * 2; }
+  __device__ uint64_t* cntw(int row) const {
+    return base + (int64_t)rows * nchunk * 2 + (int64_t)row * nchunk;
+  }
+  __device__ uint64_t* candw(int row, int c) const {
+    return base + (int64_t)rows * nchunk * 3 + ((int64_t)row * nchunk + c) * (3 * kTopkSlots);
+  }
+};
+
+__device__ __forceinline__ TopkWords topk_words(const Work& W, int rows, int nchunk) {
+  TopkWords t;
+  t.base = W.tags + kSmallTagBytes / 8;
+  t.rows = rows;
+  t.nchunk = nchunk;
+  return t;
+}
+
+// Candidates of one row gathered by one wave: entries [b0, b0 + 64*NPL) of the
+// row's list (chunk order), written through the wave's LDS buffer into the
+// sort layout (position s*64 + lane); positions past n hold key 0.
+template <int NPL>
+__device__ __forceinline__ void gather_cands(const TopkWords& TW, int row, const uint32_t (&cnt)[4],
+                                             const uint32_t (&off)[4], int nchunk, int b0, int n,
+                                             uint32_t tag, SmallSync* sy, int* bad, int lane,
+                                             uint64_t* buf_p, uint32_t* buf_q, uint64_t (&v)[NPL],
+                                             uint32_t (&pl)[NPL]) {
+  const int b1 = b0 + NPL * kWave;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = lane + i * kWave;
+    if (c >= nchunk) continue;
+    const int lo = (int)off[i] > b0 ? (int)off[i] : b0;
+    const int hi = (int)(off[i] + cnt[i]) < b1 ? (int)(off[i] + cnt[i]) : b1;
+    const uint64_t* cw = TW.candw(row, c);
+    for (int e = lo; e < hi; ++e) {
+      const uint64_t* w = cw + 3 * (e - (int)off[i]);
+      const uint32_t key = get_tagged(w, tag, sy, bad);
+      const uint32_t idx = get_tagged(w + 1, tag, sy, bad);
+      const uint32_t q = get_tagged(w + 2, tag, sy, bad);
+      buf_p[e - b0] = rank_pair(key, idx);
+      buf_q[e - b0] = q;
+    }
+  }
+  // other lanes of the wave read these entries: the writes complete first
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int s = 0; s < NPL; ++s) {
+    const int e = b0 + s * kWave + lane;
+    const bool ok = e < n;
+    v[s] = ok ? buf_p[s * kWave + lane] : 0ull;
+    pl[s] = ok ? buf_q[s * kWave + lane] : 0u;
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_wave_barrier();
+}
+
+template <typename T, int G>
+__global__ __launch_bounds__(SmallShape<G>::kThreads) void k_accept_small_topk(Problem P,
+                                                                               AcceptArgs A,
+                                                                               Work W,
+                                                                               SampleOut O) {
+  using S = SmallShape<G>;
+  constexpr int R = S::R, NG = S::NG, RPG = S::RPG, NW = S::NW, NT = S::kThreads;
+  constexpr int kOv = kChunk;  // overflow sort buffer: one row's chunk
+  __shared__ uint64_t s_pm[NW][RPG];
+  __shared__ uint32_t s_cn[NW][RPG];
+  __shared__ uint64_t s_tau[R];
+  __shared__ RowDesc s_desc[R];
+  __shared__ float s_xd[G], s_qd[G];
+  __shared__ int64_t s_dt[G];
+  __shared__ int s_nacc;
+  __shared__ uint32_t s_tag;
+  __shared__ int s_bad;
+  __shared__ long long s_tok;
+  __shared__ int s_nb[R];
+  __shared__ uint32_t s_kidx[R][kTopkMax];
+  __shared__ float s_ke[R][kTopkMax];
+  __shared__ uint32_t s_kq[R][kTopkMax];
+  // overflow sort of one row's chunk (phase B), or the gather buffers of the
+  // waves of workgroup 0 (phase C)
+  __shared__ uint64_t s_big[kOv];
+  __shared__ uint32_t s_bigq[kOv];
+  // phase C: per row the exclusive candidate offsets of the chunks (and the
+  // total at [nchunk]), the positions of the k largest, the draw's kept set
+  __shared__ int s_off[R][4 * kWave + 1];
+  __shared__ int s_sorted[R][kTopkMax];
+  __shared__ uint64_t s_dw[kWave];
+  __shared__ uint32_t s_didx[kWave];
+
+  const int c = blockIdx.x;
+  const int unit = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wid >> 2;
+  const int gt = tid & 255;
+  const uint32_t nwg = gridDim.x * gridDim.y;
+  SmallSync* sy = W.sync;
+  const int rows = P.units * R;
+  const TopkWords TW = topk_words(W, rows, P.nchunk);
+  const int64_t i0 = chunk_elem(c, gt, 0);
+  const bool in = i0 < P.V;
+  const T* lrow = reinterpret_cast<const T*>(P.logits) + (int64_t)unit * R * P.row_stride;
+  const float* qrow = A.q + (int64_t)unit * G * A.q_stride;
+
+  int64_t d = -1;
+  float u_acc = 1.0f;
+  const int jl = lane < G ? lane : 0;
+  if (wid == 0) {
+    d = A.dtok[(int64_t)unit * G + jl];
+    u_acc = A.u_acc[(int64_t)unit * G + jl];
+  }
+  const float u_res = O.uniforms[unit];
+  const float Tt = P.temps[unit];
+  const int topk = P.top_ks[unit];
+  const float topp = P.top_ps[unit];
+  const float rT = 1.0f / Tt;
+  const bool fastT = hs_rcp_ok(Tt);
+
+  // ---- phase A: rows in registers, chunk maximum pairs ----
+  float x[RPG][8], q[RPG][8];
+#pragma unroll
+  for (int s = 0; s < RPG; ++s) {
+    const int j = grp + NG * s;
+    load8_row<T>(lrow + (j < R ? j : R - 1) * P.row_stride, i0, in && j < R, x[s]);
+    load8_row<float>(qrow + (j < G ? j : G - 1) * A.q_stride, i0, in && j < G, q[s]);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const bool dok = lane < G && d >= 0 && d < P.V;
+  T xd_raw = 0;
+  float qd = 0.0f;
+  uint64_t start = 0;
+  if (wid == 0) {
+    const int64_t dc = dok ? d : 0;
+    xd_raw = lrow[jl * P.row_stride + dc];
+    qd = qrow[jl * A.q_stride + dc];
+    if (lane == 0) {
+      start = __hip_atomic_fetch_add(&sy->start, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if ((uint32_t)start == nwg - 1)
+        __hip_atomic_store(&sy->start, ((start >> 32) + 1) << 32, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  const bool entry_bad = wid == 0 && lane == 0 && (uint32_t)start >= nwg;
+  if (entry_bad) __hip_atomic_store(&sy->err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // a top-k outside [1, kTopkMax] (or above the chunk count) breaks the caller's promise
+  const bool k_bad = topk < 1 || topk > kTopkMax || topk > P.nchunk;
+
+  uint32_t key[RPG][8];
+#pragma unroll
+  for (int s = 0; s < RPG; ++s) {
+    uint64_t pm = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      x[s][k] = hs_div_temp(x[s][k], Tt, rT, fastT);
+      key[s][k] = hs_key(x[s][k]);
+      const uint64_t pr = rank_pair(key[s][k], (uint32_t)(i0 + k));
+      if (in && pr > pm) pm = pr;
+    }
+    pm = wave_max_u64(pm);
+    if (lane == 0) s_pm[wid][s] = pm;
+  }
+  if (tid == 0) {
+    s_tag = (uint32_t)(start >> 32) + 1u;
+    s_bad = (entry_bad || k_bad) ? 1 : 0;
+  }
+  if (tid < R) s_tau[tid] = 0ull;
+  __syncthreads();
+  const uint32_t tag = s_tag;
+  if (gt == 0) {
+#pragma unroll
+    for (int s = 0; s < RPG; ++s) {
+      const int j = grp + NG * s;
+      if (j < R) {
+        uint64_t pm = s_pm[grp * 4][s];
+#pragma unroll
+        for (int w = 1; w < 4; ++w) pm = s_pm[grp * 4 + w][s] > pm ? s_pm[grp * 4 + w][s] : pm;
+        uint64_t* mw = TW.maxw(unit * R + j) + c * 2;
+        put_u64(mw, tagged(tag, (uint32_t)(pm >> 32)));
+        put_u64(mw + 1, tagged(tag, (uint32_t)pm));
+      }
+    }
+  }
+  if (wid == 0 && lane < G) {
+    s_dt[lane] = d;
+    s_xd[lane] = dok ? hs_div_t(ld1<T>(&xd_raw), Tt) : 0.0f;
+    s_qd[lane] = qd;
+  }
+
+  // ---- phase B: tau per row, this chunk's candidates ----
+  const int kk = k_bad ? 1 : topk;
+  // the chunk maxima of every row into LDS (wave j: row j); each thread then
+  // ranks one of them against the others of its row (broadcast reads) and the
+  // one ranked k - 1 is tau (pairs are distinct: their indices differ)
+  if (wid < R) {
+    uint32_t w[4][2];
+    read_tagged<4, 2>(TW.maxw(unit * R + wid), P.nchunk, lane, tag, w, sy, &s_bad);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int cc = lane + i * kWave;
+      if (cc < P.nchunk) s_big[wid * P.nchunk + cc] = ((uint64_t)w[i][0] << 32) | w[i][1];
+    }
+  }
+  __syncthreads();
+  for (int t = tid; t < R * P.nchunk; t += NT) {
+    const int j = t / P.nchunk;
+    const uint64_t* rp = s_big + j * P.nchunk;
+    const uint64_t mine = rp[t - j * P.nchunk];
+    if (count_greater(rp, P.nchunk, mine) == kk - 1) s_tau[j] = mine;
+  }
+  __syncthreads();
+  uint32_t cmask[RPG];  // bit k: element k is a candidate of row slot s
+#pragma unroll
+  for (int s = 0; s < RPG; ++s) {
+    const int j = grp + NG * s;
+    const uint64_t tau = s_tau[j < R ? j : 0];
+    uint32_t m = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (in && j < R && rank_pair(key[s][k], (uint32_t)(i0 + k)) >= tau) m |= 1u << k;
+    cmask[s] = m;
+    const uint32_t n = wave_sum_u32((uint32_t)__builtin_popcount(m));
+    if (lane == 0) s_cn[wid][s] = n;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int s = 0; s < RPG; ++s) {
+    const int j = grp + NG * s;
+    if (j >= R) continue;
+    const uint32_t* gc = &s_cn[grp * 4][0];
+    const uint32_t n = gc[0 * RPG + s] + gc[1 * RPG + s] + gc[2 * RPG + s] + gc[3 * RPG + s];
+    if (n > (uint32_t)kTopkSlots) continue;  // published below, after an LDS sort
+    uint32_t woff = 0;
+    for (int w = 0; w < (wid & 3); ++w) woff += gc[w * RPG + s];
+    const uint32_t mine = (uint32_t)__builtin_popcount(cmask[s]);
+    const uint32_t before = wave_incl_scan_u32(mine, lane) - mine;
+    uint64_t* cw = TW.candw(unit * R + j, c);
+    uint32_t slot = woff + before;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if (cmask[s] & (1u << k)) {
+        put_u64(cw + 3 * slot, tagged(tag, key[s][k]));
+        put_u64(cw + 3 * slot + 1, tagged(tag, (uint32_t)(i0 + k)));
+        put_u64(cw + 3 * slot + 2, tagged(tag, f2u(j < G ? q[s][k] : 0.0f)));
+        ++slot;
+      }
+    }
+    if (gt == 0) put_u64(TW.cntw(unit * R + j) + c, tagged(tag, n));
+  }
+  // rows with more than kTopkSlots candidates in this chunk (ties, or rows whose
+  // largest values crowd into one chunk): sort the chunk's candidate pairs in
+  // LDS with the whole workgroup and publish the 64 largest
+  for (int j = 0; j < R; ++j) {
+    const int g = j % NG, s = j / NG;
+    const uint32_t* gc = &s_cn[g * 4][0];
+    const uint32_t n = gc[0 * RPG + s] + gc[1 * RPG + s] + gc[2 * RPG + s] + gc[3 * RPG + s];
+    if (n <= (uint32_t)kTopkSlots) continue;  // workgroup-uniform
+    __syncthreads();
+    if (grp == g) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        s_big[gt * 8 + k] = (cmask[s] & (1u << k)) ? rank_pair(key[s][k], (uint32_t)(i0 + k))
+                                                  : 0ull;
+    }
+    __syncthreads();
+    for (int size = 2; size <= kOv; size <<= 1) {
+      for (int stride = size >> 1; stride > 0; stride >>= 1) {
+        for (int i = tid; i < kOv; i += NT) {
+          const int l = i ^ stride;
+          if (l > i) {
+            const uint64_t a = s_big[i], b = s_big[l];
+            const bool desc = (i & size) == 0;
+            if (desc ? (a < b) : (a > b)) {
+              s_big[i] = b;
+              s_big[l] = a;
+            }
+          }
+        }
+        __syncthreads();
+      }
+    }
+    if (tid < kTopkSlots) {
+      const uint64_t pr = s_big[tid];
+      const uint32_t idx = pair_idx(pr);
+      const float qv = j < G ? qrow[j * A.q_stride + idx] : 0.0f;
+      uint64_t* cw = TW.candw(unit * R + j, c) + 3 * tid;
+      put_u64(cw, tagged(tag, (uint32_t)(pr >> 32)));
+      put_u64(cw + 1, tagged(tag, idx));
+      put_u64(cw + 2, tagged(tag, f2u(qv)));
+      if (tid == 0) put_u64(TW.cntw(unit * R + j) + c, tagged(tag, (uint32_t)kTopkSlots));
+    }
+  }
+  __syncthreads();     // s_big is reused below
+  if (c != 0) return;  // workgroup 0 of the sequence gathers and decides
+
+  // ---- phase C (workgroup 0): kept sets, decision, draw ----
+  // candidate counts of every (row, chunk) -> exclusive offsets (wave j: row j)
+  if (wid < R) {
+    uint32_t cnt[4][1];
+    read_tagged<4, 1>(TW.cntw(unit * R + wid), P.nchunk, lane, tag, cnt, sy, &s_bad);
+    uint32_t run = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int cc = lane + i * kWave;
+      const uint32_t cn = cc < P.nchunk ? (cnt[i][0] <= (uint32_t)kTopkSlots ? cnt[i][0] : 0u)
+                                        : 0u;
+      if (cc < P.nchunk && cnt[i][0] > (uint32_t)kTopkSlots) s_bad = 1;
+      const uint32_t inc = wave_incl_scan_u32(cn, lane);
+      if (cc < P.nchunk) s_off[wid][cc] = (int)(run + inc - cn);
+      run += (uint32_t)__builtin_amdgcn_readlane((int)inc, 63);
+    }
+    if (lane == 0) s_off[wid][P.nchunk] = (int)run;
+  }
+  __syncthreads();
+  int rb[R + 1];  // first entry of each row in the workgroup's list
+  rb[0] = 0;
+#pragma unroll
+  for (int j = 0; j < R; ++j) rb[j + 1] = rb[j] + s_off[j][P.nchunk];
+  const int total = rb[R];
+  const bool in_lds = total <= kOv;  // workgroup-uniform
+  if (in_lds) {
+    // every candidate's three words, all of a thread's loads in flight together
+    constexpr int kPer = (kOv + NT - 1) / NT;
+    const uint64_t* ad[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int e = tid + i * NT;
+      ad[i] = nullptr;
+      if (e < total) {
+        int j = 0;
+#pragma unroll
+        for (int jj = 1; jj < R; ++jj) j += rb[jj] <= e ? 1 : 0;
+        const int el = e - rb[j];
+        int lo = 0, hi = P.nchunk;  // s_off[j][lo] <= el < s_off[j][hi]
+        while (hi - lo > 1) {
+          const int mid = (lo + hi) >> 1;
+          if (s_off[j][mid] <= el) lo = mid;
+          else hi = mid;
+        }
+        ad[i] = TW.candw(unit * R + j, lo) + 3 * (el - s_off[j][lo]);
+      }
+    }
+    uint64_t wv[kPer][3];
+    for (uint32_t spins = 0;; ++spins) {
+#pragma unroll
+      for (int i = 0; i < kPer; ++i)
+#pragma unroll
+        for (int k = 0; k < 3; ++k) wv[i][k] = ad[i] ? get_u64(ad[i] + k) : tagged(tag, 0u);
+      bool ok = true;
+#pragma unroll
+      for (int i = 0; i < kPer; ++i)
+#pragma unroll
+        for (int k = 0; k < 3; ++k) ok = ok && (uint32_t)(wv[i][k] >> 32) == tag;
+      if (ok) break;
+      if (spins == kSpinLimit) {
+        s_bad = 1;
+        __hip_atomic_store(&sy->err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int e = tid + i * NT;
+      if (e < total) {
+        s_big[e] = rank_pair((uint32_t)wv[i][0], (uint32_t)wv[i][1]);
+        s_bigq[e] = (uint32_t)wv[i][2];
+      }
+    }
+    __syncthreads();
+    // rank every candidate within its row (broadcast reads); the k largest are
+    // listed in rank order
+    for (int e = tid; e < total; e += NT) {
+      int j = 0;
+#pragma unroll
+      for (int jj = 1; jj < R; ++jj) j += rb[jj] <= e ? 1 : 0;
+      const int rank = count_greater(s_big + rb[j], rb[j + 1] - rb[j], s_big[e]);
+      if (rank < kk) s_sorted[j][rank] = e;
+    }
+    __syncthreads();
+  }
+  if (wid < R) {
+    const int row = unit * R + wid;
+    const int n = s_off[wid][P.nchunk];
+    uint64_t top = 0ull;
+    uint32_t topq = 0u;
+    if (in_lds) {
+      if (lane < kk && lane < n) {
+        const int e = s_sorted[wid][lane];
+        top = s_big[e];
+        topq = s_bigq[e];
+      }
+    } else {
+      // more than kOv candidates in all (ties, crowded chunks): each wave merges its
+      // row's list 192 entries at a time into the 64 largest
+      uint32_t off[4], cn[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int cc = lane + i * kWave;
+        off[i] = cc < P.nchunk ? (uint32_t)s_off[wid][cc] : 0u;
+        cn[i] = cc < P.nchunk ? (uint32_t)(s_off[wid][cc + 1] - s_off[wid][cc]) : 0u;
+      }
+      uint64_t* bp = s_big + wid * 256;
+      uint32_t* bq = s_bigq + wid * 256;
+      uint64_t v[4];
+      uint32_t pl[4];
+      gather_cands<4>(TW, row, cn, off, P.nchunk, 0, n, tag, sy, &s_bad, lane, bp, bq, v, pl);
+      wave_sort_desc<4>(v, pl, lane);
+      for (int b0 = 4 * kWave; b0 < n; b0 += 3 * kWave) {
+        uint64_t v2[4];
+        uint32_t p2[4];
+        gather_cands<4>(TW, row, cn, off, P.nchunk, b0 - kWave, n, tag, sy, &s_bad, lane, bp,
+                        bq, v2, p2);
+        v2[0] = v[0];
+        p2[0] = pl[0];
+        wave_sort_desc<4>(v2, p2, lane);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          v[s] = v2[s];
+          pl[s] = p2[s];
+        }
+      }
+      top = v[0];
+      topq = pl[0];
+    }
+    // lane r < k holds rank r of the row's top k
+    const int kn = kk;
+    const bool rk = lane < kn;
+    const float xr = hs_unkey((uint32_t)(top >> 32));
+    const float M = u2f((uint32_t)__builtin_amdgcn_readlane((int)f2u(xr), 0));
+    const float er = rk ? hs_exp(xr - M) : 0.0f;
+    const uint64_t fe = rk ? hs_fx44(er) : 0ull;
+    const float SA = hs_f32_rz_of_u64(__ockl_wfred_add_u64(fe)) * kTwoM44;
+    int nb = kn;
+    float Sk = SA;
+    if (topp < 1.0f) {
+      const float mr = rk ? er / SA : 0.0f;
+      const uint64_t cum = wave_incl_scan_u64(rk ? hs_fx44(mr) : 0ull, lane);
+      const bool keep = rk && (lane == 0 || hs_f32_of_u64(cum) * kTwoM44 < topp);
+      nb = __popcll(__ballot(keep));
+      if (nb < kn) Sk = hs_f32_rz_of_u64(__ockl_wfred_add_u64(lane < nb ? fe : 0ull)) * kTwoM44;
+    }
+    // the last kept pair (both halves zero-extended: the low half has its top bit set)
+    const uint64_t last =
+        (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)top, nb - 1) |
+        ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(top >> 32), nb - 1) << 32);
+    if (lane < nb) {
+      s_kidx[wid][lane] = pair_idx(top);
+      s_ke[wid][lane] = er;
+      s_kq[wid][lane] = topq;
+    }
+    if (lane == 0) {
+      RowDesc dd;
+      dd.m = M;
+      dd.s = Sk;
+      dd.tkey = (uint32_t)(last >> 32);
+      dd.tidx = (int32_t)pair_idx(last);
+      dd.all = 0;
+      dd.token = -1;
+      dd.s_full = Sk;
+      dd.pad = 0;
+      s_desc[wid] = dd;
+      s_nb[wid] = nb;
+      if (n < kn) s_bad = 1;  // fewer candidates than k: inconsistent words
+      if (O.row_stats) {
+        O.row_stats[2 * (int64_t)row] = M;
+        O.row_stats[2 * (int64_t)row + 1] = Sk;
+      }
+    }
+  }
+  __syncthreads();
+  if (wid == 0) {
+    bool rej = false;
+    if (lane < G) {
+      float pt = 0.0f, pd = 0.0f;
+      if (dok) {
+        pt = desc_prob(s_desc[lane], s_xd[lane], d);
+        pd = s_qd[lane];
+      }
+      const float ratio = pt / fmaxf(pd, 1e-10f);
+      const float a = fminf(ratio, 1.0f);
+      rej = !(u_acc < a);
+    }
+    const uint64_t mask = __ballot(rej);
+    const int r = mask ? (__ffsll((long long)mask) - 1) : G;
+    // resample (residual max(P - Q, 0), or P when its sum is <= 1e-10) or bonus
+    // draw over the kept set of row r, in index order
+    const int nb = s_nb[r];
+    const bool has = lane < nb;
+    const float Sr = s_desc[r].s;
+    const uint32_t idx = has ? s_kidx[r][lane] : 0xffffffffu;
+    const float p = has ? s_ke[r][lane] / Sr : 0.0f;
+    const float qv = has ? u2f(s_kq[r][lane]) : 0.0f;
+    const uint64_t pw = hs_fx44(p);
+    const uint64_t w = (r < G) ? hs_fx44(fmaxf(p - qv, 0.0f)) : 0ull;
+    const uint64_t wt = __ockl_wfred_add_u64(w);
+    const uint64_t pt = __ockl_wfred_add_u64(pw);
+    const bool use_res = (r < G) && (hs_f32_of_u64(wt) * kTwoM44 > 1e-10f);
+    const uint64_t total_w = use_res ? wt : pt;
+    const uint64_t t = hs_mulshift24(hs_u24(u_res), total_w);
+    // inclusive prefix of the weights in index order: each kept element sums the
+    // weights of the kept elements at or below its index; the token is the one
+    // element whose prefix passes t while its exclusive prefix does not
+    const uint64_t mywt = use_res ? w : pw;
+    s_dw[lane] = mywt;
+    s_didx[lane] = idx;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_wave_barrier();
+    uint64_t incl = 0;
+    int x = 0;
+    for (; x + 8 <= nb; x += 8) {
+      uint32_t ix[8];
+      uint64_t wx[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        ix[u] = s_didx[x + u];
+        wx[u] = s_dw[x + u];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) incl += ix[u] <= idx ? wx[u] : 0ull;
+    }
+    for (; x < nb; ++x) incl += s_didx[x] <= idx ? s_dw[x] : 0ull;
+    const uint64_t hit = __ballot(has && incl > t && incl - mywt <= t);
+    const int first = hit ? __ffsll((long long)hit) - 1 : 0;
+    const uint32_t tok_idx = (uint32_t)__builtin_amdgcn_readlane((int)idx, first);
+    if (lane == 0) {
+      s_nacc = r;
+      s_tok = hit ? (long long)tok_idx : -1ll;
+    }
+  }
+  __syncthreads();
+  const bool bad = s_bad != 0;
+  const int r = s_nacc;
+  if (tid <= G) {
+    int64_t v;
+    if (bad) v = -1;
+    else if (tid < r) v = s_dt[tid];
+    else if (tid == r) v = (int64_t)s_tok;
+    else v = -1;
+    A.tok_out[(int64_t)unit * R + tid] = v;
+  }
+  if (tid == 0) {
+    A.nacc_out[unit] = bad ? -1 : r;
+    A.len_out[unit] = bad ? 0 : r + 1;
+  }
+}
+
 }  // namespace
 
 int small_accept_ok(const Problem& P, const AcceptArgs& A, int mode, int esz) {
@@ -537,8 +1209,50 @@ int launch_accept_small(const Problem& P, const AcceptArgs& A, const Work& W, co
   return hipGetLastError() == hipSuccess ? HS_OK : HS_ERR_LAUNCH;
 }
 
+int small_topk_ok(const Problem& P, const AcceptArgs& A, int esz) {
+  if (A.gamma < 1 || A.gamma > 7) return 0;
+  if ((P.V % 8) || (((uintptr_t)P.logits | (uintptr_t)A.q) & 15) || ((P.row_stride * esz) % 16) ||
+      ((A.q_stride * 4) % 16))
+    return 0;
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return 0;
+  // every workgroup resident at once; at least kTopkMax chunk maxima per row
+  // (tau needs k of them); the words fit their region
+  return (P.nchunk >= kTopkMax && P.nchunk <= 4 * kWave && (int64_t)P.nchunk * P.units <= cus &&
+          (int64_t)P.units * (A.gamma + 1) * P.nchunk <= kTopkPairs) ? 1 : 0;
+}
+
+template <typename T>
+int launch_accept_small_topk(const Problem& P, const AcceptArgs& A, const Work& W,
+                             const SampleOut& O, hipStream_t stream) {
+  const dim3 grid(P.nchunk, P.units);
+  switch (A.gamma) {
+#define HS_TOPK_CASE(G)                                                                     \
+  case G:                                                                                   \
+    hipLaunchKernelGGL((k_accept_small_topk<T, G>), grid, dim3(SmallShape<G>::kThreads), 0, \
+                       stream, P, A, W, O);                                                 \
+    break;
+    HS_TOPK_CASE(1)
+    HS_TOPK_CASE(2)
+    HS_TOPK_CASE(3)
+    HS_TOPK_CASE(4)
+    HS_TOPK_CASE(5)
+    HS_TOPK_CASE(6)
+    HS_TOPK_CASE(7)
+#undef HS_TOPK_CASE
+    default: return HS_ERR_UNSUPPORTED;
+  }
+  return hipGetLastError() == hipSuccess ? HS_OK : HS_ERR_LAUNCH;
+}
+
 template int launch_accept_small<float>(const Problem&, const AcceptArgs&, const Work&,
                                         const SampleOut&, hipStream_t);
+template int launch_accept_small_topk<float>(const Problem&, const AcceptArgs&, const Work&,
+                                             const SampleOut&, hipStream_t);
+template int launch_accept_small_topk<uint16_t>(const Problem&, const AcceptArgs&, const Work&,
+                                                const SampleOut&, hipStream_t);
 template int launch_accept_small<uint16_t>(const Problem&, const AcceptArgs&, const Work&,
                                            const SampleOut&, hipStream_t);
 

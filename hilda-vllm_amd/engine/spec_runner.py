@@ -81,6 +81,7 @@ class SpecRunner:
         self.temps = torch.full((batch,), float(temperature), **f32)
         self.top_ks = torch.full((batch,), int(top_k), dtype=torch.int32, device=dev)
         self.top_ps = torch.full((batch,), float(top_p), **f32)
+        self.topk_le64 = mode == "filtered" and 1 <= int(top_k) <= 64
         self.tok_scratch = torch.zeros(batch, dtype=torch.int64, device=dev)
         self.u_res = torch.zeros(batch, **f32)
         self.d_stage = self._stage_bufs(batch)
@@ -346,7 +347,8 @@ class SpecRunner:
         self.u_res.uniform_()
         nacc, out, olen = ops.spec_accept(logits, G.draft_probs, G.draft_tokens, self.temps,
                                           G.u_acc, self.u_res, mode=self.mode,
-                                          top_ks=self.top_ks, top_ps=self.top_ps)
+                                          top_ks=self.top_ks, top_ps=self.top_ps,
+                                          topk_le64=self.topk_le64)
         ops.spec_commit(st, g, out, olen, eligible=G.elig)
         G.last = (nacc, out, olen)
         self.last = G.last

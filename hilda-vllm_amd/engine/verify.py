@@ -178,9 +178,12 @@ class VerifyRunner:
         for i, d in enumerate(draft_tokens):
             groups.setdefault(len(d), []).append(i)
         temps = torch.tensor(temps_l, dtype=torch.float32).to(dev, non_blocking=True)
+        topk_le64 = False
         if self.mode == "filtered":
-            tks = torch.tensor([int(s.top_k) for s in seqs], dtype=torch.int32).to(dev)
+            ks = [int(s.top_k) for s in seqs]
+            tks = torch.tensor(ks, dtype=torch.int32).to(dev)
             tps = torch.tensor([float(s.top_p) for s in seqs], dtype=torch.float32).to(dev)
+            topk_le64 = all(1 <= k <= 64 for k in ks)
         if uniforms is not None:
             u_acc_all, u_res_all = uniforms
             u_acc_all = torch.as_tensor(u_acc_all, dtype=torch.float32).to(dev)
@@ -218,7 +221,8 @@ class VerifyRunner:
             nacc, out, _ = _ops.spec_accept(
                 lg, q, dt, temps[ix], u_acc_all[ix, :g], u_res_all[ix], mode=mode,
                 top_ks=tks[ix] if mode == "filtered" else None,
-                top_ps=tps[ix] if mode == "filtered" else None)
+                top_ps=tps[ix] if mode == "filtered" else None,
+                topk_le64=topk_le64 and mode == "filtered")
             packed[ix, :g + 1] = out
             packed[ix, -1] = nacc.to(torch.int64)
         host = packed.cpu().numpy()  # the one D2H copy (synchronises)

@@ -77,8 +77,13 @@ def spec_accept(target_logits: torch.Tensor, draft_probs: torch.Tensor | None,
                 draft_tokens: torch.Tensor, temperatures: torch.Tensor | None,
                 u_accept: torch.Tensor | None, u_resample: torch.Tensor | None, *,
                 mode="reference", top_ks: torch.Tensor | None = None,
-                top_ps: torch.Tensor | None = None, row_stats: bool = False):
+                top_ps: torch.Tensor | None = None, row_stats: bool = False,
+                topk_le64: bool = False):
     """Fused acceptance sampler (drop-in for model_runner.py:387-428).
+
+    topk_le64 (filtered mode): the caller knows every entry of top_ks is in
+    [1, 64]; small batches then run as one launch. A sequence breaking that
+    promise gets num_accepted -1.
 
     target_logits [B, gamma+1, V] f32/bf16, draft_probs [B, gamma, V] f32,
     draft_tokens [B, gamma] int64, temperatures [B] f32, u_accept [B, gamma],
@@ -121,6 +126,8 @@ def spec_accept(target_logits: torch.Tensor, draft_probs: torch.Tensor | None,
             raise ValueError("filtered mode needs top_ks and top_ps")
         top_ks = top_ks.to(torch.int32).contiguous()
         top_ps = top_ps.to(torch.float32).contiguous()
+    elif topk_le64:
+        raise ValueError("topk_le64 applies to filtered mode only")
     nacc = torch.empty(B, dtype=torch.int32, device=dev)
     out = torch.empty((B, R), dtype=torch.int64, device=dev)
     olen = torch.empty(B, dtype=torch.int32, device=dev)
@@ -138,7 +145,8 @@ def spec_accept(target_logits: torch.Tensor, draft_probs: torch.Tensor | None,
                             p(top_ps) if m == L.HS_ACCEPT_FILTERED else None,
                             p(u_accept) if m != L.HS_ACCEPT_GREEDY else None,
                             p(u_resample) if m != L.HS_ACCEPT_GREEDY else None,
-                            B, gamma, V, m, p(nacc), p(out), p(olen), p(stats), ws.data_ptr(),
+                            B, gamma, V, m | (L.HS_ACCEPT_TOPK_LE64 if topk_le64 else 0),
+                            p(nacc), p(out), p(olen), p(stats), ws.data_ptr(),
                             ws.numel(), _stream(dev))
     L.check(rc, "hs_spec_accept")
     if row_stats:

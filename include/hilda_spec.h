@@ -45,6 +45,10 @@ extern "C" {
 #define HS_ACCEPT_REFERENCE 0 /* temperature-only softmax (model_runner.py:398) */
 #define HS_ACCEPT_FILTERED 1  /* temperature, top-k, top-p (sampler.py:20-49)   */
 #define HS_ACCEPT_GREEDY 2    /* argmax match; temperature ignored             */
+/* Flag OR-ed into HS_ACCEPT_FILTERED by a caller that knows every sequence's */
+/* top-k is in [1, 64] (top-p any): small batches then run as a single launch */
+/* (a sequence whose top-k breaks the promise gets num_accepted -1).          */
+#define HS_ACCEPT_TOPK_LE64 0x100
 
 /* Human-readable text for a status code (static storage). */
 const char* hs_status_string(int status);
@@ -81,7 +85,8 @@ int hs_version(void);
 /*                 Small batches (batch x ceil(vocab/2048) workgroups fit one */
 /*                 per CU, gamma <= 7, aligned rows, vocab a multiple of 8)  */
 /*                 run as a single launch whose workgroups exchange data     */
-/*                 through the workspace. If one of its bounded waits ever   */
+/*                 through the workspace: in reference mode, and in filtered */
+/*                 mode with HS_ACCEPT_TOPK_LE64 when vocab >= 64 * 2048. If one of its bounded waits ever   */
 /*                 ran out, or its launch counter was not left by a completed */
 /*                 call, that sequence's num_accepted is -1 and out_len 0,   */
 /*                 and the 32-bit word at byte offset 8 of the workspace is  */

@@ -111,6 +111,47 @@ def test_graph_replay_matches_eager(cuda):
         assert graph.tokens(b) == eager.tokens(b)
 
 
+def test_filtered_topk_graph_replay_matches_eager(cuda):
+    """Filtered mode with top-k 50 / top-p 0.9 at the full 151936-token vocabulary:
+    the runner passes the top-k <= 64 promise, so acceptance runs as the single
+    top-k launch inside the captured verify graph; replays must reproduce eager
+    steps token for token, and every step emits 1..gamma+1 tokens."""
+    q3, sr = _mods()
+    gt = _small(q3, layers=2, vocab=151936)
+    gd = _small(q3, layers=1, vocab=151936)
+
+    def make():
+        target = q3.Qwen3Host(gt, device=cuda, seed=23)
+        draft = q3.Qwen3Host(gd, device=cuda, seed=24)
+        r = sr.SpecRunner(target, draft, batch=2, gamma=3, max_model_len=400, block_size=32,
+                          temperature=0.9, top_k=50, top_p=0.9, mode="filtered", device=cuda)
+        assert r.topk_le64
+        r.load_prompts([[3, 4, 5, 6], list(range(200, 240))])
+        torch.manual_seed(6)
+        r.prefill()
+        return r
+
+    eager = make()
+    torch.manual_seed(78)
+    prev = eager.lengths()
+    for _ in range(7):
+        eager.step()
+        cur = eager.lengths()
+        assert all(1 <= a - b <= 4 for a, b in zip(cur, prev)), (prev, cur)
+        prev = cur
+    graph = make()
+    torch.manual_seed(78)
+    graph.step()
+    graph.capture()
+    for _ in range(6):
+        graph.replay()
+    torch.cuda.synchronize()
+    graph.check()
+    assert graph.lengths() == eager.lengths()
+    for b in range(2):
+        assert graph.tokens(b) == eager.tokens(b)
+
+
 def test_fused_layer_matches_eager(cuda):
     """Fused kernels (RMSNorm inside the projections, qk-norm + RoPE + KV store,
     SwiGLU epilogue) vs the eager restatement of qwen3.py:72-185 (same attention
