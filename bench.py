@@ -110,9 +110,27 @@ def _accept_inputs(torch, hv, dev, args):
     return target, q, small
 
 
+def _topk_hint(args) -> bool:
+    """The caller-side promise that every top-k is in [1, 64] (the single top-k
+    launch for small batches)."""
+    return (args.mode == "filtered" and not args.per_seq and 1 <= args.top_k <= 64
+            and not args.no_topk_hint)
+
+
+def _accept_valu_busy(tag: str):
+    """VALU-busy percentage of the acceptance call's longest-running profiled kernel
+    (the single launch, or the chain's row-statistics / filter passes)."""
+    for k in ("k_accept_small_topk<float, 3>", "k_accept_small<bf16, 3>",
+              "k_chunk_stats_w<bf16>", "k_filter_pass1<float>", "k_filter_pass1<bf16>"):
+        v = profiled_counter(k, tag, "VALUBusy %")
+        if v is not None:
+            return v
+    return None
+
+
 def _accept_tag(args) -> str:
     tag = f"accept-b{args.batch}-g{args.gamma}-{args.mode}-{args.logits}"
-    return tag + ("-perseq" if args.per_seq else "")
+    return tag + ("-perseq" if args.per_seq else "") + ("-topk" if _topk_hint(args) else "")
 
 
 def bench_accept(args, torch, hv):
@@ -126,9 +144,7 @@ def bench_accept(args, torch, hv):
     bufs = [(target.clone(), None if q is None else q.clone()) for _ in range(copies)]
     del target, q
 
-    # the caller-side promise that every top-k is in [1, 64] (single launch for small B)
-    topk_le64 = (args.mode == "filtered" and not args.per_seq and 1 <= args.top_k <= 64
-                 and not args.no_topk_hint)
+    topk_le64 = _topk_hint(args)
 
     def step(i):
         lg, qq = bufs[i % copies]
@@ -177,6 +193,8 @@ def bench_accept(args, torch, hv):
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": profiled_traffic("hs_spec_accept call", _accept_tag(args)),
+                     "mfma_util": 0.0,
+                     "valu_busy": _accept_valu_busy(_accept_tag(args)),
                      "bytes_per_step": step_bytes,
                      "kernels": "one hs_spec_accept call: k_accept_small for reference-mode "
                                 "calls that fit one workgroup per CU, k_accept_small_topk "
@@ -280,6 +298,8 @@ def bench_attention(args, torch, hv):
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": call_traffic([main_kernel, "k_attn_combine_sk<true>"],
                                              f"attention-{args.kv}"),
+                     "mfma_util": profiled_counter(main_kernel, f"attention-{args.kv}",
+                                                   "MfmaUtil %"),
                      "bytes_per_launch": per_launch,
                      "kernel": f"{main_kernel} + k_attn_combine_sk<true> (one call, timed together)"},
     }
@@ -623,6 +643,7 @@ def attention_probe(torch, hv, kv: str = "auto", L: int = PROBE_CONTEXT, layers:
     kernel = f"k_verify_attn<{'true' if fp8 else 'false'}, 4>"
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": profiled_traffic(kernel, "attention-b1"),
+            "mfma_util": profiled_counter(kernel, "attention-b1", "MfmaUtil %"),
             "kernel": kernel, "bytes_per_launch": per_launch, "avg_launch_us": round(us, 3),
             "shape": f"B=1 q={R} Hq={Hq} Hkv={Hkv} D={D} L={L} block {bs}",
             "launches": reps * layers}
@@ -640,6 +661,27 @@ def profiled_traffic(kernel: str, workload: str):
         if len(cells) >= 5 and cells[0] == workload and cells[1] == kernel:
             try:
                 return int(float(cells[4]))
+            except ValueError:
+                return None
+    return None
+
+
+def profiled_counter(kernel: str, workload: str, column: str):
+    """A compute counter (column "MfmaUtil %" or "VALUBusy %") of `kernel` in
+    `workload` from the compute-counter table of profiles/traffic.md, or None."""
+    path = ROOT / "profiles" / "traffic.md"
+    if not path.exists():
+        return None
+    header = None
+    for line in path.read_text().splitlines():
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) >= 3 and cells[:2] == ["workload", "kernel"]:
+            header = cells
+            continue
+        if header and column in header and len(cells) == len(header) and \
+                cells[0] == workload and cells[1] == kernel:
+            try:
+                return float(cells[header.index(column)])
             except ValueError:
                 return None
     return None
