@@ -43,9 +43,17 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
 
 
+# Per-file flags. verify_attention: the per-tile kernel's 10 leading scalar
+# arguments (13 dwords) are preloaded into SGPRs at dispatch; kernels whose
+# first argument is the argument block get nothing preloaded.
+FILE_FLAGS = {
+    "verify_attention": ["-mllvm", "-amdgpu-kernarg-preload-count=10"],
+}
+
+
 def _compile(src: Path) -> Path:
     obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [HIPCC, *COMMON_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *COMMON_FLAGS, *FILE_FLAGS.get(src.stem, []), "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stdout}\n{res.stderr}")

@@ -62,6 +62,7 @@ struct AttnArgs {
   const int32_t* cu_q;
   const int32_t* cu_k;
   int B, Hkv, G, block_size, qtiles, nsplit, split_len;
+  int bs_shift;               // log2(block_size) for power-of-two block sizes, else -1
   float scale_log2;          // softmax_scale * k_scale * log2(e)
   uint16_t* out;
   int64_t o_st, o_sh;
@@ -72,6 +73,12 @@ struct AttnArgs {
   int sk_nwg;                // balanced launch: workgroups
   int xcd_pack;              // per-tile grid: only workgroups x % xcd_pack == 0 work
 };
+
+// block of a key position: a shift for power-of-two block sizes, a division
+// (several dependent scalar and VALU steps) otherwise
+__device__ __forceinline__ int key_block(int key, int bs_shift, int block_size) {
+  return bs_shift >= 0 ? key >> bs_shift : key / block_size;
+}
 
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
   return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));  // v_cvt_pk_bf16_f32
@@ -214,14 +221,19 @@ __device__ __forceinline__ int tile_keys(const TileRef& t, int G) {
   return hi > 0 ? hi : 0;
 }
 
-constexpr int kOStride = kD + 8;  // floats per row of a wave's partial output
+// floats per row of a wave's partial output: rows 4 banks apart, so the
+// 16-byte writes (lanes = rows) and the merge's reads fall in distinct banks
+constexpr int kOStride = kD + 4;
 template <bool kFp8>
 struct AttnLds {
   static constexpr int kRowB = kFp8 ? 128 : 256;
   static constexpr int kTileB = kWin * kRowB;
   static constexpr int kKvBytes = kAW * 2 * kTileB;
   static constexpr int kOBytes = kAW * kRows * kOStride * 4;
-  static constexpr int kRawBytes = kKvBytes > kOBytes ? kKvBytes : kOBytes;
+  // 16 zero bytes after the tiles and partials: the merge reads them in place
+  // of the partials of waves that held no keys
+  static constexpr int kZeroOff = kKvBytes > kOBytes ? kKvBytes : kOBytes;
+  static constexpr int kRawBytes = kZeroOff + 16;
 };
 
 // Running softmax state of one wave: per query row (lane column n) the max
@@ -251,8 +263,8 @@ __device__ __forceinline__ void wave_walk(const AttnArgs& a, const TileRef& t, i
   const int n = lane & 15;  // query row of this lane (B-operand column)
   const int g = lane >> 4;  // k-group of this lane
   const int r0 = t.qt * kRows;
-  const int bt0 = lo / a.block_size;
-  const int nbt_used = (hi > lo) ? (hi - 1) / a.block_size - bt0 + 1 : 0;
+  const int bt0 = key_block(lo, a.bs_shift, a.block_size);
+  const int nbt_used = (hi > lo) ? key_block(hi - 1, a.bs_shift, a.block_size) - bt0 + 1 : 0;
 
   // query row of this lane
   const int r = r0 + n;
@@ -281,7 +293,7 @@ __device__ __forceinline__ void wave_walk(const AttnArgs& a, const TileRef& t, i
   // window ws of this wave -> cache row bases (bytes) of its K and V head rows;
   // false when its block is not a valid cache block (the window is skipped)
   auto window_base = [&](int ws, const uint8_t*& kb, const uint8_t*& vb) -> bool {
-    const int blk_idx = ws / a.block_size;
+    const int blk_idx = key_block(ws, a.bs_shift, a.block_size);
     const int bi = blk_idx - bt0;
     const int blk = (bi < nbt_used && bi < bt_cap && bt0 + bi < a.bt_width) ? s_bt[bi] : -1;
     if (blk < 0 || blk >= a.num_blocks) return false;
@@ -413,6 +425,38 @@ __device__ __forceinline__ void wave_walk(const AttnArgs& a, const TileRef& t, i
   for (int db = 0; db < 8; ++db) acc.oacc[db] = oacc[db];
 }
 
+// Merge of the first NW waves' partials for one query row and dims d0..d0+3,
+// d0+64..d0+67: running max M, sum L and unnormalised output o (waves w >=
+// nact hold no keys and weigh 0).
+template <int NW>
+__device__ __forceinline__ void merge_waves(const float (*s_m)[kRows], const float (*s_l)[kRows],
+                                            const float* s_o, const float* s_zero, int wave_o,
+                                            int nact, int row, int d0, float& M, float& L,
+                                            float (&o)[8]) {
+  float mw[NW];
+  M = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    mw[w] = w < nact ? s_m[w][row] : -INFINITY;
+    M = fmaxf(M, mw[w]);
+  }
+  const float Mb = (M == -INFINITY) ? 0.0f : M;
+  L = 0.0f;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) o[t] = 0.0f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    const float f = __builtin_amdgcn_exp2f(mw[w] - Mb);
+    L += (w < nact ? s_l[w][row] : 0.0f) * f;
+    const float* src0 = w < nact ? &s_o[w * wave_o + row * kOStride + d0] : s_zero;
+    const float* src1 = w < nact ? src0 + 64 : s_zero;
+    const float4 x0 = *reinterpret_cast<const float4*>(src0);
+    const float4 x1 = *reinterpret_cast<const float4*>(src1);
+    o[0] += x0.x * f; o[1] += x0.y * f; o[2] += x0.z * f; o[3] += x0.w * f;
+    o[4] += x1.x * f; o[5] += x1.y * f; o[6] += x1.z * f; o[7] += x1.w * f;
+  }
+}
+
 // Attends query tile t over keys [klo, khi) with the 8 waves of the workgroup
 // (wave w takes windows w, w + 8, ...), merges the waves and writes the
 // normalised output (pslot < 0) or the unnormalised partial (o, running max,
@@ -433,56 +477,66 @@ __device__ __forceinline__ void attend_keys(const AttnArgs& a, const TileRef& t,
   WaveAcc acc;
   wave_walk<kFp8, kG>(a, t, kvh, klo, khi, klo + wid * kWin, kAW * kWin, s_bt, bt_cap, tile_k,
                       tile_v, acc);
-  if (g == 0) {
+  // waves that hold keys (wave w starts at klo + 32w): the others have nothing
+  // to merge
+  const int nkeys = khi - klo;
+  const int nact = nkeys <= 0 ? 0 : (nkeys + kWin - 1) / kWin < kAW ? (nkeys + kWin - 1) / kWin : kAW;
+  // bf16 tiles: a wave's partial output fits its own K/V tiles, which it has
+  // finished reading (its last window's reads were waited on), so it needs no
+  // barrier before writing it; fp8 tiles are smaller and the partials go over
+  // the whole tile area after every wave is done with its tiles
+  constexpr bool kOwn = kRows * kOStride * 4 <= 2 * kTileB;
+  constexpr int kWaveO = kOwn ? 2 * kTileB / 4 : kRows * kOStride;  // floats between waves
+  float* s_o = reinterpret_cast<float*>(s_raw);
+  float* s_zero = reinterpret_cast<float*>(s_raw + AttnLds<kFp8>::kZeroOff);
+  if (tid == 0) *reinterpret_cast<float4*>(s_zero) = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (wid < nact && g == 0) {
     s_m[wid][n] = acc.m;
     s_l[wid][n] = acc.lsum;
   }
-  __syncthreads();  // every wave is done with its tiles
-  float* s_o = reinterpret_cast<float*>(s_raw);
+  if constexpr (!kOwn) __syncthreads();  // every wave is done with its tiles
+  if (wid < nact) {
 #pragma unroll
-  for (int db = 0; db < 8; ++db)
-    *reinterpret_cast<float4*>(&s_o[(wid * kRows + n) * kOStride + db * 16 + 4 * g]) =
-        make_float4(acc.oacc[db][0], acc.oacc[db][1], acc.oacc[db][2], acc.oacc[db][3]);
+    for (int db = 0; db < 8; ++db)
+      *reinterpret_cast<float4*>(&s_o[wid * kWaveO + n * kOStride + db * 16 + 4 * g]) =
+          make_float4(acc.oacc[db][0], acc.oacc[db][1], acc.oacc[db][2], acc.oacc[db][3]);
+  }
   __syncthreads();
-  // merge the waves: thread handles row tid/16, dims (tid%16)*8 .. +8 (the
-  // other threads have no row; there is no barrier below)
+  // merge the waves: thread handles row tid/16, dims 4(tid%16) .. +4 and
+  // 64 + 4(tid%16) .. +4 (the other threads have no row; there is no barrier
+  // below)
   const int row = tid >> 4;
   const int rr = r0 + row;
   if (tid >= kRows * 16 || rr >= rows) return;
-  const int d0 = (tid & 15) * 8;
-  float M = -INFINITY;
-#pragma unroll
-  for (int w = 0; w < kAW; ++w) M = fmaxf(M, s_m[w][row]);
-  const float Mb = (M == -INFINITY) ? 0.0f : M;
-  float L = 0.0f, f[kAW];
-#pragma unroll
-  for (int w = 0; w < kAW; ++w) {
-    f[w] = __builtin_amdgcn_exp2f(s_m[w][row] - Mb);
-    L += s_l[w][row] * f[w];
-  }
-  float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int w = 0; w < kAW; ++w) {
-    const float4 x0 = *reinterpret_cast<const float4*>(&s_o[(w * kRows + row) * kOStride + d0]);
-    const float4 x1 = *reinterpret_cast<const float4*>(&s_o[(w * kRows + row) * kOStride + d0 + 4]);
-    o[0] += x0.x * f[w]; o[1] += x0.y * f[w]; o[2] += x0.z * f[w]; o[3] += x0.w * f[w];
-    o[4] += x1.x * f[w]; o[5] += x1.y * f[w]; o[6] += x1.z * f[w]; o[7] += x1.w * f[w];
-  }
+  const int d0 = (tid & 15) * 4;
+  // branch-free over the first 4 or all 8 waves, so that all LDS reads go out
+  // together: a wave without keys contributes weight 0 and reads the zero
+  // bytes (one address for every lane)
+  float M, L, o[8];
+  if (nact <= 4)
+    merge_waves<4>(s_m, s_l, s_o, s_zero, kWaveO, nact, row, d0, M, L, o);
+  else
+    merge_waves<kAW>(s_m, s_l, s_o, s_zero, kWaveO, nact, row, d0, M, L, o);
   const int oi = rr / G, oh = kvh * G + rr % G;
   if (pslot < 0) {
     const float inv = (L > 0.0f) ? a.v_scale / L : 0.0f;
     union {
-      uint16_t h[8];
-      uint4 u;
-    } ob;
+      uint16_t h[4];
+      uint2 u;
+    } ob0, ob1;
 #pragma unroll
-    for (int t = 0; t < 8; ++t) ob.h[t] = f32_to_bf16_rne(o[t] * inv);
-    *reinterpret_cast<uint4*>(a.out + (int64_t)(qs + oi) * a.o_st + (int64_t)oh * a.o_sh + d0) = ob.u;
+    for (int t = 0; t < 4; ++t) {
+      ob0.h[t] = f32_to_bf16_rne(o[t] * inv);
+      ob1.h[t] = f32_to_bf16_rne(o[4 + t] * inv);
+    }
+    uint16_t* po = a.out + (int64_t)(qs + oi) * a.o_st + (int64_t)oh * a.o_sh + d0;
+    *reinterpret_cast<uint2*>(po) = ob0.u;
+    *reinterpret_cast<uint2*>(po + 64) = ob1.u;
   } else {
     const int64_t pidx = pslot * kRows + row;
     float* po = a.part_o + pidx * kD + d0;
     *reinterpret_cast<float4*>(po) = make_float4(o[0], o[1], o[2], o[3]);
-    *reinterpret_cast<float4*>(po + 4) = make_float4(o[4], o[5], o[6], o[7]);
+    *reinterpret_cast<float4*>(po + 64) = make_float4(o[4], o[5], o[6], o[7]);
     if ((tid & 15) == 0) {
       a.part_ml[pidx * 2] = M;
       a.part_ml[pidx * 2 + 1] = L;
@@ -500,52 +554,61 @@ __device__ __forceinline__ void attend_keys(const AttnArgs& a, const TileRef& t,
 // workgroups with x % 8 == 0, which the dispatcher places on the same XCD,
 // do the work; otherwise the workgroups of the XCDs dispatched last start up
 // to ~2 us after the first (measured on an idle GPU; ~0.25 us in a graph).
+// Small calls are latency-bound: every memory round trip and every long
+// dependent computation before the first K/V window is issued adds to the
+// kernel. The fields the prologue needs come ahead of the argument block as
+// scalar arguments, which the dispatcher preloads into SGPRs (this file is built
+// with -amdgpu-kernarg-preload-count covering them), so the first loads go out
+// without waiting for the argument block; the prologue has no integer division
+// for power-of-two block sizes and a single query tile (the host passes shifts
+// and the block-table entries one split can touch).
 template <bool kFp8, int kG>
-__global__ __launch_bounds__(kAT) void k_verify_attn(AttnArgs a) {
+__global__ __launch_bounds__(kAT) void k_verify_attn(const int32_t* cu_q, const int32_t* cu_k,
+                                                     const int32_t* bt, int bt_stride,
+                                                     int xcd_shift, int qtiles, int split_len,
+                                                     int bs_shift, int bt_width, int nbt_split,
+                                                     AttnArgs a) {
   const int G = kG ? kG : a.G;
   __shared__ __attribute__((aligned(16))) uint8_t s_raw[AttnLds<kFp8>::kRawBytes];
   __shared__ float s_m[kAW][kRows], s_l[kAW][kRows];
   __shared__ int s_bt[kBtCap];
-  // Small calls are latency-bound: every memory round trip before the first
-  // K/V window is issued adds to the kernel. The argument block's four 64-byte
-  // lines are requested together (one use of a field in each), not one miss
-  // per line as fields are first needed.
-  asm volatile("" ::"s"(a.q), "s"(a.bt), "s"(a.block_size), "s"(a.xcd_pack));
-  if (blockIdx.x % a.xcd_pack) return;
-  const int bx = blockIdx.x / a.xcd_pack;
-  const int kvh = bx / a.qtiles;
-  const int qt = bx % a.qtiles;
+  if (blockIdx.x & ((1u << xcd_shift) - 1)) return;
+  const int bx = blockIdx.x >> xcd_shift;
   const int split = blockIdx.y;
   const int b = blockIdx.z;
   const int tid = threadIdx.x;
 
   // The sequence bounds and the block-table entries this split can touch
   // (they only depend on the split) are requested before either is waited on.
-  const int cq0 = a.cu_q[b], cq1 = a.cu_q[b + 1], ck0 = a.cu_k[b], ck1 = a.cu_k[b + 1];
-  const int lo = split * a.split_len;
-  const int bt0 = lo / a.block_size;
-  int nbt = (lo + a.split_len - 1) / a.block_size - bt0 + 1;
-  if (nbt > a.bt_width - bt0) nbt = a.bt_width - bt0;
-  if (nbt > kBtCap) nbt = kBtCap;
-  const int32_t* btrow = a.bt + (int64_t)b * a.bt_stride;
+  const int cq0 = cu_q[b], cq1 = cu_q[b + 1], ck0 = cu_k[b], ck1 = cu_k[b + 1];
+  const int lo = split * split_len;
+  const int bt0 = split == 0 ? 0 : key_block(lo, bs_shift, a.block_size);
+  int nbt = nbt_split;
+  if (nbt > bt_width - bt0) nbt = bt_width - bt0;
+  const int32_t* btrow = bt + (int64_t)b * bt_stride;
   // branchless (a branch here would wait for the bounds first): entry
   // bt0 + tid clamped into the row (bt_width >= 1, checked by the host)
-  const int bi = bt0 + tid < a.bt_width ? bt0 + tid : a.bt_width - 1;
+  const int bi = bt0 + tid < bt_width ? bt0 + tid : bt_width - 1;
   const int bt_mine = btrow[bi];
+  // the argument block's four 64-byte lines are requested now, together (one
+  // field of each), while the loads above are in flight
+  asm volatile("" ::"s"(a.q), "s"(a.c_sh), "s"(a.scale_log2), "s"(a.sk_pre));
+  const int kvh = qtiles == 1 ? bx : bx / qtiles;
+  const int qt = bx - kvh * qtiles;
   // one wait for all five loads (otherwise the compiler sinks the table load
   // into the store below, behind the wait for the bounds)
   asm volatile("" ::"v"(bt_mine), "v"(cq0), "v"(cq1), "v"(ck0), "v"(ck1));
   const TileRef t = tile_ref_of(b, kvh, qt, G, cq0, cq1, ck0, ck1);
   if (tid < nbt) s_bt[tid] = bt_mine;
   for (int i = tid + kAT; i < nbt; i += kAT) s_bt[i] = btrow[bt0 + i];
-  if (qt * kRows >= t.rows || t.Lk <= 0) return;
-  const int nsplit_b = (t.Lk + a.split_len - 1) / a.split_len;
-  if (split >= nsplit_b) return;
-  int hi = lo + a.split_len;
+  // this split holds keys [lo, lo + split_len) of the sequence's Lk; a tile
+  // with more than split_len keys is split and writes partials
+  if (qt * kRows >= t.rows || lo >= t.Lk) return;
+  int hi = lo + split_len;
   const int vis = tile_keys(t, G);
   if (vis < hi) hi = vis;
   const int64_t pslot =
-      nsplit_b == 1 ? -1 : (((int64_t)b * a.Hkv + kvh) * a.qtiles + qt) * a.nsplit + split;
+      t.Lk <= split_len ? -1 : (((int64_t)b * a.Hkv + kvh) * qtiles + qt) * a.nsplit + split;
   attend_keys<kFp8, kG>(a, t, lo, hi, pslot, s_raw, s_m, s_l, s_bt, kBtCap);
 }
 
@@ -709,8 +772,8 @@ __global__ __launch_bounds__(kAT) void k_verify_attn_sk(AttnArgs a) {
     if (vis < khi) khi = vis;
     const int64_t pslot = (w == s0 && seg_end == s1) ? -1 : 2 * k + (seg > 0 ? 1 : 0);
     __syncthreads();  // the previous piece's readers of s_bt and the tiles are done
-    const int bt0 = klo / a.block_size;
-    const int nbt = (khi - 1) / a.block_size - bt0 + 1;
+    const int bt0 = key_block(klo, a.bs_shift, a.block_size);
+    const int nbt = key_block(khi - 1, a.bs_shift, a.block_size) - bt0 + 1;
     for (int i = tid; i < nbt && i < kSkBtCap && bt0 + i < a.bt_width; i += kAT)
       s_bt[i] = a.bt[(int64_t)b * a.bt_stride + bt0 + i];
     if constexpr (kHeads)
@@ -839,11 +902,20 @@ __global__ __launch_bounds__(kRows * 16) void k_attn_combine(AttnArgs a) {
 
 template <bool kFp8>
 static void launch_attn(int G, dim3 grid, hipStream_t s, const AttnArgs& a) {
+  const int bts = (int)a.bt_stride;
+  const int xs = a.xcd_pack == 8 ? 3 : 0;
+  // block-table entries one split can touch (it may start inside a block)
+  int nbt = (a.split_len + a.block_size - 1) / a.block_size + 1;
+  if (nbt > kBtCap) nbt = kBtCap;
   switch (G) {
-    case 2: hipLaunchKernelGGL((k_verify_attn<kFp8, 2>), grid, dim3(kAT), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((k_verify_attn<kFp8, 4>), grid, dim3(kAT), 0, s, a); break;
-    case 8: hipLaunchKernelGGL((k_verify_attn<kFp8, 8>), grid, dim3(kAT), 0, s, a); break;
-    default: hipLaunchKernelGGL((k_verify_attn<kFp8, 0>), grid, dim3(kAT), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((k_verify_attn<kFp8, 2>), grid, dim3(kAT), 0, s, a.cu_q, a.cu_k, a.bt, bts,
+                                 xs, a.qtiles, a.split_len, a.bs_shift, a.bt_width, nbt, a); break;
+    case 4: hipLaunchKernelGGL((k_verify_attn<kFp8, 4>), grid, dim3(kAT), 0, s, a.cu_q, a.cu_k, a.bt, bts,
+                                 xs, a.qtiles, a.split_len, a.bs_shift, a.bt_width, nbt, a); break;
+    case 8: hipLaunchKernelGGL((k_verify_attn<kFp8, 8>), grid, dim3(kAT), 0, s, a.cu_q, a.cu_k, a.bt, bts,
+                                 xs, a.qtiles, a.split_len, a.bs_shift, a.bt_width, nbt, a); break;
+    default: hipLaunchKernelGGL((k_verify_attn<kFp8, 0>), grid, dim3(kAT), 0, s, a.cu_q, a.cu_k, a.bt, bts,
+                                 xs, a.qtiles, a.split_len, a.bs_shift, a.bt_width, nbt, a); break;
   }
 }
 
@@ -980,7 +1052,7 @@ int hs_verify_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_he
     return HS_ERR_INVALID;
   if (num_seqs <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || max_seqlen_q <= 0 ||
       max_seqlen_k <= 0 || num_blocks <= 0 || block_size <= 0 || block_table_width <= 0 ||
-      block_table_stride < block_table_width)
+      block_table_stride < block_table_width || block_table_stride > INT32_MAX)
     return HS_ERR_INVALID;
   if (num_q_heads % num_kv_heads) return HS_ERR_INVALID;
   if (head_dim != kD) return HS_ERR_UNSUPPORTED;
@@ -1025,6 +1097,7 @@ int hs_verify_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_he
   a.Hkv = num_kv_heads;
   a.G = G;
   a.block_size = block_size;
+  a.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz((unsigned)block_size) : -1;
   a.scale_log2 = softmax_scale * (a.fp8 ? k_scale : 1.0f) * 1.4426950408889634f;
   a.out = static_cast<uint16_t*>(out);
   a.o_st = out_stride_tok;
