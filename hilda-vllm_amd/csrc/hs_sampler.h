@@ -57,9 +57,10 @@ struct FilterScratch {
   int32_t kept;
   int32_t path;
   int32_t ncand;   // candidates appended by the filter passes
-  int32_t b1;      // coarse boundary bucket (-1: the row never reaches p)
+  int32_t b1;      // coarse boundary bucket (-1: the row never reaches p; -2: not
+                   // within buckets 0..jmax, the row filter streams the row)
   int32_t b2;      // fine boundary bucket (-1: not refined)
-  int32_t pad;
+  int32_t jmax;    // pass 1 histograms buckets 0..jmax only (see mass_skip_bucket)
   float m;         // row max and normaliser (x = logit / T)
   float s;
   uint32_t tau;    // top-k gather threshold (order key)

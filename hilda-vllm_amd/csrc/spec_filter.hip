@@ -103,6 +103,27 @@ __device__ __forceinline__ uint64_t mass_threshold(float p) {
   return x0;
 }
 
+// Last coarse bucket whose elements top-p can keep, from a bound that needs
+// no pass over the row: an element in bucket b > J has x - M <= -(J+1)/8 (up
+// to one rounding of M - x), so its fixed-point mass is at most
+// e^-(J+1)/8 / S (1 + 1e-5) (exp within 2.5e-7 relative, one rounding of its
+// argument and of the division), and all of them together at most
+// U = V e^-(J+1)/8 (1 + 1e-5) / S. The masses of the whole row sum to at
+// least 1 - 1e-5 (S is a rounded-toward-zero sum of the same exponentials,
+// each floor loses < 2^-44), so when U <= 1 - p - 2e-5 the cumulative mass
+// reaches p (the threshold of mass_threshold) inside buckets 0..J. J is the
+// smallest bucket with V e^-(J+1)/8 1.001 / S <= (1 - p) - 1e-4 (wider
+// margins than the bound needs); kCB - 1 (no bucket skipped) when p is too
+// close to 1 or J would reach the last buckets.
+__device__ __forceinline__ int mass_skip_bucket(int V, float S, float p) {
+  const double room = (1.0 - (double)p) - 1e-4;
+  if (!(room > 0.0) || !(S > 0.0f)) return kCB - 1;
+  const double t = 8.0 * log((double)V * 1.001 / ((double)S * room));  // need J + 1 >= t
+  if (!(t < (double)(kCB - 2))) return kCB - 1;
+  const int j = (int)ceil(t) - 1;
+  return j < 0 ? 0 : j;
+}
+
 template <typename T>
 struct RowCtx {
   const T* rp;
@@ -708,6 +729,7 @@ __global__ __launch_bounds__(kPT) void k_filter_plan1(Problem P, Work W) {
       f.b2 = -1;
       f.ac = f.am = f.ae = 0ull;
       f.theta = (mode == 2) ? mass_threshold(P.top_ps[unit]) : 0ull;
+      f.jmax = (mode == 2) ? mass_skip_bucket(P.V, d.s, P.top_ps[unit]) : kCB - 1;
     }
   }
   if (mode != 1) return;
@@ -747,7 +769,9 @@ __global__ __launch_bounds__(kPT) void k_filter_plan2(Problem P, Work W) {
   const Crossing cr = find_crossing<kPT>(W.h1c[hb], W.h1m[hb], W.h1e[hb], 0ull, f.theta, ps.wsum,
                                          &ps.b, ps.v);
   if (t == 0) {
-    f.b1 = cr.b;
+    // no crossing although pass 1 skipped buckets: the bound did not hold
+    // (it always should); the row filter then streams the row
+    f.b1 = (cr.b < 0 && f.jmax < kCB - 1) ? -2 : cr.b;
     f.b2 = -1;
     f.ac = cr.c;
     f.am = cr.m;
@@ -780,12 +804,17 @@ __global__ __launch_bounds__(kPT) void k_filter_plan3(Problem P, Work W) {
 // only2: walk the top-p rows only (k_filter_gather_k takes the top-k rows).
 // Workgroups take segments of chunks (seg_plan): a top-p row's histogram
 // accumulates in LDS over the segment and reaches global memory once (flushes
-// per chunk made the global atomics a third of the pass).
+// per chunk made the global atomics a third of the pass). Top-p rows
+// histogram only buckets 0..jmax (mass_skip_bucket): a wave packs those
+// elements of a chunk into its LDS queue and its lanes then take the exp,
+// fixed-point masses and atomics of the queue densely.
 template <typename T>
 __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_filter_pass1(
     Problem P, Work W, int only2) {
   __shared__ PassShared ps;
+  __shared__ float s_q[kPT / kWave][8 * kWave];
   const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
   const int rows = P.units * P.rows_per_unit;
   const SegPlan sp = seg_plan(P, only2 ? W.flist[1] : rows);
   for (int it = blockIdx.x; it < sp.items; it += gridDim.x) {
@@ -824,14 +853,29 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
       const float M = f.m, S = f.s;
       const float rS = 1.0f / S;
       const bool fastS = hs_rcp_ok(S);
+      const int jmax = f.jmax;
+      float* q = s_q[tid / kWave];
       for (int c = c_lo; c < c_hi; ++c) {
         const int64_t i0 = chunk_elem(c, tid, 0);
         float x[8];
         load8<T>(rp, i0, P.V, vec_ok, x);
+        uint32_t flags = 0;
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
-          if (i0 + k >= P.V) continue;
-          const float xv = hs_div_temp(x[k], Tt, rT, fast);
+          x[k] = hs_div_temp(x[k], Tt, rT, fast);
+          if (i0 + k < P.V && coarse_bucket(x[k], M) <= jmax) flags |= 1u << k;
+        }
+        const uint32_t nf = (uint32_t)__popc(flags);
+        const uint32_t incl = wave_incl_scan_u32(nf, lane);
+        const uint32_t total = (uint32_t)__shfl((int)incl, kWave - 1, kWave);
+        uint32_t slot = incl - nf;
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          if (flags & (1u << k)) q[slot++] = x[k];
+        // the queue is this wave's: its LDS writes land before its reads
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        for (uint32_t j = (uint32_t)lane; j < total; j += kWave) {
+          const float xv = q[j];
           const int b = coarse_bucket(xv, M);
           atomicAdd(&ps.hc[b], 1u);
           if (b < kCB - 1) {  // the last bucket holds only zero masses
@@ -842,6 +886,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
             if (em) atomicAdd((unsigned long long*)&ps.he[b], (unsigned long long)em);
           }
         }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       }
       __syncthreads();
       const int64_t hb = (int64_t)row * kCB + tid;
@@ -1089,6 +1134,7 @@ __device__ __forceinline__ bool top_p_from_hist(const Work& W, int row, FilterSm
   (void)theta;
   const FilterScratch& f = W.filt[row];
   const int b1 = f.b1;
+  if (b1 == -2) return false;
   if (b1 < 0) {
     out.all = true;
     return true;
