@@ -69,6 +69,12 @@ struct FilterScratch {
   uint64_t ac;     // count, mass and e-mass of the elements before the boundary bucket
   uint64_t am;
   uint64_t ae;
+  // raw-value (logit) thresholds of the top-p passes, exact images of their
+  // bucket tests (x = logit / T is monotone in the logit): pass 1 takes
+  // logit >= rj (coarse bucket <= jmax), pass 2 rlo <= logit < rhi (coarse
+  // bucket b1), pass 3 flo <= logit < fhi (fine bucket b2 of b1)
+  float rj, rlo, rhi, flo, fhi;
+  uint32_t c1;     // elements in coarse bucket b1 (k_filter_plan2)
 };
 
 struct Problem {

@@ -586,6 +586,32 @@ __device__ __forceinline__ int fine_bucket(float x, float M, int b1) {
   return b < 0 ? 0 : (b > kCB - 1 ? kCB - 1 : b);
 }
 
+// Smallest float r (in hs_key order, over [-inf, +inf]) with pred(r) true, for
+// a pred that is false below some value and true from it on; NaN when pred
+// holds nowhere (every comparison with it is false). Called by a whole wave
+// (wave-uniform arguments): each round the 64 lanes test 63 keys spread over
+// the open interval, so the 2^32 keys take at most 6 rounds of one pred each.
+template <typename F>
+__device__ float raw_threshold(F pred) {
+  const int lane = threadIdx.x & (kWave - 1);
+  uint32_t lo = 0x007fffffu, hi = 0xff800000u;  // keys of -inf and +inf
+  if (!pred(hs_unkey(hi))) return __builtin_nanf("");
+  if (pred(hs_unkey(lo))) return -INFINITY;
+  // invariant: pred(lo) false, pred(hi) true
+  while (hi - lo > 1u) {
+    const uint32_t span = hi - lo;
+    const uint32_t pt = lo + (uint32_t)(((uint64_t)span * (uint64_t)(lane + 1)) >> 6);
+    const bool t = (lane == kWave - 1) || pred(hs_unkey(pt));  // lane 63 tests hi
+    const uint64_t m = __ballot(t);
+    const int first = __ffsll((long long)m) - 1;
+    const uint32_t nhi = (uint32_t)__shfl((int)pt, first, kWave);
+    const uint32_t nlo = first == 0 ? lo : (uint32_t)__shfl((int)pt, first - 1, kWave);
+    lo = nlo;
+    hi = nhi;
+  }
+  return hs_unkey(hi);
+}
+
 // exclusive scan over the kNT threads of a workgroup (kNT / 64 waves)
 template <int kNT>
 __device__ __forceinline__ uint64_t blk_scan(uint64_t v, uint64_t* wsum, uint64_t* total) {
@@ -638,28 +664,42 @@ __device__ __forceinline__ Crossing find_crossing(uint64_t hc, uint64_t hm, uint
   return r;
 }
 
-// Appends the (up to 8) flagged elements of every lane of the calling wave to
-// the row's candidate list: slots placed by a wave scan of the lanes' counts
-// and one global atomic per wave, no barrier. Slots past kCand are counted but
-// not written (the row filter then falls back to its radix select).
+// Slots of the flagged elements (bit k of flags) of the calling wave's lanes,
+// numbered element-major (every lane's element 0 in lane order, then element
+// 1, ...) from ballots and lane counts, with no LDS round trip; returns the
+// wave's total (wave-uniform).
+template <int N = 8>
+__device__ __forceinline__ uint32_t wave_slots8(uint32_t flags, uint32_t (&slot)[8]) {
+  uint32_t total = 0;
+#pragma unroll
+  for (int k = 0; k < N; ++k) {
+    const uint64_t m = __ballot((flags >> k) & 1u);
+    slot[k] = total + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+    total += (uint32_t)__popcll(m);
+  }
+  return total;
+}
+
+// Appends the (up to 8) flagged elements of every lane of the calling wave (all
+// lanes active) to the row's candidate list: slots from wave_slots8 and one
+// global atomic per wave, no barrier. Slots past kCand are counted but not
+// written (the row filter then falls back to its radix select).
 __device__ __forceinline__ void wave_append_cands(const Work& W, int row, const uint32_t (&key)[8],
                                                   uint32_t flags, int64_t i0) {
   const int lane = threadIdx.x & 63;
-  const uint32_t n = (uint32_t)__popc(flags);
-  const uint32_t incl = wave_incl_scan_u32(n, lane);
-  const uint32_t total = (uint32_t)__shfl((int)incl, kWave - 1, kWave);
+  uint32_t slot[8];
+  const uint32_t total = wave_slots8(flags, slot);
   if (total == 0) return;  // wave-uniform
   int base = 0;
   if (lane == 0) base = atomicAdd(&W.filt[row].ncand, (int)total);
-  int slot = __shfl(base, 0, kWave) + (int)(incl - n);
+  base = __builtin_amdgcn_readlane(base, 0);
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
-    if (flags & (1u << k)) {
-      if (slot < kCand)
-        W.cand[(int64_t)row * kCand + slot] =
-            ((uint64_t)key[k] << 32) | (uint64_t)(0xffffffffu - (uint32_t)(i0 + k));
-      ++slot;
-    }
+    const int sl = base + (int)slot[k];
+    if ((flags & (1u << k)) && sl < kCand)
+      W.cand[(int64_t)row * kCand + sl] =
+          ((uint64_t)key[k] << 32) | (uint64_t)(0xffffffffu - (uint32_t)(i0 + k));
   }
 }
 
@@ -722,6 +762,17 @@ __global__ __launch_bounds__(kPT) void k_filter_plan1(Problem P, Work W) {
   }
   if (wid == 0) {
     const RowDesc d = fold_row_desc(P, W, row, lane);
+    const int jmax = (mode == 2) ? mass_skip_bucket(P.V, d.s, P.top_ps[unit]) : kCB - 1;
+    // the logits pass 1 histograms; a row whose max is not finite takes none
+    // and goes to the row filter's radix path (k_filter_plan2)
+    float rj = 0.0f;
+    if (mode == 2) {
+      const float Tt = P.temps[unit], rT = 1.0f / Tt, M = d.m;
+      const bool fast = hs_rcp_ok(Tt);
+      rj = isfinite(M) ? raw_threshold([&](float r) {
+        return coarse_bucket(hs_div_temp(r, Tt, rT, fast), M) <= jmax;
+      }) : __builtin_nanf("");
+    }
     if (lane == 0) {
       f.m = d.m;
       f.s = d.s;
@@ -729,7 +780,8 @@ __global__ __launch_bounds__(kPT) void k_filter_plan1(Problem P, Work W) {
       f.b2 = -1;
       f.ac = f.am = f.ae = 0ull;
       f.theta = (mode == 2) ? mass_threshold(P.top_ps[unit]) : 0ull;
-      f.jmax = (mode == 2) ? mass_skip_bucket(P.V, d.s, P.top_ps[unit]) : kCB - 1;
+      f.jmax = jmax;
+      f.rj = rj;
     }
   }
   if (mode != 1) return;
@@ -766,16 +818,38 @@ __global__ __launch_bounds__(kPT) void k_filter_plan2(Problem P, Work W) {
   if (filter_mode(P, row / P.rows_per_unit) != 2) return;
   FilterScratch& f = W.filt[row];
   const int64_t hb = (int64_t)row * kCB + t;
-  const Crossing cr = find_crossing<kPT>(W.h1c[hb], W.h1m[hb], W.h1e[hb], 0ull, f.theta, ps.wsum,
+  const uint32_t hc = W.h1c[hb];
+  const Crossing cr = find_crossing<kPT>(hc, W.h1m[hb], W.h1e[hb], 0ull, f.theta, ps.wsum,
                                          &ps.b, ps.v);
-  if (t == 0) {
-    // no crossing although pass 1 skipped buckets: the bound did not hold
-    // (it always should); the row filter then streams the row
-    f.b1 = (cr.b < 0 && f.jmax < kCB - 1) ? -2 : cr.b;
-    f.b2 = -1;
-    f.ac = cr.c;
-    f.am = cr.m;
-    f.ae = cr.e;
+  if (cr.b >= 0 && t == cr.b) f.c1 = hc;
+  if (t < kWave) {
+    // no crossing although pass 1 skipped buckets (the bound did not hold; it
+    // always should), or a row max that is not finite: the row filter then
+    // streams the row
+    const float M = f.m;
+    const int b1 = !isfinite(M) ? -2 : (cr.b < 0 && f.jmax < kCB - 1) ? -2 : cr.b;
+    float rlo = 0.0f, rhi = 0.0f;
+    if (b1 >= 0) {
+      // logits of coarse bucket b1: [min with bucket <= b1, min with bucket < b1)
+      const int unit = row / P.rows_per_unit;
+      const float Tt = P.temps[unit], rT = 1.0f / Tt;
+      const bool fast = hs_rcp_ok(Tt);
+      rlo = raw_threshold([&](float r) {
+        return coarse_bucket(hs_div_temp(r, Tt, rT, fast), M) <= b1;
+      });
+      rhi = b1 == 0 ? INFINITY : raw_threshold([&](float r) {
+        return coarse_bucket(hs_div_temp(r, Tt, rT, fast), M) < b1;
+      });
+    }
+    if (t == 0) {
+      f.b1 = b1;
+      f.b2 = -1;
+      f.rlo = rlo;
+      f.rhi = rhi;
+      f.ac = cr.c;
+      f.am = cr.m;
+      f.ae = cr.e;
+    }
   }
 }
 
@@ -791,12 +865,31 @@ __global__ __launch_bounds__(kPT) void k_filter_plan3(Problem P, Work W) {
   const uint64_t am = f.am, ac = f.ac, ae = f.ae;
   const Crossing cf = find_crossing<kPT>(W.h2c[hb], W.h2m[hb], W.h2e[hb], am, f.theta, ps.wsum,
                                          &ps.b, ps.v);
-  if (t == 0) {
-    f.b2 = cf.b;
+  if (t < kWave) {
+    float flo = 0.0f, fhi = 0.0f;
     if (cf.b >= 0) {
-      f.ac = ac + cf.c;
-      f.am = cf.m;  // includes the base
-      f.ae = ae + cf.e;
+      // logits of fine bucket b2 of b1: x above b1, or in b1 at fine bucket
+      // <= b2 (resp. < b2), is monotone in the logit
+      const int unit = row / P.rows_per_unit, b2 = cf.b;
+      const float Tt = P.temps[unit], rT = 1.0f / Tt, M = f.m;
+      const bool fast = hs_rcp_ok(Tt);
+      auto at_most = [&](float r, int fb) {
+        const float x = hs_div_temp(r, Tt, rT, fast);
+        const int cb = coarse_bucket(x, M);
+        return cb < b1 || (cb == b1 && fine_bucket(x, M, b1) <= fb);
+      };
+      flo = raw_threshold([&](float r) { return at_most(r, b2); });
+      fhi = raw_threshold([&](float r) { return at_most(r, b2 - 1); });
+    }
+    if (t == 0) {
+      f.b2 = cf.b;
+      if (cf.b >= 0) {
+        f.ac = ac + cf.c;
+        f.am = cf.m;  // includes the base
+        f.ae = ae + cf.e;
+        f.flo = flo;
+        f.fhi = fhi;
+      }
     }
   }
 }
@@ -853,29 +946,26 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
       const float M = f.m, S = f.s;
       const float rS = 1.0f / S;
       const bool fastS = hs_rcp_ok(S);
-      const int jmax = f.jmax;
+      const float rj = f.rj;  // logit >= rj <=> coarse bucket <= jmax
       float* q = s_q[tid / kWave];
       for (int c = c_lo; c < c_hi; ++c) {
         const int64_t i0 = chunk_elem(c, tid, 0);
         float x[8];
         load8<T>(rp, i0, P.V, vec_ok, x);
+        const bool full = i0 + 8 <= P.V;
         uint32_t flags = 0;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          x[k] = hs_div_temp(x[k], Tt, rT, fast);
-          if (i0 + k < P.V && coarse_bucket(x[k], M) <= jmax) flags |= 1u << k;
-        }
-        const uint32_t nf = (uint32_t)__popc(flags);
-        const uint32_t incl = wave_incl_scan_u32(nf, lane);
-        const uint32_t total = (uint32_t)__shfl((int)incl, kWave - 1, kWave);
-        uint32_t slot = incl - nf;
+        for (int k = 0; k < 8; ++k)
+          if (x[k] >= rj && (full || i0 + k < P.V)) flags |= 1u << k;
+        uint32_t slot[8];
+        const uint32_t total = wave_slots8(flags, slot);
 #pragma unroll
         for (int k = 0; k < 8; ++k)
-          if (flags & (1u << k)) q[slot++] = x[k];
+          if (flags & (1u << k)) q[slot[k]] = x[k];
         // the queue is this wave's: its LDS writes land before its reads
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         for (uint32_t j = (uint32_t)lane; j < total; j += kWave) {
-          const float xv = q[j];
+          const float xv = hs_div_temp(q[j], Tt, rT, fast);
           const int b = coarse_bucket(xv, M);
           atomicAdd(&ps.hc[b], 1u);
           if (b < kCB - 1) {  // the last bucket holds only zero masses
@@ -894,6 +984,197 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
         atomicAdd(&W.h1c[hb], ps.hc[tid]);
         if (ps.hm[tid]) atomicAdd((unsigned long long*)&W.h1m[hb], (unsigned long long)ps.hm[tid]);
         if (ps.he[tid]) atomicAdd((unsigned long long*)&W.h1e[hb], (unsigned long long)ps.he[tid]);
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// Top-p rows with 16-byte aligned rows and V % 8 == 0: the work of
+// k_filter_pass1 for mode-2 rows with one wave per chunk of the workgroup's
+// segment, so that each wave has the chunk's four 1 KB (bf16) or 2 KB (f32)
+// loads in flight together (lane_chunk_load); the histogram accumulates in LDS
+// over the segment as there, and the logits at or above rj are packed per
+// 512-element group into the wave's LDS queue.
+template <typename T>
+__global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_filter_pass1_w(
+    Problem P, Work W) {
+  __shared__ PassShared ps;
+  __shared__ float s_q[kPT / kWave][kWave * kGroupElems];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
+  const int rows = P.units * P.rows_per_unit;
+  const SegPlan sp = seg_plan(P, W.flist[1]);  // top-p rows only
+  float* q = s_q[wid];
+  for (int it = blockIdx.x; it < sp.items; it += gridDim.x) {
+    const int ri = it / sp.nseg;
+    const int row = W.flist[2 + rows + ri];
+    const int unit = row / P.rows_per_unit;
+    if (filter_mode(P, unit) != 2) continue;
+    int c_lo, c_hi;
+    seg_chunks(sp, it - ri * sp.nseg, c_lo, c_hi);
+    const FilterScratch& f = W.filt[row];
+    const float Tt = P.temps[unit];
+    const float rT = 1.0f / Tt;
+    const bool fast = hs_rcp_ok(Tt);
+    const float M = f.m, S = f.s;
+    const float rS = 1.0f / S;
+    const bool fastS = hs_rcp_ok(S);
+    const float rj = f.rj;  // logit >= rj <=> coarse bucket <= jmax
+    const T* rp = reinterpret_cast<const T*>(P.logits) + (int64_t)row * P.row_stride;
+    ps.hm[tid] = 0ull;
+    ps.he[tid] = 0ull;
+    ps.hc[tid] = 0u;
+    __syncthreads();
+    for (int c = c_lo + wid; c < c_hi; c += kPT / kWave) {
+      const int64_t c0 = (int64_t)c * kChunk;
+      LaneChunk<T> r;
+      lane_chunk_load<T>(rp, c0, P.V, lane, true, r);
+#pragma unroll
+      for (int g = 0; g < kLaneChunkGroups; ++g) {
+        const bool in = lane_chunk_idx(c0, g, lane, 0) < P.V;
+        uint32_t flags = 0;
+#pragma unroll
+        for (int k = 0; k < kGroupElems; ++k)
+          if (in && lane_chunk_val<T>(r, g, k) >= rj) flags |= 1u << k;
+        uint32_t slot[8];
+        const uint32_t total = wave_slots8(flags, slot);
+        if (total == 0) continue;  // wave-uniform
+#pragma unroll
+        for (int k = 0; k < kGroupElems; ++k)
+          if (flags & (1u << k)) q[slot[k]] = lane_chunk_val<T>(r, g, k);
+        // the queue is this wave's: its LDS writes land before its reads
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        for (uint32_t j = (uint32_t)lane; j < total; j += kWave) {
+          const float xv = hs_div_temp(q[j], Tt, rT, fast);
+          const int b = coarse_bucket(xv, M);
+          atomicAdd(&ps.hc[b], 1u);
+          if (b < kCB - 1) {  // the last bucket holds only zero masses
+            const float e = hs_exp(xv - M);
+            const uint64_t em = hs_fx44(e);
+            const uint64_t mm = hs_fx44(hs_div_temp(e, S, rS, fastS));
+            if (mm) atomicAdd((unsigned long long*)&ps.hm[b], (unsigned long long)mm);
+            if (em) atomicAdd((unsigned long long*)&ps.he[b], (unsigned long long)em);
+          }
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      }
+    }
+    __syncthreads();
+    const int64_t hb = (int64_t)row * kCB + tid;
+    if (ps.hc[tid]) {
+      atomicAdd(&W.h1c[hb], ps.hc[tid]);
+      if (ps.hm[tid]) atomicAdd((unsigned long long*)&W.h1m[hb], (unsigned long long)ps.hm[tid]);
+      if (ps.he[tid]) atomicAdd((unsigned long long*)&W.h1e[hb], (unsigned long long)ps.he[tid]);
+    }
+    __syncthreads();
+  }
+}
+
+// Top-p rows with 16-byte aligned rows and V % 8 == 0: the work of
+// k_filter_pass2 with one wave per chunk of the segment (loads as in
+// k_filter_pass1_w).
+template <typename T>
+__global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_filter_pass2_w(
+    Problem P, Work W) {
+  __shared__ PassShared ps;
+  __shared__ float s_qv[kPT / kWave][kWave * 4];
+  __shared__ uint32_t s_qi[kPT / kWave][kWave * 4];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
+  const int rows = P.units * P.rows_per_unit;
+  const SegPlan sp = seg_plan(P, W.flist[1]);  // top-p rows only
+  float* qv = s_qv[wid];
+  uint32_t* qi = s_qi[wid];
+  for (int it = blockIdx.x; it < sp.items; it += gridDim.x) {
+    const int ri = it / sp.nseg;
+    const int row = W.flist[2 + rows + ri];
+    const int unit = row / P.rows_per_unit;  // a top-p row (the list holds no others)
+    const FilterScratch& f = W.filt[row];
+    const int b1 = f.b1;
+    if (b1 < 0) continue;
+    const uint32_t c1 = f.c1;
+    const bool fine = c1 > kDirect;                  // workgroup-uniform
+    const bool listed = c1 <= (uint32_t)kCand;      // see k_filter_pass2
+    if (fine) {
+      ps.hm[tid] = 0ull;
+      ps.he[tid] = 0ull;
+      ps.hc[tid] = 0u;
+      __syncthreads();
+    }
+    int c_lo, c_hi;
+    seg_chunks(sp, it - ri * sp.nseg, c_lo, c_hi);
+    const float M = f.m, S = f.s;
+    const float Tt = P.temps[unit];
+    const float rT = 1.0f / Tt;
+    const bool fast = hs_rcp_ok(Tt);
+    const float rS = 1.0f / S;
+    const bool fastS = hs_rcp_ok(S);
+    const float rlo = f.rlo, rhi = f.rhi;  // coarse bucket b1 <=> rlo <= logit < rhi
+    const T* rp = reinterpret_cast<const T*>(P.logits) + (int64_t)row * P.row_stride;
+    for (int c = c_lo + wid; c < c_hi; c += kPT / kWave) {
+      const int64_t c0 = (int64_t)c * kChunk;
+      LaneChunk<T> r;
+      lane_chunk_load<T>(rp, c0, P.V, lane, true, r);
+#pragma unroll
+      for (int h = 0; h < 2 * kLaneChunkGroups; ++h) {
+        // half h of the lane's chunk: group h / 2, elements 4 (h % 2) .. + 4
+        const int g = h >> 1, k0 = 4 * (h & 1);
+        const int64_t i0 = lane_chunk_idx(c0, g, lane, k0);
+        const bool in = i0 < P.V;
+        uint32_t flags = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const float v = lane_chunk_val<T>(r, g, k0 + k);
+          if (in && v >= rlo && v < rhi) flags |= 1u << k;
+        }
+        uint32_t slot[8];
+        const uint32_t total = wave_slots8<4>(flags, slot);
+        if (total == 0) continue;  // wave-uniform; the common case
+        // the elements of bucket b1 through the wave's LDS queue, so that the
+        // code below exists once
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          if (flags & (1u << k)) {
+            qv[slot[k]] = lane_chunk_val<T>(r, g, k0 + k);
+            qi[slot[k]] = (uint32_t)(i0 + k);
+          }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        for (uint32_t j0 = 0; j0 < total; j0 += kWave) {
+          const uint32_t j = j0 + (uint32_t)lane;
+          const bool have = j < total;
+          const float xv = have ? hs_div_temp(qv[j], Tt, rT, fast) : 0.0f;
+          const uint32_t idx = have ? qi[j] : 0u;
+          if (listed) {
+            const uint64_t m = __ballot(have);
+            const uint32_t n = (uint32_t)__popcll(m);
+            int base = 0;
+            if (lane == 0) base = atomicAdd(&W.filt[row].ncand, (int)n);
+            base = __builtin_amdgcn_readlane(base, 0) +
+                   (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                  __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+            if (have && base < kCand)
+              W.cand[(int64_t)row * kCand + base] =
+                  ((uint64_t)hs_key(xv) << 32) | (uint64_t)(0xffffffffu - idx);
+          }
+          if (fine && have) {
+            const int b = fine_bucket(xv, M, b1);
+            const float e = hs_exp(xv - M);
+            atomicAdd(&ps.hc[b], 1u);
+            const uint64_t mm = hs_fx44(hs_div_temp(e, S, rS, fastS));
+            const uint64_t em = hs_fx44(e);
+            if (mm) atomicAdd((unsigned long long*)&ps.hm[b], (unsigned long long)mm);
+            if (em) atomicAdd((unsigned long long*)&ps.he[b], (unsigned long long)em);
+          }
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      }
+    }
+    if (fine) {
+      __syncthreads();
+      const int64_t hb = (int64_t)row * kCB + tid;
+      if (ps.hc[tid]) {
+        atomicAdd(&W.h2c[hb], ps.hc[tid]);
+        if (ps.hm[tid]) atomicAdd((unsigned long long*)&W.h2m[hb], (unsigned long long)ps.hm[tid]);
+        if (ps.he[tid]) atomicAdd((unsigned long long*)&W.h2e[hb], (unsigned long long)ps.he[tid]);
       }
       __syncthreads();
     }
@@ -1004,17 +1285,18 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
     const bool vec_ok = ((reinterpret_cast<uintptr_t>(rp) & 15u) == 0);
     const float rS = 1.0f / S;
     const bool fastS = hs_rcp_ok(S);
+    const float rlo = f.rlo, rhi = f.rhi;  // coarse bucket b1 <=> rlo <= logit < rhi
     for (int c = c_lo; c < c_hi; ++c) {
       const int64_t i0 = chunk_elem(c, tid, 0);
       float x[8];
       load8<T>(rp, i0, P.V, vec_ok, x);
+      const bool full = i0 + 8 <= P.V;
       uint32_t key[8], flags = 0;
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         key[k] = 0;
-        if (i0 + k >= P.V) continue;
+        if (!(x[k] >= rlo && x[k] < rhi) || !(full || i0 + k < P.V)) continue;
         const float xv = hs_div_temp(x[k], Tt, rT, fast);
-        if (coarse_bucket(xv, M) != b1) continue;
         if (listed) {
           key[k] = hs_key(xv);
           flags |= 1u << k;
@@ -1069,18 +1351,18 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
     const bool fast = hs_rcp_ok(Tt);
     const T* rp = reinterpret_cast<const T*>(P.logits) + (int64_t)row * P.row_stride;
     const bool vec_ok = ((reinterpret_cast<uintptr_t>(rp) & 15u) == 0);
+    const float flo = f.flo, fhi = f.fhi;  // fine bucket b2 of b1 <=> flo <= logit < fhi
     for (int c = c_lo; c < c_hi; ++c) {
       const int64_t i0 = chunk_elem(c, tid, 0);
       float x[8];
       load8<T>(rp, i0, P.V, vec_ok, x);
+      const bool full = i0 + 8 <= P.V;
       uint32_t key[8], flags = 0;
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         key[k] = 0;
-        if (i0 + k >= P.V) continue;
-        const float xv = hs_div_temp(x[k], Tt, rT, fast);
-        if (coarse_bucket(xv, M) == b1 && fine_bucket(xv, M, b1) == b2) {
-          key[k] = hs_key(xv);
+        if (x[k] >= flo && x[k] < fhi && (full || i0 + k < P.V)) {
+          key[k] = hs_key(hs_div_temp(x[k], Tt, rT, fast));
           flags |= 1u << k;
         }
       }
@@ -1534,12 +1816,15 @@ int launch_filter(const Problem& P, const Work& W, float* row_stats, bool wave,
     const int64_t wgs = (items + kPT / kWave - 1) / (kPT / kWave);
     hipLaunchKernelGGL(k_filter_gather_k<T>, dim3((int)(wgs < 2048 ? wgs : 2048)), dim3(kPT), 0,
                        stream, P, W);
-    hipLaunchKernelGGL(k_filter_pass1<T>, dim3(grid1), dim3(kPT), 0, stream, P, W, 1);
+    hipLaunchKernelGGL(k_filter_pass1_w<T>, dim3(grid1), dim3(kPT), 0, stream, P, W);
   } else {
     hipLaunchKernelGGL(k_filter_pass1<T>, dim3(grid1), dim3(kPT), 0, stream, P, W, 0);
   }
   hipLaunchKernelGGL(k_filter_plan2, dim3(rows), dim3(kPT), 0, stream, P, W);
-  hipLaunchKernelGGL(k_filter_pass2<T>, dim3(grid1), dim3(kPT), 0, stream, P, W);
+  if (wave)
+    hipLaunchKernelGGL(k_filter_pass2_w<T>, dim3(grid1), dim3(kPT), 0, stream, P, W);
+  else
+    hipLaunchKernelGGL(k_filter_pass2<T>, dim3(grid1), dim3(kPT), 0, stream, P, W);
   hipLaunchKernelGGL(k_filter_plan3, dim3(rows), dim3(kPT), 0, stream, P, W);
   hipLaunchKernelGGL(k_filter_pass3<T>, dim3(grid1), dim3(kPT), 0, stream, P, W);
   hipLaunchKernelGGL(k_row_filter<T>, dim3(rows), dim3(kFT), 0, stream, P, W, row_stats);
