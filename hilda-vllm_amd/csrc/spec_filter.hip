@@ -564,6 +564,12 @@ static_assert(kPT == kCB, "one histogram bucket per thread");
 // a coarse boundary bucket with more elements than this is refined into fine
 // sub-buckets first (small candidate sets sort in one wave)
 constexpr uint32_t kDirect = 256;
+// pass 1 (wave kernel) keeps a bucket's count above bit 45 of its mass word
+constexpr int kPackShift = 45;
+// per-wave candidate buffer of k_filter_pass2_w
+constexpr uint32_t kCandBuf = 128;
+// per-wave element queue of k_filter_pass2_w (holds a half group: 256)
+constexpr uint32_t kQueue = 256;
 
 __device__ __forceinline__ int filter_mode(const Problem& P, int unit) {
   const int kk = P.top_ks[unit];
@@ -1008,8 +1014,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
   for (int it = blockIdx.x; it < sp.items; it += gridDim.x) {
     const int ri = it / sp.nseg;
     const int row = W.flist[2 + rows + ri];
-    const int unit = row / P.rows_per_unit;
-    if (filter_mode(P, unit) != 2) continue;
+    const int unit = row / P.rows_per_unit;  // a top-p row (the list holds no others)
     int c_lo, c_hi;
     seg_chunks(sp, it - ri * sp.nseg, c_lo, c_hi);
     const FilterScratch& f = W.filt[row];
@@ -1023,8 +1028,30 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
     const T* rp = reinterpret_cast<const T*>(P.logits) + (int64_t)row * P.row_stride;
     ps.hm[tid] = 0ull;
     ps.he[tid] = 0ull;
-    ps.hc[tid] = 0u;
     __syncthreads();
+    // the queue fills over several groups and chunks before the wave works
+    // through it, so its passes over the queue run with full lanes
+    uint32_t nq = 0;  // wave-uniform: logits in the queue
+    auto drain = [&]() {
+      // the queue is this wave's: its LDS writes land before its reads
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      for (uint32_t j = (uint32_t)lane; j < nq; j += kWave) {
+        const float xv = hs_div_temp(q[j], Tt, rT, fast);
+        const int b = coarse_bucket(xv, M);
+        // count and mass in one word (kPackShift): the masses of a row sum to
+        // at most 2^44 (1 + 1e-5), a segment holds fewer than 2^19 elements
+        uint64_t cm = 1ull << kPackShift;
+        if (b < kCB - 1) {  // the last bucket holds only zero masses
+          const float e = hs_exp(xv - M);
+          const uint64_t em = hs_fx44(e);
+          cm += hs_fx44(hs_div_temp(e, S, rS, fastS));
+          if (em) atomicAdd((unsigned long long*)&ps.he[b], (unsigned long long)em);
+        }
+        atomicAdd((unsigned long long*)&ps.hm[b], (unsigned long long)cm);
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      nq = 0;
+    };
     for (int c = c_lo + wid; c < c_hi; c += kPT / kWave) {
       const int64_t c0 = (int64_t)c * kChunk;
       LaneChunk<T> r;
@@ -1039,31 +1066,21 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
         uint32_t slot[8];
         const uint32_t total = wave_slots8(flags, slot);
         if (total == 0) continue;  // wave-uniform
+        if (nq + total > kWave * kGroupElems) drain();
 #pragma unroll
         for (int k = 0; k < kGroupElems; ++k)
-          if (flags & (1u << k)) q[slot[k]] = lane_chunk_val<T>(r, g, k);
-        // the queue is this wave's: its LDS writes land before its reads
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        for (uint32_t j = (uint32_t)lane; j < total; j += kWave) {
-          const float xv = hs_div_temp(q[j], Tt, rT, fast);
-          const int b = coarse_bucket(xv, M);
-          atomicAdd(&ps.hc[b], 1u);
-          if (b < kCB - 1) {  // the last bucket holds only zero masses
-            const float e = hs_exp(xv - M);
-            const uint64_t em = hs_fx44(e);
-            const uint64_t mm = hs_fx44(hs_div_temp(e, S, rS, fastS));
-            if (mm) atomicAdd((unsigned long long*)&ps.hm[b], (unsigned long long)mm);
-            if (em) atomicAdd((unsigned long long*)&ps.he[b], (unsigned long long)em);
-          }
-        }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          if (flags & (1u << k)) q[nq + slot[k]] = lane_chunk_val<T>(r, g, k);
+        nq += total;
       }
     }
+    if (nq) drain();
     __syncthreads();
     const int64_t hb = (int64_t)row * kCB + tid;
-    if (ps.hc[tid]) {
-      atomicAdd(&W.h1c[hb], ps.hc[tid]);
-      if (ps.hm[tid]) atomicAdd((unsigned long long*)&W.h1m[hb], (unsigned long long)ps.hm[tid]);
+    const uint32_t cnt = (uint32_t)(ps.hm[tid] >> kPackShift);
+    const uint64_t mass = ps.hm[tid] & ((1ull << kPackShift) - 1);
+    if (cnt) {
+      atomicAdd(&W.h1c[hb], cnt);
+      if (mass) atomicAdd((unsigned long long*)&W.h1m[hb], (unsigned long long)mass);
       if (ps.he[tid]) atomicAdd((unsigned long long*)&W.h1e[hb], (unsigned long long)ps.he[tid]);
     }
     __syncthreads();
@@ -1077,13 +1094,18 @@ template <typename T>
 __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_filter_pass2_w(
     Problem P, Work W) {
   __shared__ PassShared ps;
-  __shared__ float s_qv[kPT / kWave][kWave * 4];
-  __shared__ uint32_t s_qi[kPT / kWave][kWave * 4];
+  __shared__ float s_qv[kPT / kWave][kQueue];
+  __shared__ uint32_t s_qi[kPT / kWave][kQueue];
+  // each wave's candidates collect here and reach the row's list in one
+  // atomic per kCandBuf / 2 of them (an atomic that returns costs a memory
+  // round trip, which per chunk was most of the pass)
+  __shared__ uint64_t s_cb[kPT / kWave][kCandBuf];
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
   const int rows = P.units * P.rows_per_unit;
   const SegPlan sp = seg_plan(P, W.flist[1]);  // top-p rows only
   float* qv = s_qv[wid];
   uint32_t* qi = s_qi[wid];
+  uint64_t* cb = s_cb[wid];
   for (int it = blockIdx.x; it < sp.items; it += gridDim.x) {
     const int ri = it / sp.nseg;
     const int row = W.flist[2 + rows + ri];
@@ -1110,6 +1132,50 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
     const bool fastS = hs_rcp_ok(S);
     const float rlo = f.rlo, rhi = f.rhi;  // coarse bucket b1 <=> rlo <= logit < rhi
     const T* rp = reinterpret_cast<const T*>(P.logits) + (int64_t)row * P.row_stride;
+    uint32_t nb = 0;  // wave-uniform: candidates in cb
+    auto flush = [&]() {
+      int base = 0;
+      if (lane == 0) base = atomicAdd(&W.filt[row].ncand, (int)nb);
+      base = __builtin_amdgcn_readlane(base, 0);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      for (uint32_t j = (uint32_t)lane; j < nb; j += kWave)
+        if (base + (int)j < kCand) W.cand[(int64_t)row * kCand + base + (int)j] = cb[j];
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      nb = 0;
+    };
+    // bucket-b1 elements wait in the wave's LDS queue and are handled a batch
+    // at a time (a handful per segment for ordinary rows): each batch is one
+    // chain of dependent latencies for the wave, where per occurrence they
+    // added up to most of the pass
+    uint32_t nq = 0;  // wave-uniform: elements in the queue
+    auto drain = [&]() {
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      for (uint32_t j0 = 0; j0 < nq; j0 += kWave) {
+        const uint32_t j = j0 + (uint32_t)lane;
+        const bool have = j < nq;
+        const float xv = have ? hs_div_temp(qv[j], Tt, rT, fast) : 0.0f;
+        const uint32_t idx = have ? qi[j] : 0u;
+        if (listed) {
+          if (nb > kCandBuf - kWave) flush();
+          const uint64_t m = __ballot(have);
+          const uint32_t sl = nb + __builtin_amdgcn_mbcnt_hi(
+                                       (uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+          if (have) cb[sl] = ((uint64_t)hs_key(xv) << 32) | (uint64_t)(0xffffffffu - idx);
+          nb += (uint32_t)__popcll(m);
+        }
+        if (fine && have) {
+          const int b = fine_bucket(xv, M, b1);
+          const float e = hs_exp(xv - M);
+          atomicAdd(&ps.hc[b], 1u);
+          const uint64_t mm = hs_fx44(hs_div_temp(e, S, rS, fastS));
+          const uint64_t em = hs_fx44(e);
+          if (mm) atomicAdd((unsigned long long*)&ps.hm[b], (unsigned long long)mm);
+          if (em) atomicAdd((unsigned long long*)&ps.he[b], (unsigned long long)em);
+        }
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      nq = 0;
+    };
     for (int c = c_lo + wid; c < c_hi; c += kPT / kWave) {
       const int64_t c0 = (int64_t)c * kChunk;
       LaneChunk<T> r;
@@ -1117,6 +1183,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
 #pragma unroll
       for (int h = 0; h < 2 * kLaneChunkGroups; ++h) {
         // half h of the lane's chunk: group h / 2, elements 4 (h % 2) .. + 4
+        // (at most 256 per wave, what the queue takes at once)
         const int g = h >> 1, k0 = 4 * (h & 1);
         const int64_t i0 = lane_chunk_idx(c0, g, lane, k0);
         const bool in = i0 < P.V;
@@ -1129,45 +1196,18 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
         uint32_t slot[8];
         const uint32_t total = wave_slots8<4>(flags, slot);
         if (total == 0) continue;  // wave-uniform; the common case
-        // the elements of bucket b1 through the wave's LDS queue, so that the
-        // code below exists once
+        if (nq + total > kQueue) drain();
 #pragma unroll
         for (int k = 0; k < 4; ++k)
           if (flags & (1u << k)) {
-            qv[slot[k]] = lane_chunk_val<T>(r, g, k0 + k);
-            qi[slot[k]] = (uint32_t)(i0 + k);
+            qv[nq + slot[k]] = lane_chunk_val<T>(r, g, k0 + k);
+            qi[nq + slot[k]] = (uint32_t)(i0 + k);
           }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        for (uint32_t j0 = 0; j0 < total; j0 += kWave) {
-          const uint32_t j = j0 + (uint32_t)lane;
-          const bool have = j < total;
-          const float xv = have ? hs_div_temp(qv[j], Tt, rT, fast) : 0.0f;
-          const uint32_t idx = have ? qi[j] : 0u;
-          if (listed) {
-            const uint64_t m = __ballot(have);
-            const uint32_t n = (uint32_t)__popcll(m);
-            int base = 0;
-            if (lane == 0) base = atomicAdd(&W.filt[row].ncand, (int)n);
-            base = __builtin_amdgcn_readlane(base, 0) +
-                   (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
-                                                  __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-            if (have && base < kCand)
-              W.cand[(int64_t)row * kCand + base] =
-                  ((uint64_t)hs_key(xv) << 32) | (uint64_t)(0xffffffffu - idx);
-          }
-          if (fine && have) {
-            const int b = fine_bucket(xv, M, b1);
-            const float e = hs_exp(xv - M);
-            atomicAdd(&ps.hc[b], 1u);
-            const uint64_t mm = hs_fx44(hs_div_temp(e, S, rS, fastS));
-            const uint64_t em = hs_fx44(e);
-            if (mm) atomicAdd((unsigned long long*)&ps.hm[b], (unsigned long long)mm);
-            if (em) atomicAdd((unsigned long long*)&ps.he[b], (unsigned long long)em);
-          }
-        }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        nq += total;
       }
     }
+    if (nq) drain();
+    if (nb) flush();
     if (fine) {
       __syncthreads();
       const int64_t hb = (int64_t)row * kCB + tid;
