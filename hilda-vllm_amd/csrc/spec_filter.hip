@@ -866,14 +866,16 @@ __global__ __launch_bounds__(kPT) void k_filter_plan3(Problem P, Work W) {
   if (filter_mode(P, row / P.rows_per_unit) != 2) return;
   FilterScratch& f = W.filt[row];
   const int b1 = f.b1;
-  if (b1 < 0 || W.h1c[(int64_t)row * kCB + b1] <= kDirect) return;
+  if (b1 < 0) return;
+  const uint32_t c1 = f.c1;
+  if (c1 <= kDirect) return;
   const int64_t hb = (int64_t)row * kCB + t;
   const uint64_t am = f.am, ac = f.ac, ae = f.ae;
   const Crossing cf = find_crossing<kPT>(W.h2c[hb], W.h2m[hb], W.h2e[hb], am, f.theta, ps.wsum,
                                          &ps.b, ps.v);
   if (t < kWave) {
     float flo = 0.0f, fhi = 0.0f;
-    if (cf.b >= 0) {
+    if (cf.b >= 0 && c1 > (uint32_t)kCand) {  // (pass 3 skips the listed rows)
       // logits of fine bucket b2 of b1: x above b1, or in b1 at fine bucket
       // <= b2 (resp. < b2), is monotone in the logit
       const int unit = row / P.rows_per_unit, b2 = cf.b;
