@@ -121,7 +121,8 @@ def _accept_valu_busy(tag: str):
     """VALU-busy percentage of the acceptance call's longest-running profiled kernel
     (the single launch, or the chain's row-statistics / filter passes)."""
     for k in ("k_accept_small_topk<float, 3>", "k_accept_small<bf16, 3>",
-              "k_chunk_stats_w<bf16>", "k_filter_pass1<float>", "k_filter_pass1<bf16>"):
+              "k_chunk_stats_w<bf16>", "k_filter_pass1_w<bf16>", "k_filter_pass1<float>",
+              "k_filter_pass1<bf16>"):
         v = profiled_counter(k, tag, "VALUBusy %")
         if v is not None:
             return v

@@ -143,8 +143,9 @@ int hs_sampler(const void* logits, int logits_dtype, int64_t logits_row_stride,
 /* k/v cache   : [num_blocks, block_size, num_kv_heads, 128] bf16 or fp8      */
 /*               e4m3fn (kv_dtype HS_BF16 / HS_FP8_E4M3), element strides    */
 /*               (block, token, head); fp8 values dequantise as code*scale.  */
-/* block_tables: int32 [num_seqs, block_table_width] (row stride given);     */
-/*               entries outside [0, num_blocks) are treated as empty.       */
+/* block_tables: int32 [num_seqs, block_table_width] (row stride given, at  */
+/*               most INT32_MAX elements); entries outside [0, num_blocks)  */
+/*               are treated as empty.                                       */
 /* cu_seqlens_q/k: int32 [num_seqs + 1] prefix sums of query/key lengths.    */
 /* The workspace (size from hs_verify_attention_workspace_size) holds the    */
 /* partial results of key splits (or of the pieces of the one-workgroup-per- */
