@@ -121,7 +121,7 @@ def _accept_valu_busy(tag: str):
     """VALU-busy percentage of the acceptance call's longest-running profiled kernel
     (the single launch, or the chain's row-statistics / filter passes)."""
     for k in ("k_accept_small_topk<float, 3>", "k_accept_small<bf16, 3>",
-              "k_chunk_stats_w<bf16>", "k_filter_pass1_w<bf16>", "k_filter_pass1<float>",
+              "k_chunk_stats_w<bf16>", "k_filter_pass1_kp<bf16>", "k_filter_pass1<float>",
               "k_filter_pass1<bf16>"):
         v = profiled_counter(k, tag, "VALUBusy %")
         if v is not None:
@@ -151,7 +151,8 @@ def bench_accept(args, torch, hv):
         lg, qq = bufs[i % copies]
         return hv.ops.spec_accept(lg, qq, s["draft_tokens"], s["temperatures"], s["u_accept"],
                                   s["u_resample"], mode=args.mode, top_ks=s["top_ks"],
-                                  top_ps=s["top_ps"], topk_le64=topk_le64)
+                                  top_ps=s["top_ps"], topk_le64=topk_le64,
+                                  chain_only=args.chain)
 
     outs = []
 
@@ -188,7 +189,8 @@ def bench_accept(args, torch, hv):
                    "vocab": V, "mode": args.mode,
                    "sampling": "per-seq T~U[0.5,1.2], top-k {0,20,50}, top-p {1,0.9,0.8}"
                    if args.per_seq else f"T={args.temperature} top-k={args.top_k} top-p={args.top_p}",
-                   "input_copies_rotated": copies, "topk_le64": topk_le64},
+                   "input_copies_rotated": copies, "topk_le64": topk_le64,
+                   "chain_only": bool(args.chain)},
         "accepted_mean": round(sum(nacc) / len(nacc), 3),
         "wall_s": round(wall, 3),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
@@ -800,6 +802,8 @@ def main(argv=None):
     ap.add_argument("--eager", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--chain", action="store_true",
+                    help="accept workload: force the launch chain (no single-launch kernel)")
     ap.add_argument("--no-topk-hint", action="store_true",
                     help="accept workload: do not pass the top-k <= 64 promise (chain path)")
     args = ap.parse_args(argv)

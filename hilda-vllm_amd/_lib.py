@@ -15,6 +15,7 @@ HS_ERR_SCRATCH_LIMIT = -5
 HS_F32, HS_BF16, HS_FP8_E4M3 = 0, 1, 2
 HS_ACCEPT_REFERENCE, HS_ACCEPT_FILTERED, HS_ACCEPT_GREEDY = 0, 1, 2
 HS_ACCEPT_TOPK_LE64 = 0x100
+HS_ACCEPT_CHAIN = 0x200
 
 _vp = ctypes.c_void_p
 _i32 = ctypes.c_int

@@ -51,7 +51,7 @@ struct SampPart {
   uint64_t p;  // probability weight sum of the chunk
 };
 
-// Per-row state of the filter passes (k_filter_plan* write it, the passes and
+// Per-row state of the filter passes (k_filter_plan1/2 write it, the passes and
 // k_row_filter read it).
 struct FilterScratch {
   int32_t kept;
@@ -59,7 +59,7 @@ struct FilterScratch {
   int32_t ncand;   // candidates appended by the filter passes
   int32_t b1;      // coarse boundary bucket (-1: the row never reaches p; -2: not
                    // within buckets 0..jmax, the row filter streams the row)
-  int32_t b2;      // fine boundary bucket (-1: not refined)
+  int32_t b2;      // unused (the row filter finds the fine boundary bucket)
   int32_t jmax;    // pass 1 histograms buckets 0..jmax only (see mass_skip_bucket)
   float m;         // row max and normaliser (x = logit / T)
   float s;
@@ -72,7 +72,7 @@ struct FilterScratch {
   // raw-value (logit) thresholds of the top-p passes, exact images of their
   // bucket tests (x = logit / T is monotone in the logit): pass 1 takes
   // logit >= rj (coarse bucket <= jmax), pass 2 rlo <= logit < rhi (coarse
-  // bucket b1), pass 3 flo <= logit < fhi (fine bucket b2 of b1)
+  // bucket b1); flo, fhi unused
   float rj, rlo, rhi, flo, fhi;
   uint32_t c1;     // elements in coarse bucket b1 (k_filter_plan2)
 };

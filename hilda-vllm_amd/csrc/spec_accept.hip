@@ -692,7 +692,8 @@ int hs_spec_accept(const void* target_logits, int logits_dtype, int64_t logits_r
   if (batch <= 0 || gamma <= 0 || gamma > kMaxGamma || vocab <= 0) return HS_ERR_INVALID;
   if (batch > kMaxRows) return HS_ERR_UNSUPPORTED;
   const bool topk_le64 = (mode & HS_ACCEPT_TOPK_LE64) != 0;
-  mode &= ~HS_ACCEPT_TOPK_LE64;
+  const bool chain_only = (mode & HS_ACCEPT_CHAIN) != 0;
+  mode &= ~(HS_ACCEPT_TOPK_LE64 | HS_ACCEPT_CHAIN);
   if (mode != HS_ACCEPT_REFERENCE && mode != HS_ACCEPT_FILTERED && mode != HS_ACCEPT_GREEDY)
     return HS_ERR_INVALID;
   if (topk_le64 && mode != HS_ACCEPT_FILTERED) return HS_ERR_INVALID;
@@ -740,11 +741,11 @@ int hs_spec_accept(const void* target_logits, int logits_dtype, int64_t logits_r
   O.row_stats = row_stats;
   Work W = bind_work(workspace, L);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (small_accept_ok(P, A, mode, logits_dtype == HS_F32 ? 4 : 2)) {
+  if (!chain_only && small_accept_ok(P, A, mode, logits_dtype == HS_F32 ? 4 : 2)) {
     if (logits_dtype == HS_F32) return launch_accept_small<float>(P, A, W, O, s);
     return launch_accept_small<uint16_t>(P, A, W, O, s);
   }
-  if (topk_le64 && small_topk_ok(P, A, logits_dtype == HS_F32 ? 4 : 2)) {
+  if (!chain_only && topk_le64 && small_topk_ok(P, A, logits_dtype == HS_F32 ? 4 : 2)) {
     if (logits_dtype == HS_F32) return launch_accept_small_topk<float>(P, A, W, O, s);
     return launch_accept_small_topk<uint16_t>(P, A, W, O, s);
   }
@@ -764,6 +765,7 @@ int hs_sampler(const void* logits, int logits_dtype, int64_t logits_row_stride, 
                void* stream) {
   if (rows <= 0 || vocab <= 0) return HS_ERR_INVALID;
   if (rows > kMaxRows) return HS_ERR_UNSUPPORTED;
+  mode &= ~HS_ACCEPT_CHAIN;  // the row sampler always runs the chain
   if (mode != HS_ACCEPT_REFERENCE && mode != HS_ACCEPT_FILTERED && mode != HS_ACCEPT_GREEDY)
     return HS_ERR_INVALID;
   if (logits_dtype != HS_F32 && logits_dtype != HS_BF16) return HS_ERR_INVALID;

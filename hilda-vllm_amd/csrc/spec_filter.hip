@@ -17,7 +17,7 @@
 //      chunk-parallel pass appends every element at or above it to the row's
 //      candidate list (a few dozen for ordinary logits); one workgroup per row
 //      sorts them in LDS and applies top-k and top-p (which only looks at the k
-//      survivors). From 32 rows up (aligned rows) the pass is k_filter_gather_k,
+//      survivors). From 32 rows up (aligned rows) the pass is gather_k_body,
 //      one wave per chunk, reading only the chunks whose maximum reaches the
 //      bound; k_filter_plan1 lists the rows of each mode for the passes;
 //   2. top-p alone: chunk-parallel passes build an exact mass histogram over
@@ -25,7 +25,8 @@
 //      the bucket where the cumulative mass reaches p and append its elements
 //      (or, when it holds more than 256, refine it into 256 sub-buckets: up to
 //      4096 elements the whole bucket is still appended and the row workgroup
-//      keeps the boundary sub-bucket's, above that a third pass appends them);
+//      keeps the boundary sub-bucket's, above that the row workgroup lists the
+//      boundary sub-bucket's elements from the row itself);
 //      the row workgroup sorts them and scans
 //      their masses from the histogram's prefix;
 //   3. otherwise (k above the chunk count, or more than 4096 candidates): the
@@ -555,8 +556,8 @@ __device__ __forceinline__ void scan_bucket(FilterSmem& sm, int n, float M, floa
 //           and appends its elements (at most kDirect of them), or else
 //           histograms them into 256 fine sub-buckets (still appending them
 //           all when they fit the kCand list, for k_row_filter to pick the
-//           fine boundary bucket from); otherwise pass 3 appends the elements
-//           of the fine boundary bucket.
+//           fine boundary bucket from); above kCand elements k_row_filter
+//           finds the fine boundary bucket and lists its elements itself.
 // k_row_filter then finishes each row in LDS from its candidates.
 // ---------------------------------------------------------------------------
 constexpr int kPT = kChunkThreads;
@@ -598,7 +599,7 @@ __device__ __forceinline__ int fine_bucket(float x, float M, int b1) {
 // (wave-uniform arguments): each round the 64 lanes test 63 keys spread over
 // the open interval, so the 2^32 keys take at most 6 rounds of one pred each.
 template <typename F>
-__device__ float raw_threshold(F pred) {
+__device__ __forceinline__ float raw_threshold(F pred) {
   const int lane = threadIdx.x & (kWave - 1);
   uint32_t lo = 0x007fffffu, hi = 0xff800000u;  // keys of -inf and +inf
   if (!pred(hs_unkey(hi))) return __builtin_nanf("");
@@ -717,8 +718,8 @@ __device__ __forceinline__ void wave_append_cands(const Work& W, int row, const 
 struct SegPlan {
   int nseg, q, r, items;
 };
-__device__ __forceinline__ SegPlan seg_plan(const Problem& P, int nr) {
-  int nseg = nr > 0 ? (int)gridDim.x / nr : 1;
+__device__ __forceinline__ SegPlan seg_plan(const Problem& P, int nr, int grid) {
+  int nseg = nr > 0 ? grid / nr : 1;
   nseg = nseg < 1 ? 1 : (nseg > P.nchunk ? P.nchunk : nseg);
   SegPlan sp;
   sp.nseg = nseg;
@@ -816,8 +817,11 @@ __global__ __launch_bounds__(kPT) void k_filter_plan1(Problem P, Work W) {
   }
 }
 
-// Per mode-2 row: the coarse bucket where the cumulative mass reaches p, whether
-// it is refined, and the sums before it.
+// Per mode-2 row: the coarse bucket where the cumulative mass reaches p, its
+// element count and logit range, and the sums before it. b1 is -1 when the
+// row never reaches p and -2 when the row filter must stream the row (no
+// crossing although pass 1 skipped buckets, which the skip bound rules out,
+// or a row maximum that is not finite).
 __global__ __launch_bounds__(kPT) void k_filter_plan2(Problem P, Work W) {
   __shared__ PassShared ps;
   const int row = blockIdx.x, t = threadIdx.x;
@@ -829,9 +833,6 @@ __global__ __launch_bounds__(kPT) void k_filter_plan2(Problem P, Work W) {
                                          &ps.b, ps.v);
   if (cr.b >= 0 && t == cr.b) f.c1 = hc;
   if (t < kWave) {
-    // no crossing although pass 1 skipped buckets (the bound did not hold; it
-    // always should), or a row max that is not finite: the row filter then
-    // streams the row
     const float M = f.m;
     const int b1 = !isfinite(M) ? -2 : (cr.b < 0 && f.jmax < kCB - 1) ? -2 : cr.b;
     float rlo = 0.0f, rhi = 0.0f;
@@ -859,50 +860,7 @@ __global__ __launch_bounds__(kPT) void k_filter_plan2(Problem P, Work W) {
   }
 }
 
-// Per refined mode-2 row: the fine sub-bucket where the cumulative mass reaches p.
-__global__ __launch_bounds__(kPT) void k_filter_plan3(Problem P, Work W) {
-  __shared__ PassShared ps;
-  const int row = blockIdx.x, t = threadIdx.x;
-  if (filter_mode(P, row / P.rows_per_unit) != 2) return;
-  FilterScratch& f = W.filt[row];
-  const int b1 = f.b1;
-  if (b1 < 0) return;
-  const uint32_t c1 = f.c1;
-  if (c1 <= kDirect) return;
-  const int64_t hb = (int64_t)row * kCB + t;
-  const uint64_t am = f.am, ac = f.ac, ae = f.ae;
-  const Crossing cf = find_crossing<kPT>(W.h2c[hb], W.h2m[hb], W.h2e[hb], am, f.theta, ps.wsum,
-                                         &ps.b, ps.v);
-  if (t < kWave) {
-    float flo = 0.0f, fhi = 0.0f;
-    if (cf.b >= 0 && c1 > (uint32_t)kCand) {  // (pass 3 skips the listed rows)
-      // logits of fine bucket b2 of b1: x above b1, or in b1 at fine bucket
-      // <= b2 (resp. < b2), is monotone in the logit
-      const int unit = row / P.rows_per_unit, b2 = cf.b;
-      const float Tt = P.temps[unit], rT = 1.0f / Tt, M = f.m;
-      const bool fast = hs_rcp_ok(Tt);
-      auto at_most = [&](float r, int fb) {
-        const float x = hs_div_temp(r, Tt, rT, fast);
-        const int cb = coarse_bucket(x, M);
-        return cb < b1 || (cb == b1 && fine_bucket(x, M, b1) <= fb);
-      };
-      flo = raw_threshold([&](float r) { return at_most(r, b2); });
-      fhi = raw_threshold([&](float r) { return at_most(r, b2 - 1); });
-    }
-    if (t == 0) {
-      f.b2 = cf.b;
-      if (cf.b >= 0) {
-        f.ac = ac + cf.c;
-        f.am = cf.m;  // includes the base
-        f.ae = ae + cf.e;
-        f.flo = flo;
-        f.fhi = fhi;
-      }
-    }
-  }
-}
-
-// only2: walk the top-p rows only (k_filter_gather_k takes the top-k rows).
+// only2: walk the top-p rows only (gather_k_body takes the top-k rows).
 // Workgroups take segments of chunks (seg_plan): a top-p row's histogram
 // accumulates in LDS over the segment and reaches global memory once (flushes
 // per chunk made the global atomics a third of the pass). Top-p rows
@@ -917,7 +875,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int rows = P.units * P.rows_per_unit;
-  const SegPlan sp = seg_plan(P, only2 ? W.flist[1] : rows);
+  const SegPlan sp = seg_plan(P, only2 ? W.flist[1] : rows, (int)gridDim.x);
   for (int it = blockIdx.x; it < sp.items; it += gridDim.x) {
     const int ri = it / sp.nseg;
     const int row = only2 ? W.flist[2 + rows + ri] : ri;
@@ -1005,15 +963,14 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
 // over the segment as there, and the logits at or above rj are packed per
 // 512-element group into the wave's LDS queue.
 template <typename T>
-__global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_filter_pass1_w(
-    Problem P, Work W) {
-  __shared__ PassShared ps;
-  __shared__ float s_q[kPT / kWave][kWave * kGroupElems];
+__device__ __forceinline__ void pass1_w_body(const Problem& P, const Work& W, int blk, int nblk,
+                                             PassShared& ps,
+                                             float (&s_q)[kPT / kWave][kWave * kGroupElems]) {
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
   const int rows = P.units * P.rows_per_unit;
-  const SegPlan sp = seg_plan(P, W.flist[1]);  // top-p rows only
+  const SegPlan sp = seg_plan(P, W.flist[1], nblk);  // top-p rows only
   float* q = s_q[wid];
-  for (int it = blockIdx.x; it < sp.items; it += gridDim.x) {
+  for (int it = blk; it < sp.items; it += nblk) {
     const int ri = it / sp.nseg;
     const int row = W.flist[2 + rows + ri];
     const int unit = row / P.rows_per_unit;  // a top-p row (the list holds no others)
@@ -1091,7 +1048,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
 
 // Top-p rows with 16-byte aligned rows and V % 8 == 0: the work of
 // k_filter_pass2 with one wave per chunk of the segment (loads as in
-// k_filter_pass1_w).
+// pass1_w_body).
 template <typename T>
 __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_filter_pass2_w(
     Problem P, Work W) {
@@ -1104,7 +1061,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
   __shared__ uint64_t s_cb[kPT / kWave][kCandBuf];
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
   const int rows = P.units * P.rows_per_unit;
-  const SegPlan sp = seg_plan(P, W.flist[1]);  // top-p rows only
+  const SegPlan sp = seg_plan(P, W.flist[1], (int)gridDim.x);  // top-p rows only
   float* qv = s_qv[wid];
   uint32_t* qi = s_qi[wid];
   uint64_t* cb = s_cb[wid];
@@ -1113,6 +1070,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
     const int row = W.flist[2 + rows + ri];
     const int unit = row / P.rows_per_unit;  // a top-p row (the list holds no others)
     const FilterScratch& f = W.filt[row];
+    const int seg = it - ri * sp.nseg;
     const int b1 = f.b1;
     if (b1 < 0) continue;
     const uint32_t c1 = f.c1;
@@ -1125,7 +1083,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
       __syncthreads();
     }
     int c_lo, c_hi;
-    seg_chunks(sp, it - ri * sp.nseg, c_lo, c_hi);
+    seg_chunks(sp, seg, c_lo, c_hi);
     const float M = f.m, S = f.s;
     const float Tt = P.temps[unit];
     const float rT = 1.0f / Tt;
@@ -1230,13 +1188,12 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
 // lanes' counts and one atomic per wave, with no barrier. Capped at 64 VGPRs
 // (8 waves per SIMD, no spills): resident waves hide the load latency.
 template <typename T>
-__global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_filter_gather_k(
-    Problem P, Work W) {
+__device__ __forceinline__ void gather_k_body(const Problem& P, const Work& W, int blk, int nblk) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int64_t items = (int64_t)W.flist[0] * P.nchunk;
-  const int64_t stride = (int64_t)gridDim.x * (kPT / kWave);
+  const int64_t stride = (int64_t)nblk * (kPT / kWave);
   const T* base = reinterpret_cast<const T*>(P.logits);
-  for (int64_t it = (int64_t)blockIdx.x * (kPT / kWave) + wid; it < items; it += stride) {
+  for (int64_t it = (int64_t)blk * (kPT / kWave) + wid; it < items; it += stride) {
     const int row = W.flist[2 + (int)(it / P.nchunk)];
     const int c = (int)(it % P.nchunk);
     const uint32_t tau = W.filt[row].tau;
@@ -1286,6 +1243,19 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
   }
 }
 
+// First pass of aligned rows, one launch for both lists: every workgroup takes
+// its share of the top-k rows' chunks (gather_k_body), then its share of the
+// top-p rows' segments (pass1_w_body), so the two kinds need no second launch
+// and a workgroup done with one kind goes straight on to the other.
+template <typename T>
+__global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_filter_pass1_kp(
+    Problem P, Work W) {
+  __shared__ PassShared ps;
+  __shared__ float s_q[kPT / kWave][kWave * kGroupElems];
+  gather_k_body<T>(P, W, (int)blockIdx.x, (int)gridDim.x);
+  pass1_w_body<T>(P, W, (int)blockIdx.x, (int)gridDim.x, ps, s_q);
+}
+
 // Top-p rows, segments of chunks: the elements of the coarse boundary bucket
 // b1 are appended to the candidates, and, when b1 holds more than kDirect
 // elements, histogrammed into fine sub-buckets (LDS over the segment, one
@@ -1296,20 +1266,20 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
   __shared__ PassShared ps;
   const int tid = threadIdx.x;
   const int rows = P.units * P.rows_per_unit;
-  const SegPlan sp = seg_plan(P, W.flist[1]);  // top-p rows only
+  const SegPlan sp = seg_plan(P, W.flist[1], (int)gridDim.x);  // top-p rows only
   for (int it = blockIdx.x; it < sp.items; it += gridDim.x) {
     const int ri = it / sp.nseg;
     const int row = W.flist[2 + rows + ri];
     const int unit = row / P.rows_per_unit;
     if (filter_mode(P, unit) != 2) continue;
     const FilterScratch& f = W.filt[row];
+    const int seg = it - ri * sp.nseg;
     const int b1 = f.b1;
     if (b1 < 0) continue;
-    const uint32_t c1 = W.h1c[(int64_t)row * kCB + b1];
+    const uint32_t c1 = f.c1;
     const bool fine = c1 > kDirect;  // workgroup-uniform
     // a refined bucket that fits the candidate list is also listed whole: the
-    // row filter then picks the fine boundary sub-bucket out of the list and
-    // pass 3 skips the row
+    // row filter then picks the fine boundary sub-bucket out of the list
     const bool listed = c1 <= (uint32_t)kCand;
     if (fine) {
       ps.hm[tid] = 0ull;
@@ -1318,7 +1288,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
       __syncthreads();
     }
     int c_lo, c_hi;
-    seg_chunks(sp, it - ri * sp.nseg, c_lo, c_hi);
+    seg_chunks(sp, seg, c_lo, c_hi);
     const float M = f.m, S = f.s;
     const float Tt = P.temps[unit];
     const float rT = 1.0f / Tt;
@@ -1370,49 +1340,6 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
 
 // Refined top-p rows, segments of chunks: appends the elements of fine
 // sub-bucket b2 of coarse bucket b1 (no LDS, no barrier).
-template <typename T>
-__global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_filter_pass3(
-    Problem P, Work W) {
-  const int tid = threadIdx.x;
-  const int rows = P.units * P.rows_per_unit;
-  const SegPlan sp = seg_plan(P, W.flist[1]);  // top-p rows only
-  for (int it = blockIdx.x; it < sp.items; it += gridDim.x) {
-    const int ri = it / sp.nseg;
-    const int row = W.flist[2 + rows + ri];
-    const int unit = row / P.rows_per_unit;
-    if (filter_mode(P, unit) != 2) continue;
-    const FilterScratch& f = W.filt[row];
-    const int b1 = f.b1, b2 = f.b2;
-    if (b1 < 0 || b2 < 0) continue;
-    if (W.h1c[(int64_t)row * kCB + b1] <= (uint32_t)kCand) continue;  // listed by pass 2
-    int c_lo, c_hi;
-    seg_chunks(sp, it - ri * sp.nseg, c_lo, c_hi);
-    const float M = f.m;
-    const float Tt = P.temps[unit];
-    const float rT = 1.0f / Tt;
-    const bool fast = hs_rcp_ok(Tt);
-    const T* rp = reinterpret_cast<const T*>(P.logits) + (int64_t)row * P.row_stride;
-    const bool vec_ok = ((reinterpret_cast<uintptr_t>(rp) & 15u) == 0);
-    const float flo = f.flo, fhi = f.fhi;  // fine bucket b2 of b1 <=> flo <= logit < fhi
-    for (int c = c_lo; c < c_hi; ++c) {
-      const int64_t i0 = chunk_elem(c, tid, 0);
-      float x[8];
-      load8<T>(rp, i0, P.V, vec_ok, x);
-      const bool full = i0 + 8 <= P.V;
-      uint32_t key[8], flags = 0;
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        key[k] = 0;
-        if (x[k] >= flo && x[k] < fhi && (full || i0 + k < P.V)) {
-          key[k] = hs_key(hs_div_temp(x[k], Tt, rT, fast));
-          flags |= 1u << k;
-        }
-      }
-      wave_append_cands(W, row, key, flags, i0);
-    }
-  }
-}
-
 // Copies the row's n candidates from the workspace into sm.cand.
 __device__ __forceinline__ void load_cands(const Work& W, int row, int n, FilterSmem& sm) {
   const uint64_t* src = W.cand + (int64_t)row * kCand;
@@ -1422,7 +1349,8 @@ __device__ __forceinline__ void load_cands(const Work& W, int row, int n, Filter
 
 // Keeps the n candidates in LDS whose value lies in fine sub-bucket b2 of
 // coarse bucket b1 (kFT threads; order not kept, the list is sorted next).
-// The key -> value map is exact, so this selects what pass 3 would append.
+// The key -> value map is exact, so this selects the elements of fine bucket
+// b2, as listing them from the row would.
 __device__ __forceinline__ int keep_fine_bucket(FilterSmem& sm, int n, float M, int b1, int b2) {
   constexpr int kPer = kCand / kFT;
   uint64_t c[kPer];
@@ -1453,26 +1381,54 @@ struct TopP {
   int64_t bidx;
   uint64_t sb_fx;
 };
-__device__ __forceinline__ bool top_p_from_hist(const Work& W, int row, FilterSmem& sm, float M, float sA,
-                                uint64_t theta, TopP& out) {
-  (void)theta;
+
+// What the histogram passes leave for a mode-2 row: the coarse boundary
+// bucket b1 (-1: the row never reaches p, -2: the row filter streams the row)
+// and its element count c1, the fine boundary bucket b2 (-1: not refined),
+// the count / mass / e-mass of the elements before the boundary, and the
+// number of candidates listed. Workgroup-uniform.
+struct TopPState {
+  int b1;
+  uint32_t c1;
+  int b2;
+  uint64_t ac, am, ae;
+  int n;
+};
+
+// The state the chunk-parallel passes left in the workspace.
+__device__ __forceinline__ TopPState top_p_state_of(const Work& W, int row) {
   const FilterScratch& f = W.filt[row];
-  const int b1 = f.b1;
-  if (b1 == -2) return false;
-  if (b1 < 0) {
-    out.all = true;
-    return true;
-  }
-  const uint32_t c1 = W.h1c[(int64_t)row * kCB + b1];
-  if (c1 > kDirect && f.b2 < 0) return false;
-  const uint64_t ac = f.ac, am = f.am, ae = f.ae;
-  int n = W.filt[row].ncand;
-  if (n > kCand || n <= 0) return false;
-  load_cands(W, row, n, sm);
+  TopPState h;
+  h.b1 = f.b1;
+  h.c1 = h.b1 >= 0 ? W.h1c[(int64_t)row * kCB + h.b1] : 0u;
+  h.b2 = f.b2;
+  h.ac = f.ac;
+  h.am = f.am;
+  h.ae = f.ae;
+  h.n = f.ncand;
+  return h;
+}
+
+// 1: the boundary is found from the candidates, 0: the whole row is kept,
+// -1: the row filter's radix path must decide.
+__device__ __forceinline__ int top_p_usable(const TopPState& h) {
+  if (h.b1 == -2) return -1;
+  if (h.b1 < 0) return 0;
+  if (h.c1 > kDirect && h.b2 < 0) return -1;
+  if (h.n > kCand || h.n <= 0) return -1;
+  return 1;
+}
+
+// top_p_usable(h) == 1 and the h.n candidates in sm.cand (unsorted).
+__device__ __forceinline__ bool top_p_from_cands(FilterSmem& sm, float M, float sA, uint64_t theta,
+                                                 const TopPState& h, TopP& out) {
+  const int b1 = h.b1;
+  const uint32_t c1 = h.c1;
+  const uint64_t ac = h.ac, am = h.am, ae = h.ae;
+  int n = h.n;
   if (c1 > kDirect && c1 <= (uint32_t)kCand) {
     // pass 2 listed the whole coarse bucket: keep its fine boundary sub-bucket
-    // (the elements pass 3 would have appended)
-    n = keep_fine_bucket(sm, n, f.m, b1, f.b2);
+    n = keep_fine_bucket(sm, n, M, b1, h.b2);
     if (n <= 0) return false;
   }
   (void)pad_sort(sm, n);
@@ -1505,11 +1461,14 @@ __device__ __forceinline__ bool top_p_from_hist(const Work& W, int row, FilterSm
   return true;
 }
 
+// The row filter proper (kFT threads, one row): the kept set of the row's
+// top-k / top-p and its normaliser, written to W.desc[row] (and row_stats),
+// from the candidates and histograms the chunk-parallel passes left in the
+// workspace. D0 is the row fold (max and normaliser over the whole row).
 template <typename T>
-__global__ __launch_bounds__(kFT) void k_row_filter(Problem P, Work W, float* row_stats) {
-  __shared__ FilterSmem sm;
-  __shared__ RowDesc s_fold;
-  const int row = blockIdx.x;
+__device__ __forceinline__ void row_filter_body(const Problem& P, const Work& W, int row,
+                                                float* row_stats, FilterSmem& sm,
+                                                const RowDesc& D0) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, wid = tid >> 6;
   const int unit = row / P.rows_per_unit;
@@ -1520,29 +1479,15 @@ __global__ __launch_bounds__(kFT) void k_row_filter(Problem P, Work W, float* ro
   const bool k_on = keff < V;
   const bool p_on = pp < 1.0f;
 
-  if (tid == 0) {
-    // the row fold of k_filter_plan1
-    RowDesc d;
-    d.m = W.filt[row].m;
-    d.s = W.filt[row].s;
-    d.tkey = 0u;
-    d.tidx = 0x7fffffff;
-    d.all = 1;
-    d.token = -1;
-    d.s_full = d.s;
-    d.pad = 0;
-    s_fold = d;
-  }
-  __syncthreads();
   if (!(k_on || p_on) && tid == 0) {
-    W.desc[row] = s_fold;
+    W.desc[row] = D0;
     if (row_stats) {
-      row_stats[2 * (int64_t)row] = s_fold.m;
-      row_stats[2 * (int64_t)row + 1] = s_fold.s;
+      row_stats[2 * (int64_t)row] = D0.m;
+      row_stats[2 * (int64_t)row + 1] = D0.s;
     }
   }
   if (k_on || p_on) {
-    RowDesc D = s_fold;
+    RowDesc D = D0;
     RowCtx<T> C;
     C.rp = reinterpret_cast<const T*>(P.logits) + (int64_t)row * P.row_stride;
     C.vec_ok = ((reinterpret_cast<uintptr_t>(C.rp) & 15u) == 0);
@@ -1711,8 +1656,66 @@ __global__ __launch_bounds__(kFT) void k_row_filter(Problem P, Work W, float* ro
         bool done = false;
         if (mode == 2) {
           // top-p alone: boundary from the chunk-parallel histograms + candidates
-          TopP tp;
-          if (top_p_from_hist(W, row, sm, C.M, sA, theta, tp)) {
+          TopPState h = top_p_state_of(W, row);
+          bool in_lds = false;
+          if (h.b1 >= 0 && h.c1 > kDirect) {
+            // the fine sub-bucket of b1 where the cumulative mass reaches p, from
+            // the second pass's fine histogram (threads >= kCB hold nothing)
+            const int64_t hb = (int64_t)row * kCB + tid;
+            uint64_t fc = 0, fm = 0, fe = 0;
+            if (tid < kCB) {
+              fc = W.h2c[hb];
+              fm = W.h2m[hb];
+              fe = W.h2e[hb];
+            }
+            const Crossing cf =
+                find_crossing<kFT>(fc, fm, fe, h.am, theta, sm.wsum, &sm.i32v[4], &sm.u64v[5]);
+            h.b2 = cf.b;
+            if (cf.b >= 0) {
+              h.ac += cf.c;
+              h.am = cf.m;  // includes the base
+              h.ae += cf.e;
+            }
+            if (cf.b >= 0 && h.c1 > (uint32_t)kCand) {
+              // more elements in b1 than the list holds (the second pass listed
+              // none): this workgroup lists those of the fine bucket b2 itself
+              const int b1 = h.b1, b2 = cf.b;
+              if (wid == 0) {
+                auto at_most = [&](float r, int fb) {
+                  const float x = C.div(r);
+                  const int cb = coarse_bucket(x, C.M);
+                  return cb < b1 || (cb == b1 && fine_bucket(x, C.M, b1) <= fb);
+                };
+                // logits of fine bucket b2 of b1: [flo, fhi)
+                const float flo = raw_threshold([&](float r) { return at_most(r, b2); });
+                const float fhi = raw_threshold([&](float r) { return at_most(r, b2 - 1); });
+                if (lane == 0) {
+                  sm.i32v[5] = __float_as_int(flo);
+                  sm.i32v[6] = __float_as_int(fhi);
+                  sm.i32v[0] = 0;
+                }
+              }
+              __syncthreads();
+              const float flo = __int_as_float(sm.i32v[5]), fhi = __int_as_float(sm.i32v[6]);
+              stream_row(C, [&](float raw, int64_t i) {
+                if (raw >= flo && raw < fhi) {
+                  const int slot = atomicAdd(&sm.i32v[0], 1);
+                  if (slot < kCand)
+                    sm.cand[slot] = ((uint64_t)hs_key(C.div(raw)) << 32) |
+                                    (uint64_t)(0xffffffffu - (uint32_t)i);
+                }
+              });
+              __syncthreads();
+              h.n = sm.i32v[0];
+              in_lds = true;
+            }
+          }
+          const int use = top_p_usable(h);
+          if (use > 0 && !in_lds) load_cands(W, row, h.n, sm);
+          TopP tpr;
+          if (use == 0) tpr.all = true;
+          if (use == 0 || (use > 0 && top_p_from_cands(sm, C.M, sA, theta, h, tpr))) {
+            const TopP& tp = tpr;
             if (tp.all) {
               ball = true;
               kept = V;
@@ -1842,6 +1845,24 @@ __global__ __launch_bounds__(kFT) void k_row_filter(Problem P, Work W, float* ro
   }
 }
 
+// One workgroup per row, after the chunk-parallel passes: the row fold of
+// k_filter_plan1 from the workspace, then the row filter proper.
+template <typename T>
+__global__ __launch_bounds__(kFT) void k_row_filter(Problem P, Work W, float* row_stats) {
+  __shared__ FilterSmem sm;
+  const int row = blockIdx.x;
+  RowDesc d;
+  d.m = W.filt[row].m;
+  d.s = W.filt[row].s;
+  d.tkey = 0u;
+  d.tidx = 0x7fffffff;
+  d.all = 1;
+  d.token = -1;
+  d.s_full = d.s;
+  d.pad = 0;
+  row_filter_body<T>(P, W, row, row_stats, sm, d);
+}
+
 template <typename T>
 int launch_filter(const Problem& P, const Work& W, float* row_stats, bool wave,
                   hipStream_t stream) {
@@ -1855,10 +1876,7 @@ int launch_filter(const Problem& P, const Work& W, float* row_stats, bool wave,
     // top-k rows by the wave-per-chunk gather (at most the 8 workgroups per CU
     // that fit at once on 256 CUs), top-p rows by the histogram pass; below 32
     // rows one launch with a workgroup per chunk is shorter
-    const int64_t wgs = (items + kPT / kWave - 1) / (kPT / kWave);
-    hipLaunchKernelGGL(k_filter_gather_k<T>, dim3((int)(wgs < 2048 ? wgs : 2048)), dim3(kPT), 0,
-                       stream, P, W);
-    hipLaunchKernelGGL(k_filter_pass1_w<T>, dim3(grid1), dim3(kPT), 0, stream, P, W);
+    hipLaunchKernelGGL(k_filter_pass1_kp<T>, dim3(grid1), dim3(kPT), 0, stream, P, W);
   } else {
     hipLaunchKernelGGL(k_filter_pass1<T>, dim3(grid1), dim3(kPT), 0, stream, P, W, 0);
   }
@@ -1867,13 +1885,12 @@ int launch_filter(const Problem& P, const Work& W, float* row_stats, bool wave,
     hipLaunchKernelGGL(k_filter_pass2_w<T>, dim3(grid1), dim3(kPT), 0, stream, P, W);
   else
     hipLaunchKernelGGL(k_filter_pass2<T>, dim3(grid1), dim3(kPT), 0, stream, P, W);
-  hipLaunchKernelGGL(k_filter_plan3, dim3(rows), dim3(kPT), 0, stream, P, W);
-  hipLaunchKernelGGL(k_filter_pass3<T>, dim3(grid1), dim3(kPT), 0, stream, P, W);
   hipLaunchKernelGGL(k_row_filter<T>, dim3(rows), dim3(kFT), 0, stream, P, W, row_stats);
   return hipGetLastError() == hipSuccess ? HS_OK : HS_ERR_LAUNCH;
 }
 
 template int launch_filter<float>(const Problem&, const Work&, float*, bool, hipStream_t);
 template int launch_filter<uint16_t>(const Problem&, const Work&, float*, bool, hipStream_t);
+
 
 }  // namespace hs

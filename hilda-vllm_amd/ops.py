@@ -78,12 +78,15 @@ def spec_accept(target_logits: torch.Tensor, draft_probs: torch.Tensor | None,
                 u_accept: torch.Tensor | None, u_resample: torch.Tensor | None, *,
                 mode="reference", top_ks: torch.Tensor | None = None,
                 top_ps: torch.Tensor | None = None, row_stats: bool = False,
-                topk_le64: bool = False):
+                topk_le64: bool = False, chain_only: bool = False):
     """Fused acceptance sampler (drop-in for model_runner.py:387-428).
 
     topk_le64 (filtered mode): the caller knows every entry of top_ks is in
     [1, 64]; small batches then run as one launch. A sequence breaking that
     promise gets num_accepted -1.
+
+    chain_only: run the launch chain even where a single-launch kernel would
+    serve the call (same results; for tests and timing).
 
     target_logits [B, gamma+1, V] f32/bf16, draft_probs [B, gamma, V] f32,
     draft_tokens [B, gamma] int64, temperatures [B] f32, u_accept [B, gamma],
@@ -145,7 +148,8 @@ def spec_accept(target_logits: torch.Tensor, draft_probs: torch.Tensor | None,
                             p(top_ps) if m == L.HS_ACCEPT_FILTERED else None,
                             p(u_accept) if m != L.HS_ACCEPT_GREEDY else None,
                             p(u_resample) if m != L.HS_ACCEPT_GREEDY else None,
-                            B, gamma, V, m | (L.HS_ACCEPT_TOPK_LE64 if topk_le64 else 0),
+                            B, gamma, V, m | (L.HS_ACCEPT_TOPK_LE64 if topk_le64 else 0)
+                            | (L.HS_ACCEPT_CHAIN if chain_only else 0),
                             p(nacc), p(out), p(olen), p(stats), ws.data_ptr(),
                             ws.numel(), _stream(dev))
     L.check(rc, "hs_spec_accept")

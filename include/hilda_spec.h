@@ -49,6 +49,12 @@ extern "C" {
 /* top-k is in [1, 64] (top-p any): small batches then run as a single launch */
 /* (a sequence whose top-k breaks the promise gets num_accepted -1).          */
 #define HS_ACCEPT_TOPK_LE64 0x100
+/* Flag OR-ed into any mode of hs_spec_accept: run the launch chain (chunk    */
+/* statistics, filter passes, row filter, decision and draw) even where a     */
+/* single-launch kernel would serve the call. The results are the same bits;  */
+/* this is for testing and timing the paths. hs_sampler accepts and ignores   */
+/* it (it always runs the chain).                                             */
+#define HS_ACCEPT_CHAIN 0x200
 
 /* Human-readable text for a status code (static storage). */
 const char* hs_status_string(int status);
