@@ -93,48 +93,6 @@ __device__ __forceinline__ float hs_div_temp(float x, float t, float rt, bool fa
   return fast ? hs_div_rcp(x, t, rt) : x / t;
 }
 
-// hs_div_temp of N values at once, for the wave-uniform division mode dm of
-// hs_div_mode (0: t == 1, 1: hs_rcp_ok(t), 2: IEEE division): the corrected
-// product runs branch-free on every value; zeros keep their sign (a / t = a
-// for t > 0); values outside the product's exact range (tiny, huge, inf,
-// NaN) take the IEEE division in a wave-uniform branch that ordinary logits
-// never enter. Same bits as hs_div_temp for every input.
-__device__ __forceinline__ int hs_div_mode(float t) {
-  return t == 1.0f ? 0 : (hs_rcp_ok(t) ? 1 : 2);
-}
-template <int N>
-__device__ __forceinline__ void hs_div_temp_n(const float (&a)[N], float (&x)[N], int dm, float t,
-                                              float rt) {
-  if (dm == 0) {
-#pragma unroll
-    for (int k = 0; k < N; ++k) x[k] = a[k];
-    return;
-  }
-  if (dm == 2) {
-#pragma unroll
-    for (int k = 0; k < N; ++k) x[k] = a[k] / t;
-    return;
-  }
-  uint32_t slow = 0;
-#pragma unroll
-  for (int k = 0; k < N; ++k) {
-    const float aa = fabsf(a[k]);
-    const bool in = aa >= 0x1p-96f && aa <= 0x1p60f;
-    const float q = a[k] * rt;
-    const float r = fmaf(-q, t, a[k]);
-    x[k] = in ? fmaf(r, rt, q) : a[k];
-    if (!in && aa != 0.0f) slow |= 1u << k;
-  }
-  if (__ballot(slow != 0u)) {
-    // an opaque statement keeps this a branch: without it the compiler
-    // computes the IEEE divisions of every value and selects
-    asm volatile("" ::: "memory");
-#pragma unroll
-    for (int k = 0; k < N; ++k)
-      if ((slow >> k) & 1u) x[k] = a[k] / t;
-  }
-}
-
 // floor(v * 2^44) for v in [0, 1] split as hi * 2^24 + lo with 32-bit parts:
 // hi = floor(v 2^20), lo = floor(frac(v 2^20) 2^24). Each step is exact
 // (scaling by powers of two, Sterbenz subtraction, truncating conversion).
@@ -262,78 +220,6 @@ __device__ __forceinline__ uint64_t wave_incl_scan_u64(uint64_t v, int lane) {
   }
   return v;
 }
-// Wave-wide max and sum through DPP (GFX9 data-parallel primitives): row
-// shifts by 1, 2, 4 and 8 leave lane 15 of each 16-lane row with its row's
-// value, row_bcast:15 (rows 1 and 3) and row_bcast:31 (rows 2 and 3) carry it
-// across rows, so lane 63 holds the wave's; it is returned wave-uniform. Six
-// VALU steps with no LDS round trip (the __shfl_xor versions above go
-// through ds_bpermute, one LDS latency per step).
-template <int ctrl, int row_mask>
-__device__ __forceinline__ float hs_dpp_max_step(float v) {
-  const int x = __float_as_int(v);
-  // lanes with no source (or outside row_mask) keep their own value
-  return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(x, x, ctrl, row_mask, 0xf, false)));
-}
-__device__ __forceinline__ float wave_max_f32_dpp(float v) {
-  v = hs_dpp_max_step<0x111, 0xf>(v);  // row_shr:1
-  v = hs_dpp_max_step<0x112, 0xf>(v);  // row_shr:2
-  v = hs_dpp_max_step<0x114, 0xf>(v);  // row_shr:4
-  v = hs_dpp_max_step<0x118, 0xf>(v);  // row_shr:8
-  v = hs_dpp_max_step<0x142, 0xa>(v);  // row_bcast:15
-  v = hs_dpp_max_step<0x143, 0xc>(v);  // row_bcast:31
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-}
-template <int ctrl, int row_mask>
-__device__ __forceinline__ uint32_t hs_dpp_add_step(uint32_t v) {
-  // lanes with no source read 0 (bound_ctrl); lanes outside row_mask keep old = 0
-  return v + (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, ctrl, row_mask, 0xf, true);
-}
-// sum of 64 lane values whose total fits 32 bits
-__device__ __forceinline__ uint32_t wave_sum_u32_dpp(uint32_t v) {
-  v = hs_dpp_add_step<0x111, 0xf>(v);
-  v = hs_dpp_add_step<0x112, 0xf>(v);
-  v = hs_dpp_add_step<0x114, 0xf>(v);
-  v = hs_dpp_add_step<0x118, 0xf>(v);
-  v = hs_dpp_add_step<0x142, 0xa>(v);
-  v = hs_dpp_add_step<0x143, 0xc>(v);
-  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
-}
-// sum over the wave of the fixed-point values hi * 2^24 + lo held as
-// hs_fx44_split accumulators of at most 8 elements per lane (hi < 2^24,
-// lo < 2^27): each lane carries lo's bits above 24 into hi first, so both
-// 32-bit sums stay below 2^31.
-__device__ __forceinline__ uint64_t wave_sum_fx44_dpp(uint32_t hi, uint32_t lo) {
-  const uint32_t h = wave_sum_u32_dpp(hi + (lo >> 24));
-  const uint32_t l = wave_sum_u32_dpp(lo & 0xffffffu);
-  return ((uint64_t)h << 24) + (uint64_t)l;
-}
-
-// exp(y) as hs_exp, without the branch: the polynomial is evaluated for every
-// lane and the result replaced by 0 below -86 (and for NaN). Same bits as
-// hs_exp for every input.
-__device__ __forceinline__ float hs_exp_nb(float y) {
-  const float kLog2e = 1.44269504088896341f;
-  const float kLn2Hi = 0.693145751953125f;
-  const float kLn2Lo = 1.428606765330187e-06f;
-  const bool ok = y >= -86.0f;
-  const float yy = ok ? y : 0.0f;  // keeps the discarded lanes' arithmetic finite
-  float t = yy * kLog2e;
-  float k = rintf(t);
-  float r = fmaf(-k, kLn2Hi, yy);
-  r = fmaf(-k, kLn2Lo, r);
-  float p = 1.98412698e-04f;
-  p = fmaf(p, r, 1.38888889e-03f);
-  p = fmaf(p, r, 8.33333333e-03f);
-  p = fmaf(p, r, 4.16666667e-02f);
-  p = fmaf(p, r, 1.66666667e-01f);
-  p = fmaf(p, r, 0.5f);
-  p = fmaf(p, r, 1.0f);
-  p = fmaf(p, r, 1.0f);
-  int ki = (int)k;
-  float scale = u2f((uint32_t)(ki + 127) << 23);
-  return ok ? p * scale : 0.0f;
-}
-
 __device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v, int lane) {
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
