@@ -423,6 +423,62 @@ def cpu_baseline_attention(torch, lens, block_size: int, R: int, Hq: int, Hkv: i
                       "the key share (torch-CPU restatement of attention.py:147-160)"}
 
 
+def _spec_run(torch, sr, target, draft, steps: int, warmup: int, kv: str, graphs: bool) -> dict:
+    """One timed config-3 run: prefill a 64-token prompt, two eager steps (they
+    create every workspace), graph capture of the draft and verify phases, then
+    `warmup` untimed and `steps` timed steps between HIP events on the stream."""
+    gamma = 3
+    dev = torch.device("cuda:0")
+    max_len = 64 + (steps + warmup + 4) * (gamma + 1) + 8
+    runner = sr.SpecRunner(target, draft, batch=1, gamma=gamma, max_model_len=max_len,
+                           temperature=0.6, mode="reference", kv_cache_dtype=kv,
+                           device=dev)
+    g = torch.Generator().manual_seed(0)
+    prompt = torch.randint(0, 10000, (64,), generator=g).tolist()
+    runner.load_prompts([prompt])
+    runner.prefill()
+    torch.manual_seed(0)
+    for _ in range(2):  # eager steps create every workspace before capture
+        runner.step()
+    torch.cuda.synchronize()
+    if graphs:
+        runner.capture()
+    run = runner.replay if graphs else runner.step
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    len0 = runner.lengths()[0]
+    stream = torch.cuda.current_stream(dev)
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(3 * steps)]
+    e_start = torch.cuda.Event(enable_timing=True)
+    e_end = torch.cuda.Event(enable_timing=True)
+    w0 = time.perf_counter()
+    e_start.record(stream)
+    for i in range(steps):
+        evs[3 * i].record(stream)
+        if graphs:
+            runner.graphs[0].replay()
+            evs[3 * i + 1].record(stream)
+            runner.graphs[1].replay()
+        else:
+            runner.draft_phase()
+            evs[3 * i + 1].record(stream)
+            runner.verify_phase()
+        evs[3 * i + 2].record(stream)
+    e_end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - w0
+    runner.check()  # no acceptance call of the timed steps produced invalid outputs
+    len1 = runner.lengths()[0]
+    res = dict(graphs=graphs, gpu_ms=e_start.elapsed_time(e_end), len0=len0, len1=len1,
+               emitted=len1 - len0, wall=wall,
+               draft_ms=sum(evs[3 * i].elapsed_time(evs[3 * i + 1]) for i in range(steps)),
+               verify_ms=sum(evs[3 * i + 1].elapsed_time(evs[3 * i + 2]) for i in range(steps)))
+    del runner
+    torch.cuda.empty_cache()
+    return res
+
+
 def bench_spec(args, torch, hv):
     """Config 3: speculative decoding at batch 1 with random-init Qwen3-8B target and
     Qwen3-0.6B draft (or the forced-acceptance draft = target's first 28 layers)."""
@@ -439,52 +495,9 @@ def bench_spec(args, torch, hv):
         draft = q3.Qwen3Host(q3.QWEN3_0_6B, device=dev, seed=2)
     torch.cuda.synchronize()
     init_s = time.perf_counter() - t0
-    max_len = 64 + (args.steps + args.warmup + 4) * (gamma + 1) + 8
-    runner = sr.SpecRunner(target, draft, batch=1, gamma=gamma, max_model_len=max_len,
-                           temperature=0.6, mode="reference", kv_cache_dtype=args.kv,
-                           device=dev)
-    g = torch.Generator().manual_seed(0)
-    prompt = torch.randint(0, 10000, (64,), generator=g).tolist()
-    runner.load_prompts([prompt])
-    runner.prefill()
-    torch.manual_seed(0)
-    for _ in range(2):  # eager steps create every workspace before capture
-        runner.step()
-    torch.cuda.synchronize()
-    graphs = not args.eager
-    if graphs:
-        runner.capture()
-    run = runner.replay if graphs else runner.step
-    for _ in range(args.warmup):
-        run()
-    torch.cuda.synchronize()
-    len0 = runner.lengths()[0]
-    stream = torch.cuda.current_stream(dev)
-    evs = [torch.cuda.Event(enable_timing=True) for _ in range(3 * args.steps)]
-    e_start = torch.cuda.Event(enable_timing=True)
-    e_end = torch.cuda.Event(enable_timing=True)
-    w0 = time.perf_counter()
-    e_start.record(stream)
-    for i in range(args.steps):
-        evs[3 * i].record(stream)
-        if graphs:
-            runner.graphs[0].replay()
-            evs[3 * i + 1].record(stream)
-            runner.graphs[1].replay()
-        else:
-            runner.draft_phase()
-            evs[3 * i + 1].record(stream)
-            runner.verify_phase()
-        evs[3 * i + 2].record(stream)
-    e_end.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - w0
-    runner.check()  # no acceptance call of the timed steps produced invalid outputs
-    gpu_ms = e_start.elapsed_time(e_end)
-    len1 = runner.lengths()[0]
-    emitted = len1 - len0
-    draft_ms = sum(evs[3 * i].elapsed_time(evs[3 * i + 1]) for i in range(args.steps))
-    verify_ms = sum(evs[3 * i + 1].elapsed_time(evs[3 * i + 2]) for i in range(args.steps))
+    m = _spec_run(torch, sr, target, draft, args.steps, args.warmup, args.kv, not args.eager)
+    graphs, gpu_ms, draft_ms, verify_ms = m["graphs"], m["gpu_ms"], m["draft_ms"], m["verify_ms"]
+    len0, len1, emitted, wall = m["len0"], m["len1"], m["emitted"], m["wall"]
     tok_s = emitted / (gpu_ms / 1e3)
     accepted_drafts = emitted - args.steps
     roof = attention_probe(torch, hv, kv=args.kv)
@@ -523,6 +536,22 @@ def bench_spec(args, torch, hv):
         "init_s": round(init_s, 1),
         "roofline": roof,
     }
+    if args.draft != "forced" and not args.no_forced:
+        # config 3's second mode: the draft is the target's first 28 layers plus
+        # its LM head, so most drafts are accepted and the accept path (bonus
+        # tokens, long commits) runs every step; a shorter timed run
+        fdraft = q3.Qwen3Host(q3.QWEN3_8B, share_from=target, num_layers=28)
+        fs = min(args.steps, 64)
+        f = _spec_run(torch, sr, target, fdraft, fs, 4, args.kv, not args.eager)
+        res["forced_acceptance"] = {
+            "draft": "target's first 28 layers + LM head", "steps": fs,
+            "value": round(f["emitted"] / (f["gpu_ms"] / 1e3), 2), "unit": "accepted tok/s",
+            "ms_per_step": round(f["gpu_ms"] / fs, 4),
+            "verify_accept_step_us": round(f["verify_ms"] / fs * 1e3, 1),
+            "draft_step_us": round(f["draft_ms"] / fs * 1e3, 1),
+            "tokens_per_step": round(f["emitted"] / fs, 3),
+            "acceptance_rate": round((f["emitted"] - fs) / (fs * gamma), 4)}
+        del fdraft
     if not args.no_cpu_baseline:
         w = hv.synthetic.accept_workload(1, gamma, seed=0, dtype="bf16", temperature=0.6)
         res["cpu_baseline"] = cpu_baseline_accept(torch, w, args.cpu_seconds)
@@ -802,6 +831,8 @@ def main(argv=None):
     ap.add_argument("--eager", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-forced", action="store_true",
+                    help="spec workload: skip the forced-acceptance companion run")
     ap.add_argument("--chain", action="store_true",
                     help="accept workload: force the launch chain (no single-launch kernel)")
     ap.add_argument("--no-topk-hint", action="store_true",

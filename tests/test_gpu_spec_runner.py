@@ -397,3 +397,48 @@ def test_config4_shape_adaptive_fp8_to_8192(cuda):
         ctl.update(acc, prop)
     gammas = [h[0] for h in runner.history]
     print("gamma histogram", {k: gammas.count(k) for k in sorted(set(gammas))}, flush=True)
+
+
+@pytest.mark.parametrize("draft_kind", ["qwen3-0.6b", "forced"])
+def test_config3_real_geometry_graph_matches_eager(cuda, draft_kind):
+    """Config 3 at its real geometry: random-init Qwen3-8B target (36 layers,
+    hidden 4096, 32 / 8 heads, FFN 12288, vocab 151936) with the Qwen3-0.6B draft
+    or the forced-acceptance draft (the target's first 28 layers and LM head),
+    batch 1, gamma 3, T 0.6, a 64-token prompt. Six steps replayed from the
+    captured HIP graphs emit the same tokens as six eager steps; every step emits
+    1 to gamma + 1 tokens; the forced draft has drafts accepted."""
+    q3, sr = _mods()
+    print(f"config 3 real geometry, draft {draft_kind}", flush=True)
+    target = q3.Qwen3Host(q3.QWEN3_8B, device=cuda, seed=1)
+    draft = (q3.Qwen3Host(q3.QWEN3_8B, share_from=target, num_layers=28)
+             if draft_kind == "forced" else q3.Qwen3Host(q3.QWEN3_0_6B, device=cuda, seed=2))
+    prompt = torch.randint(0, 10000, (64,), generator=torch.Generator().manual_seed(0)).tolist()
+
+    def run(graphs):
+        r = sr.SpecRunner(target, draft, batch=1, gamma=3, max_model_len=160, temperature=0.6,
+                          mode="reference", device=cuda)
+        r.load_prompts([prompt])
+        torch.manual_seed(3)
+        r.prefill()
+        torch.manual_seed(77)
+        r.step()
+        if graphs:
+            r.capture()
+        lens = [r.lengths()[0]]
+        for _ in range(6):
+            r.replay() if graphs else r.step()
+            torch.cuda.synchronize()
+            lens.append(r.lengths()[0])
+        r.check()
+        toks = r.tokens(0)
+        del r
+        torch.cuda.empty_cache()
+        return lens, toks
+
+    lens_e, toks_e = run(False)
+    lens_g, toks_g = run(True)
+    assert lens_g == lens_e and toks_g == toks_e
+    steps = [b - a for a, b in zip(lens_e, lens_e[1:])]
+    assert all(1 <= s <= 4 for s in steps), steps
+    if draft_kind == "forced":
+        assert sum(steps) > len(steps), steps  # some drafts accepted
