@@ -567,6 +567,9 @@ static_assert(kPT == kCB, "one histogram bucket per thread");
 constexpr uint32_t kDirect = 256;
 // pass 1 (wave kernel) keeps a bucket's count above bit 45 of its mass word
 constexpr int kPackShift = 45;
+// per-wave logit queue of the top-p first pass (a 512-element group adds at
+// most 512; 12 KB per workgroup keeps 8 workgroups per CU within the LDS)
+constexpr uint32_t kQ1 = 768;
 // per-wave candidate buffer of k_filter_pass2_w
 constexpr uint32_t kCandBuf = 128;
 // per-wave element queue of k_filter_pass2_w (holds a half group: 256)
@@ -687,6 +690,40 @@ __device__ __forceinline__ uint32_t wave_slots8(uint32_t flags, uint32_t (&slot)
   }
   return total;
 }
+
+// The same numbering taken straight from the comparisons: build(mask) keeps
+// one lane mask per element (bit l of m[k] is set when lane l's element k is
+// flagged) and the running totals before each, so a lane's slot for element k
+// is off[k] plus the flagged lanes below it. Callers form each mask from
+// ballots of single comparisons (a v_cmp result in scalar registers, used as
+// is) combined with scalar mask operations; a ballot of a compound condition
+// goes through a 0/1 register and a second comparison, and a per-lane flag
+// word that the ballots are re-derived from (wave_slots8) compiles to
+// per-element branches and bit-field extractions, which were most of a filter
+// pass's instructions.
+__device__ __forceinline__ uint64_t lanes_where(bool c) { return __builtin_amdgcn_ballot_w64(c); }
+template <int N>
+struct WaveMasks {
+  uint64_t m[N];
+  uint32_t off[N];
+  template <typename F>
+  __device__ __forceinline__ uint32_t build(F mask) {
+    uint32_t total = 0;
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+      m[k] = mask(k);
+      off[k] = total;
+      total += (uint32_t)__popcll(m[k]);
+    }
+    return total;
+  }
+  // lane's bit of ballot k (for use after code that ends the comparisons' lifetimes)
+  __device__ __forceinline__ bool has(int k, int lane) const { return (m[k] >> lane) & 1ull; }
+  __device__ __forceinline__ uint32_t slot(int k) const {
+    return off[k] + __builtin_amdgcn_mbcnt_hi((uint32_t)(m[k] >> 32),
+                                              __builtin_amdgcn_mbcnt_lo((uint32_t)m[k], 0u));
+  }
+};
 
 // Appends the (up to 8) flagged elements of every lane of the calling wave (all
 // lanes active) to the row's candidate list: slots from wave_slots8 and one
@@ -965,7 +1002,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
 template <typename T>
 __device__ __forceinline__ void pass1_w_body(const Problem& P, const Work& W, int blk, int nblk,
                                              PassShared& ps,
-                                             float (&s_q)[kPT / kWave][kWave * kGroupElems]) {
+                                             float (&s_q)[kPT / kWave][kQ1]) {
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
   const int rows = P.units * P.rows_per_unit;
   const SegPlan sp = seg_plan(P, W.flist[1], nblk);  // top-p rows only
@@ -1017,18 +1054,18 @@ __device__ __forceinline__ void pass1_w_body(const Problem& P, const Work& W, in
       lane_chunk_load<T>(rp, c0, P.V, lane, true, r);
 #pragma unroll
       for (int g = 0; g < kLaneChunkGroups; ++g) {
+        // room for a whole group first, so the comparisons below serve as the
+        // ballots and as the write masks with nothing kept across a drain
+        if (nq > kQ1 - kWave * kGroupElems) drain();
         const bool in = lane_chunk_idx(c0, g, lane, 0) < P.V;
-        uint32_t flags = 0;
-#pragma unroll
-        for (int k = 0; k < kGroupElems; ++k)
-          if (in && lane_chunk_val<T>(r, g, k) >= rj) flags |= 1u << k;
-        uint32_t slot[8];
-        const uint32_t total = wave_slots8(flags, slot);
+        auto hit = [&](int k) { return lane_chunk_val<T>(r, g, k) >= rj; };
+        const uint64_t inm = lanes_where(in);
+        WaveMasks<kGroupElems> wm;
+        const uint32_t total = wm.build([&](int k) { return lanes_where(hit(k)) & inm; });
         if (total == 0) continue;  // wave-uniform
-        if (nq + total > kWave * kGroupElems) drain();
 #pragma unroll
         for (int k = 0; k < kGroupElems; ++k)
-          if (flags & (1u << k)) q[nq + slot[k]] = lane_chunk_val<T>(r, g, k);
+          if (in && hit(k)) q[nq + wm.slot(k)] = lane_chunk_val<T>(r, g, k);
         nq += total;
       }
     }
@@ -1147,21 +1184,21 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
         const int g = h >> 1, k0 = 4 * (h & 1);
         const int64_t i0 = lane_chunk_idx(c0, g, lane, k0);
         const bool in = i0 < P.V;
-        uint32_t flags = 0;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
+        // rlo <= v < rhi as (v >= rlo) and not (v >= rhi): the same set for every
+        // v (a NaN fails the first comparison)
+        const uint64_t inm = lanes_where(in);
+        WaveMasks<4> wm;
+        const uint32_t total = wm.build([&](int k) {
           const float v = lane_chunk_val<T>(r, g, k0 + k);
-          if (in && v >= rlo && v < rhi) flags |= 1u << k;
-        }
-        uint32_t slot[8];
-        const uint32_t total = wave_slots8<4>(flags, slot);
+          return lanes_where(v >= rlo) & ~lanes_where(v >= rhi) & inm;
+        });
         if (total == 0) continue;  // wave-uniform; the common case
         if (nq + total > kQueue) drain();
 #pragma unroll
         for (int k = 0; k < 4; ++k)
-          if (flags & (1u << k)) {
-            qv[nq + slot[k]] = lane_chunk_val<T>(r, g, k0 + k);
-            qi[nq + slot[k]] = (uint32_t)(i0 + k);
+          if (wm.has(k, lane)) {
+            qv[nq + wm.slot(k)] = lane_chunk_val<T>(r, g, k0 + k);
+            qi[nq + wm.slot(k)] = (uint32_t)(i0 + k);
           }
         nq += total;
       }
@@ -1251,7 +1288,7 @@ template <typename T>
 __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_filter_pass1_kp(
     Problem P, Work W) {
   __shared__ PassShared ps;
-  __shared__ float s_q[kPT / kWave][kWave * kGroupElems];
+  __shared__ float s_q[kPT / kWave][kQ1];
   gather_k_body<T>(P, W, (int)blockIdx.x, (int)gridDim.x);
   pass1_w_body<T>(P, W, (int)blockIdx.x, (int)gridDim.x, ps, s_q);
 }
