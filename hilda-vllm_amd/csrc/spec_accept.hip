@@ -403,6 +403,70 @@ __global__ __launch_bounds__(kT) void k_sample_part(Problem P, AcceptArgs A, Wor
   }
 }
 
+// The same partial sums with one wave per chunk (aligned target and draft
+// rows, V % 8 == 0, no probabilities written): a workgroup's four waves take
+// the chunks of its range with all of a chunk's loads in flight, and each
+// wave writes its chunk's sums itself (no barrier per chunk). kPartWaveChunks
+// chunks per wave: the grid then holds about nchunk / 4 workgroups per unit,
+// all resident at B = 64, each paying the decision prologue once.
+constexpr int kPartWaveChunks = 1;
+template <typename T>
+__global__ __launch_bounds__(kT) void k_sample_part_w(Problem P, AcceptArgs A, Work W, SampleOut O,
+                                                      int desc_ready) {
+  __shared__ RowDesc s_desc[kMaxGamma + 1];
+  __shared__ SeqState s_st;
+  const int unit = blockIdx.y;
+  const int split = blockIdx.x;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int R = P.rows_per_unit;
+  const SeqState st = part_prologue<T>(P, A, W, O, desc_ready, unit, split, s_desc, &s_st);
+  const int row = st.row;
+  const bool residual = (st.kind == kKindResidual);
+  const RowDesc D = s_desc[row - unit * R];
+  const float Tt = P.temps[unit];
+  const float rT = 1.0f / Tt;
+  const bool fastT = hs_rcp_ok(Tt);
+  const float rS = 1.0f / D.s;
+  const bool fastS = hs_rcp_ok(D.s);
+  const T* rp = reinterpret_cast<const T*>(P.logits) + (int64_t)row * P.row_stride;
+  const float* qp = residual ? A.q + (int64_t)st.qrow * A.q_stride : nullptr;
+  constexpr int kPerWg = (kT / kWave) * kPartWaveChunks;
+  const int c_end = (split + 1) * kPerWg < P.nchunk ? (split + 1) * kPerWg : P.nchunk;
+  for (int c = split * kPerWg + wid; c < c_end; c += kT / kWave) {
+    const int64_t c0 = (int64_t)c * kChunk;
+    LaneChunk<T> r;
+    LaneChunk<float> qr;
+    lane_chunk_load<T>(rp, c0, P.V, lane, true, r);
+    if (residual) lane_chunk_load<float>(qp, c0, P.V, lane, true, qr);
+    uint32_t whi = 0, wlo = 0, phi = 0, plo = 0;
+#pragma unroll
+    for (int g = 0; g < kLaneChunkGroups; ++g) {
+      const bool in = lane_chunk_idx(c0, g, lane, 0) < P.V;
+#pragma unroll
+      for (int k = 0; k < kGroupElems; ++k) {
+        float p = 0.0f;
+        if (in) {
+          const float x = hs_div_temp(lane_chunk_val<T>(r, g, k), Tt, rT, fastT);
+          if (desc_keep(D, hs_key(x), lane_chunk_idx(c0, g, lane, k))) {
+            const float e = hs_exp(x - D.m);
+            p = fastS ? hs_div_rcp(e, D.s, rS) : e / D.s;
+          }
+        }
+        hs_fx44_split(p, phi, plo);
+        if (residual) hs_fx44_split(fmaxf(p - lane_chunk_val<float>(qr, g, k), 0.0f), whi, wlo);
+      }
+    }
+    const uint64_t sw = wave_sum_u64(hs_join44(whi, wlo));
+    const uint64_t sp = wave_sum_u64(hs_join44(phi, plo));
+    if (lane == 0) {
+      SampPart sps;
+      sps.w = sw;
+      sps.p = sp;
+      W.spart[(int64_t)unit * P.nchunk + c] = sps;
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // 4. final inverse-CDF search
 // ---------------------------------------------------------------------------
@@ -647,9 +711,18 @@ int run_sampler_chain(const Problem& P0, const AcceptArgs& A, const Work& W, int
                        filtered ? 1 : 0);
     return launch_ok();
   }
-  P.nsplit = pick_split(P.units, P.nchunk);
-  hipLaunchKernelGGL(k_sample_part<T>, dim3(P.nsplit, P.units), dim3(kT), 0, stream, P, A, W, O,
-                     mode, filtered ? 1 : 0);
+  if (wave && !O.probs) {
+    // (split 0 of either kernel writes the unit's state; k_sample_final reads
+    // only the per-chunk sums)
+    constexpr int kPerWg = (kT / kWave) * kPartWaveChunks;
+    P.nsplit = (P.nchunk + kPerWg - 1) / kPerWg;
+    hipLaunchKernelGGL(k_sample_part_w<T>, dim3(P.nsplit, P.units), dim3(kT), 0, stream, P, A, W,
+                       O, filtered ? 1 : 0);
+  } else {
+    P.nsplit = pick_split(P.units, P.nchunk);
+    hipLaunchKernelGGL(k_sample_part<T>, dim3(P.nsplit, P.units), dim3(kT), 0, stream, P, A, W, O,
+                       mode, filtered ? 1 : 0);
+  }
   if (O.sample)
     hipLaunchKernelGGL(k_sample_final<T>, dim3(P.units), dim3(kT), 0, stream, P, A, W, O);
   return launch_ok();

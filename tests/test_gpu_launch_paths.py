@@ -68,7 +68,8 @@ def _filter_rows(hv, rng):
     top-p / top-k / both / neither rows, boundary buckets of ~1000 and ~10000
     elements (listed whole, refined into fine sub-buckets, fine bucket listed by
     the third pass), top-k above the chunk count (radix path), rows with -inf
-    entries, rows of one repeated value (ties everywhere) and a nearly flat row."""
+    entries, rows of one repeated value (ties everywhere), nearly flat rows and
+    top-p near its limits."""
     rows, T, K, P = [], [], [], []
 
     def add(x, t, k, p):
@@ -95,6 +96,14 @@ def _filter_rows(hv, rng):
     add(np.full(V, 0.5), 1.0, 0, 0.5)
     add(np.full(V, 0.5), 1.0, 40, 1.0)
     add(rng.standard_normal(V) * 0.01, 1.0, 0, 0.9)
+    # top-p near its limits: p close to 1 (wide boundary region), a peaked row
+    # (boundary at the top bucket), logits spread far beyond the skipped
+    # buckets, a maximum far from 0, a nearly flat row at p = 0.99
+    add(rng.standard_normal(V) * 2.0, 0.6, 0, 0.999)
+    add(rng.standard_normal(V) * 8.0, 1.0, 0, 0.5)
+    add(rng.standard_normal(V) * 6.0, 1.0, 0, 0.95)
+    add(rng.standard_normal(V) * 2.0 + 300000.0, 1.0, 0, 0.9)
+    add(rng.standard_normal(V) * 0.01, 1.0, 0, 0.99)
     bits = hv.synthetic.f32_to_bf16_bits(np.stack(rows))
     return (bits, hv.synthetic.bf16_bits_to_f32(bits), np.array(T, np.float32),
             np.array(K, np.int32), np.array(P, np.float32))
