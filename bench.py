@@ -20,14 +20,21 @@ Prints ONE JSON line (rank 0). Workloads:
             other sampler shapes (config 0: --logits f32 --mode filtered
             --temperature 1 --top-k 50 --top-p 0.9; config 1: --batch 8|64|256
             --gamma 1|3|5 --per-seq --mode filtered, or --mode greedy).
+  gemm    - the spec step's dominant kernel alone: the 8B target's gate/up
+            projection at the verify shape over 36 weight sets.
   attention - config 2: paged verify attention, B=64, 4 queries, 16 Q / 8 KV
             heads, D=128, context ~ U[64, 2048], 256-token blocks in a random
             permutation, bf16 or (--kv fp8) fp8-e4m3 cache.
 Timed launches are captured in HIP graphs and replayed between two HIP events
 on the launch stream; inputs rotate over enough copies that every step reads
 HBM (the MI355X MALL is 256 MB).
-The roofline figure is algorithmic bytes per step divided by the HIP-event
-time of the step measured on the launch stream; cpu_baseline times the
+The roofline figure is algorithmic bytes per launch of the workload's dominant
+kernel divided by its HIP-event time measured on the launch stream (spec: the
+gate/up projection of the target at the verify shape, the largest share of the
+step's kernel time, probed over the target's own weights; roofline_step is the
+whole verify+accept step against the target weights it streams, and
+roofline_attention the verify-attention kernel at the batch-1 verify shape;
+accept and attention: the whole call); cpu_baseline times the
 torch-CPU restatement of the reference loop (oracle/torch_port.py) on the
 host cores of the same machine on a bounded sample.
 """
@@ -500,7 +507,16 @@ def bench_spec(args, torch, hv):
     len0, len1, emitted, wall = m["len0"], m["len1"], m["emitted"], m["wall"]
     tok_s = emitted / (gpu_ms / 1e3)
     accepted_drafts = emitted - args.steps
-    roof = attention_probe(torch, hv, kv=args.kv)
+    roof = gemm_probe(torch, hv, target)
+    roof_attn = attention_probe(torch, hv, kv=args.kv)
+    step_bytes = target_step_bytes(target)
+    step_us = verify_ms / args.steps * 1e3
+    roof_step = {"bound": "hbm", "achieved": round(step_bytes / (step_us * 1e-6) / 1e9, 1),
+                 "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                 "frac": round(step_bytes / (step_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                 "bytes_per_step": step_bytes, "step_us": round(step_us, 1),
+                 "what": "verify+accept step: the target's layer weights and LM head, each read "
+                         "once per step, over the step's HIP-event time"}
     res = {
         "metric": METRIC,
         "value": round(tok_s, 2),
@@ -535,6 +551,8 @@ def bench_spec(args, torch, hv):
         "wall_s": round(wall, 3),
         "init_s": round(init_s, 1),
         "roofline": roof,
+        "roofline_step": roof_step,
+        "roofline_attention": roof_attn,
     }
     if args.draft != "forced" and not args.no_forced:
         # config 3's second mode: the draft is the target's first 28 layers plus
@@ -638,6 +656,76 @@ def bench_adaptive(args, torch, hv):
 
 
 PROBE_CONTEXT = 320  # config-3 end state: 64 prompt tokens + 256 generated tokens
+
+
+def target_step_bytes(target) -> int:
+    """Bytes a verify step of the target must read at least once: every layer's
+    projection weights and the LM head (bf16)."""
+    n = target.lm_head.numel()
+    for lyr in target.layers:
+        n += lyr.qkv.numel() + lyr.o.numel() + lyr.gate_up.numel() + lyr.down.numel()
+    return 2 * n
+
+
+class _GateUpLayers:
+    """The gate/up weights (and post-attention norm weights) of an 8B-shaped target,
+    N(0, 0.02^2) bf16, without the rest of the model (the gemm workload)."""
+
+    def __init__(self, torch, g, device):
+        gen = torch.Generator(device=device).manual_seed(4)
+        self.g = g
+        self.layers = []
+        for _ in range(g.num_layers):
+            lyr = type("L", (), {})()
+            lyr.gate_up = (torch.randn((2 * g.ffn, g.hidden), generator=gen, device=device)
+                           * 0.02).to(torch.bfloat16)
+            lyr.ln2 = torch.ones(g.hidden, dtype=torch.bfloat16, device=device)
+            self.layers.append(lyr)
+
+
+def bench_gemm(args, torch, hv):
+    """The spec step's dominant kernel alone (gemm_probe over 36 fresh weight sets)."""
+    q3 = importlib.import_module("hilda-vllm_amd.engine.qwen3_host")
+    model = _GateUpLayers(torch, q3.QWEN3_8B, torch.device("cuda:0"))
+    roof = gemm_probe(torch, hv, model, reps=max(1, args.steps // 36))
+    return {"metric": METRIC, "value": roof["avg_launch_us"],
+            "unit": "us/launch (gate/up projection)", "n_gpus": 1, "steps": roof["launches"],
+            "warmup": 36, "ms_per_step": roof["avg_launch_us"] / 1e3, "higher_is_better": False,
+            "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic (N(0,0.02^2) weights, N(0,1) rows)",
+            "config": {"workload": "gate/up projection of the 8B target at the verify shape, "
+                                   "36 layers"},
+            "roofline": roof}
+
+
+def gemm_probe(torch, hv, target, rows: int = 4, reps: int = 10):
+    """The step's dominant kernel (the largest share of the step's kernel time,
+    profiles/trace_spec-config3.md): the target's gate/up projection at the verify
+    shape (4 rows, K = 4096, 2 x 12288 weight rows, RMSNorm with the residual add in
+    its prologue, SwiGLU in its epilogue). One launch per layer over the target's own
+    36 weight matrices (as in one verify step), captured in a HIP graph and replayed
+    `reps` times between two HIP events on the launch stream."""
+    dev = torch.device("cuda:0")
+    g = target.g
+    gen = torch.Generator(device=dev).manual_seed(3)
+    h = torch.randn((rows, g.hidden), generator=gen, device=dev).to(torch.bfloat16)
+    res = torch.randn((rows, g.hidden), generator=gen, device=dev).to(torch.bfloat16)
+    layers = list(target.layers)
+
+    def launch_all():
+        for lyr in layers:
+            hv.ops.linear_rmsnorm(h, lyr.ln2, g.rms_eps, lyr.gate_up, residual=res, swiglu=True)
+
+    us = graph_time_us(torch, dev, launch_all, reps) / len(layers)
+    # weights, norm weight, input and residual rows in, residual rows and SwiGLU rows out
+    per_launch = 2 * (2 * g.ffn * g.hidden + g.hidden + 3 * rows * g.hidden + rows * g.ffn)
+    achieved = per_launch / (us * 1e-6) / 1e9
+    kernel = "k_skinny<4, 1, 1, true, true>"
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(kernel, "gemm-gate-up"),
+            "kernel": kernel, "bytes_per_launch": per_launch, "avg_launch_us": round(us, 3),
+            "shape": f"M={rows} K={g.hidden} N=2x{g.ffn} (gate/up, RMSNorm prologue, SwiGLU)",
+            "launches": reps * len(layers)}
 
 
 def attention_probe(torch, hv, kv: str = "auto", L: int = PROBE_CONTEXT, layers: int = 36,
@@ -813,7 +901,8 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="spec",
-                    choices=["spec", "accept", "attention", "attention-b1", "copy", "adaptive"])
+                    choices=["spec", "accept", "attention", "attention-b1", "gemm", "copy",
+                             "adaptive"])
     ap.add_argument("--max-context", type=int, default=8192)
     ap.add_argument("--rocprof-summary", metavar="DIR", default=None,
                     help="print a text summary of a rocprofv3 CSV output directory and exit")
@@ -848,7 +937,8 @@ def main(argv=None):
         return 2
     if args.steps is None:
         # spec: ~256 generated tokens over warm-up + timed steps at random-weight acceptance
-        args.steps = {"spec": 180, "attention-b1": 720, "adaptive": 1 << 30}.get(args.workload, 200)
+        args.steps = {"spec": 180, "attention-b1": 720, "gemm": 360,
+                      "adaptive": 1 << 30}.get(args.workload, 200)
     if args.warmup is None:
         args.warmup = 8 if args.workload == "spec" else 20
     import torch
@@ -861,6 +951,8 @@ def main(argv=None):
         res = bench_copy(args, torch, hv)
     elif args.workload == "attention-b1":
         res = bench_attention_b1(args, torch, hv)
+    elif args.workload == "gemm":
+        res = bench_gemm(args, torch, hv)
     elif args.workload == "adaptive":
         res = bench_adaptive(args, torch, hv)
     else:
