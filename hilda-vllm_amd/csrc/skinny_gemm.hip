@@ -415,6 +415,11 @@ void launch_skinny(const SkinnyArgs& a, int waves, hipStream_t stream) {
   // has enough tiles to keep every CU busy with half as many workgroups
   constexpr bool kDouble = (EPI ? 2 * kR : kR) * S <= 12;
   if (kDouble && a.ntiles >= 2 * cus && grid > a.ntiles / 2) grid = a.ntiles / 2;
+  // verify-row projections with the RMSNorm prologue: at least 6 tiles per
+  // workgroup once the matrix has a CU's worth of them, so that the prologue
+  // (activation loads, a barrier, the norm) is paid by fewer workgroups and the
+  // double buffer streams behind it (8B qkv, 4 rows: 13.3 -> 12.5 us)
+  if (NORM && M >= 2 && a.ntiles >= 6 * cus && grid > a.ntiles / 6) grid = a.ntiles / 6;
   if (grid > a.ntiles) grid = a.ntiles;
   hipLaunchKernelGGL((k_skinny<M, S, EPI, NORM, RES>), dim3((unsigned)grid), dim3(64 * waves), 0,
                      stream, a);
