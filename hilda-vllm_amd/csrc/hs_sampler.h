@@ -59,12 +59,12 @@ struct FilterScratch {
   int32_t ncand;   // candidates appended by the filter passes
   int32_t b1;      // coarse boundary bucket (-1: the row never reaches p; -2: not
                    // within buckets 0..jmax, the row filter streams the row)
-  int32_t b2;      // unused (the row filter finds the fine boundary bucket)
   int32_t jmax;    // pass 1 histograms buckets 0..jmax only (see mass_skip_bucket)
+  uint32_t c1;     // elements in coarse bucket b1 (k_filter_plan2)
   float m;         // row max and normaliser (x = logit / T)
   float s;
   uint32_t tau;    // top-k gather threshold (order key)
-  uint32_t pad2;
+  uint32_t pad;
   uint64_t theta;  // top-p mass threshold (fixed point)
   uint64_t ac;     // count, mass and e-mass of the elements before the boundary bucket
   uint64_t am;
@@ -72,9 +72,8 @@ struct FilterScratch {
   // raw-value (logit) thresholds of the top-p passes, exact images of their
   // bucket tests (x = logit / T is monotone in the logit): pass 1 takes
   // logit >= rj (coarse bucket <= jmax), pass 2 rlo <= logit < rhi (coarse
-  // bucket b1); flo, fhi unused
-  float rj, rlo, rhi, flo, fhi;
-  uint32_t c1;     // elements in coarse bucket b1 (k_filter_plan2)
+  // bucket b1)
+  float rj, rlo, rhi, pad2;
 };
 
 struct Problem {

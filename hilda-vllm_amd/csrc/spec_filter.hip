@@ -821,7 +821,6 @@ __global__ __launch_bounds__(kPT) void k_filter_plan1(Problem P, Work W) {
       f.m = d.m;
       f.s = d.s;
       f.b1 = -1;
-      f.b2 = -1;
       f.ac = f.am = f.ae = 0ull;
       f.theta = (mode == 2) ? mass_threshold(P.top_ps[unit]) : 0ull;
       f.jmax = jmax;
@@ -887,7 +886,6 @@ __global__ __launch_bounds__(kPT) void k_filter_plan2(Problem P, Work W) {
     }
     if (t == 0) {
       f.b1 = b1;
-      f.b2 = -1;
       f.rlo = rlo;
       f.rhi = rhi;
       f.ac = cr.c;
@@ -1438,7 +1436,7 @@ __device__ __forceinline__ TopPState top_p_state_of(const Work& W, int row) {
   TopPState h;
   h.b1 = f.b1;
   h.c1 = h.b1 >= 0 ? W.h1c[(int64_t)row * kCB + h.b1] : 0u;
-  h.b2 = f.b2;
+  h.b2 = -1;  // the row filter resolves the fine boundary bucket
   h.ac = f.ac;
   h.am = f.am;
   h.ae = f.ae;
