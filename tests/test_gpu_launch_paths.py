@@ -131,3 +131,35 @@ def test_filter_chain_every_branch_vs_oracle(hv, orc, cuda):
     np.testing.assert_array_equal(kept, probs > 0)
     xs = (xf / T[:, None]).astype(np.float32)
     np.testing.assert_array_equal(masked[kept], xs[kept])
+
+
+@pytest.mark.parametrize("mode", ["reference", "filtered"])
+def test_wave_and_scalar_chains_agree(hv, orc, cuda, mode):
+    """B = 64, gamma = 3, per-sequence settings: the chain's wave-per-chunk kernels
+    (aligned rows) and its workgroup-per-chunk kernels (draft probabilities at an odd
+    row stride, so no row is 16-byte aligned) give the same bits, and the oracle's
+    decisions."""
+    B, gamma = 64, 3
+    print(f"wave vs scalar chain B={B} gamma={gamma} {mode}", flush=True)
+    w = hv.synthetic.accept_workload(B, gamma, seed=4242, dtype="bf16", mode=mode,
+                                     per_seq_settings=True)
+    lg = _logits(w, cuda)
+    t = _dev(w, cuda, ["draft_probs", "draft_tokens", "temperatures", "u_accept",
+                       "u_resample", "top_ks", "top_ps"])
+    padded = torch.zeros((B * gamma, V + 1), dtype=torch.float32, device=cuda)
+    padded[:, :V] = t["draft_probs"].reshape(B * gamma, V)
+    q_odd = padded[:, :V].reshape(B, gamma, V)
+    assert q_odd.stride(1) == V + 1
+    got = []
+    for q in (t["draft_probs"], q_odd):
+        r = hv.ops.spec_accept(lg, q, t["draft_tokens"], t["temperatures"], t["u_accept"],
+                               t["u_resample"], mode=mode, top_ks=t["top_ks"],
+                               top_ps=t["top_ps"], row_stats=True)
+        got.append([x.cpu().numpy() for x in r])
+    for a, b in zip(*got):
+        np.testing.assert_array_equal(a, b)
+    ref = orc.spec_accept(w["logits"], w["draft_probs"], w["draft_tokens"], w["temperatures"],
+                          w["u_accept"], w["u_resample"], mode=mode, top_ks=w["top_ks"],
+                          top_ps=w["top_ps"])
+    np.testing.assert_array_equal(got[0][0], ref["num_accepted"])
+    np.testing.assert_array_equal(got[0][1], ref["out_tokens"])
