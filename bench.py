@@ -667,6 +667,14 @@ def target_step_bytes(target) -> int:
     return 2 * n
 
 
+class _GateUpLayer:
+    """One layer's gate/up weight and post-attention norm weight."""
+
+    def __init__(self, gate_up, ln2):
+        self.gate_up = gate_up
+        self.ln2 = ln2
+
+
 class _GateUpLayers:
     """The gate/up weights (and post-attention norm weights) of an 8B-shaped target,
     N(0, 0.02^2) bf16, without the rest of the model (the gemm workload)."""
@@ -674,13 +682,11 @@ class _GateUpLayers:
     def __init__(self, torch, g, device):
         gen = torch.Generator(device=device).manual_seed(4)
         self.g = g
-        self.layers = []
-        for _ in range(g.num_layers):
-            lyr = type("L", (), {})()
-            lyr.gate_up = (torch.randn((2 * g.ffn, g.hidden), generator=gen, device=device)
-                           * 0.02).to(torch.bfloat16)
-            lyr.ln2 = torch.ones(g.hidden, dtype=torch.bfloat16, device=device)
-            self.layers.append(lyr)
+        self.layers = [
+            _GateUpLayer((torch.randn((2 * g.ffn, g.hidden), generator=gen, device=device)
+                          * 0.02).to(torch.bfloat16),
+                         torch.ones(g.hidden, dtype=torch.bfloat16, device=device))
+            for _ in range(g.num_layers)]
 
 
 def bench_gemm(args, torch, hv):
