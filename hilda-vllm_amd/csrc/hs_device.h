@@ -66,6 +66,41 @@ __device__ __forceinline__ float hs_exp(float y) {
   return p * scale;
 }
 
+// hs_exp(y) * 2^20, equal bit for bit to that product, without a branch:
+//   * every coefficient of the polynomial carries the factor 2^20; scaling by
+//     a power of two commutes with each rounding while the values stay normal,
+//     which they do here (p in [2^19, 2^21), result >= 2^-105);
+//   * k = rint(t) by the rounding constant 1.5 * 2^23: t + 1.5 * 2^23 rounds t
+//     to the nearest integer, ties to even (the constant is even), as rintf
+//     does for |t| < 2^22, and the sum's low bits are 0x4B400000 + k, which
+//     give 2^k without a float->int conversion. k's zero may be +0 where
+//     rintf gives -0; r is then the same value, and fma(p, r, c) with r = +-0
+//     returns c;
+//   * for y < -86 and NaN the value is computed and then discarded.
+__device__ __forceinline__ float hs_exp_2p20(float y) {
+  const float kLog2e = 1.44269504088896341f;
+  const float kLn2Hi = 0.693145751953125f;
+  const float kLn2Lo = 1.428606765330187e-06f;
+  const float kS = 1048576.0f;       // 2^20
+  const float kRound = 12582912.0f;  // 1.5 * 2^23
+  const float t = y * kLog2e;
+  const float kf = t + kRound;
+  const float k = kf - kRound;
+  float r = fmaf(-k, kLn2Hi, y);
+  r = fmaf(-k, kLn2Lo, r);
+  float p = 1.98412698e-04f * kS;
+  p = fmaf(p, r, 1.38888889e-03f * kS);
+  p = fmaf(p, r, 8.33333333e-03f * kS);
+  p = fmaf(p, r, 4.16666667e-02f * kS);
+  p = fmaf(p, r, 1.66666667e-01f * kS);
+  p = fmaf(p, r, 0.5f * kS);
+  p = fmaf(p, r, 1.0f * kS);
+  p = fmaf(p, r, 1.0f * kS);
+  const float scale = u2f((f2u(kf) - 0x4B400000u + 127u) << 23);
+  const float v = p * scale;
+  return (y >= -86.0f) ? v : 0.0f;
+}
+
 // Correctly rounded x / t. For t == 1 the division is skipped (exact).
 __device__ __forceinline__ float hs_div_t(float x, float t) {
   return (t == 1.0f) ? x : x / t;
@@ -79,6 +114,12 @@ __device__ __forceinline__ float hs_div_t(float x, float t) {
 __device__ __forceinline__ float hs_div_rcp(float a, float b, float rb) {
   const float aa = fabsf(a);
   if (!(aa >= 0x1p-96f && aa <= 0x1p60f)) return a / b;
+  const float q = a * rb;
+  const float r = fmaf(-q, b, a);
+  return fmaf(r, rb, q);
+}
+// The corrected product alone, for callers that have checked the range.
+__device__ __forceinline__ float hs_div_rcp_in_range(float a, float b, float rb) {
   const float q = a * rb;
   const float r = fmaf(-q, b, a);
   return fmaf(r, rb, q);
@@ -102,6 +143,12 @@ __device__ __forceinline__ void hs_fx44_split(float v, uint32_t& hi, uint32_t& l
   const float f = t - (float)h;
   hi += h;
   lo += (uint32_t)(f * 16777216.0f);
+}
+// hs_fx44_split of v given t = v * 2^20 (hs_exp_2p20's output): the same two
+// parts, the fraction by v_fract (t - floor(t), exact for t in [0, 2^20]).
+__device__ __forceinline__ void hs_fx44_acc(float t, uint32_t& hi, uint32_t& lo) {
+  hi += (uint32_t)t;
+  lo += (uint32_t)(__builtin_amdgcn_fractf(t) * 16777216.0f);
 }
 __device__ __forceinline__ uint64_t hs_join44(uint32_t hi, uint32_t lo) {
   return ((uint64_t)hi << 24) + (uint64_t)lo;

@@ -129,6 +129,70 @@ __device__ __forceinline__ float lane_chunk_val(const LaneChunk<T>& r, int s, in
   }
 }
 
+// True when every value held in the lane's chunk words has |x| in
+// [2^-96, 2^60], the numerator range in which hs_div_rcp's corrected product
+// is exact (zeros, subnormals, infinities and NaN fail). On the bit patterns,
+// with lo/hi the patterns of 2^-96 and 2^60: 2|x| - 2 lo, taken modulo 2^16
+// (bf16, both halves of a word at once) or 2^32 (f32), is at most 2 (hi - lo)
+// exactly for |x| in range; doubling drops the sign bit and values below lo
+// wrap above the bound.
+template <typename T>
+__device__ __forceinline__ bool lane_chunk_rcp_ok(const LaneChunk<T>& r) {
+  if constexpr (sizeof(T) == 2) {
+    using u16x2 = unsigned short __attribute__((ext_vector_type(2)));
+    const u16x2 two = {2, 2}, off = {0xE100, 0xE100};  // -2 * 0x0F80 mod 2^16
+    u16x2 acc = {0, 0};
+#pragma unroll
+    for (int i = 0; i < LaneChunk<T>::kWords; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const u16x2 v = __builtin_bit_cast(u16x2, u4_word(r.w[i], j));
+        acc = __builtin_elementwise_max(acc, v * two + off);
+      }
+    return acc.x <= 0x9C00 && acc.y <= 0x9C00;  // 2 * (0x5D80 - 0x0F80)
+  } else {
+    uint32_t acc = 0;
+#pragma unroll
+    for (int i = 0; i < LaneChunk<T>::kWords; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t t = (u4_word(r.w[i], j) << 1) + 0xE1000000u;  // -2 * 0x0F800000
+        acc = t > acc ? t : acc;
+      }
+    return acc <= 0x9C000000u;  // 2 * (0x5D800000 - 0x0F800000)
+  }
+}
+
+// x / T (hs_div_temp) for every element of a lane's chunk, with one
+// wave-uniform choice per chunk instead of per element: the identity for
+// T = 1; the corrected product when hs_rcp_ok(T) and every numerator of the
+// wave's chunk is in its exact range; hs_div_temp per element otherwise.
+// T must be the same in every lane.
+template <typename T>
+__device__ __forceinline__ void lane_chunk_div_temp(const LaneChunk<T>& r, float Tt,
+                                                    float (&x)[kLaneChunkGroups][kGroupElems]) {
+  const float rT = 1.0f / Tt;
+  const bool fast = hs_rcp_ok(Tt);
+  if (Tt == 1.0f) {
+#pragma unroll
+    for (int s = 0; s < kLaneChunkGroups; ++s)
+#pragma unroll
+      for (int k = 0; k < kGroupElems; ++k) x[s][k] = lane_chunk_val<T>(r, s, k);
+  } else if (fast && __builtin_amdgcn_ballot_w64(!lane_chunk_rcp_ok<T>(r)) == 0) {
+#pragma unroll
+    for (int s = 0; s < kLaneChunkGroups; ++s)
+#pragma unroll
+      for (int k = 0; k < kGroupElems; ++k)
+        x[s][k] = hs_div_rcp_in_range(lane_chunk_val<T>(r, s, k), Tt, rT);
+  } else {
+#pragma unroll
+    for (int s = 0; s < kLaneChunkGroups; ++s)
+#pragma unroll
+      for (int k = 0; k < kGroupElems; ++k)
+        x[s][k] = hs_div_temp(lane_chunk_val<T>(r, s, k), Tt, rT, fast);
+  }
+}
+
 // Folds the chunk partials of one row into its max M and normaliser
 //   S = f32rz(sum_c floor(2^40 * f32rz(E_c) 2^-44 * exp(m_c - M))) 2^-40
 // (one wave; every lane returns the same descriptor, kept set = whole row).

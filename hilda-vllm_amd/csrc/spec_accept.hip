@@ -106,29 +106,45 @@ __device__ __forceinline__ void chunk_stats_wave(const Problem& P, const Work& W
   const int row = (int)(it / P.nchunk);
   const int c = (int)(it % P.nchunk);
   const int unit = row / P.rows_per_unit;
-  const float Tt = P.temps[unit];
-  const float rT = 1.0f / Tt;
-  const bool fast = hs_rcp_ok(Tt);
   const int64_t c0 = (int64_t)c * kChunk;
   float x[kLaneChunkGroups][kGroupElems];
+  lane_chunk_div_temp<T>(r, P.temps[unit], x);
+  // every group of a chunk that ends inside the row is in it (wave-uniform)
+  const bool full = c0 + kChunk <= P.V;
   float m = -INFINITY;
-#pragma unroll
-  for (int s = 0; s < kLaneChunkGroups; ++s) {
-    const bool in = lane_chunk_idx(c0, s, lane, 0) < P.V;
-#pragma unroll
-    for (int k = 0; k < kGroupElems; ++k) {
-      x[s][k] = hs_div_temp(lane_chunk_val<T>(r, s, k), Tt, rT, fast);
-      if (in) m = fmaxf(m, x[s][k]);
-    }
-  }
-  m = wave_max_f32(m);
   uint32_t hi = 0, lo = 0;
+  if (full) {
 #pragma unroll
-  for (int s = 0; s < kLaneChunkGroups; ++s) {
-    const bool in = lane_chunk_idx(c0, s, lane, 0) < P.V;
+    for (int s = 0; s < kLaneChunkGroups; ++s)
 #pragma unroll
-    for (int k = 0; k < kGroupElems; ++k)
-      if (in) hs_fx44_split(hs_exp(x[s][k] - m), hi, lo);
+      for (int k = 0; k < kGroupElems; ++k) m = fmaxf(m, x[s][k]);
+    m = wave_max_f32(m);
+#pragma unroll
+    for (int s = 0; s < kLaneChunkGroups; ++s)
+#pragma unroll
+      for (int k = 0; k < kGroupElems; ++k) {
+        hs_fx44_acc(hs_exp_2p20(x[s][k] - m), hi, lo);
+        // the running sums are taken every 4 elements: left alone, the
+        // compiler regroups the 32 integer additions into one tree at the end
+        // and keeps every element's two parts live (spills past 64 VGPRs)
+        if (k % 4 == 3) asm volatile("" : "+v"(hi), "+v"(lo));
+      }
+  } else {
+#pragma unroll
+    for (int s = 0; s < kLaneChunkGroups; ++s) {
+      const bool in = lane_chunk_idx(c0, s, lane, 0) < P.V;
+#pragma unroll
+      for (int k = 0; k < kGroupElems; ++k)
+        if (in) m = fmaxf(m, x[s][k]);
+    }
+    m = wave_max_f32(m);
+#pragma unroll
+    for (int s = 0; s < kLaneChunkGroups; ++s) {
+      const bool in = lane_chunk_idx(c0, s, lane, 0) < P.V;
+#pragma unroll
+      for (int k = 0; k < kGroupElems; ++k)
+        if (in) hs_fx44_acc(hs_exp_2p20(x[s][k] - m), hi, lo);
+    }
   }
   const uint64_t e = wave_sum_u64(hs_join44(hi, lo));
   if (lane == 0) {
@@ -155,8 +171,11 @@ __device__ __forceinline__ void chunk_stats_wave(const Problem& P, const Work& W
 }
 
 template <typename T>
-__global__ __launch_bounds__(kT) void k_chunk_stats_w(Problem P, Work W) {
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+__global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(8))) void k_chunk_stats_w(Problem P, Work W) {
+  const int lane = threadIdx.x & 63;
+  // the wave index is uniform across the wave: kept in a scalar register, the
+  // chunk, row and temperature are too, and the branches on them are uniform
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t items = (int64_t)P.units * P.rows_per_unit * P.nchunk;
   const int64_t stride = (int64_t)gridDim.x * (kT / kWave);
   int64_t it = (int64_t)blockIdx.x * (kT / kWave) + wid;

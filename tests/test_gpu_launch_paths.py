@@ -163,3 +163,74 @@ def test_wave_and_scalar_chains_agree(hv, orc, cuda, mode):
                           top_ps=w["top_ps"])
     np.testing.assert_array_equal(got[0][0], ref["num_accepted"])
     np.testing.assert_array_equal(got[0][1], ref["out_tokens"])
+
+
+def _edge_targets(hv, rng, B, gamma):
+    """Target logit patterns [B, gamma+1, V] (bf16) whose numerators leave the
+    range [2^-96, 2^60] in which x / T is taken as a corrected product: exact
+    zeros of both signs, tiny normals and subnormals, the range ends and their
+    neighbours, huge values, -inf entries; spread over a whole row or confined
+    to one chunk (so that fast and fallback chunks meet in one row), including
+    the row's last, partial chunk."""
+    f = hv.synthetic.f32_to_bf16_bits
+    tb = f((rng.standard_normal((B, gamma + 1, V)) * 2.0).astype(np.float32))
+
+    def put(b, j, idx, vals):
+        tb[b, j, idx] = np.asarray(vals, np.uint16)
+
+    spread = lambda n: rng.choice(V, size=n, replace=False)
+    in_chunk = lambda c, n: c * 2048 + rng.choice(min(2048, V - c * 2048), size=n, replace=False)
+    put(0, 0, spread(400), [0x0000] * 200 + [0x8000] * 200)
+    put(1, 1, spread(150), f(np.r_[np.full(50, 1e-35), np.full(50, -1e-35),
+                                  np.full(25, 1e-40), np.full(25, -1e-40)].astype(np.float32)))
+    put(2, 2, in_chunk(10, 8), [0x0F80, 0x8F80, 0x0F7F, 0x8F7F, 0x5D80, 0xDD80, 0x5D81, 0xDD81])
+    put(3, 0, in_chunk(74, 6), f(np.array([-1e25, -3e19, 0.0, -0.0, 1e-38, -np.inf],
+                                          np.float32)))
+    put(4, 3, spread(V // 2), [0xFF80] * (V // 2))  # -inf
+    put(5, 1, in_chunk(0, 4), [0x0000, 0x0001, 0x8001, 0x4780])  # 0, +-min subnormal, 2^16
+    put(6, 0, in_chunk(40, 3), f(np.array([1e30, -1e30, 0.0], np.float32)))
+    return tb
+
+
+@pytest.mark.parametrize("mode", ["reference", "filtered"])
+def test_temperature_division_range_edges(hv, orc, cuda, mode):
+    """x / T where the numerators leave the corrected product's exact range:
+    the chain (row statistics, partial sums, final search), the single launch
+    and the row sampler agree with the oracle bit for bit. Temperatures include
+    1 (no division), 2^-12 and 2^21 (outside the corrected product's divisor
+    range) and ordinary values."""
+    B, gamma = 8, 3
+    print(f"division range edges B={B} gamma={gamma} {mode}", flush=True)
+    rng = np.random.default_rng(2718)
+    w = hv.synthetic.accept_workload(B, gamma, seed=2718, dtype="bf16", mode=mode,
+                                     per_seq_settings=True)
+    tb = _edge_targets(hv, rng, B, gamma)
+    xf = hv.synthetic.bf16_bits_to_f32(tb)
+    temps = w["temperatures"].copy()
+    temps[5], temps[6], temps[7] = 2.0 ** -12, 1.0, 2.0 ** 21
+    lg = torch.from_numpy(tb.view(np.int16)).to(cuda).view(torch.bfloat16)
+    t = _dev(w, cuda, ["draft_probs", "draft_tokens", "u_accept", "u_resample", "top_ks",
+                       "top_ps"])
+    tt = torch.from_numpy(temps).to(cuda)
+    ref = orc.spec_accept(xf, w["draft_probs"], w["draft_tokens"], temps, w["u_accept"],
+                          w["u_resample"], mode=mode, top_ks=w["top_ks"], top_ps=w["top_ps"])
+    for chain in (False, True):
+        r = hv.ops.spec_accept(lg, t["draft_probs"], t["draft_tokens"], tt, t["u_accept"],
+                               t["u_resample"], mode=mode, top_ks=t["top_ks"],
+                               top_ps=t["top_ps"], row_stats=True, chain_only=chain)
+        got = [x.cpu().numpy() for x in r]
+        np.testing.assert_array_equal(got[0], ref["num_accepted"])
+        np.testing.assert_array_equal(got[1], ref["out_tokens"])
+        np.testing.assert_array_equal(got[3].reshape(-1, 2), ref["row_stats"].reshape(-1, 2))
+    rows = B * (gamma + 1)
+    rt = np.repeat(temps, gamma + 1)
+    rk = np.repeat(w["top_ks"], gamma + 1).astype(np.int32)
+    rp = np.repeat(w["top_ps"], gamma + 1).astype(np.float32)
+    u = rng.random(rows).astype(np.float32)
+    s = hv.ops.sample_rows(lg.reshape(rows, V), *[torch.from_numpy(a).to(cuda) for a in (rt, rk, rp)],
+                           mode=mode, uniforms=torch.from_numpy(u).to(cuda), want_probs=True,
+                           row_stats=True)
+    sref = orc.sampler(xf.reshape(rows, V), rt, rk, rp, mode=mode, uniforms=u)
+    np.testing.assert_array_equal(s["probs"].cpu().numpy(), sref["probs"])
+    np.testing.assert_array_equal(s["tokens"].cpu().numpy(), sref["tokens"])
+    np.testing.assert_array_equal(s["row_stats"].cpu().numpy(), sref["row_stats"])
