@@ -436,7 +436,8 @@ __global__ __launch_bounds__(kT) void k_sample_part_w(Problem P, AcceptArgs A, W
   __shared__ SeqState s_st;
   const int unit = blockIdx.y;
   const int split = blockIdx.x;
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: chunk choices too
   const int R = P.rows_per_unit;
   const SeqState st = part_prologue<T>(P, A, W, O, desc_ready, unit, split, s_desc, &s_st);
   const int row = st.row;
@@ -457,24 +458,63 @@ __global__ __launch_bounds__(kT) void k_sample_part_w(Problem P, AcceptArgs A, W
     LaneChunk<float> qr;
     lane_chunk_load<T>(rp, c0, P.V, lane, true, r);
     if (residual) lane_chunk_load<float>(qp, c0, P.V, lane, true, qr);
-    uint32_t whi = 0, wlo = 0, phi = 0, plo = 0;
+    uint32_t whi, wlo, phi, plo;
+    const bool full = c0 + kChunk <= P.V;  // wave-uniform
+    // One pass per element: x = x / T, kept or not (p = 0 outside the kept set
+    // and the row), e * 2^20 = hs_exp_2p20(x - m), p * 2^20 from it, and the
+    // fixed-point sums of p and max(p - q, 0). p * 2^20 = (e * 2^20) / S by the
+    // corrected product equals 2^20 hs_div_rcp(e, S) when e is 0 or in
+    // [2^-96, 1] (the quotient is then normal); a chunk where some e lies in
+    // (0, 2^-96), or whose S or T rule the corrected product out, is summed
+    // with hs_div_temp and hs_div_rcp on e itself. max(p - q, 0) * 2^20 =
+    // max(p * 2^20 - q * 2^20, 0): scaling commutes with the rounding of a
+    // normal difference, and a subnormal difference is exact.
+    auto sums = [&](auto x_of, auto keep_of, auto p20_of) {
+      uint32_t umin = 0xffffffffu;  // min over the lane of bits(e * 2^20) - 1 (0 -> max)
+      phi = plo = whi = wlo = 0;
 #pragma unroll
-    for (int g = 0; g < kLaneChunkGroups; ++g) {
-      const bool in = lane_chunk_idx(c0, g, lane, 0) < P.V;
+      for (int g = 0; g < kLaneChunkGroups; ++g) {
+        const bool in = full || lane_chunk_idx(c0, g, lane, 0) < P.V;
 #pragma unroll
-      for (int k = 0; k < kGroupElems; ++k) {
-        float p = 0.0f;
-        if (in) {
-          const float x = hs_div_temp(lane_chunk_val<T>(r, g, k), Tt, rT, fastT);
-          if (desc_keep(D, hs_key(x), lane_chunk_idx(c0, g, lane, k))) {
-            const float e = hs_exp(x - D.m);
-            p = fastS ? hs_div_rcp(e, D.s, rS) : e / D.s;
+        for (int k = 0; k < kGroupElems; ++k) {
+          const float x = x_of(lane_chunk_val<T>(r, g, k));
+          const bool kept = in && keep_of(x, lane_chunk_idx(c0, g, lane, k));
+          const float ev = hs_exp_2p20(x - D.m);  // computed for every lane: no branch
+          const float e20 = kept ? ev : 0.0f;
+          const uint32_t u = f2u(e20) - 1u;
+          umin = u < umin ? u : umin;
+          const float p20 = p20_of(e20);
+          hs_fx44_acc(p20, phi, plo);
+          if (residual)
+            hs_fx44_acc(fmaxf(p20 - lane_chunk_val<float>(qr, g, k) * 1048576.0f, 0.0f), whi,
+                        wlo);
+          // running sums taken every 4 elements (see chunk_stats_wave), and
+          // no more than 4 elements' work interleaved (register pressure)
+          if (k % 4 == 3) {
+            asm volatile("" : "+v"(phi), "+v"(plo), "+v"(whi), "+v"(wlo), "+v"(umin));
+            __builtin_amdgcn_sched_barrier(0);
           }
         }
-        hs_fx44_split(p, phi, plo);
-        if (residual) hs_fx44_split(fmaxf(p - lane_chunk_val<float>(qr, g, k), 0.0f), whi, wlo);
       }
+      return __builtin_amdgcn_ballot_w64(umin < f2u(0x1p-76f) - 1u) == 0;
+    };
+    auto p20_fast = [&](float e20) { return hs_div_rcp_in_range(e20, D.s, rS); };
+    auto keep_all = [](float, int64_t) { return true; };
+    auto keep_desc = [&](float x, int64_t i) { return desc_keep(D, hs_key(x), i); };
+    auto x_same = [](float v) { return v; };
+    auto x_rcp = [&](float v) { return hs_div_rcp_in_range(v, Tt, rT); };
+    bool ok = false;
+    if (fastS) {
+      if (Tt == 1.0f)
+        ok = D.all ? sums(x_same, keep_all, p20_fast) : sums(x_same, keep_desc, p20_fast);
+      else if (fastT && __builtin_amdgcn_ballot_w64(!lane_chunk_rcp_ok<T>(r)) == 0)
+        ok = D.all ? sums(x_rcp, keep_all, p20_fast) : sums(x_rcp, keep_desc, p20_fast);
     }
+    if (!ok)
+      sums([&](float v) { return hs_div_temp(v, Tt, rT, fastT); }, keep_desc, [&](float e20) {
+        const float e = e20 * 0x1p-20f;
+        return (fastS ? hs_div_rcp(e, D.s, rS) : e / D.s) * 1048576.0f;
+      });
     const uint64_t sw = wave_sum_u64(hs_join44(whi, wlo));
     const uint64_t sp = wave_sum_u64(hs_join44(phi, plo));
     if (lane == 0) {
