@@ -992,6 +992,32 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
 }
 
 // Top-p rows with 16-byte aligned rows and V % 8 == 0: the work of
+// hs_div_temp(v, T, 1/T, fast) for one queued element per lane: the
+// corrected product for every lane, then the IEEE quotient for the lanes whose
+// numerator lies outside [2^-96, 2^60] (a branch the wave takes only when one
+// of its lanes has such a value). T is the same in every lane.
+__device__ __forceinline__ float drain_div_temp(float v, float Tt, float rT, bool fast) {
+  if (Tt == 1.0f) return v;
+  if (!fast) return v / Tt;
+  float x = hs_div_rcp_in_range(v, Tt, rT);
+  const bool out = ((f2u(v) << 1) + 0xE1000000u) > 0x9C000000u;  // see lane_chunk_rcp_ok
+  if (__builtin_amdgcn_ballot_w64(out) != 0 && out) x = v / Tt;
+  return x;
+}
+
+// (e / S) * 2^20 given e20 = e * 2^20 (hs_exp_2p20), equal to
+// 2^20 hs_div_temp(e, S, 1/S, fastS): the corrected product on e20 when e is
+// 0 or in [2^-96, 1] (the quotient is then normal), else hs_div_rcp on e
+// (lanes of a wave taking that branch only when one of its lanes needs it).
+__device__ __forceinline__ float drain_p20(float e20, float S, float rS, bool fastS) {
+  if (!fastS) return (e20 * 0x1p-20f / S) * 1048576.0f;
+  float p20 = hs_div_rcp_in_range(e20, S, rS);
+  const bool small = f2u(e20) - 1u < f2u(0x1p-76f) - 1u;  // e20 in (0, 2^-76)
+  if (__builtin_amdgcn_ballot_w64(small) != 0 && small)
+    p20 = hs_div_rcp(e20 * 0x1p-20f, S, rS) * 1048576.0f;
+  return p20;
+}
+
 // k_filter_pass1 for mode-2 rows with one wave per chunk of the workgroup's
 // segment, so that each wave has the chunk's four 1 KB (bf16) or 2 KB (f32)
 // loads in flight together (lane_chunk_load); the histogram accumulates in LDS
@@ -1030,15 +1056,19 @@ __device__ __forceinline__ void pass1_w_body(const Problem& P, const Work& W, in
       // the queue is this wave's: its LDS writes land before its reads
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       for (uint32_t j = (uint32_t)lane; j < nq; j += kWave) {
-        const float xv = hs_div_temp(q[j], Tt, rT, fast);
+        const float v = q[j];
+        const float xv = drain_div_temp(v, Tt, rT, fast);
         const int b = coarse_bucket(xv, M);
         // count and mass in one word (kPackShift): the masses of a row sum to
         // at most 2^44 (1 + 1e-5), a segment holds fewer than 2^19 elements
         uint64_t cm = 1ull << kPackShift;
         if (b < kCB - 1) {  // the last bucket holds only zero masses
-          const float e = hs_exp(xv - M);
-          const uint64_t em = hs_fx44(e);
-          cm += hs_fx44(hs_div_temp(e, S, rS, fastS));
+          const float e20 = hs_exp_2p20(xv - M);  // hs_exp * 2^20
+          uint32_t eh = 0, el = 0, ph = 0, pl = 0;
+          hs_fx44_acc(e20, eh, el);  // hs_fx44(e)
+          hs_fx44_acc(drain_p20(e20, S, rS, fastS), ph, pl);  // hs_fx44(e / S)
+          const uint64_t em = hs_join44(eh, el);
+          cm += hs_join44(ph, pl);
           if (em) atomicAdd((unsigned long long*)&ps.he[b], (unsigned long long)em);
         }
         atomicAdd((unsigned long long*)&ps.hm[b], (unsigned long long)cm);
@@ -1148,7 +1178,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
       for (uint32_t j0 = 0; j0 < nq; j0 += kWave) {
         const uint32_t j = j0 + (uint32_t)lane;
         const bool have = j < nq;
-        const float xv = have ? hs_div_temp(qv[j], Tt, rT, fast) : 0.0f;
+        const float xv = have ? drain_div_temp(qv[j], Tt, rT, fast) : 0.0f;
         const uint32_t idx = have ? qi[j] : 0u;
         if (listed) {
           if (nb > kCandBuf - kWave) flush();
@@ -1160,10 +1190,13 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
         }
         if (fine && have) {
           const int b = fine_bucket(xv, M, b1);
-          const float e = hs_exp(xv - M);
+          const float e20 = hs_exp_2p20(xv - M);  // hs_exp * 2^20
           atomicAdd(&ps.hc[b], 1u);
-          const uint64_t mm = hs_fx44(hs_div_temp(e, S, rS, fastS));
-          const uint64_t em = hs_fx44(e);
+          uint32_t eh = 0, el = 0, ph = 0, pl = 0;
+          hs_fx44_acc(e20, eh, el);                           // hs_fx44(e)
+          hs_fx44_acc(drain_p20(e20, S, rS, fastS), ph, pl);  // hs_fx44(e / S)
+          const uint64_t mm = hs_join44(ph, pl);
+          const uint64_t em = hs_join44(eh, el);
           if (mm) atomicAdd((unsigned long long*)&ps.hm[b], (unsigned long long)mm);
           if (em) atomicAdd((unsigned long long*)&ps.he[b], (unsigned long long)em);
         }
