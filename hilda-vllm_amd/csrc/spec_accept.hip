@@ -154,24 +154,30 @@ __device__ __forceinline__ void chunk_stats_wave(const Problem& P, const Work& W
     cs.e = e;
     W.part[it] = cs;
   }
-  if (P.filtered && c == 0) {
-    // the filter passes accumulate into these (kernel order: this launch first)
-    for (int i = lane; i < kCB; i += kWave) {
-      const int64_t hb = (int64_t)row * kCB + i;
-      W.h1m[hb] = 0ull;
-      W.h1e[hb] = 0ull;
-      W.h1c[hb] = 0u;
-      W.h2m[hb] = 0ull;
-      W.h2e[hb] = 0ull;
-      W.h2c[hb] = 0u;
-    }
-    if (lane == 0) W.filt[row].ncand = 0;
-    if (lane == 0 && row == 0) W.flist[0] = W.flist[1] = 0;
+}
+
+// The filter passes accumulate into these (kernel order: this launch first);
+// the wave of a row's first chunk clears them, before it loads the chunk (no
+// statistics registers are live then).
+__device__ __forceinline__ void clear_filter_row(const Problem& P, const Work& W, int64_t it,
+                                                 int lane) {
+  const int row = (int)(it / P.nchunk);
+  if (!P.filtered || it - (int64_t)row * P.nchunk != 0) return;
+  for (int i = lane; i < kCB; i += kWave) {
+    const int64_t hb = (int64_t)row * kCB + i;
+    W.h1m[hb] = 0ull;
+    W.h1e[hb] = 0ull;
+    W.h1c[hb] = 0u;
+    W.h2m[hb] = 0ull;
+    W.h2e[hb] = 0ull;
+    W.h2c[hb] = 0u;
   }
+  if (lane == 0) W.filt[row].ncand = 0;
+  if (lane == 0 && row == 0) W.flist[0] = W.flist[1] = 0;
 }
 
 template <typename T>
-__global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(8))) void k_chunk_stats_w(Problem P, Work W) {
+__global__ __launch_bounds__(kT) void k_chunk_stats_w(Problem P, Work W) {
   const int lane = threadIdx.x & 63;
   // the wave index is uniform across the wave: kept in a scalar register, the
   // chunk, row and temperature are too, and the branches on them are uniform
@@ -191,6 +197,7 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(8))) void k_
   // resident waves hide a wave's load latency, which measured faster than
   // holding the next chunk in flight (80 VGPRs, 6 waves per SIMD).
   for (; it < items; it += stride) {
+    clear_filter_row(P, W, it, lane);
     LaneChunk<T> a;
     load(it, a);
     chunk_stats_wave<T>(P, W, it, a, lane);
