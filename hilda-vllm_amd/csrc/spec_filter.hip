@@ -1001,7 +1001,12 @@ __device__ __forceinline__ float drain_div_temp(float v, float Tt, float rT, boo
   if (!fast) return v / Tt;
   float x = hs_div_rcp_in_range(v, Tt, rT);
   const bool out = ((f2u(v) << 1) + 0xE1000000u) > 0x9C000000u;  // see lane_chunk_rcp_ok
-  if (__builtin_amdgcn_ballot_w64(out) != 0 && out) x = v / Tt;
+  if (__builtin_amdgcn_ballot_w64(out) != 0 && out) {
+    // a side effect the compiler cannot move: a division is one IR instruction,
+    // which it otherwise evaluates for every lane and selects
+    asm volatile("" : "+v"(v));
+    x = v / Tt;
+  }
   return x;
 }
 
