@@ -1129,7 +1129,12 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
   // atomic per kCandBuf / 2 of them (an atomic that returns costs a memory
   // round trip, which per chunk was most of the pass)
   __shared__ uint64_t s_cb[kPT / kWave][kCandBuf];
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
+  // the wave index in a scalar register and the thread index rebuilt from it
+  // and the lane: kept whole through the segment loop, threadIdx.x was the
+  // value spilled (8 bytes per lane at entry) under the 64-VGPR cap
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int tid = wid * kWave + lane;
   const int rows = P.units * P.rows_per_unit;
   const SegPlan sp = seg_plan(P, W.flist[1], (int)gridDim.x);  // top-p rows only
   float* qv = s_qv[wid];
