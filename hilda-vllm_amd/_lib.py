@@ -76,6 +76,10 @@ SIGNATURES.update({
     "hs_qk_norm_rope_store": (_i32, [_vp, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _f32, _vp,
                                      _vp, _vp, _i32, _i64, _i64, _i64, _f32, _f32, _vp, _i32,
                                      _i32, _i32, _vp]),
+    "hs_qk_norm_rope_attend": (_i32, [_vp, _i64, _i32, _vp, _vp, _vp, _i32, _vp, _f32, _vp, _vp,
+                                      _vp, _vp, _i32, _i64, _i64, _i64, _f32, _f32, _vp, _i64,
+                                      _i32, _i32, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32,
+                                      _i32, _f32, _vp, _i64, _i64, _vp, _sz, _vp]),
 })
 
 _lib = None

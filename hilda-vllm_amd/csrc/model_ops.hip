@@ -19,16 +19,9 @@
 
 #include "../../include/hilda_spec.h"
 #include "hs_fp8.h"
+#include "hs_model_dev.h"
 
 namespace hs {
-
-__device__ __forceinline__ float bf(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
-// f32 -> bf16, round to nearest even
-__device__ __forceinline__ uint16_t to_bf(float f) {
-  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));  // v_cvt_pk_bf16_f32 (RNE)
-}
-// bf16 * bf16 rounded to bf16 (the product is exact in fp32)
-__device__ __forceinline__ uint16_t bf_mul(uint16_t a, uint16_t b) { return to_bf(bf(a) * bf(b)); }
 
 constexpr int kNT = 256;
 
@@ -96,25 +89,6 @@ __global__ __launch_bounds__(kNT) void k_rmsnorm(const uint16_t* __restrict__ x,
   }
 }
 
-// RMSNorm (layernorm.py:18-25: normalise in fp32, round, multiply by the
-// weight) and neox RoPE (rotary_embedding.py:8-16, cos/sin cache [pos, 64 | 64])
-// of one 128-wide head held as the pair (l, l + 64) by lane l; returns the
-// rotated pair rounded to bf16
-__device__ __forceinline__ void norm_rope_pair(const uint16_t* src, const uint16_t* w,
-                                               const float* cs, float eps, int lane,
-                                               uint16_t& o1, uint16_t& o2) {
-  float x1 = bf(src[lane]), x2 = bf(src[lane + 64]);
-  float ss = x1 * x1 + x2 * x2;
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-  const float inv = rsqrtf(ss / 128.0f + eps);
-  x1 = bf(bf_mul(to_bf(x1 * inv), w[lane]));
-  x2 = bf(bf_mul(to_bf(x2 * inv), w[lane + 64]));
-  const float c = cs[lane], s = cs[64 + lane];
-  o1 = to_bf(x1 * c - x2 * s);
-  o2 = to_bf(x2 * c + x1 * s);
-}
-
 // one wave per (token, head); heads [0, Hq) are q, [Hq, Hq+Hkv) are k
 __global__ __launch_bounds__(kNT) void k_qk_norm_rope(const uint16_t* __restrict__ qkv, int64_t ts,
                                                       int Hq, int Hkv,
@@ -155,19 +129,6 @@ struct NormRopeStoreArgs {
   const int32_t* slots;
   int block_size, num_blocks, N;
 };
-
-template <bool kFp8>
-__device__ __forceinline__ void store_pair(uint8_t* base, int64_t elem, int lane, uint16_t a,
-                                           uint16_t b, float scale) {
-  if constexpr (kFp8) {
-    base[elem + lane] = f32_to_e4m3fn_sat(bf(a) / scale);
-    base[elem + lane + 64] = f32_to_e4m3fn_sat(bf(b) / scale);
-  } else {
-    uint16_t* p = reinterpret_cast<uint16_t*>(base) + elem;
-    p[lane] = a;
-    p[lane + 64] = b;
-  }
-}
 
 // one wave per (token, head) over the q, k and v heads of the fused qkv row:
 // q heads are normalised, rotated and written to qo; k heads are normalised,

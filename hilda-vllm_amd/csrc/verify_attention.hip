@@ -33,6 +33,7 @@
 #include <mutex>
 
 #include "../../include/hilda_spec.h"
+#include "hs_model_dev.h"
 
 namespace hs {
 
@@ -72,6 +73,24 @@ struct AttnArgs {
   int* sk_w0;                // balanced launch: first window of each workgroup [nwg + 1]
   int sk_nwg;                // balanced launch: workgroups
   int xcd_pack;              // per-tile grid: only workgroups x % xcd_pack == 0 work
+};
+
+// The q/k-norm + RoPE + KV-store step run inside the per-tile kernel
+// (k_verify_attn_qkv): the fused qkv rows of the call's tokens (token-major,
+// the sequences' query tokens in cu_seqlens_q order), the norm weights, the
+// RoPE table and the tokens' positions and cache slots.
+struct QkvArgs {
+  const uint16_t* qkv;
+  int64_t ts;                // qkv token stride (elements)
+  const uint16_t* qw;
+  const uint16_t* kw;
+  const float* cos_sin;      // [max_position, 128]: cos | sin
+  const int64_t* positions;
+  const int32_t* slots;
+  float eps;
+  float k_scale, v_scale;    // store scales (fp8 caches)
+  int Hq;
+  int cs_rows;               // rows of cos_sin
 };
 
 // block of a key position: a shift for power-of-two block sizes, a division
@@ -244,6 +263,113 @@ struct WaveAcc {
   f32x4_t oacc[8];
 };
 
+// The q/k-norm + RoPE + KV store of one (sequence, kv head) tile, by all the
+// workgroup's waves, each item one head in norm_rope_pair's layout (lane l
+// holds dims l and l + 64, so the bits equal hs_qk_norm_rope_store's): the
+// kv head's k and v rows of the sequence's query tokens go to their cache
+// slots (slots < 0 and blocks past num_blocks store nothing), the tile's q
+// rows to s_q (16 rows x 128 bf16). The host runs this only when one
+// workgroup holds every query row of the (sequence, kv head), so no other
+// workgroup reads these rows.
+// qkv_load issues every load of the wave's items (it = wid + kAW i, the k/v
+// tokens first so their stores go out first) at kernel start; the cos/sin
+// row is fetched at the position the token holds in its sequence
+// (Lk - Lq + i, clamped into the table) together with positions[], and
+// fetched again in qkv_finish where positions[] says otherwise. qkv_finish
+// computes and stores, waits for the stores and ends at a workgroup barrier.
+constexpr int kQkvItems = 4;  // up to 32 items: 16 q rows and at most 16 tokens
+struct QkvLoads {
+  int nrows, nitems;
+  int64_t pos[kQkvItems];
+  int guess[kQkvItems], slot[kQkvItems];
+  uint16_t x1[kQkvItems], x2[kQkvItems], w1[kQkvItems], w2[kQkvItems];
+  uint16_t v1[kQkvItems], v2[kQkvItems];
+  float c[kQkvItems], sn[kQkvItems];
+};
+
+__device__ __forceinline__ void qkv_load(const AttnArgs& a, const QkvArgs& qa, const TileRef& t,
+                                         int kvh, int G, QkvLoads& L) {
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r0 = t.qt * kRows;
+  L.nrows = t.rows - r0 < kRows ? t.rows - r0 : kRows;
+  L.nitems = t.Lq + L.nrows;  // k/v of each query token, then the q rows
+  // a zero the compiler cannot see as uniform: the slot loads stay vector
+  // loads whose values are not moved to scalar registers at once (which would
+  // wait for each item's loads before the next item's are issued)
+  int vzero;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(vzero));
+#pragma unroll
+  for (int i = 0; i < kQkvItems; ++i) {
+    const int it = wid + kAW * i;
+    L.slot[i] = -1;
+    if (it < L.nitems) {
+      const bool iskv = it < t.Lq;
+      const int r = r0 + (it - t.Lq);
+      const int qi = iskv ? it : r / G;
+      const int tok = t.qs + qi;
+      const int head = iskv ? qa.Hq + kvh : kvh * G + r % G;
+      const uint16_t* src = qa.qkv + (int64_t)tok * qa.ts + (int64_t)head * kD;
+      const uint16_t* w = iskv ? qa.kw : qa.qw;
+      int g = t.Lk - t.Lq + qi;
+      g = g < 0 ? 0 : (g >= qa.cs_rows ? qa.cs_rows - 1 : g);
+      L.guess[i] = g;
+      L.pos[i] = qa.positions[tok];
+      L.x1[i] = src[lane];
+      L.x2[i] = src[lane + 64];
+      L.w1[i] = w[lane];
+      L.w2[i] = w[lane + 64];
+      const float* cs = qa.cos_sin + (int64_t)g * kD;
+      L.c[i] = cs[lane];
+      L.sn[i] = cs[64 + lane];
+      if (iskv) {
+        L.slot[i] = qa.slots[tok + vzero];
+        const uint16_t* vs = src + (int64_t)a.Hkv * kD;
+        L.v1[i] = vs[lane];
+        L.v2[i] = vs[lane + 64];
+      }
+    }
+  }
+}
+
+template <bool kFp8>
+__device__ __forceinline__ void qkv_finish(const AttnArgs& a, const QkvArgs& qa, const TileRef& t,
+                                           int kvh, QkvLoads& L, uint16_t* s_q) {
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  uint8_t* kc = const_cast<uint8_t*>(a.kc);
+  uint8_t* vc = const_cast<uint8_t*>(a.vc);
+#pragma unroll
+  for (int i = 0; i < kQkvItems; ++i) {
+    const int it = wid + kAW * i;
+    if (it >= L.nitems) break;
+    if (L.pos[i] != L.guess[i]) {  // the token sits elsewhere than its key index
+      const float* cs = qa.cos_sin + L.pos[i] * kD;
+      L.c[i] = cs[lane];
+      L.sn[i] = cs[64 + lane];
+    }
+    uint16_t y1, y2;
+    norm_rope_vals(bf(L.x1[i]), bf(L.x2[i]), L.w1[i], L.w2[i], L.c[i], L.sn[i], qa.eps, y1, y2);
+    if (it >= t.Lq) {
+      const int row = it - t.Lq;
+      s_q[row * kD + lane] = y1;
+      s_q[row * kD + lane + 64] = y2;
+    } else if (L.slot[i] >= 0) {
+      // store_kvcache semantics: slots < 0 and blocks past num_blocks store nothing
+      const int blk = L.slot[i] / a.block_size, off = L.slot[i] % a.block_size;
+      if (blk < a.num_blocks) {
+        const int64_t elem = (int64_t)blk * a.c_sb + (int64_t)off * a.c_st + (int64_t)kvh * a.c_sh;
+        store_pair<kFp8>(kc, elem, lane, y1, y2, qa.k_scale);
+        store_pair<kFp8>(vc, elem, lane, L.v1[i], L.v2[i], qa.v_scale);
+      }
+    }
+  }
+  // the cache stores have reached the L2 before any wave of the workgroup
+  // loads those rows (their lines were not read by this workgroup before)
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+}
+
 // Walks keys [lo, hi) of query tile t (hi clipped to the keys the tile's
 // last row sees) against kv head kvh in this wave: 32-key windows ws0,
 // ws0 + step, ... below hi, the next window's K/V rows in flight while the
@@ -252,10 +378,16 @@ struct WaveAcc {
 // block lo / block_size on, up to bt_cap of them, filled by the caller.
 // kG: query heads per KV head as a compile-time constant (2, 4 or 8), or 0 to
 // read it from the arguments (any other group size).
-template <bool kFp8, int kG>
+// kQkv: the tile's q rows and its new k/v rows are made here from the loads
+// the kernel issued at its start (qkv_finish, after the s_bt barrier): a
+// first window holding only earlier keys is issued before, one reaching the
+// sequence's query tokens after it.
+template <bool kFp8, int kG, bool kQkv = false>
 __device__ __forceinline__ void wave_walk(const AttnArgs& a, const TileRef& t, int kvh, int lo,
                                           int hi, int ws0, int step, const int* s_bt, int bt_cap,
-                                          uint8_t* tile_k, uint8_t* tile_v, WaveAcc& acc) {
+                                          uint8_t* tile_k, uint8_t* tile_v, WaveAcc& acc,
+                                          const QkvArgs* qa = nullptr, QkvLoads* ql = nullptr,
+                                          uint16_t* s_q = nullptr) {
   const int G = kG ? kG : a.G;
   constexpr int kRowB = AttnLds<kFp8>::kRowB;
   const int qs = t.qs, Lq = t.Lq, Lk = t.Lk, rows = t.rows;
@@ -273,13 +405,16 @@ __device__ __forceinline__ void wave_walk(const AttnArgs& a, const TileRef& t, i
   const int qh = kvh * G + (r_ok ? r % G : 0);
   const int lim_r = Lk - Lq + qi;  // last visible key of this row
   bf16x8_t qv[4];
+  if constexpr (!kQkv) {
 #pragma unroll
-  for (int ds = 0; ds < 4; ++ds) {
-    if (r_ok) {
-      const uint16_t* qp = a.q + (int64_t)(qs + qi) * a.q_st + (int64_t)qh * a.q_sh + ds * 32 + g * 8;
-      qv[ds] = u4_to_bf16x8(*reinterpret_cast<const uint4*>(qp));
-    } else {
-      qv[ds] = u4_to_bf16x8(make_uint4(0, 0, 0, 0));
+    for (int ds = 0; ds < 4; ++ds) {
+      if (r_ok) {
+        const uint16_t* qp =
+            a.q + (int64_t)(qs + qi) * a.q_st + (int64_t)qh * a.q_sh + ds * 32 + g * 8;
+        qv[ds] = u4_to_bf16x8(*reinterpret_cast<const uint4*>(qp));
+      } else {
+        qv[ds] = u4_to_bf16x8(make_uint4(0, 0, 0, 0));
+      }
     }
   }
 
@@ -306,10 +441,24 @@ __device__ __forceinline__ void wave_walk(const AttnArgs& a, const TileRef& t, i
 
   int ws = ws0;
   bool have = false;
-  if (ws < hi) {
+  // kQkv: keys from Lk - Lq on are the query tokens' own, stored by the prologue
+  const bool early = !kQkv || (ws + kWin < hi ? ws + kWin : hi) <= Lk - Lq;
+  if (ws < hi && early) {
     const uint8_t *kb, *vb;
     have = window_base(ws, kb, vb);
     if (have) issue_window<kFp8>(a, kb, vb, ws, hi, tile_k, tile_v, lane);
+  }
+  if constexpr (kQkv) {
+    qkv_finish<kFp8>(a, *qa, t, kvh, *ql, s_q);
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds)
+      qv[ds] = r_ok ? u4_to_bf16x8(*reinterpret_cast<const uint4*>(s_q + n * kD + ds * 32 + g * 8))
+                    : u4_to_bf16x8(make_uint4(0, 0, 0, 0));
+    if (ws < hi && !early) {
+      const uint8_t *kb, *vb;
+      have = window_base(ws, kb, vb);
+      if (have) issue_window<kFp8>(a, kb, vb, ws, hi, tile_k, tile_v, lane);
+    }
   }
   while (ws < hi) {
     const int ws_next = ws + step;
@@ -462,10 +611,12 @@ __device__ __forceinline__ void merge_waves(const float (*s_m)[kRows], const flo
 // normalised output (pslot < 0) or the unnormalised partial (o, running max,
 // sum) at partial slot pslot. s_bt as for wave_walk. s_raw holds the per-wave
 // K and V window tiles and, after the key loop, the per-wave partial outputs.
-template <bool kFp8, int kG>
+template <bool kFp8, int kG, bool kQkv = false>
 __device__ __forceinline__ void attend_keys(const AttnArgs& a, const TileRef& t, int klo, int khi,
                                             int64_t pslot, uint8_t* s_raw, float (*s_m)[kRows],
-                                            float (*s_l)[kRows], const int* s_bt, int bt_cap) {
+                                            float (*s_l)[kRows], const int* s_bt, int bt_cap,
+                                            const QkvArgs* qa = nullptr,
+                                            QkvLoads* ql = nullptr, uint16_t* s_q = nullptr) {
   const int G = kG ? kG : a.G;
   constexpr int kTileB = AttnLds<kFp8>::kTileB;
   const int kvh = t.kvh, qs = t.qs, rows = t.rows;
@@ -475,8 +626,8 @@ __device__ __forceinline__ void attend_keys(const AttnArgs& a, const TileRef& t,
   uint8_t* tile_k = s_raw + wid * 2 * kTileB;
   uint8_t* tile_v = tile_k + kTileB;
   WaveAcc acc;
-  wave_walk<kFp8, kG>(a, t, kvh, klo, khi, klo + wid * kWin, kAW * kWin, s_bt, bt_cap, tile_k,
-                      tile_v, acc);
+  wave_walk<kFp8, kG, kQkv>(a, t, kvh, klo, khi, klo + wid * kWin, kAW * kWin, s_bt, bt_cap,
+                            tile_k, tile_v, acc, qa, ql, s_q);
   // waves that hold keys (wave w starts at klo + 32w): the others have nothing
   // to merge
   const int nkeys = khi - klo;
@@ -610,6 +761,45 @@ __global__ __launch_bounds__(kAT) void k_verify_attn(const int32_t* cu_q, const 
   const int64_t pslot =
       t.Lk <= split_len ? -1 : (((int64_t)b * a.Hkv + kvh) * qtiles + qt) * a.nsplit + split;
   attend_keys<kFp8, kG>(a, t, lo, hi, pslot, s_raw, s_m, s_l, s_bt, kBtCap);
+}
+
+// k_verify_attn with the q/k-norm + RoPE + KV-store step of its tile's tokens
+// in the prologue (qkv_load at the start, qkv_finish after the block-table
+// barrier): the host launches it only where every
+// (sequence, kv head) is one workgroup (one query tile, no key split), which
+// then alone writes and reads its new k/v rows. Replaces hs_qk_norm_rope_store
+// + hs_verify_attention (two launches) for decode and verify steps.
+template <bool kFp8, int kG>
+__global__ __launch_bounds__(kAT) void k_verify_attn_qkv(const int32_t* cu_q, const int32_t* cu_k,
+                                                         const int32_t* bt, int bt_stride,
+                                                         int xcd_shift, int bs_shift,
+                                                         int bt_width, int nbt_split, AttnArgs a,
+                                                         QkvArgs qa) {
+  __shared__ __attribute__((aligned(16))) uint8_t s_raw[AttnLds<kFp8>::kRawBytes];
+  __shared__ float s_m[kAW][kRows], s_l[kAW][kRows];
+  __shared__ int s_bt[kBtCap];
+  __shared__ __attribute__((aligned(16))) uint16_t s_q[kRows * kD];
+  const int G = kG ? kG : a.G;
+  if (blockIdx.x & ((1u << xcd_shift) - 1)) return;
+  const int kvh = blockIdx.x >> xcd_shift;
+  const int b = blockIdx.z;
+  const int tid = threadIdx.x;
+  const int cq0 = cu_q[b], cq1 = cu_q[b + 1], ck0 = cu_k[b], ck1 = cu_k[b + 1];
+  int nbt = nbt_split;
+  if (nbt > bt_width) nbt = bt_width;
+  const int32_t* btrow = bt + (int64_t)b * bt_stride;
+  const int bi = tid < bt_width ? tid : bt_width - 1;
+  const int bt_mine = btrow[bi];
+  asm volatile("" ::"s"(a.q), "s"(a.c_sh), "s"(a.scale_log2), "s"(a.sk_pre));
+  asm volatile("" ::"v"(bt_mine), "v"(cq0), "v"(cq1), "v"(ck0), "v"(ck1));
+  const TileRef t = tile_ref_of(b, kvh, 0, G, cq0, cq1, ck0, ck1);
+  if (tid < nbt) s_bt[tid] = bt_mine;
+  for (int i = tid + kAT; i < nbt; i += kAT) s_bt[i] = btrow[i];
+  if (t.rows <= 0 || t.Lk <= 0) return;  // no query token: nothing to store or attend
+  QkvLoads ql;
+  qkv_load(a, qa, t, kvh, G, ql);
+  attend_keys<kFp8, kG, true>(a, t, 0, tile_keys(t, G), -1, s_raw, s_m, s_l, s_bt, kBtCap, &qa,
+                              &ql, s_q);
 }
 
 // Balanced launch: one workgroup per CU. The 32-key windows of all tiles
@@ -919,6 +1109,24 @@ static void launch_attn(int G, dim3 grid, hipStream_t s, const AttnArgs& a) {
   }
 }
 
+template <bool kFp8>
+static void launch_attn_qkv(int G, dim3 grid, hipStream_t s, const AttnArgs& a, const QkvArgs& qa) {
+  const int bts = (int)a.bt_stride;
+  const int xs = a.xcd_pack == 8 ? 3 : 0;
+  int nbt = (a.split_len + a.block_size - 1) / a.block_size + 1;
+  if (nbt > kBtCap) nbt = kBtCap;
+  switch (G) {
+    case 2: hipLaunchKernelGGL((k_verify_attn_qkv<kFp8, 2>), grid, dim3(kAT), 0, s, a.cu_q, a.cu_k, a.bt,
+                                 bts, xs, a.bs_shift, a.bt_width, nbt, a, qa); break;
+    case 4: hipLaunchKernelGGL((k_verify_attn_qkv<kFp8, 4>), grid, dim3(kAT), 0, s, a.cu_q, a.cu_k, a.bt,
+                                 bts, xs, a.bs_shift, a.bt_width, nbt, a, qa); break;
+    case 8: hipLaunchKernelGGL((k_verify_attn_qkv<kFp8, 8>), grid, dim3(kAT), 0, s, a.cu_q, a.cu_k, a.bt,
+                                 bts, xs, a.bs_shift, a.bt_width, nbt, a, qa); break;
+    default: hipLaunchKernelGGL((k_verify_attn_qkv<kFp8, 0>), grid, dim3(kAT), 0, s, a.cu_q, a.cu_k, a.bt,
+                                  bts, xs, a.bs_shift, a.bt_width, nbt, a, qa); break;
+  }
+}
+
 template <bool kFp8, bool kHeads>
 static void launch_attn_sk(int G, int nwg, hipStream_t s, const AttnArgs& a) {
   switch (G) {
@@ -1018,36 +1226,20 @@ static void* scratch_of_current_device() {
 
 using namespace hs;
 
-extern "C" {
-
-size_t hs_verify_attention_workspace_size(int num_seqs, int num_q_heads, int num_kv_heads,
-                                          int max_seqlen_q, int max_seqlen_k) {
-  if (num_seqs <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 || max_seqlen_q <= 0 ||
-      max_seqlen_k <= 0 || num_q_heads % num_kv_heads)
-    return 0;
-  const int G = num_q_heads / num_kv_heads;
-  const int qtiles = (max_seqlen_q * G + kRows - 1) / kRows;
-  int nsplit, split_len;
-  attn_plan(num_seqs, num_kv_heads, qtiles, max_seqlen_k, &nsplit, &split_len);
-  const size_t parts = (size_t)num_seqs * num_kv_heads * qtiles * nsplit * kRows;
-  const size_t classic = parts * kD * sizeof(float) + parts * 2 * sizeof(float) + 256;
-  bool heads = false;
-  const int nwg = attn_sk_plan(num_seqs, num_kv_heads, qtiles, max_seqlen_k, &heads);
-  const size_t sk = nwg ? attn_sk_workspace(num_seqs, num_kv_heads, qtiles, nwg, heads) : 0;
-  return classic > sk ? classic : sk;
-}
-
-int hs_verify_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+// Argument checks and the launch plan shared by hs_verify_attention and
+// hs_qk_norm_rope_attend: fills *pa (everything but the partial-result
+// pointers) and *pneed (the workspace size of the call).
+static int attn_prepare(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
                         const void* k_cache, const void* v_cache, int kv_dtype,
                         int64_t cache_stride_block, int64_t cache_stride_tok,
                         int64_t cache_stride_head, float k_scale, float v_scale,
                         const int32_t* block_tables, int64_t block_table_stride,
-                        int block_table_width, int num_blocks,
-                        const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int num_seqs,
-                        int max_seqlen_q, int max_seqlen_k, int num_q_heads, int num_kv_heads,
-                        int head_dim, int block_size, float softmax_scale, void* out,
-                        int64_t out_stride_tok, int64_t out_stride_head, void* workspace,
-                        size_t workspace_bytes, void* stream) {
+                        int block_table_width, int num_blocks, const int32_t* cu_seqlens_q,
+                        const int32_t* cu_seqlens_k, int num_seqs, int max_seqlen_q,
+                        int max_seqlen_k, int num_q_heads, int num_kv_heads, int head_dim,
+                        int block_size, float softmax_scale, void* out, int64_t out_stride_tok,
+                        int64_t out_stride_head, void* workspace, size_t workspace_bytes,
+                        AttnArgs* pa, size_t* pneed) {
   if (!q || !k_cache || !v_cache || !block_tables || !cu_seqlens_q || !cu_seqlens_k || !out)
     return HS_ERR_INVALID;
   if (num_seqs <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || max_seqlen_q <= 0 ||
@@ -1069,9 +1261,9 @@ int hs_verify_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_he
     return HS_ERR_UNSUPPORTED;
   if (((uintptr_t)q | (uintptr_t)out | (uintptr_t)k_cache | (uintptr_t)v_cache) & 15)
     return HS_ERR_UNSUPPORTED;
-  const size_t need = hs_verify_attention_workspace_size(num_seqs, num_q_heads, num_kv_heads,
+  const size_t need = *pneed = hs_verify_attention_workspace_size(num_seqs, num_q_heads, num_kv_heads,
                                                          max_seqlen_q, max_seqlen_k);
-  AttnArgs a;
+  AttnArgs& a = *pa;
   a.qtiles = (max_seqlen_q * G + kRows - 1) / kRows;
   attn_plan(num_seqs, num_kv_heads, a.qtiles, max_seqlen_k, &a.nsplit, &a.split_len);
   if (a.nsplit > 1 && (!workspace || workspace_bytes < need)) return HS_ERR_WORKSPACE;
@@ -1102,6 +1294,50 @@ int hs_verify_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_he
   a.out = static_cast<uint16_t*>(out);
   a.o_st = out_stride_tok;
   a.o_sh = out_stride_head;
+  return HS_OK;
+}
+
+extern "C" {
+
+size_t hs_verify_attention_workspace_size(int num_seqs, int num_q_heads, int num_kv_heads,
+                                          int max_seqlen_q, int max_seqlen_k) {
+  if (num_seqs <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 || max_seqlen_q <= 0 ||
+      max_seqlen_k <= 0 || num_q_heads % num_kv_heads)
+    return 0;
+  const int G = num_q_heads / num_kv_heads;
+  const int qtiles = (max_seqlen_q * G + kRows - 1) / kRows;
+  int nsplit, split_len;
+  attn_plan(num_seqs, num_kv_heads, qtiles, max_seqlen_k, &nsplit, &split_len);
+  const size_t parts = (size_t)num_seqs * num_kv_heads * qtiles * nsplit * kRows;
+  const size_t classic = parts * kD * sizeof(float) + parts * 2 * sizeof(float) + 256;
+  bool heads = false;
+  const int nwg = attn_sk_plan(num_seqs, num_kv_heads, qtiles, max_seqlen_k, &heads);
+  const size_t sk = nwg ? attn_sk_workspace(num_seqs, num_kv_heads, qtiles, nwg, heads) : 0;
+  return classic > sk ? classic : sk;
+}
+
+int hs_verify_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                        const void* k_cache, const void* v_cache, int kv_dtype,
+                        int64_t cache_stride_block, int64_t cache_stride_tok,
+                        int64_t cache_stride_head, float k_scale, float v_scale,
+                        const int32_t* block_tables, int64_t block_table_stride,
+                        int block_table_width, int num_blocks,
+                        const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int num_seqs,
+                        int max_seqlen_q, int max_seqlen_k, int num_q_heads, int num_kv_heads,
+                        int head_dim, int block_size, float softmax_scale, void* out,
+                        int64_t out_stride_tok, int64_t out_stride_head, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  AttnArgs a;
+  size_t need = 0;
+  const int prc = attn_prepare(q, q_stride_tok, q_stride_head, k_cache, v_cache, kv_dtype,
+                               cache_stride_block, cache_stride_tok, cache_stride_head, k_scale,
+                               v_scale, block_tables, block_table_stride, block_table_width,
+                               num_blocks, cu_seqlens_q, cu_seqlens_k, num_seqs, max_seqlen_q,
+                               max_seqlen_k, num_q_heads, num_kv_heads, head_dim, block_size,
+                               softmax_scale, out, out_stride_tok, out_stride_head, workspace,
+                               workspace_bytes, &a, &need);
+  if (prc != HS_OK) return prc;
+  const int G = a.G;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   bool heads = false;
   const int nwg = attn_sk_plan(num_seqs, num_kv_heads, a.qtiles, max_seqlen_k, &heads);
@@ -1147,6 +1383,92 @@ int hs_verify_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_he
   if (a.nsplit > 1)
     hipLaunchKernelGGL(k_attn_combine, dim3(num_seqs, num_kv_heads * a.qtiles),
                        dim3(kRows * 16), 0, s, a);
+  return hipGetLastError() == hipSuccess ? HS_OK : HS_ERR_LAUNCH;
+}
+
+int hs_qk_norm_rope_attend(const void* qkv, int64_t token_stride, int num_tokens,
+                           const void* q_weight, const void* k_weight, const float* cos_sin,
+                           int cos_sin_rows, const int64_t* positions, float eps,
+                           const int32_t* slot_mapping,
+                           void* q_out, void* k_cache, void* v_cache, int kv_dtype,
+                           int64_t cache_stride_block, int64_t cache_stride_tok,
+                           int64_t cache_stride_head, float k_scale, float v_scale,
+                           const int32_t* block_tables, int64_t block_table_stride,
+                           int block_table_width, int num_blocks, const int32_t* cu_seqlens_q,
+                           const int32_t* cu_seqlens_k, int num_seqs, int max_seqlen_q,
+                           int max_seqlen_k, int num_q_heads, int num_kv_heads, int head_dim,
+                           int block_size, float softmax_scale, void* out,
+                           int64_t out_stride_tok, int64_t out_stride_head, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+  if (num_tokens <= 0) return num_tokens == 0 ? HS_OK : HS_ERR_INVALID;
+  if (!qkv || !q_weight || !k_weight || !cos_sin || !positions || !slot_mapping || !q_out ||
+      cos_sin_rows <= 0)
+    return HS_ERR_INVALID;
+  if (num_q_heads <= 0 || num_kv_heads <= 0) return HS_ERR_INVALID;
+  if (head_dim != kD) return HS_ERR_UNSUPPORTED;
+  if (kv_dtype != HS_BF16 && kv_dtype != HS_FP8_E4M3) return HS_ERR_INVALID;
+  if (token_stride < (int64_t)(num_q_heads + 2 * num_kv_heads) * kD) return HS_ERR_INVALID;
+  if (kv_dtype == HS_FP8_E4M3 && !(k_scale > 0.0f && v_scale > 0.0f)) return HS_ERR_INVALID;
+  if ((uintptr_t)qkv & 1) return HS_ERR_UNSUPPORTED;
+  // q_out [num_tokens, Hq, 128]: the two-launch path's q, and the argument
+  // checks' stand-in for q (the fused kernel does not write it)
+  AttnArgs a;
+  size_t need = 0;
+  const int prc = attn_prepare(q_out, (int64_t)num_q_heads * kD, kD, k_cache, v_cache, kv_dtype,
+                               cache_stride_block, cache_stride_tok, cache_stride_head, k_scale,
+                               v_scale, block_tables, block_table_stride, block_table_width,
+                               num_blocks, cu_seqlens_q, cu_seqlens_k, num_seqs, max_seqlen_q,
+                               max_seqlen_k, num_q_heads, num_kv_heads, head_dim, block_size,
+                               softmax_scale, out, out_stride_tok, out_stride_head, workspace,
+                               workspace_bytes, &a, &need);
+  if (prc != HS_OK) return prc;
+  bool heads = false;
+  const int nwg = attn_sk_plan(num_seqs, num_kv_heads, a.qtiles, max_seqlen_k, &heads);
+  const bool sk = nwg && workspace && workspace_bytes >= need &&
+                  (max_seqlen_k + block_size - 1) / block_size + 1 <= kSkBtCap;
+  const int64_t wgs = (int64_t)num_kv_heads * num_seqs;
+  if (sk || a.nsplit > 1 || a.qtiles > 1 || max_seqlen_q > kRows) {
+    // a (sequence, kv head) over several workgroups: the store first, then the
+    // attention over the stored cache
+    const int rc = hs_qk_norm_rope_store(
+        qkv, token_stride, num_q_heads, num_kv_heads, head_dim, q_weight, k_weight, cos_sin,
+        positions, eps, q_out, k_cache, v_cache, kv_dtype, cache_stride_block, cache_stride_tok,
+        cache_stride_head, k_scale, v_scale, slot_mapping, block_size, num_blocks, num_tokens,
+        stream);
+    if (rc != HS_OK) return rc;
+    return hs_verify_attention(q_out, (int64_t)num_q_heads * kD, kD, k_cache, v_cache, kv_dtype,
+                               cache_stride_block, cache_stride_tok, cache_stride_head, k_scale,
+                               v_scale, block_tables, block_table_stride, block_table_width,
+                               num_blocks, cu_seqlens_q, cu_seqlens_k, num_seqs, max_seqlen_q,
+                               max_seqlen_k, num_q_heads, num_kv_heads, head_dim, block_size,
+                               softmax_scale, out, out_stride_tok, out_stride_head, workspace,
+                               workspace_bytes, stream);
+  }
+  QkvArgs qa;
+  qa.qkv = static_cast<const uint16_t*>(qkv);
+  qa.ts = token_stride;
+  qa.qw = static_cast<const uint16_t*>(q_weight);
+  qa.kw = static_cast<const uint16_t*>(k_weight);
+  qa.cos_sin = cos_sin;
+  qa.positions = positions;
+  qa.slots = slot_mapping;
+  qa.eps = eps;
+  qa.k_scale = k_scale;
+  qa.v_scale = v_scale;
+  qa.Hq = num_q_heads;
+  qa.cs_rows = cos_sin_rows;
+  a.part_o = nullptr;
+  a.part_ml = nullptr;
+  a.sk_pre = nullptr;
+  a.sk_w0 = nullptr;
+  a.sk_nwg = 0;
+  a.xcd_pack = (wgs <= 32) ? 8 : 1;  // as hs_verify_attention's per-tile grid
+  const dim3 grid(a.xcd_pack * num_kv_heads, 1, num_seqs);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (a.fp8)
+    launch_attn_qkv<true>(a.G, grid, s, a, qa);
+  else
+    launch_attn_qkv<false>(a.G, grid, s, a, qa);
   return hipGetLastError() == hipSuccess ? HS_OK : HS_ERR_LAUNCH;
 }
 

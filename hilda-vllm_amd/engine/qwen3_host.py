@@ -106,9 +106,10 @@ class Qwen3Layer(nn.Module):
         self.attn = Attention(g.num_heads, D, D ** -0.5, g.num_kv_heads)
 
     def forward(self, positions, h, residual):
-        """qwen3.py:148-161 in four fused launches plus attention: input RMSNorm (+ the
-        residual add) inside the qkv projection, q/k-norm + RoPE + KV store, o projection,
-        post-attention RMSNorm inside the gate_up projection with SwiGLU, down projection."""
+        """qwen3.py:148-161 in five fused launches: input RMSNorm (+ the residual add)
+        inside the qkv projection; q/k-norm + RoPE + KV store + attention (one launch for
+        decode and verify steps, two for prefill); o projection; post-attention RMSNorm
+        inside the gate_up projection with SwiGLU; down projection."""
         g = self.g
         qkv, residual = _ops.linear_rmsnorm(h, self.ln1, g.rms_eps, self.qkv, residual=residual)
         attn = self.attn
@@ -121,11 +122,9 @@ class Qwen3Layer(nn.Module):
             vv = qkv[:, self.q_size + self.kv_size:]
             torch.maximum(attn.calib, torch.stack([kk.abs().amax(), vv.abs().amax()]).float(),
                           out=attn.calib)
-        q = _ops.qk_norm_rope_store(qkv, g.num_heads, g.num_kv_heads, self.q_norm, self.k_norm,
-                                    self.rope.cos_sin, positions, g.rms_eps, attn.k_cache,
-                                    attn.v_cache, ctx.slot_mapping, k_scale=attn.k_scale,
-                                    v_scale=attn.v_scale)
-        o = attn.attend(q)
+        # q/k-norm + RoPE + KV store + attention: one launch for decode and verify steps
+        o = attn.attend_qkv(qkv, self.q_norm, self.k_norm, self.rope.cos_sin, positions,
+                            g.rms_eps)
         h = _ops.linear(o.reshape(o.shape[0], -1), self.o)
         x, residual = _ops.linear_rmsnorm(h, self.ln2, g.rms_eps, self.gate_up, residual=residual,
                                           swiglu=True)

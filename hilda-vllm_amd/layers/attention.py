@@ -87,20 +87,42 @@ class Attention(nn.Module):
         current tokens a fused producer (ops.qk_norm_rope_store) has already stored."""
         ctx = get_context()
         self._check_bound(ctx)
-        k_cache, v_cache = self.k_cache, self.v_cache
         q = q.view(-1, self.num_heads, self.head_dim)
+        cu_q, cu_k, max_q, max_k = self._bounds(ctx, q.shape[0], q.device)
+        return _ops.verify_attention(q, self.k_cache, self.v_cache, ctx.block_tables, cu_q, cu_k,
+                                     max_q, max_k, self.scale, k_scale=self.k_scale,
+                                     v_scale=self.v_scale)
+
+    def attend_qkv(self, qkv: torch.Tensor, q_norm, k_norm, cos_sin: torch.Tensor,
+                   positions: torch.Tensor, eps: float) -> torch.Tensor:
+        """q/k-norm + RoPE of the fused qkv rows, the K/V store of the current tokens
+        and the attention, one launch for decode and verify steps
+        (ops.qk_norm_rope_attend; qwen3.py:83-86 then forward)."""
+        ctx = get_context()
+        self._check_bound(ctx)
+        cu_q, cu_k, max_q, max_k = self._bounds(ctx, qkv.shape[0], qkv.device)
+        return _ops.qk_norm_rope_attend(qkv, self.num_heads, self.num_kv_heads, q_norm, k_norm,
+                                        cos_sin, positions, eps, self.k_cache, self.v_cache,
+                                        ctx.slot_mapping, ctx.block_tables, cu_q, cu_k, max_q,
+                                        max_k, self.scale, k_scale=self.k_scale,
+                                        v_scale=self.v_scale)
+
+    def _bounds(self, ctx, num_tokens: int, device):
+        """cu_seqlens_q / cu_seqlens_k and the maximum query and key lengths of the
+        context (decode contexts carry context_lens instead of cu_seqlens_k)."""
+        k_cache = self.k_cache
         if ctx.is_prefill:
             cu_q, cu_k = ctx.cu_seqlens_q, ctx.cu_seqlens_k
             max_q, max_k = ctx.max_seqlen_q, ctx.max_seqlen_k
         else:
-            B = q.shape[0]
+            B = num_tokens
             cu_q = ctx.cu_seqlens_q
             if cu_q is None:
-                cu_q = torch.arange(B + 1, dtype=torch.int32, device=q.device)
+                cu_q = torch.arange(B + 1, dtype=torch.int32, device=device)
             if ctx.cu_seqlens_k is not None:
                 cu_k = ctx.cu_seqlens_k
             else:
-                cu_k = torch.zeros(B + 1, dtype=torch.int32, device=q.device)
+                cu_k = torch.zeros(B + 1, dtype=torch.int32, device=device)
                 torch.cumsum(ctx.context_lens.to(torch.int32), 0, out=cu_k[1:])
             max_q, max_k = 1, ctx.max_seqlen_k
         if self.max_model_len:
@@ -110,6 +132,4 @@ class Attention(nn.Module):
             # (model_runner.py:310 set_context(False, slot_mapping, context_lens,
             # block_tables)); the table width bounds every context without a sync
             max_k = ctx.block_tables.shape[1] * k_cache.shape[1]
-        return _ops.verify_attention(q, k_cache, v_cache, ctx.block_tables, cu_q, cu_k, max_q,
-                                     max_k, self.scale, k_scale=self.k_scale,
-                                     v_scale=self.v_scale)
+        return cu_q, cu_k, max_q, max_k

@@ -543,6 +543,64 @@ def qk_norm_rope_store(qkv: torch.Tensor, num_q_heads: int, num_kv_heads: int, q
     return q
 
 
+def qk_norm_rope_attend(qkv: torch.Tensor, num_q_heads: int, num_kv_heads: int, q_weight,
+                        k_weight, cos_sin: torch.Tensor, positions: torch.Tensor, eps: float,
+                        k_cache: torch.Tensor, v_cache: torch.Tensor, slot_mapping: torch.Tensor,
+                        block_tables: torch.Tensor, cu_seqlens_q: torch.Tensor,
+                        cu_seqlens_k: torch.Tensor, max_seqlen_q: int, max_seqlen_k: int,
+                        softmax_scale: float, *, k_scale: float = 1.0, v_scale: float = 1.0,
+                        out: torch.Tensor | None = None) -> torch.Tensor:
+    """qk_norm_rope_store then verify_attention on the stored cache
+    (qwen3.py:83-86 with attention.py:59-90, :145-160), one launch for decode and
+    verify steps (hs_qk_norm_rope_attend); returns the attention output
+    [tokens, Hq, 128]. qkv holds the query tokens of the sequences in
+    cu_seqlens_q order."""
+    dev = _need_cuda(qkv, q_weight, k_weight, cos_sin, positions, k_cache, v_cache, slot_mapping,
+                     block_tables, cu_seqlens_q, cu_seqlens_k, out)
+    N = qkv.shape[0]
+    if qkv.dtype != torch.bfloat16 or qkv.dim() != 2 or qkv.stride(1) != 1:
+        raise ValueError("qkv must be [tokens, (Hq + 2 Hkv) * 128] bf16 with contiguous rows")
+    if qkv.shape[1] != (num_q_heads + 2 * num_kv_heads) * 128:
+        raise ValueError("qkv width does not match the head counts")
+    if slot_mapping.numel() != N or positions.numel() != N:
+        raise ValueError("slot_mapping and positions need one entry per token")
+    if k_cache.shape != v_cache.shape or k_cache.dtype != v_cache.dtype:
+        raise ValueError("k_cache and v_cache must match")
+    if k_cache.stride() != v_cache.stride() or k_cache.stride(3) != 1:
+        raise ValueError("k_cache and v_cache need identical strides with contiguous head_dim")
+    nb, bs, Hc, Dc = k_cache.shape
+    if (Hc, Dc) != (num_kv_heads, 128):
+        raise ValueError("cache geometry mismatch")
+    if cos_sin.dtype != torch.float32 or not cos_sin.is_contiguous() or cos_sin.shape[1] != 128:
+        raise ValueError("cos_sin must be a contiguous f32 [max_position, 128] table")
+    pos = positions if positions.dtype == torch.int64 else positions.to(torch.int64)
+    sm = slot_mapping if slot_mapping.dtype == torch.int32 else slot_mapping.to(torch.int32)
+    pos, sm = pos.contiguous(), sm.contiguous()
+    B = cu_seqlens_q.numel() - 1
+    bt = block_tables if block_tables.dtype == torch.int32 else block_tables.to(torch.int32)
+    if bt.dim() != 2 or bt.shape[0] < B or bt.stride(1) != 1:
+        bt = bt.contiguous()
+    cq = cu_seqlens_q.to(torch.int32).contiguous()
+    ck = cu_seqlens_k.to(torch.int32).contiguous()
+    q = torch.empty((N, num_q_heads, 128), dtype=torch.bfloat16, device=dev)
+    if out is None:
+        out = torch.empty((N, num_q_heads, 128), dtype=torch.bfloat16, device=dev)
+    lib = L.lib()
+    nbytes = lib.hs_verify_attention_workspace_size(B, num_q_heads, num_kv_heads,
+                                                    int(max_seqlen_q), int(max_seqlen_k))
+    ws = workspace(dev, nbytes, "attention")
+    L.check(lib.hs_qk_norm_rope_attend(
+        qkv.data_ptr(), qkv.stride(0), N, q_weight.data_ptr(), k_weight.data_ptr(),
+        cos_sin.data_ptr(), cos_sin.shape[0], pos.data_ptr(), float(eps), sm.data_ptr(),
+        q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), _kv_code(k_cache), k_cache.stride(0),
+        k_cache.stride(1), k_cache.stride(2), float(k_scale), float(v_scale), bt.data_ptr(),
+        bt.stride(0), bt.shape[1], nb, cq.data_ptr(), ck.data_ptr(), B, int(max_seqlen_q),
+        int(max_seqlen_k), num_q_heads, num_kv_heads, 128, bs, float(softmax_scale),
+        out.data_ptr(), out.stride(0), out.stride(1), ws.data_ptr(), ws.numel(), _stream(dev)),
+        "hs_qk_norm_rope_attend")
+    return out
+
+
 def silu_mul(gate_up: torch.Tensor) -> torch.Tensor:
     """activation.py:8-16: silu(gate) * up of a fused [N, 2F] projection."""
     dev = _need_cuda(gate_up)

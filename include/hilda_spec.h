@@ -367,6 +367,38 @@ int hs_qk_norm_rope_store(const void* qkv, int64_t token_stride, int num_q_heads
                           const int32_t* slot_mapping, int block_size, int num_blocks,
                           int num_tokens, void* stream);
 
+/* hs_qk_norm_rope_store followed by hs_verify_attention on the stored cache */
+/* (Qwen3Attention.forward, mini_vllm/models/qwen3.py:83-86: q_norm, k_norm,  */
+/* rotary_emb, then Attention.forward's store_kvcache and paged attention,    */
+/* mini_vllm/layers/attention.py:59-90, :145-160), as one launch where every */
+/* (sequence, kv head) fits one workgroup (one 16-row query tile, keys not   */
+/* split; decode and verify steps): that workgroup normalises and rotates   */
+/* its q rows in LDS and stores its kv head's k/v rows of the sequence's    */
+/* query tokens before reading them. Other calls run the two launches, with */
+/* q_out receiving q. Same outputs and cache contents either way.           */
+/* qkv: [num_tokens, (Hq + 2 Hkv) * 128] bf16 holding the query tokens of    */
+/* the sequences in cu_seqlens_q order (num_tokens = cu_seqlens_q[num_seqs]), */
+/* cos_sin: [cos_sin_rows, 128] f32 (cos | sin), every position below       */
+/* cos_sin_rows; positions / slot_mapping one entry per token (slots < 0    */
+/* store nothing);                                                           */
+/* q_out: [num_tokens, Hq, 128] bf16 (contents unspecified after a fused     */
+/* call); the cache, table, length, scale and output arguments are those of  */
+/* hs_verify_attention (k_scale / v_scale also scale the fp8 stores).        */
+int hs_qk_norm_rope_attend(const void* qkv, int64_t token_stride, int num_tokens,
+                           const void* q_weight, const void* k_weight, const float* cos_sin,
+                           int cos_sin_rows, const int64_t* positions, float eps,
+                           const int32_t* slot_mapping,
+                           void* q_out, void* k_cache, void* v_cache, int kv_dtype,
+                           int64_t cache_stride_block, int64_t cache_stride_tok,
+                           int64_t cache_stride_head, float k_scale, float v_scale,
+                           const int32_t* block_tables, int64_t block_table_stride,
+                           int block_table_width, int num_blocks, const int32_t* cu_seqlens_q,
+                           const int32_t* cu_seqlens_k, int num_seqs, int max_seqlen_q,
+                           int max_seqlen_k, int num_q_heads, int num_kv_heads, int head_dim,
+                           int block_size, float softmax_scale, void* out,
+                           int64_t out_stride_tok, int64_t out_stride_head, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
 /* out[r, :ffn] = silu(gate_up[r, :ffn]) * gate_up[r, ffn:2*ffn]. */
 int hs_silu_mul(const void* gate_up, int64_t gate_up_stride, int ffn, void* out,
                 int64_t out_stride, int rows, void* stream);

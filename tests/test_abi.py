@@ -130,3 +130,21 @@ def test_qk_norm_rope_store_rejects_bad_arguments_on_host(hv):
     assert call(dtype=2, ks=0.0) == -1
     assert call(ts=100) == -1
     assert call(bs=0) == -1
+
+
+def test_qk_norm_rope_attend_rejects_bad_arguments_on_host(hv):
+    lib = hv._lib.lib()
+    buf = ctypes.create_string_buffer(256)
+    p = (ctypes.cast(buf, ctypes.c_void_p).value + 15) // 16 * 16
+
+    def call(hd=128, dtype=1, ks=1.0, ts=(4 + 2 * 2) * 128, n=3, qkv=p):
+        return lib.hs_qk_norm_rope_attend(qkv, ts, n, p, p, p, 64, p, 1e-6, p, p, p, p, dtype, 0,
+                                          0, 0, ks, 1.0, p, 8, 8, 8, p, p, 1, 4, 64, 4, 2, hd,
+                                          16, 0.1, p, 512, 128, None, 0, None)
+    assert call(n=0) == 0
+    assert call(n=-1) == -1
+    assert call(qkv=None) == -1
+    assert call(hd=64) == -4
+    assert call(dtype=7) == -1
+    assert call(dtype=2, ks=0.0) == -1
+    assert call(ts=100) == -1

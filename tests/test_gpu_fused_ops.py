@@ -10,6 +10,9 @@
 * hs_qk_norm_rope_store against hs_qk_norm_rope + hs_store_kvcache: the same
   per-lane arithmetic, so q and both caches (bf16 and FP8) are bit-exact,
   including tokens whose slot is -1 (nothing stored).
+* hs_qk_norm_rope_attend against hs_qk_norm_rope_store + hs_verify_attention:
+  outputs and both caches bit-exact, for the fused launch and the shapes that
+  run as two launches.
 """
 import pytest
 import torch
@@ -125,3 +128,87 @@ def test_qk_norm_rope_store_matches_separate(hv, cuda, kv, N, Hq, Hkv):
     u8 = lambda t: t.view(torch.uint8)  # noqa: E731
     assert torch.equal(u8(kc1), u8(kc2))
     assert torch.equal(u8(vc1), u8(vc2))
+
+
+# (name, Hq, Hkv, query lengths, earlier keys per sequence, block size): the
+# verify step of the 8B target, decode of the 0.6B draft (one sequence with no
+# earlier key: its first window holds the new key), a batch over several
+# blocks, a padding token (slot -1), G = 1, RoPE positions that differ from
+# the key index, and two shapes that run as two launches (two query tiles;
+# the balanced launch of a large batch)
+_ATTEND_CASES = [
+    ("verify-8b", 32, 8, [4], [316], 256),
+    ("decode-06b", 16, 8, [1, 1, 1], [76, 299, 0], 256),
+    ("verify-batch", 32, 8, [4, 4, 4, 4], [1, 36, 300, 700], 32),
+    ("padding-slot", 16, 8, [2, 2], [10, 20], 32),
+    ("g1", 8, 8, [4], [100], 256),
+    ("pos-offset", 32, 8, [4, 4], [60, 200], 256),
+    ("two-tiles", 32, 8, [5, 3], [50, 100], 256),
+    ("balanced", 32, 8, [4] * 32, [1500 + 17 * i for i in range(32)], 256),
+]
+
+
+@pytest.mark.parametrize("kv", ["bf16", "fp8"])
+@pytest.mark.parametrize("case", _ATTEND_CASES, ids=[c[0] for c in _ATTEND_CASES])
+def test_qk_norm_rope_attend_matches_two_launches(hv, cuda, kv, case):
+    """hs_qk_norm_rope_attend against hs_qk_norm_rope_store + hs_verify_attention:
+    the fused prologue uses the same per-lane arithmetic and the attention the same
+    kernel body, so the outputs and both caches are bit-exact."""
+    name, Hq, Hkv, qls, ctxs, bs = case
+    ops = hv.ops
+    B = len(qls)
+    g = torch.Generator(device=cuda).manual_seed(sum(qls) * 1000 + sum(ctxs) + Hq + bs)
+    lks = [c + q for c, q in zip(ctxs, qls)]
+    nblk = [(lk + bs - 1) // bs for lk in lks]
+    nb = sum(nblk) + 3
+    perm = torch.randperm(nb, generator=g, device=cuda).to(torch.int32)
+    W = max(nblk)
+    bt = torch.full((B, W), -1, dtype=torch.int32, device=cuda)
+    o = 0
+    for b in range(B):
+        bt[b, :nblk[b]] = perm[o:o + nblk[b]]
+        o += nblk[b]
+    btc = bt.cpu()
+    pos, slots = [], []
+    for b in range(B):
+        for i in range(qls[b]):
+            p = ctxs[b] + i
+            # RoPE positions other than the key index (the kernel's cos/sin guess)
+            pos.append(p + 7 if name == "pos-offset" else p)
+            slots.append(int(btc[b, p // bs]) * bs + p % bs)
+    if name == "padding-slot":
+        slots[1] = -1  # a padding token: nothing stored, the cache keeps its old row
+    N = len(pos)
+    pos_t = torch.tensor(pos, dtype=torch.int64, device=cuda)
+    slots_t = torch.tensor(slots, dtype=torch.int32, device=cuda)
+    cu_q = torch.tensor([0] + list(torch.tensor(qls).cumsum(0)), dtype=torch.int32, device=cuda)
+    cu_k = torch.tensor([0] + list(torch.tensor(lks).cumsum(0)), dtype=torch.int32, device=cuda)
+    qkv = (torch.randn((N, (Hq + 2 * Hkv) * 128), generator=g, device=cuda) * 2).to(
+        torch.bfloat16)
+    qw = (1 + 0.1 * torch.randn(128, generator=g, device=cuda)).to(torch.bfloat16)
+    kw = (1 + 0.1 * torch.randn(128, generator=g, device=cuda)).to(torch.bfloat16)
+    cs = _rope_table(4096, cuda)
+    dt = torch.bfloat16 if kv == "bf16" else torch.float8_e4m3fn
+    ksc, vsc = (1.0, 1.0) if kv == "bf16" else (0.05, 0.03)
+    if dt == torch.bfloat16:
+        kc1 = torch.randn((nb, bs, Hkv, 128), generator=g, device=cuda).to(dt)
+        vc1 = torch.randn((nb, bs, Hkv, 128), generator=g, device=cuda).to(dt)
+    else:
+        fill = torch.randint(0, 255, (2, nb, bs, Hkv, 128), generator=g, device=cuda,
+                             dtype=torch.uint8) & 0x77  # finite e4m3 codes
+        kc1, vc1 = fill[0].clone().view(dt), fill[1].clone().view(dt)
+    kc2, vc2 = kc1.clone(), vc1.clone()
+    max_q, max_k = max(qls), max(lks)
+    scale = 128 ** -0.5
+    print(f"qk_norm_rope_attend {name} kv={kv} B={B} N={N}", flush=True)
+    q = ops.qk_norm_rope_store(qkv, Hq, Hkv, qw, kw, cs, pos_t, 1e-6, kc1, vc1, slots_t,
+                               k_scale=ksc, v_scale=vsc)
+    out1 = ops.verify_attention(q, kc1, vc1, bt, cu_q, cu_k, max_q, max_k, scale, k_scale=ksc,
+                                v_scale=vsc)
+    out2 = ops.qk_norm_rope_attend(qkv, Hq, Hkv, qw, kw, cs, pos_t, 1e-6, kc2, vc2, slots_t, bt,
+                                   cu_q, cu_k, max_q, max_k, scale, k_scale=ksc, v_scale=vsc)
+    torch.cuda.synchronize()
+    u8 = lambda t: t.view(torch.uint8)  # noqa: E731
+    assert torch.equal(u8(kc1), u8(kc2))
+    assert torch.equal(u8(vc1), u8(vc2))
+    assert torch.equal(out1.view(torch.int16), out2.view(torch.int16))
