@@ -33,7 +33,9 @@ kernel divided by its HIP-event time measured on the launch stream (spec: the
 gate/up projection of the target at the verify shape, the largest share of the
 step's kernel time, probed over the target's own weights; roofline_step is the
 whole verify+accept step against the target weights it streams, and
-roofline_attention the verify-attention kernel at the batch-1 verify shape;
+roofline_attention the verify-attention kernel at the batch-1 verify shape, and
+roofline_attention_fused the launch the step runs there (q/k-norm + RoPE + KV store
+in the attention prologue);
 accept and attention: the whole call); cpu_baseline times the
 torch-CPU restatement of the reference loop (oracle/torch_port.py) on the
 host cores of the same machine on a bounded sample.
@@ -509,6 +511,7 @@ def bench_spec(args, torch, hv):
     accepted_drafts = emitted - args.steps
     roof = gemm_probe(torch, hv, target)
     roof_attn = attention_probe(torch, hv, kv=args.kv)
+    roof_attn_fused = attention_probe(torch, hv, kv=args.kv, fused=True)
     step_bytes = target_step_bytes(target)
     step_us = verify_ms / args.steps * 1e3
     roof_step = {"bound": "hbm", "achieved": round(step_bytes / (step_us * 1e-6) / 1e9, 1),
@@ -553,6 +556,7 @@ def bench_spec(args, torch, hv):
         "roofline": roof,
         "roofline_step": roof_step,
         "roofline_attention": roof_attn,
+        "roofline_attention_fused": roof_attn_fused,
     }
     if args.draft != "forced" and not args.no_forced:
         # config 3's second mode: the draft is the target's first 28 layers plus
@@ -735,12 +739,15 @@ def gemm_probe(torch, hv, target, rows: int = 4, reps: int = 10):
 
 
 def attention_probe(torch, hv, kv: str = "auto", L: int = PROBE_CONTEXT, layers: int = 36,
-                    reps: int = 20):
+                    reps: int = 20, fused: bool = False):
     """The verify-attention kernel at the batch-1 verify shape of the 8B target
     (B=1, gamma+1=4 queries, 32 Q / 8 KV heads, D=128, context L, 256-token blocks):
     one launch per layer over `layers` separate random caches (as in one verify
     step), captured in a HIP graph and replayed `reps` times between two HIP events
-    on the launch stream. avg_launch_us includes the graph's per-node dispatch gap."""
+    on the launch stream. avg_launch_us includes the graph's per-node dispatch gap.
+    fused: the launch the spec step runs, hs_qk_norm_rope_attend (q/k-norm + RoPE
+    of the 4 qkv rows, their k/v stored at keys L-4 .. L-1, then the attention);
+    its bytes add the qkv rows read and the k/v rows stored, less the q read."""
     dev = torch.device("cuda:0")
     R, Hq, Hkv, D, bs = 4, 32, 8, 128, 256
     nb = (L + bs - 1) // bs
@@ -759,14 +766,34 @@ def attention_probe(torch, hv, kv: str = "auto", L: int = PROBE_CONTEXT, layers:
     bt = bt.view(1, nb).to(dev)
     outs = [torch.empty((R, Hq, D), dtype=torch.bfloat16, device=dev) for _ in range(layers)]
 
-    def launch_all():
-        for i, (k, v) in enumerate(caches):
-            hv.ops.verify_attention(q, k, v, bt, cu_q, cu_k, R, L, D ** -0.5, out=outs[i])
+    skv = 1 if fp8 else 2
+    if fused:
+        qkv = torch.randn((R, (Hq + 2 * Hkv) * D), generator=gen, device=dev).to(torch.bfloat16)
+        qw = torch.ones(D, dtype=torch.bfloat16, device=dev)
+        inv = 1.0 / (1e6 ** (torch.arange(0, D, 2, dtype=torch.float32, device=dev) / D))
+        f = torch.outer(torch.arange(L, dtype=torch.float32, device=dev), inv)
+        cs = torch.cat([f.cos(), f.sin()], -1).contiguous()
+        pos = torch.arange(L - R, L, dtype=torch.int64, device=dev)
+        btc = bt.view(-1).cpu()
+        slots = torch.tensor([int(btc[p // bs]) * bs + p % bs for p in range(L - R, L)],
+                             dtype=torch.int32, device=dev)
+
+        def launch_all():
+            for i, (k, v) in enumerate(caches):
+                hv.ops.qk_norm_rope_attend(qkv, Hq, Hkv, qw, qw, cs, pos, 1e-6, k, v, slots, bt,
+                                           cu_q, cu_k, R, L, D ** -0.5, out=outs[i])
+        per_launch = (L * Hkv * D * 2 * skv + R * (Hq + 2 * Hkv) * D * 2 + R * Hq * D * 2
+                      + R * 2 * Hkv * D * skv)
+        kernel = f"k_verify_attn_qkv<{'true' if fp8 else 'false'}, 4>"
+    else:
+        def launch_all():
+            for i, (k, v) in enumerate(caches):
+                hv.ops.verify_attention(q, k, v, bt, cu_q, cu_k, R, L, D ** -0.5, out=outs[i])
+        per_launch = L * Hkv * D * 2 * skv + 2 * R * Hq * D * 2
+        kernel = f"k_verify_attn<{'true' if fp8 else 'false'}, 4>"
 
     us = graph_time_us(torch, dev, launch_all, reps) / layers
-    per_launch = L * Hkv * D * 2 * (1 if fp8 else 2) + 2 * R * Hq * D * 2
     achieved = per_launch / (us * 1e-6) / 1e9
-    kernel = f"k_verify_attn<{'true' if fp8 else 'false'}, 4>"
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": profiled_traffic(kernel, "attention-b1"),
             "mfma_util": profiled_counter(kernel, "attention-b1", "MfmaUtil %"),
