@@ -794,9 +794,10 @@ def attention_probe(torch, hv, kv: str = "auto", L: int = PROBE_CONTEXT, layers:
 
     us = graph_time_us(torch, dev, launch_all, reps) / layers
     achieved = per_launch / (us * 1e-6) / 1e9
+    workload = "attention-b1-fused" if fused else "attention-b1"
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": profiled_traffic(kernel, "attention-b1"),
-            "mfma_util": profiled_counter(kernel, "attention-b1", "MfmaUtil %"),
+            "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": profiled_traffic(kernel, workload),
+            "mfma_util": profiled_counter(kernel, workload, "MfmaUtil %"),
             "kernel": kernel, "bytes_per_launch": per_launch, "avg_launch_us": round(us, 3),
             "shape": f"B=1 q={R} Hq={Hq} Hkv={Hkv} D={D} L={L} block {bs}",
             "launches": reps * layers}
@@ -847,13 +848,15 @@ def call_traffic(kernels, workload: str):
 
 
 def bench_attention_b1(args, torch, hv):
-    roof = attention_probe(torch, hv, kv=args.kv, reps=max(1, args.steps // 36))
+    roof = attention_probe(torch, hv, kv=args.kv, reps=max(1, args.steps // 36),
+                           fused=args.attn_fused)
     return {"metric": METRIC, "value": roof["avg_launch_us"], "unit": "us/launch (verify attention)",
             "n_gpus": 1, "steps": roof["launches"], "warmup": 36, "ms_per_step": roof["avg_launch_us"] / 1e3,
             "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
             "dtype": "fp8-e4m3 KV, bf16 MFMA" if args.kv == "fp8" else "bf16",
             "data": "synthetic (seeded N(0,1) q/k/v, random block permutation)",
-            "config": {"workload": "verify attention at the config-3 batch-1 verify shape, 36 layers",
+            "config": {"workload": "verify attention at the config-3 batch-1 verify shape, 36 layers"
+                       + (" (q/k-norm + RoPE + KV store in the prologue)" if args.attn_fused else ""),
                        "kv_cache": args.kv, "context": PROBE_CONTEXT},
             "roofline": roof}
 
@@ -950,6 +953,8 @@ def main(argv=None):
     ap.add_argument("--top-p", type=float, default=1.0)
     ap.add_argument("--draft", default="qwen3-0.6b", choices=["qwen3-0.6b", "forced"])
     ap.add_argument("--kv", default="auto", choices=["auto", "fp8"])
+    ap.add_argument("--attn-fused", action="store_true",
+                    help="attention-b1: the fused launch (hs_qk_norm_rope_attend) of the spec step")
     ap.add_argument("--eager", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
