@@ -53,7 +53,9 @@ class SpecRunner:
         self.W = math.ceil((max_model_len + self.max_gamma + 2) / block_size)
         self.num_blocks = num_blocks or batch * self.W + 2
         self.mode = mode
-        self.device = torch.device(device)
+        # index-qualified ("cuda" -> "cuda:<current>"), so per-device lookups such
+        # as ops.accept_error find the workspaces the kernels were given
+        self.device = torch.device("cuda", ops._dev_index(device))
         self.V = target.g.vocab
         dev = self.device
         kv_dtype = torch.float8_e4m3fn if kv_cache_dtype == "fp8" else torch.bfloat16

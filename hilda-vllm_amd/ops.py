@@ -18,10 +18,24 @@ _WS: dict = {}
 _RETIRED: list = []
 
 
+def _dev_index(device) -> int:
+    """Ordinal of a GPU device ("cuda", "cuda:1", torch.device or int): a device
+    without an index means the current device, as torch resolves it for tensors."""
+    if isinstance(device, int):
+        return device
+    d = torch.device(device)
+    if d.index is not None:
+        return d.index
+    try:
+        return torch.cuda.current_device()
+    except (RuntimeError, AssertionError):  # no GPU here: the only ordinal is 0
+        return 0
+
+
 def workspace(device: torch.device, nbytes: int, kind: str) -> torch.Tensor:
     """Workspace of one kind on one device, grown on demand. A superseded buffer is
     kept alive (never freed) because HIP graphs captured earlier still point at it."""
-    key = (device.index, kind)
+    key = (_dev_index(device), kind)
     ws = _WS.get(key)
     if ws is None or ws.numel() < nbytes:
         if ws is not None:
@@ -162,7 +176,7 @@ def accept_error(device, clear: bool = False) -> bool:
     """True once a spec_accept call on this device's shared acceptance workspace
     produced invalid outputs (num_accepted -1): the sticky 32-bit word at byte 8
     of the workspace (include/hilda_spec.h). Synchronises with the device."""
-    ws = _WS.get((torch.device(device).index, "spec_accept"))
+    ws = _WS.get((_dev_index(device), "spec_accept"))
     if ws is None:
         return False
     word = ws[8:12]

@@ -151,12 +151,35 @@ def test_spec_runner_raises_on_invalid_acceptance():
 
 def test_accept_error_flag_is_read_and_cleared(monkeypatch):
     """The sticky word at byte 8 of the acceptance workspace (set by the kernel
-    when a wait ran out) is what SpecRunner.check reads for fixed-gamma runs."""
+    when a wait ran out) is what SpecRunner.check reads for fixed-gamma runs.
+    ops.workspace keys it by the ordinal of the tensors' device (0), and a device
+    given without an index ("cuda", SpecRunner's default) must find that key."""
     import torch
     ops = importlib.import_module("hilda-vllm_amd.ops")
     ws = torch.zeros(256, dtype=torch.uint8)
-    monkeypatch.setitem(ops._WS, (None, "spec_accept"), ws)
-    assert not ops.accept_error("cpu")
+    monkeypatch.setitem(ops._WS, (0, "spec_accept"), ws)
+    assert not ops.accept_error("cuda")
     ws[8] = 1
-    assert ops.accept_error("cpu", clear=True)
-    assert not ops.accept_error("cpu")
+    assert ops.accept_error("cuda")
+    assert ops.accept_error(torch.device("cuda"))
+    assert ops.accept_error("cuda:0", clear=True)
+    assert not ops.accept_error("cuda")
+    ws[8] = 1
+    assert not ops.accept_error("cuda:1")  # another device's workspace is not this one
+
+
+def test_workspace_key_resolves_the_device_index():
+    ops = importlib.import_module("hilda-vllm_amd.ops")
+    assert ops._dev_index("cuda:3") == 3
+    assert ops._dev_index(2) == 2
+    # no index: the current device (0 where no GPU is visible, as here on the CPU)
+    expect = torch_current_device_or_zero()
+    assert ops._dev_index("cuda") == expect
+
+
+def torch_current_device_or_zero():
+    import torch
+    try:
+        return torch.cuda.current_device()
+    except (RuntimeError, AssertionError):
+        return 0
