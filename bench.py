@@ -29,16 +29,17 @@ Timed launches are captured in HIP graphs and replayed between two HIP events
 on the launch stream; inputs rotate over enough copies that every step reads
 HBM (the MI355X MALL is 256 MB).
 The roofline figure is algorithmic bytes per launch of the workload's dominant
-kernel divided by its HIP-event time measured on the launch stream (spec: the
-gate/up projection of the target at the verify shape, the largest share of the
-step's kernel time, probed over the target's own weights; roofline_step is the
-whole verify+accept step against the target weights it streams, and
-roofline_attention the verify-attention kernel at the batch-1 verify shape, and
-roofline_attention_fused the launch the step runs there (q/k-norm + RoPE + KV store
-in the attention prologue);
-accept and attention: the whole call); cpu_baseline times the
-torch-CPU restatement of the reference loop (oracle/torch_port.py) on the
-host cores of the same machine on a bounded sample.
+kernel divided by its HIP-event time measured on the launch stream. spec: the
+verify-attention launch the step runs once per layer (hs_qk_norm_rope_attend:
+q/k-norm + RoPE of the 4 qkv rows, their K/V stored, then the attention) at the
+batch-1 verify shape with context 320 (64 prompt + 256 generated tokens);
+roofline_inscope_step is the verify+accept step's own work (36 such launches,
+the acceptance call, the bookkeeping launches) against its bytes, without the
+projection weights; roofline_gemm is the gate/up projection of the target (the
+largest share of the step's kernel time, a weight stream) and roofline_step the
+whole verify phase against the weights it streams. accept and attention: the
+whole call. cpu_baseline times the torch-CPU restatement of the reference loop
+(oracle/torch_port.py) on the host cores of the same machine on a bounded sample.
 """
 from __future__ import annotations
 
@@ -432,16 +433,27 @@ def cpu_baseline_attention(torch, lens, block_size: int, R: int, Hq: int, Hkv: i
                       "the key share (torch-CPU restatement of attention.py:147-160)"}
 
 
-def _spec_run(torch, sr, target, draft, steps: int, warmup: int, kv: str, graphs: bool) -> dict:
+def _spec_runner(torch, sr, target, draft, kv: str, max_model_len: int, need: int):
+    """A batch-1 config-3 runner: the reference's max_model_len (benchmarks/bench.py:181
+    uses 4096) sizes the block tables and every attention launch plan; 0 sizes them
+    to the `need` tokens of the run."""
+    return sr.SpecRunner(target, draft, batch=1, gamma=3,
+                         max_model_len=max_model_len if max_model_len > 0 else need,
+                         temperature=0.6, mode="reference", kv_cache_dtype=kv,
+                         device=torch.device("cuda:0"))
+
+
+def _spec_run(torch, sr, target, draft, steps: int, warmup: int, kv: str, graphs: bool,
+              max_model_len: int = 0) -> dict:
     """One timed config-3 run: prefill a 64-token prompt, two eager steps (they
     create every workspace), graph capture of the draft and verify phases, then
     `warmup` untimed and `steps` timed steps between HIP events on the stream."""
     gamma = 3
     dev = torch.device("cuda:0")
     max_len = 64 + (steps + warmup + 4) * (gamma + 1) + 8
-    runner = sr.SpecRunner(target, draft, batch=1, gamma=gamma, max_model_len=max_len,
-                           temperature=0.6, mode="reference", kv_cache_dtype=kv,
-                           device=dev)
+    if max_model_len > 0 and max_len > max_model_len:
+        raise ValueError(f"--steps/--warmup need {max_len} tokens, past --max-model-len")
+    runner = _spec_runner(torch, sr, target, draft, kv, max_model_len, max_len)
     g = torch.Generator().manual_seed(0)
     prompt = torch.randint(0, 10000, (64,), generator=g).tolist()
     runner.load_prompts([prompt])
@@ -488,6 +500,64 @@ def _spec_run(torch, sr, target, draft, steps: int, warmup: int, kv: str, graphs
     return res
 
 
+def _spec_full_run(torch, sr, target, draft, kv: str, max_model_len: int = 0,
+                   output_tokens: int = 256, chunk: int = 16) -> dict:
+    """Config 3 as stated: a 64-token prompt decoded to `output_tokens` completion
+    tokens (max_tokens, so the sequence finishes exactly there as in
+    llm_engine.py:154-160), every step through the HIP graphs after the two eager
+    steps that precede capture. Each step is timed with HIP events on the stream and
+    the context length after it is copied aside (outside the timed events); the GPU
+    time of the steps up to the one that finished the sequence is the run's time."""
+    gamma = 3
+    dev = torch.device("cuda:0")
+    runner = _spec_runner(torch, sr, target, draft, kv, max_model_len,
+                          64 + output_tokens + gamma + 8)
+    g = torch.Generator().manual_seed(0)
+    prompt = torch.randint(0, 10000, (64,), generator=g).tolist()
+    runner.load_prompts([prompt], max_tokens=output_tokens)
+    runner.prefill()
+    torch.manual_seed(0)
+    eager_ms = []
+    stream = torch.cuda.current_stream(dev)
+    for _ in range(2):  # eager steps create every workspace before capture
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        runner.step()
+        e1.record(stream)
+        eager_ms.append((e0, e1))
+    torch.cuda.synchronize()
+    runner.capture()
+    end = 64 + output_tokens
+    lens, evs = [], []
+    hist = torch.zeros(4 * output_tokens, dtype=torch.int32, device=dev)
+    n = 0
+    while True:
+        for _ in range(chunk):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            runner.replay()
+            e1.record(stream)
+            hist[n:n + 1].copy_(runner.state.context_lens[:1])
+            evs.append((e0, e1))
+            n += 1
+        torch.cuda.synchronize()
+        lens = hist[:n].cpu().tolist()
+        if lens[-1] >= end or n + chunk > hist.numel():
+            break
+    runner.check()
+    if lens[-1] < end:
+        raise RuntimeError(f"full run stopped at {lens[-1]} of {end} tokens")
+    last = next(i for i, x in enumerate(lens) if x >= end)
+    steps = 2 + last + 1
+    gpu_ms = sum(a.elapsed_time(b) for a, b in eager_ms + evs[:last + 1])
+    emitted = end - (64 + 1)  # the first completion token comes from the prefill
+    res = dict(steps=steps, gpu_ms=gpu_ms, emitted=emitted,
+               final_tokens=runner.lengths()[0])
+    del runner
+    torch.cuda.empty_cache()
+    return res
+
+
 def bench_spec(args, torch, hv):
     """Config 3: speculative decoding at batch 1 with random-init Qwen3-8B target and
     Qwen3-0.6B draft (or the forced-acceptance draft = target's first 28 layers)."""
@@ -504,22 +574,33 @@ def bench_spec(args, torch, hv):
         draft = q3.Qwen3Host(q3.QWEN3_0_6B, device=dev, seed=2)
     torch.cuda.synchronize()
     init_s = time.perf_counter() - t0
-    m = _spec_run(torch, sr, target, draft, args.steps, args.warmup, args.kv, not args.eager)
+    mml = args.max_model_len
+    m = _spec_run(torch, sr, target, draft, args.steps, args.warmup, args.kv, not args.eager,
+                  max_model_len=mml)
     graphs, gpu_ms, draft_ms, verify_ms = m["graphs"], m["gpu_ms"], m["draft_ms"], m["verify_ms"]
     len0, len1, emitted, wall = m["len0"], m["len1"], m["emitted"], m["wall"]
     tok_s = emitted / (gpu_ms / 1e3)
     accepted_drafts = emitted - args.steps
-    roof = gemm_probe(torch, hv, target)
-    roof_attn = attention_probe(torch, hv, kv=args.kv)
+    full = None
+    if not args.eager and not args.no_full_run:
+        full = _spec_full_run(torch, sr, target, draft, args.kv, max_model_len=mml)
+    # the step's in-scope kernels: the fused attention launch (one per layer) is the
+    # headline roofline; acceptance and bookkeeping complete the in-scope step
     roof_attn_fused = attention_probe(torch, hv, kv=args.kv, fused=True)
+    roof_attn = attention_probe(torch, hv, kv=args.kv)
+    roof_inscope = inscope_step_probe(torch, hv, roof_attn_fused, target.g.num_layers)
+    # the projections' weight stream (not part of the verify+accept object)
+    roof_gemm = gemm_probe(torch, hv, target)
     step_bytes = target_step_bytes(target)
     step_us = verify_ms / args.steps * 1e3
     roof_step = {"bound": "hbm", "achieved": round(step_bytes / (step_us * 1e-6) / 1e9, 1),
                  "peak": HBM_PEAK_GBS, "unit": "GB/s",
                  "frac": round(step_bytes / (step_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                  "bytes_per_step": step_bytes, "step_us": round(step_us, 1),
-                 "what": "verify+accept step: the target's layer weights and LM head, each read "
-                         "once per step, over the step's HIP-event time"}
+                 "scope": "includes the projection and LM-head weights, which the "
+                          "verify+accept object leaves out (see roofline_inscope_step)",
+                 "what": "whole verify phase: the target's layer weights and LM head, each "
+                         "read once per step, over the phase's HIP-event time"}
     res = {
         "metric": METRIC,
         "value": round(tok_s, 2),
@@ -539,7 +620,8 @@ def bench_spec(args, torch, hv):
                    "acceptance": "reference", "kv_cache": args.kv,
                    "hip_graphs": graphs, "output_tokens_timed": emitted,
                    "context_range_timed": [len0, len1],
-                   "roofline_probe_context": 320},
+                   "max_model_len": mml if mml > 0 else "sized to the run",
+                   "roofline_probe_context": PROBE_CONTEXT},
         "verify_accept_step_us": round(verify_ms / args.steps * 1e3, 1),
         # published reference numbers (RTX 5090, trained Qwen3-8B / 0.6B, 65.5% acceptance,
         # prompt 256): benchmarks/results/20260322T104708Z-spec-decode-batch1.json:40,45-49;
@@ -553,18 +635,30 @@ def bench_spec(args, torch, hv):
         "context_len_end": len1,
         "wall_s": round(wall, 3),
         "init_s": round(init_s, 1),
-        "roofline": roof,
+        "roofline": roof_attn_fused,
+        "roofline_inscope_step": roof_inscope,
+        "roofline_attention_unfused": roof_attn,
+        "roofline_gemm": roof_gemm,
         "roofline_step": roof_step,
-        "roofline_attention": roof_attn,
-        "roofline_attention_fused": roof_attn_fused,
     }
+    if full is not None:
+        res["full_run"] = {
+            "what": "config 3 as stated: 64-token prompt to 256 completion tokens (the first "
+                    "from the prefill), every spec step timed",
+            "steps": full["steps"], "tokens_emitted": full["emitted"],
+            "value": round(full["emitted"] / (full["gpu_ms"] / 1e3), 2),
+            "unit": "accepted tok/s", "ms_per_step": round(full["gpu_ms"] / full["steps"], 4),
+            "acceptance_rate": round((full["emitted"] - full["steps"]) / (full["steps"] * gamma),
+                                     4),
+            "final_context": full["final_tokens"]}
     if args.draft != "forced" and not args.no_forced:
         # config 3's second mode: the draft is the target's first 28 layers plus
         # its LM head, so most drafts are accepted and the accept path (bonus
         # tokens, long commits) runs every step; a shorter timed run
         fdraft = q3.Qwen3Host(q3.QWEN3_8B, share_from=target, num_layers=28)
         fs = min(args.steps, 64)
-        f = _spec_run(torch, sr, target, fdraft, fs, 4, args.kv, not args.eager)
+        f = _spec_run(torch, sr, target, fdraft, fs, 4, args.kv, not args.eager,
+                      max_model_len=mml)
         res["forced_acceptance"] = {
             "draft": "target's first 28 layers + LM head", "steps": fs,
             "value": round(f["emitted"] / (f["gpu_ms"] / 1e3), 2), "unit": "accepted tok/s",
@@ -803,6 +897,95 @@ def attention_probe(torch, hv, kv: str = "auto", L: int = PROBE_CONTEXT, layers:
             "launches": reps * layers}
 
 
+def _accept_args(**kw):
+    """Arguments of the acceptance workload (bench_accept) at the spec step's shape."""
+    ns = argparse.Namespace(batch=1, gamma=3, mode="reference", logits="bf16", per_seq=False,
+                            temperature=0.6, top_k=0, top_p=1.0, chain=False,
+                            no_topk_hint=False, no_cpu_baseline=True, steps=200, warmup=20,
+                            cpu_seconds=0.0)
+    for k, v in kw.items():
+        setattr(ns, k, v)
+    return ns
+
+
+def bookkeeping_probe(torch, hv, context: int = PROBE_CONTEXT - 4, gamma: int = 3,
+                      out_len: int = 2, reps: int = 20):
+    """The spec step's bookkeeping launches at batch 1 (hs_spec_prealloc at the start of
+    the draft phase, hs_verify_prepare at the start of the verify phase, hs_spec_commit
+    after the acceptance), graph-timed together from a sequence of `context` tokens;
+    every replay commits `out_len` tokens (one accepted draft and the resample, the
+    typical outcome). Returns (µs per step, bytes per step): the state words, the
+    staging rows and the committed tokens the three launches read and write."""
+    dev = torch.device("cuda:0")
+    bs = 256
+    end = context + (reps + 2) * out_len + gamma + 2
+    W = (end + bs - 1) // bs + 1
+    st = hv.ops.SpecStateTensors(1, W, end + 8, W + 2, bs, -1, dev)
+    nblk = (context + bs - 1) // bs
+    bt = torch.full((1, W), -1, dtype=torch.int32)
+    bt[0, :nblk] = torch.arange(nblk, dtype=torch.int32)
+    st.block_tables.copy_(bt)
+    st.num_seq_blocks.fill_(nblk)
+    st.context_lens.fill_(context)
+    st.num_prompt.fill_(64)
+    st.max_tokens.fill_(1 << 30)
+    st.ignore_eos.fill_(1)
+    st.tokens.copy_(torch.randint(0, V, st.tokens.shape, generator=torch.Generator().manual_seed(5)))
+    ring = torch.zeros(W + 2, dtype=torch.int32)
+    ring[:W + 2 - nblk] = torch.arange(nblk, W + 2, dtype=torch.int32)
+    st.free_ring.copy_(ring)
+    st.free_hdr.copy_(torch.tensor([0, W + 2 - nblk], dtype=torch.int32))
+    ref = torch.zeros(W + 2, dtype=torch.int32)
+    ref[:nblk] = 1
+    st.ref_count.copy_(ref)
+    elig = torch.empty(1, dtype=torch.int32, device=dev)
+    draft = torch.randint(0, V, (1, gamma), dtype=torch.int64, device=dev)
+    out = torch.randint(0, V, (1, gamma + 1), dtype=torch.int64, device=dev)
+    olen = torch.full((1,), out_len, dtype=torch.int32, device=dev)
+
+    def step():
+        hv.ops.spec_prealloc(st, gamma, out=elig)
+        hv.ops.verify_prepare(st, draft, gamma)
+        hv.ops.spec_commit(st, gamma, out, olen, eligible=elig)
+
+    us = graph_time_us(torch, dev, step, reps)
+    R = gamma + 1
+    nbytes = (4 * 6 + 4 * W  # prealloc: lengths, counts, free header, table row, ref counts
+              + 8 + gamma * 8 + R * (8 + 8 + 4) + 2 * 2 * 4  # prepare: ids, positions, slots, cu
+              + R * 8 + 4 + out_len * 8 + 4 * 6)  # commit: emitted tokens in, tokens appended
+    return us, nbytes
+
+
+def inscope_step_probe(torch, hv, attn_roof: dict, layers: int):
+    """The verify+accept step's own work at batch 1, gamma 3, context PROBE_CONTEXT:
+    `layers` fused attention launches (q/k-norm + RoPE + KV store + attention, each
+    `attn_roof`'s bytes and graph-timed average), the fused acceptance call (bf16
+    target rows and f32 draft rows, (gamma+1)V*2 + gamma*V*4 bytes; inputs rotated so
+    every call reads HBM) and the bookkeeping launches (bookkeeping_probe). The
+    projection and LM-head weights are left out. achieved = in-scope bytes over the
+    sum of those kernels' graph-timed durations (each including its graph node's
+    dispatch gap, as in the step)."""
+    acc = bench_accept(_accept_args(), torch, hv)
+    acc_us = acc["value"]
+    acc_bytes = acc["roofline"]["bytes_per_step"]
+    bk_us, bk_bytes = bookkeeping_probe(torch, hv)
+    attn_us = layers * attn_roof["avg_launch_us"]
+    attn_bytes = layers * attn_roof["bytes_per_launch"]
+    nbytes = attn_bytes + acc_bytes + bk_bytes
+    us = attn_us + acc_us + bk_us
+    achieved = nbytes / (us * 1e-6) / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 5), "bytes_per_step": nbytes,
+            "us_per_step": round(us, 2),
+            "parts": {"attention": {"launches": layers, "bytes": attn_bytes,
+                                    "us": round(attn_us, 2)},
+                      "acceptance": {"bytes": acc_bytes, "us": round(acc_us, 2)},
+                      "bookkeeping": {"launches": 3, "bytes": bk_bytes, "us": round(bk_us, 2)}},
+            "what": f"verify+accept step without the projection weights: {layers} fused "
+                    f"attention launches at L={PROBE_CONTEXT}, the acceptance call, prealloc + "
+                    "verify staging + commit; graph-timed per part"}
+
+
 def profiled_traffic(kernel: str, workload: str):
     """HBM bytes per launch of `kernel` in `workload` from the committed rocprofv3
     counter summary profiles/traffic.md (FETCH_SIZE and WRITE_SIZE in KiB per
@@ -958,6 +1141,11 @@ def main(argv=None):
     ap.add_argument("--eager", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--max-model-len", type=int, default=4096,
+                    help="spec/adaptive: the runner's max_model_len (block tables, attention "
+                         "launch plans); the reference's benchmarks use 4096; 0 = sized to the run")
+    ap.add_argument("--no-full-run", action="store_true",
+                    help="spec: skip the 256-token full-run companion")
     ap.add_argument("--no-forced", action="store_true",
                     help="spec workload: skip the forced-acceptance companion run")
     ap.add_argument("--chain", action="store_true",
