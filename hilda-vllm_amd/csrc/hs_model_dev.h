@@ -45,13 +45,18 @@ __device__ __forceinline__ void norm_rope_pair(const uint16_t* src, const uint16
                  cs[64 + lane], eps, o1, o2);
 }
 
+// the e4m3fn code a cache with per-tensor scale `scale` stores for bf16 value a
+__device__ __forceinline__ uint8_t e4m3_of_bf16(uint16_t a, float scale) {
+#pragma clang fp contract(off)
+  return f32_to_e4m3fn_sat(bf(a) / scale);
+}
+
 template <bool kFp8>
 __device__ __forceinline__ void store_pair(uint8_t* base, int64_t elem, int lane, uint16_t a,
                                            uint16_t b, float scale) {
-#pragma clang fp contract(off)
   if constexpr (kFp8) {
-    base[elem + lane] = f32_to_e4m3fn_sat(bf(a) / scale);
-    base[elem + lane + 64] = f32_to_e4m3fn_sat(bf(b) / scale);
+    base[elem + lane] = e4m3_of_bf16(a, scale);
+    base[elem + lane + 64] = e4m3_of_bf16(b, scale);
   } else {
     uint16_t* p = reinterpret_cast<uint16_t*>(base) + elem;
     p[lane] = a;

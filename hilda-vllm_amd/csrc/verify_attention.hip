@@ -73,6 +73,7 @@ struct AttnArgs {
   int* sk_w0;                // balanced launch: first window of each workgroup [nwg + 1]
   int sk_nwg;                // balanced launch: workgroups
   int xcd_pack;              // per-tile grid: only workgroups x % xcd_pack == 0 work
+  unsigned* tickets;         // fused kernel: split-merge tickets per (sequence, kv head)
 };
 
 // The q/k-norm + RoPE + KV-store step run inside the per-tile kernel
@@ -606,17 +607,53 @@ __device__ __forceinline__ void merge_waves(const float (*s_m)[kRows], const flo
   }
 }
 
+// Merges the ns key-split partials of query row rr = qt*16 + row of tile
+// (b, kvh, qt) (query start qs) and writes its normalised output, dims d0 ..
+// d0 + 7: k_attn_combine's arithmetic, shared with the fused kernel's
+// in-kernel merge so that both give the same bits.
+__device__ __forceinline__ void combine_splits(const AttnArgs& a, int b, int kvh, int qt, int qs,
+                                               int ns, int row, int rr, int d0) {
+  const int64_t base = (((int64_t)b * a.Hkv + kvh) * a.qtiles + qt) * a.nsplit;
+  float M = -INFINITY;
+  for (int s = 0; s < ns; ++s) M = fmaxf(M, a.part_ml[((base + s) * kRows + row) * 2]);
+  const float Mb = (M == -INFINITY) ? 0.0f : M;
+  float L = 0.0f, o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int s = 0; s < ns; ++s) {
+    const int64_t pidx = (base + s) * kRows + row;
+    const float f = __builtin_amdgcn_exp2f(a.part_ml[pidx * 2] - Mb);
+    L += a.part_ml[pidx * 2 + 1] * f;
+    const float4 x0 = *reinterpret_cast<const float4*>(a.part_o + pidx * kD + d0);
+    const float4 x1 = *reinterpret_cast<const float4*>(a.part_o + pidx * kD + d0 + 4);
+    o[0] += x0.x * f; o[1] += x0.y * f; o[2] += x0.z * f; o[3] += x0.w * f;
+    o[4] += x1.x * f; o[5] += x1.y * f; o[6] += x1.z * f; o[7] += x1.w * f;
+  }
+  const float inv = (L > 0.0f) ? a.v_scale / L : 0.0f;
+  const int oi = rr / a.G, oh = kvh * a.G + rr % a.G;
+  union {
+    uint16_t h[8];
+    uint4 u;
+  } ob;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) ob.h[t] = f32_to_bf16_rne(o[t] * inv);
+  *reinterpret_cast<uint4*>(a.out + (int64_t)(qs + oi) * a.o_st + (int64_t)oh * a.o_sh + d0) = ob.u;
+}
+
 // Attends query tile t over keys [klo, khi) with the 8 waves of the workgroup
 // (wave w takes windows w, w + 8, ...), merges the waves and writes the
 // normalised output (pslot < 0) or the unnormalised partial (o, running max,
 // sum) at partial slot pslot. s_bt as for wave_walk. s_raw holds the per-wave
 // K and V window tiles and, after the key loop, the per-wave partial outputs.
+// kQkv (the fused kernel, one query tile): the prologue runs inside the walk,
+// and a partial (the tile's keys span ns > 1 splits) is merged in the
+// kernel: the last of the tile's ns workgroups to take its ticket
+// (a.tickets[b * Hkv + kvh], zero between calls) merges them all.
 template <bool kFp8, int kG, bool kQkv = false>
 __device__ __forceinline__ void attend_keys(const AttnArgs& a, const TileRef& t, int klo, int khi,
                                             int64_t pslot, uint8_t* s_raw, float (*s_m)[kRows],
                                             float (*s_l)[kRows], const int* s_bt, int bt_cap,
                                             const QkvArgs* qa = nullptr,
-                                            QkvLoads* ql = nullptr, uint16_t* s_q = nullptr) {
+                                            QkvLoads* ql = nullptr, uint16_t* s_q = nullptr,
+                                            int ns = 1) {
   const int G = kG ? kG : a.G;
   constexpr int kTileB = AttnLds<kFp8>::kTileB;
   const int kvh = t.kvh, qs = t.qs, rows = t.rows;
@@ -654,43 +691,66 @@ __device__ __forceinline__ void attend_keys(const AttnArgs& a, const TileRef& t,
   }
   __syncthreads();
   // merge the waves: thread handles row tid/16, dims 4(tid%16) .. +4 and
-  // 64 + 4(tid%16) .. +4 (the other threads have no row; there is no barrier
-  // below)
+  // 64 + 4(tid%16) .. +4 (the other threads have no row)
   const int row = tid >> 4;
   const int rr = r0 + row;
-  if (tid >= kRows * 16 || rr >= rows) return;
-  const int d0 = (tid & 15) * 4;
-  // branch-free over the first 4 or all 8 waves, so that all LDS reads go out
-  // together: a wave without keys contributes weight 0 and reads the zero
-  // bytes (one address for every lane)
-  float M, L, o[8];
-  if (nact <= 4)
-    merge_waves<4>(s_m, s_l, s_o, s_zero, kWaveO, nact, row, d0, M, L, o);
-  else
-    merge_waves<kAW>(s_m, s_l, s_o, s_zero, kWaveO, nact, row, d0, M, L, o);
-  const int oi = rr / G, oh = kvh * G + rr % G;
-  if (pslot < 0) {
-    const float inv = (L > 0.0f) ? a.v_scale / L : 0.0f;
-    union {
-      uint16_t h[4];
-      uint2 u;
-    } ob0, ob1;
+  const bool act = tid < kRows * 16 && rr < rows;
+  if (act) {
+    const int d0 = (tid & 15) * 4;
+    // branch-free over the first 4 or all 8 waves, so that all LDS reads go
+    // out together: a wave without keys contributes weight 0 and reads the
+    // zero bytes (one address for every lane)
+    float M, L, o[8];
+    if (nact <= 4)
+      merge_waves<4>(s_m, s_l, s_o, s_zero, kWaveO, nact, row, d0, M, L, o);
+    else
+      merge_waves<kAW>(s_m, s_l, s_o, s_zero, kWaveO, nact, row, d0, M, L, o);
+    const int oi = rr / G, oh = kvh * G + rr % G;
+    if (pslot < 0) {
+      const float inv = (L > 0.0f) ? a.v_scale / L : 0.0f;
+      union {
+        uint16_t h[4];
+        uint2 u;
+      } ob0, ob1;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      ob0.h[t] = f32_to_bf16_rne(o[t] * inv);
-      ob1.h[t] = f32_to_bf16_rne(o[4 + t] * inv);
+      for (int t = 0; t < 4; ++t) {
+        ob0.h[t] = f32_to_bf16_rne(o[t] * inv);
+        ob1.h[t] = f32_to_bf16_rne(o[4 + t] * inv);
+      }
+      uint16_t* po = a.out + (int64_t)(qs + oi) * a.o_st + (int64_t)oh * a.o_sh + d0;
+      *reinterpret_cast<uint2*>(po) = ob0.u;
+      *reinterpret_cast<uint2*>(po + 64) = ob1.u;
+    } else {
+      const int64_t pidx = pslot * kRows + row;
+      float* po = a.part_o + pidx * kD + d0;
+      *reinterpret_cast<float4*>(po) = make_float4(o[0], o[1], o[2], o[3]);
+      *reinterpret_cast<float4*>(po + 64) = make_float4(o[4], o[5], o[6], o[7]);
+      if ((tid & 15) == 0) {
+        a.part_ml[pidx * 2] = M;
+        a.part_ml[pidx * 2 + 1] = L;
+      }
     }
-    uint16_t* po = a.out + (int64_t)(qs + oi) * a.o_st + (int64_t)oh * a.o_sh + d0;
-    *reinterpret_cast<uint2*>(po) = ob0.u;
-    *reinterpret_cast<uint2*>(po + 64) = ob1.u;
-  } else {
-    const int64_t pidx = pslot * kRows + row;
-    float* po = a.part_o + pidx * kD + d0;
-    *reinterpret_cast<float4*>(po) = make_float4(o[0], o[1], o[2], o[3]);
-    *reinterpret_cast<float4*>(po + 64) = make_float4(o[4], o[5], o[6], o[7]);
-    if ((tid & 15) == 0) {
-      a.part_ml[pidx * 2] = M;
-      a.part_ml[pidx * 2 + 1] = L;
+  }
+  if constexpr (kQkv) {
+    if (pslot >= 0) {
+      // in-kernel merge of the ns splits: every thread's partial stores are
+      // made visible at agent scope before the workgroup takes its ticket;
+      // the last workgroup acquires them all and merges
+      __shared__ int s_last;
+      unsigned* ticket = a.tickets + (int64_t)t.b * a.Hkv + kvh;
+      __threadfence();
+      __syncthreads();
+      if (tid == 0) {
+        __threadfence();
+        const unsigned prev =
+            __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = prev + 1 == (unsigned)ns;
+      }
+      __syncthreads();
+      if (!s_last) return;
+      __threadfence();
+      if (tid == 0) __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (act) combine_splits(a, t.b, kvh, t.qt, qs, ns, row, rr, (tid & 15) * 8);
     }
   }
 }
@@ -763,43 +823,65 @@ __global__ __launch_bounds__(kAT) void k_verify_attn(const int32_t* cu_q, const 
   attend_keys<kFp8, kG>(a, t, lo, hi, pslot, s_raw, s_m, s_l, s_bt, kBtCap);
 }
 
-// k_verify_attn with the q/k-norm + RoPE + KV-store step of its tile's tokens
-// in the prologue (qkv_load at the start, qkv_finish after the block-table
-// barrier): the host launches it only where every
-// (sequence, kv head) is one workgroup (one query tile, no key split), which
-// then alone writes and reads its new k/v rows. Replaces hs_qk_norm_rope_store
-// + hs_verify_attention (two launches) for decode and verify steps.
+// k_verify_attn with the q/k-norm + RoPE + KV-store step of its tile's
+// tokens in the prologue (qkv_load at the start, qkv_finish after the
+// block-table barrier): the host launches it where one query tile holds
+// every query row of each (sequence, kv head). The grid is (kv head x xcd
+// pack, key split, sequence); split s holds keys [s * split_len, (s + 1) *
+// split_len) of the sequence, so a sequence whose keys fit one split is one
+// workgroup per kv head (which alone writes and reads its new k/v rows) and
+// the other splits' workgroups return at once; longer sequences write
+// partials that the last of their workgroups merges (attend_keys), every
+// workgroup of the sequence storing the new k/v rows before it reads them
+// (the same bytes). With xcd_shift = 3 the workgroups that work are those
+// with x % 8 == split % 8, so the kv heads of one split are dispatched to one
+// XCD and consecutive splits to different XCDs (placement only). Replaces
+// hs_qk_norm_rope_store + hs_verify_attention (+ the split combine) for
+// decode and verify steps.
 template <bool kFp8, int kG>
 __global__ __launch_bounds__(kAT) void k_verify_attn_qkv(const int32_t* cu_q, const int32_t* cu_k,
                                                          const int32_t* bt, int bt_stride,
                                                          int xcd_shift, int bs_shift,
-                                                         int bt_width, int nbt_split, AttnArgs a,
-                                                         QkvArgs qa) {
+                                                         int bt_width, int nbt_split, int split_len,
+                                                         AttnArgs a, QkvArgs qa) {
   __shared__ __attribute__((aligned(16))) uint8_t s_raw[AttnLds<kFp8>::kRawBytes];
   __shared__ float s_m[kAW][kRows], s_l[kAW][kRows];
   __shared__ int s_bt[kBtCap];
   __shared__ __attribute__((aligned(16))) uint16_t s_q[kRows * kD];
   const int G = kG ? kG : a.G;
-  if (blockIdx.x & ((1u << xcd_shift) - 1)) return;
+  const unsigned xm = (1u << xcd_shift) - 1;
+  if ((blockIdx.x & xm) != (blockIdx.y & xm)) return;
   const int kvh = blockIdx.x >> xcd_shift;
+  const int split = blockIdx.y;
   const int b = blockIdx.z;
   const int tid = threadIdx.x;
   const int cq0 = cu_q[b], cq1 = cu_q[b + 1], ck0 = cu_k[b], ck1 = cu_k[b + 1];
+  const int lo = split * split_len;
+  const int bt0 = split == 0 ? 0 : key_block(lo, bs_shift, a.block_size);
   int nbt = nbt_split;
-  if (nbt > bt_width) nbt = bt_width;
+  if (nbt > bt_width - bt0) nbt = bt_width - bt0;
   const int32_t* btrow = bt + (int64_t)b * bt_stride;
-  const int bi = tid < bt_width ? tid : bt_width - 1;
+  const int bi = bt0 + tid < bt_width ? bt0 + tid : bt_width - 1;
   const int bt_mine = btrow[bi];
   asm volatile("" ::"s"(a.q), "s"(a.c_sh), "s"(a.scale_log2), "s"(a.sk_pre));
   asm volatile("" ::"v"(bt_mine), "v"(cq0), "v"(cq1), "v"(ck0), "v"(ck1));
   const TileRef t = tile_ref_of(b, kvh, 0, G, cq0, cq1, ck0, ck1);
   if (tid < nbt) s_bt[tid] = bt_mine;
-  for (int i = tid + kAT; i < nbt; i += kAT) s_bt[i] = btrow[i];
-  if (t.rows <= 0 || t.Lk <= 0) return;  // no query token: nothing to store or attend
+  for (int i = tid + kAT; i < nbt; i += kAT) s_bt[i] = btrow[bt0 + i];
+  // no query token or no key of this split: nothing to store or attend
+  if (t.rows <= 0 || t.Lk <= 0 || lo >= t.Lk) return;
+  int hi = lo + split_len;
+  const int vis = tile_keys(t, G);
+  if (vis < hi) hi = vis;
   QkvLoads ql;
   qkv_load(a, qa, t, kvh, G, ql);
-  attend_keys<kFp8, kG, true>(a, t, 0, tile_keys(t, G), -1, s_raw, s_m, s_l, s_bt, kBtCap, &qa,
-                              &ql, s_q);
+  // splits holding keys (at most the launched ones: keys past the declared
+  // maximum are not attended, as in the per-tile kernel)
+  int ns = (t.Lk + split_len - 1) / split_len;
+  if (ns > (int)gridDim.y) ns = (int)gridDim.y;
+  const int64_t pslot = ns <= 1 ? -1 : ((int64_t)b * a.Hkv + kvh) * a.nsplit + split;
+  attend_keys<kFp8, kG, true>(a, t, lo, hi, pslot, s_raw, s_m, s_l, s_bt, kBtCap, &qa, &ql, s_q,
+                              ns);
 }
 
 // Balanced launch: one workgroup per CU. The 32-key windows of all tiles
@@ -1062,32 +1144,9 @@ __global__ __launch_bounds__(kRows * 16) void k_attn_combine(AttnArgs a) {
   const int ns = (Lk + a.split_len - 1) / a.split_len;
   if (ns <= 1) return;
   const int row = tid >> 4;
-  const int d0 = (tid & 15) * 8;
   const int rr = r0 + row;
   if (rr >= rows) return;
-  const int64_t base = (((int64_t)b * a.Hkv + kvh) * a.qtiles + qt) * a.nsplit;
-  float M = -INFINITY;
-  for (int s = 0; s < ns; ++s) M = fmaxf(M, a.part_ml[((base + s) * kRows + row) * 2]);
-  const float Mb = (M == -INFINITY) ? 0.0f : M;
-  float L = 0.0f, o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  for (int s = 0; s < ns; ++s) {
-    const int64_t pidx = (base + s) * kRows + row;
-    const float f = __builtin_amdgcn_exp2f(a.part_ml[pidx * 2] - Mb);
-    L += a.part_ml[pidx * 2 + 1] * f;
-    const float4 x0 = *reinterpret_cast<const float4*>(a.part_o + pidx * kD + d0);
-    const float4 x1 = *reinterpret_cast<const float4*>(a.part_o + pidx * kD + d0 + 4);
-    o[0] += x0.x * f; o[1] += x0.y * f; o[2] += x0.z * f; o[3] += x0.w * f;
-    o[4] += x1.x * f; o[5] += x1.y * f; o[6] += x1.z * f; o[7] += x1.w * f;
-  }
-  const float inv = (L > 0.0f) ? a.v_scale / L : 0.0f;
-  const int oi = rr / a.G, oh = kvh * a.G + rr % a.G;
-  union {
-    uint16_t h[8];
-    uint4 u;
-  } ob;
-#pragma unroll
-  for (int t = 0; t < 8; ++t) ob.h[t] = f32_to_bf16_rne(o[t] * inv);
-  *reinterpret_cast<uint4*>(a.out + (int64_t)(qs + oi) * a.o_st + (int64_t)oh * a.o_sh + d0) = ob.u;
+  combine_splits(a, b, kvh, qt, qs, ns, row, rr, (tid & 15) * 8);
 }
 
 template <bool kFp8>
@@ -1110,20 +1169,22 @@ static void launch_attn(int G, dim3 grid, hipStream_t s, const AttnArgs& a) {
 }
 
 template <bool kFp8>
-static void launch_attn_qkv(int G, dim3 grid, hipStream_t s, const AttnArgs& a, const QkvArgs& qa) {
+static void launch_attn_qkv(int G, dim3 grid, hipStream_t s, const AttnArgs& a,
+                            const QkvArgs& qa) {
   const int bts = (int)a.bt_stride;
   const int xs = a.xcd_pack == 8 ? 3 : 0;
   int nbt = (a.split_len + a.block_size - 1) / a.block_size + 1;
   if (nbt > kBtCap) nbt = kBtCap;
+  const int sl = a.split_len;
   switch (G) {
     case 2: hipLaunchKernelGGL((k_verify_attn_qkv<kFp8, 2>), grid, dim3(kAT), 0, s, a.cu_q, a.cu_k, a.bt,
-                                 bts, xs, a.bs_shift, a.bt_width, nbt, a, qa); break;
+                                 bts, xs, a.bs_shift, a.bt_width, nbt, sl, a, qa); break;
     case 4: hipLaunchKernelGGL((k_verify_attn_qkv<kFp8, 4>), grid, dim3(kAT), 0, s, a.cu_q, a.cu_k, a.bt,
-                                 bts, xs, a.bs_shift, a.bt_width, nbt, a, qa); break;
+                                 bts, xs, a.bs_shift, a.bt_width, nbt, sl, a, qa); break;
     case 8: hipLaunchKernelGGL((k_verify_attn_qkv<kFp8, 8>), grid, dim3(kAT), 0, s, a.cu_q, a.cu_k, a.bt,
-                                 bts, xs, a.bs_shift, a.bt_width, nbt, a, qa); break;
+                                 bts, xs, a.bs_shift, a.bt_width, nbt, sl, a, qa); break;
     default: hipLaunchKernelGGL((k_verify_attn_qkv<kFp8, 0>), grid, dim3(kAT), 0, s, a.cu_q, a.cu_k, a.bt,
-                                  bts, xs, a.bs_shift, a.bt_width, nbt, a, qa); break;
+                                  bts, xs, a.bs_shift, a.bt_width, nbt, sl, a, qa); break;
   }
 }
 
@@ -1192,6 +1253,14 @@ static void attn_plan(int B, int Hkv, int qtiles, int max_seqlen_k, int* nsplit,
   *nsplit = (int)((max_seqlen_k + len - 1) / len);
   if (*nsplit < 1) *nsplit = 1;
 }
+
+// The first kTicketBytes of an attention workspace hold the fused kernel's
+// split-merge tickets (one 32-bit counter per (sequence, kv head), zero
+// between calls: the workgroup that merges a tile resets its counter); the
+// partial results follow. Fused calls with more (sequence, kv head) pairs
+// than tickets run as the store and attention launches.
+constexpr size_t kTicketBytes = 16384;
+constexpr int kTicketSlots = (int)(kTicketBytes / sizeof(unsigned));
 
 // Scratch of hs_verify_attention_noalloc: the partial results of key splits
 // or of the balanced launch's shared tile pieces, which hs_verify_attention
@@ -1294,6 +1363,7 @@ static int attn_prepare(const void* q, int64_t q_stride_tok, int64_t q_stride_he
   a.out = static_cast<uint16_t*>(out);
   a.o_st = out_stride_tok;
   a.o_sh = out_stride_head;
+  a.tickets = static_cast<unsigned*>(workspace);
   return HS_OK;
 }
 
@@ -1313,7 +1383,7 @@ size_t hs_verify_attention_workspace_size(int num_seqs, int num_q_heads, int num
   bool heads = false;
   const int nwg = attn_sk_plan(num_seqs, num_kv_heads, qtiles, max_seqlen_k, &heads);
   const size_t sk = nwg ? attn_sk_workspace(num_seqs, num_kv_heads, qtiles, nwg, heads) : 0;
-  return classic > sk ? classic : sk;
+  return kTicketBytes + (classic > sk ? classic : sk);
 }
 
 int hs_verify_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
@@ -1344,7 +1414,7 @@ int hs_verify_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_he
   if (nwg && workspace && workspace_bytes >= need &&
       (max_seqlen_k + block_size - 1) / block_size + 1 <= kSkBtCap) {
     const size_t slots = 2 * (size_t)nwg * kRows * (heads ? num_kv_heads : 1);
-    a.part_o = static_cast<float*>(workspace);
+    a.part_o = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + kTicketBytes);
     a.part_ml = a.part_o + slots * kD;
     const int ntiles = num_seqs * a.qtiles * (heads ? 1 : num_kv_heads);
     a.sk_pre = reinterpret_cast<int*>(a.part_ml + slots * 2);
@@ -1368,8 +1438,9 @@ int hs_verify_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_he
     return hipGetLastError() == hipSuccess ? HS_OK : HS_ERR_LAUNCH;
   }
   const size_t parts = (size_t)num_seqs * num_kv_heads * a.qtiles * a.nsplit * kRows;
-  a.part_o = static_cast<float*>(workspace);
-  a.part_ml = workspace ? static_cast<float*>(workspace) + parts * kD : nullptr;
+  a.part_o = workspace ? reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + kTicketBytes)
+                       : nullptr;
+  a.part_ml = workspace ? a.part_o + parts * kD : nullptr;
   a.sk_pre = nullptr;
   a.sk_w0 = nullptr;
   a.sk_nwg = 0;
@@ -1426,8 +1497,14 @@ int hs_qk_norm_rope_attend(const void* qkv, int64_t token_stride, int num_tokens
   const int nwg = attn_sk_plan(num_seqs, num_kv_heads, a.qtiles, max_seqlen_k, &heads);
   const bool sk = nwg && workspace && workspace_bytes >= need &&
                   (max_seqlen_k + block_size - 1) / block_size + 1 <= kSkBtCap;
-  const int64_t wgs = (int64_t)num_kv_heads * num_seqs;
-  if (sk || a.nsplit > 1 || a.qtiles > 1 || max_seqlen_q > kRows) {
+  const int64_t pairs = (int64_t)num_kv_heads * num_seqs;
+  // one launch where one query tile holds every query row of a (sequence, kv
+  // head) and the classic grid serves the call; key splits need the
+  // workspace (partials and tickets)
+  const bool fused = !sk && a.qtiles == 1 && max_seqlen_q * a.G <= kRows &&
+                     (a.nsplit == 1 || (workspace && workspace_bytes >= need &&
+                                        pairs <= kTicketSlots));
+  if (!fused) {
     // a (sequence, kv head) over several workgroups: the store first, then the
     // attention over the stored cache
     const int rc = hs_qk_norm_rope_store(
@@ -1457,13 +1534,20 @@ int hs_qk_norm_rope_attend(const void* qkv, int64_t token_stride, int num_tokens
   qa.v_scale = v_scale;
   qa.Hq = num_q_heads;
   qa.cs_rows = cos_sin_rows;
-  a.part_o = nullptr;
-  a.part_ml = nullptr;
+  if (a.nsplit > 1) {
+    const size_t parts = (size_t)num_seqs * num_kv_heads * a.nsplit * kRows;
+    a.part_o = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + kTicketBytes);
+    a.part_ml = a.part_o + parts * kD;
+  } else {
+    a.part_o = nullptr;
+    a.part_ml = nullptr;
+  }
   a.sk_pre = nullptr;
   a.sk_w0 = nullptr;
   a.sk_nwg = 0;
-  a.xcd_pack = (wgs <= 32) ? 8 : 1;  // as hs_verify_attention's per-tile grid
-  const dim3 grid(a.xcd_pack * num_kv_heads, 1, num_seqs);
+  // kv heads of one split packed onto one XCD when they fit its 32 CUs
+  a.xcd_pack = (pairs <= 32) ? 8 : 1;
+  const dim3 grid(a.xcd_pack * num_kv_heads, a.nsplit, num_seqs);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (a.fp8)
     launch_attn_qkv<true>(a.G, grid, s, a, qa);

@@ -8,10 +8,15 @@
  *
  * Workspaces: query the size with the matching *_workspace_size() function
  * and pass a buffer at least that large. Two calls that share one workspace
- * must not overlap in time. Two kinds:
- *  - hs_sampler and hs_verify_attention: the workspace only carries partial
- *    results from one launch of a call to the next launch of the same call;
- *    it needs no initialisation and may be shared between these calls.
+ * must not overlap in time. Three kinds:
+ *  - hs_sampler: the workspace only carries partial results from one launch
+ *    of a call to the next launch of the same call; it needs no
+ *    initialisation.
+ *  - hs_verify_attention and hs_qk_norm_rope_attend: likewise, except that
+ *    its first 16 KiB hold counters of the fused call's in-kernel merge of
+ *    key splits; they must be zero before the first call and every call
+ *    leaves them zero. These two entry points may share a workspace with
+ *    each other but not with any other entry point.
  *  - hs_spec_accept and hs_spec_commit: the workspace also carries state from
  *    one call to the next. It must be zero-filled before its first use, every
  *    call leaves it ready for the next (so the calls can be recorded into a
@@ -153,11 +158,12 @@ int hs_sampler(const void* logits, int logits_dtype, int64_t logits_row_stride,
 /*               most INT32_MAX elements); entries outside [0, num_blocks)  */
 /*               are treated as empty.                                       */
 /* cu_seqlens_q/k: int32 [num_seqs + 1] prefix sums of query/key lengths.    */
-/* The workspace (size from hs_verify_attention_workspace_size) holds the    */
-/* partial results of key splits (or of the pieces of the one-workgroup-per- */
-/* CU launch used for large calls); it needs no initialisation. With none,  */
-/* or a smaller one, the call uses the per-tile grid and returns             */
-/* HS_ERR_WORKSPACE if that grid splits the keys.                            */
+/* The workspace (size from hs_verify_attention_workspace_size) holds, after */
+/* 16 KiB of merge counters (zero-filled before the first call, left zero),  */
+/* the partial results of key splits (or of the pieces of the one-workgroup- */
+/* per-CU launch used for large calls). With none, or a smaller one, the     */
+/* call uses the per-tile grid and returns HS_ERR_WORKSPACE if that grid     */
+/* splits the keys.                                                          */
 /* ------------------------------------------------------------------------ */
 size_t hs_verify_attention_workspace_size(int num_seqs, int num_q_heads, int num_kv_heads,
                                           int max_seqlen_q, int max_seqlen_k);
@@ -184,6 +190,7 @@ int hs_verify_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_he
 /* returns HS_ERR_SCRATCH_LIMIT. Every call on one GPU shares that GPU's     */
 /* scratch: calls that overlap in time on one GPU (two streams) race.        */
 /* The scratch needs no clearing: each call writes the partials it reads.    */
+/* (It starts zero-filled, as a workspace of hs_verify_attention must.)     */
 int hs_verify_attention_noalloc(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
                                 const void* k_cache, const void* v_cache, int kv_dtype,
                                 int64_t cache_stride_block, int64_t cache_stride_tok,
@@ -370,12 +377,15 @@ int hs_qk_norm_rope_store(const void* qkv, int64_t token_stride, int num_q_heads
 /* hs_qk_norm_rope_store followed by hs_verify_attention on the stored cache */
 /* (Qwen3Attention.forward, mini_vllm/models/qwen3.py:83-86: q_norm, k_norm,  */
 /* rotary_emb, then Attention.forward's store_kvcache and paged attention,    */
-/* mini_vllm/layers/attention.py:59-90, :145-160), as one launch where every */
-/* (sequence, kv head) fits one workgroup (one 16-row query tile, keys not   */
-/* split; decode and verify steps): that workgroup normalises and rotates   */
-/* its q rows in LDS and stores its kv head's k/v rows of the sequence's    */
-/* query tokens before reading them. Other calls run the two launches, with */
-/* q_out receiving q. Same outputs and cache contents either way.           */
+/* mini_vllm/layers/attention.py:59-90, :145-160), as one launch where one   */
+/* 16-row query tile holds every query row of a (sequence, kv head) (decode */
+/* and verify steps): each workgroup normalises and rotates its q rows in   */
+/* LDS and stores its kv head's k/v rows of the sequence's query tokens     */
+/* before reading them; keys past one split of the launch plan are spread   */
+/* over several workgroups whose partial results the last of them merges    */
+/* (the workspace's merge counters). Other calls run the two launches (and  */
+/* the split combine), with q_out receiving q. Same outputs and cache        */
+/* contents either way.                                                      */
 /* qkv: [num_tokens, (Hq + 2 Hkv) * 128] bf16 holding the query tokens of    */
 /* the sequences in cu_seqlens_q order (num_tokens = cu_seqlens_q[num_seqs]), */
 /* cos_sin: [cos_sin_rows, 128] f32 (cos | sin), every position below       */
