@@ -108,7 +108,11 @@ struct AcceptArgs {
 struct SmallSync {
   uint64_t start;  // epoch << 32 | workgroups of the current launch that started
   uint32_t err;
-  uint32_t pad[61];
+  // polls a thread of a single-launch acceptance may spend waiting, over all
+  // its waits of one launch: 0 (a zero-filled workspace) the default budget,
+  // n > 0 a budget of n - 1 (set from the host to test the failure path)
+  uint32_t spin_limit;
+  uint32_t pad[60];
 };
 
 struct Work {

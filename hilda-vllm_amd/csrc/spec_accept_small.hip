@@ -48,7 +48,38 @@ namespace hs {
 
 namespace {
 
+// polls a thread may spend waiting over all its waits of one launch (unless
+// the workspace's spin_limit word sets another budget)
 constexpr uint32_t kSpinLimit = 1u << 20;
+// tags carry an epoch in bits 0..30; a word published by a workgroup whose
+// own waits failed carries the tag with this bit set, so that its readers
+// fail at once instead of taking values computed from incomplete data
+constexpr uint32_t kPoison = 0x80000000u;
+
+// the launch's tag from the entry word's epoch: never 0 (a zeroed word) and
+// never with kPoison set
+__device__ __forceinline__ uint32_t launch_tag(uint64_t start) {
+  return (uint32_t)((start >> 32) % 0x7fffffffull) + 1u;
+}
+
+// the wait budget of this launch (SmallSync::spin_limit)
+__device__ __forceinline__ uint32_t spin_budget(const SmallSync* sy) {
+  const uint32_t w = __hip_atomic_load(const_cast<uint32_t*>(&sy->spin_limit), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+  return w ? w - 1u : kSpinLimit;
+}
+
+// marks the workgroup's outputs invalid (its LDS flag) and the workspace's
+// sticky error word
+__device__ __forceinline__ void fail_wait(SmallSync* sy, int* bad) {
+  *bad = 1;
+  __hip_atomic_store(&sy->err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// the workgroup's flag as other waves may have set it (no barrier between)
+__device__ __forceinline__ bool is_bad(int* bad) {
+  return __hip_atomic_load(bad, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0;
+}
 
 __device__ __forceinline__ void put_u64(uint64_t* p, uint64_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -63,13 +94,15 @@ __device__ __forceinline__ uint64_t tagged(uint32_t tag, uint32_t payload) {
 // Reads the N tagged words at base[c * N + k] of the NC chunks
 // c = lane + i * 64 (chunks past nchunk read chunk 0 and are ignored) until
 // every used word carries `tag`. All loads of a round are issued before any is
-// waited for. The wait is bounded: when it runs out, the workgroup's flag
-// *bad (LDS) and the workspace's error flag are set.
+// waited for. The wait is bounded: it gives up at once when the workgroup's
+// flag *bad (LDS) is set or a word carries the poisoned tag, and when the
+// thread's polls this launch (*spent) reach `limit`; giving up sets *bad and
+// the workspace's error flag.
 template <int NC, int N>
 __device__ __forceinline__ void read_tagged(const uint64_t* base, int nchunk, int lane,
                                             uint32_t tag, uint32_t (&out)[NC][N], SmallSync* sy,
-                                            int* bad) {
-  for (uint32_t spins = 0;; ++spins) {
+                                            int* bad, uint32_t& spent, uint32_t limit) {
+  for (;;) {
     uint64_t v[NC][N];
 #pragma unroll
     for (int i = 0; i < NC; ++i) {
@@ -78,22 +111,24 @@ __device__ __forceinline__ void read_tagged(const uint64_t* base, int nchunk, in
 #pragma unroll
       for (int k = 0; k < N; ++k) v[i][k] = get_u64(base + (int64_t)cc * N + k);
     }
-    bool ok = true;
+    bool ok = true, poisoned = false;
 #pragma unroll
     for (int i = 0; i < NC; ++i) {
       const bool used = lane + i * kWave < nchunk;
 #pragma unroll
       for (int k = 0; k < N; ++k) {
+        const uint32_t t = (uint32_t)(v[i][k] >> 32);
         out[i][k] = used ? (uint32_t)v[i][k] : 0u;
-        ok = ok && (!used || (uint32_t)(v[i][k] >> 32) == tag);
+        ok = ok && (!used || t == tag);
+        poisoned = poisoned || (used && t == (tag | kPoison));
       }
     }
     if (ok) return;
-    if (spins == kSpinLimit) {
-      *bad = 1;
-      __hip_atomic_store(&sy->err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (poisoned || spent >= limit || is_bad(bad)) {
+      fail_wait(sy, bad);
       return;
     }
+    ++spent;
     __builtin_amdgcn_s_sleep(1);
   }
 }
@@ -147,13 +182,15 @@ __device__ __forceinline__ uint64_t* samp_words(const Work& W, int rows, int uni
 // Row descriptor from the chunk statistics of one row (one wave): the fold of
 // fold_row_desc (hs_sampler_dev.h) over the tagged copies.
 __device__ __forceinline__ RowDesc fold_row_tagged(const Problem& P, const Work& W, int row,
-                                                   uint32_t tag, int lane, int* bad) {
+                                                   uint32_t tag, int lane, int* bad,
+                                                   uint32_t& spent, uint32_t limit) {
   float M = -INFINITY;
   float mc[4];
   uint64_t ec[4];
   // nchunk <= 256 (one workgroup per CU): at most 4 chunks per lane
   uint32_t w[4][3];
-  read_tagged<4, 3>(stat_words(W, row, P.nchunk), P.nchunk, lane, tag, w, W.sync, bad);
+  read_tagged<4, 3>(stat_words(W, row, P.nchunk), P.nchunk, lane, tag, w, W.sync, bad, spent,
+                    limit);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     mc[i] = lane + i * kWave < P.nchunk ? u2f(w[i][0]) : -INFINITY;
@@ -213,6 +250,16 @@ __global__ __launch_bounds__(SmallShape<G>::kThreads) void k_accept_small(Proble
   const bool in = i0 < P.V;
   const T* lrow = reinterpret_cast<const T*>(P.logits) + (int64_t)unit * R * P.row_stride;
   const float* qrow = A.q + (int64_t)unit * G * A.q_stride;
+  const uint32_t limit = spin_budget(sy);
+  uint32_t spent = 0;
+  // the unit's outputs are marked invalid first (by its chunk-0 workgroup,
+  // acknowledged before that workgroup publishes anything): only a workgroup
+  // whose own waits all succeeded writes them again at the end, so a unit
+  // without such a writer keeps -1 / 0 rather than a partial write
+  if (c == 0 && tid == 0) {
+    __hip_atomic_store(&A.nacc_out[unit], -1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&A.len_out[unit], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 
   // small inputs of wave 0 (it takes the decision): draft tokens and
   // acceptance uniforms, issued first so that their waits cover only them
@@ -279,7 +326,7 @@ __global__ __launch_bounds__(SmallShape<G>::kThreads) void k_accept_small(Proble
     if (lane == 0) s_m[wid][s] = m[s];
   }
   if (tid == 0) {
-    s_tag = (uint32_t)(start >> 32) + 1u;  // tag 0 never matches a zeroed word
+    s_tag = launch_tag(start);
     s_bad = entry_bad ? 1 : 0;
   }
   __syncthreads();
@@ -302,6 +349,9 @@ __global__ __launch_bounds__(SmallShape<G>::kThreads) void k_accept_small(Proble
   }
   __syncthreads();
   if (gt == 0) {
+    // the invalid marks above reach memory before this workgroup's first word
+    if (c == 0 && tid == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    const uint32_t ptag = s_bad ? (tag | kPoison) : tag;
 #pragma unroll
     for (int s = 0; s < RPG; ++s) {
       const int j = grp + NG * s;
@@ -309,16 +359,16 @@ __global__ __launch_bounds__(SmallShape<G>::kThreads) void k_accept_small(Proble
         const uint64_t* ge = &s_e[grp * 4][0];
         const uint64_t es = ge[0 * RPG + s] + ge[1 * RPG + s] + ge[2 * RPG + s] + ge[3 * RPG + s];
         uint64_t* sw = stat_words(W, unit * R + j, P.nchunk) + c * 3;
-        put_u64(sw, tagged(tag, f2u(m[s])));
-        put_u64(sw + 1, tagged(tag, (uint32_t)es));
-        put_u64(sw + 2, tagged(tag, (uint32_t)(es >> 32)));
+        put_u64(sw, tagged(ptag, f2u(m[s])));
+        put_u64(sw + 1, tagged(ptag, (uint32_t)es));
+        put_u64(sw + 2, tagged(ptag, (uint32_t)(es >> 32)));
       }
     }
   }
 
   // ---- phase B: row normalisers, decision, weights of this chunk ----
   if (wid < R) {
-    const RowDesc dd = fold_row_tagged(P, W, unit * R + wid, tag, lane, &s_bad);
+    const RowDesc dd = fold_row_tagged(P, W, unit * R + wid, tag, lane, &s_bad, spent, limit);
     if (lane == 0) s_desc[wid] = dd;
   }
   __syncthreads();
@@ -401,10 +451,11 @@ __global__ __launch_bounds__(SmallShape<G>::kThreads) void k_accept_small(Proble
     const uint64_t bw = s_e[0][0] + s_e[1][0] + s_e[2][0] + s_e[3][0];
     const uint64_t bp = s_e[4][0] + s_e[5][0] + s_e[6][0] + s_e[7][0];
     uint64_t* sw = samp_words(W, rows, unit, P.nchunk) + c * 4;
-    put_u64(sw, tagged(tag, (uint32_t)bw));
-    put_u64(sw + 1, tagged(tag, (uint32_t)(bw >> 32)));
-    put_u64(sw + 2, tagged(tag, (uint32_t)bp));
-    put_u64(sw + 3, tagged(tag, (uint32_t)(bp >> 32)));
+    const uint32_t ptag = s_bad ? (tag | kPoison) : tag;
+    put_u64(sw, tagged(ptag, (uint32_t)bw));
+    put_u64(sw + 1, tagged(ptag, (uint32_t)(bw >> 32)));
+    put_u64(sw + 2, tagged(ptag, (uint32_t)bp));
+    put_u64(sw + 3, tagged(ptag, (uint32_t)(bp >> 32)));
   }
 
   // ---- phase C: chunk of the inverse-CDF point, token in its owner ----
@@ -412,7 +463,8 @@ __global__ __launch_bounds__(SmallShape<G>::kThreads) void k_accept_small(Proble
     uint64_t cw[4], cp[4];
     uint64_t wt = 0, pt = 0;
     uint32_t v[4][4];
-    read_tagged<4, 4>(samp_words(W, rows, unit, P.nchunk), P.nchunk, lane, tag, v, sy, &s_bad);
+    read_tagged<4, 4>(samp_words(W, rows, unit, P.nchunk), P.nchunk, lane, tag, v, sy, &s_bad,
+                      spent, limit);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       cw[i] = ((uint64_t)v[i][1] << 32) | v[i][0];
@@ -482,20 +534,22 @@ __global__ __launch_bounds__(SmallShape<G>::kThreads) void k_accept_small(Proble
     __syncthreads();
   }
   // the outputs depend only on data this workgroup read, so they are valid
-  // unless one of its own waits ran out
-  const bool bad = s_bad != 0;
+  // unless one of its own waits failed (then they keep the invalid marks of
+  // the chunk-0 workgroup, written through before any word this workgroup
+  // read); stored at agent scope, after those marks
+  if (s_bad != 0) return;
   const int64_t token = (int64_t)s_tok;
   if (tid <= G) {
     int64_t v;
-    if (bad) v = -1;
-    else if (tid < r) v = s_dt[tid];
+    if (tid < r) v = s_dt[tid];
     else if (tid == r) v = token;
     else v = -1;
-    A.tok_out[(int64_t)unit * R + tid] = v;
+    __hip_atomic_store(&A.tok_out[(int64_t)unit * R + tid], v, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
   }
   if (tid == 0) {
-    A.nacc_out[unit] = bad ? -1 : r;
-    A.len_out[unit] = bad ? 0 : r + 1;
+    __hip_atomic_store(&A.len_out[unit], r + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&A.nacc_out[unit], r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -601,15 +655,16 @@ __device__ __forceinline__ int count_greater(const uint64_t* v, int n, uint64_t 
 
 // One tagged word, re-read until it carries `tag` (bounded as read_tagged).
 __device__ __forceinline__ uint32_t get_tagged(const uint64_t* p, uint32_t tag, SmallSync* sy,
-                                               int* bad) {
-  for (uint32_t spins = 0;; ++spins) {
+                                               int* bad, uint32_t& spent, uint32_t limit) {
+  for (;;) {
     const uint64_t v = get_u64(p);
-    if ((uint32_t)(v >> 32) == tag) return (uint32_t)v;
-    if (spins == kSpinLimit) {
-      *bad = 1;
-      __hip_atomic_store(&sy->err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t t = (uint32_t)(v >> 32);
+    if (t == tag) return (uint32_t)v;
+    if (t == (tag | kPoison) || spent >= limit || is_bad(bad)) {
+      fail_wait(sy, bad);
       return 0u;
     }
+    ++spent;
     __builtin_amdgcn_s_sleep(1);
   }
 }
@@ -641,7 +696,8 @@ __device__ __forceinline__ TopkWords topk_words(const Work& W, int rows, int nch
 template <int NPL>
 __device__ __forceinline__ void gather_cands(const TopkWords& TW, int row, const uint32_t (&cnt)[4],
                                              const uint32_t (&off)[4], int nchunk, int b0, int n,
-                                             uint32_t tag, SmallSync* sy, int* bad, int lane,
+                                             uint32_t tag, SmallSync* sy, int* bad,
+                                             uint32_t& spent, uint32_t limit, int lane,
                                              uint64_t* buf_p, uint32_t* buf_q, uint64_t (&v)[NPL],
                                              uint32_t (&pl)[NPL]) {
   const int b1 = b0 + NPL * kWave;
@@ -654,9 +710,9 @@ __device__ __forceinline__ void gather_cands(const TopkWords& TW, int row, const
     const uint64_t* cw = TW.candw(row, c);
     for (int e = lo; e < hi; ++e) {
       const uint64_t* w = cw + 3 * (e - (int)off[i]);
-      const uint32_t key = get_tagged(w, tag, sy, bad);
-      const uint32_t idx = get_tagged(w + 1, tag, sy, bad);
-      const uint32_t q = get_tagged(w + 2, tag, sy, bad);
+      const uint32_t key = get_tagged(w, tag, sy, bad, spent, limit);
+      const uint32_t idx = get_tagged(w + 1, tag, sy, bad, spent, limit);
+      const uint32_t q = get_tagged(w + 2, tag, sy, bad, spent, limit);
       buf_p[e - b0] = rank_pair(key, idx);
       buf_q[e - b0] = q;
     }
@@ -691,7 +747,8 @@ __global__ __launch_bounds__(SmallShape<G>::kThreads) void k_accept_small_topk(P
   __shared__ int64_t s_dt[G];
   __shared__ int s_nacc;
   __shared__ uint32_t s_tag;
-  __shared__ int s_bad;
+  __shared__ int s_bad;   // outputs invalid (a broken top-k promise, inconsistent words)
+  __shared__ int s_fail;  // a wait failed: this workgroup's later words are poisoned
   __shared__ long long s_tok;
   __shared__ int s_nb[R];
   __shared__ uint32_t s_kidx[R][kTopkMax];
@@ -720,6 +777,8 @@ __global__ __launch_bounds__(SmallShape<G>::kThreads) void k_accept_small_topk(P
   const TopkWords TW = topk_words(W, rows, P.nchunk);
   const int64_t i0 = chunk_elem(c, gt, 0);
   const bool in = i0 < P.V;
+  const uint32_t limit = spin_budget(sy);
+  uint32_t spent = 0;
   const T* lrow = reinterpret_cast<const T*>(P.logits) + (int64_t)unit * R * P.row_stride;
   const float* qrow = A.q + (int64_t)unit * G * A.q_stride;
 
@@ -781,13 +840,15 @@ __global__ __launch_bounds__(SmallShape<G>::kThreads) void k_accept_small_topk(P
     if (lane == 0) s_pm[wid][s] = pm;
   }
   if (tid == 0) {
-    s_tag = (uint32_t)(start >> 32) + 1u;
-    s_bad = (entry_bad || k_bad) ? 1 : 0;
+    s_tag = launch_tag(start);
+    s_bad = k_bad ? 1 : 0;
+    s_fail = entry_bad ? 1 : 0;
   }
   if (tid < R) s_tau[tid] = 0ull;
   __syncthreads();
   const uint32_t tag = s_tag;
   if (gt == 0) {
+    const uint32_t ptag = s_fail ? (tag | kPoison) : tag;
 #pragma unroll
     for (int s = 0; s < RPG; ++s) {
       const int j = grp + NG * s;
@@ -796,8 +857,8 @@ __global__ __launch_bounds__(SmallShape<G>::kThreads) void k_accept_small_topk(P
 #pragma unroll
         for (int w = 1; w < 4; ++w) pm = s_pm[grp * 4 + w][s] > pm ? s_pm[grp * 4 + w][s] : pm;
         uint64_t* mw = TW.maxw(unit * R + j) + c * 2;
-        put_u64(mw, tagged(tag, (uint32_t)(pm >> 32)));
-        put_u64(mw + 1, tagged(tag, (uint32_t)pm));
+        put_u64(mw, tagged(ptag, (uint32_t)(pm >> 32)));
+        put_u64(mw + 1, tagged(ptag, (uint32_t)pm));
       }
     }
   }
@@ -814,7 +875,7 @@ __global__ __launch_bounds__(SmallShape<G>::kThreads) void k_accept_small_topk(P
   // one ranked k - 1 is tau (pairs are distinct: their indices differ)
   if (wid < R) {
     uint32_t w[4][2];
-    read_tagged<4, 2>(TW.maxw(unit * R + wid), P.nchunk, lane, tag, w, sy, &s_bad);
+    read_tagged<4, 2>(TW.maxw(unit * R + wid), P.nchunk, lane, tag, w, sy, &s_fail, spent, limit);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int cc = lane + i * kWave;
@@ -843,6 +904,8 @@ __global__ __launch_bounds__(SmallShape<G>::kThreads) void k_accept_small_topk(P
     if (lane == 0) s_cn[wid][s] = n;
   }
   __syncthreads();
+  // words of a workgroup whose waits failed carry the poisoned tag
+  const uint32_t ptag = s_fail ? (tag | kPoison) : tag;
 #pragma unroll
   for (int s = 0; s < RPG; ++s) {
     const int j = grp + NG * s;
@@ -859,13 +922,13 @@ __global__ __launch_bounds__(SmallShape<G>::kThreads) void k_accept_small_topk(P
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       if (cmask[s] & (1u << k)) {
-        put_u64(cw + 3 * slot, tagged(tag, key[s][k]));
-        put_u64(cw + 3 * slot + 1, tagged(tag, (uint32_t)(i0 + k)));
-        put_u64(cw + 3 * slot + 2, tagged(tag, f2u(j < G ? q[s][k] : 0.0f)));
+        put_u64(cw + 3 * slot, tagged(ptag, key[s][k]));
+        put_u64(cw + 3 * slot + 1, tagged(ptag, (uint32_t)(i0 + k)));
+        put_u64(cw + 3 * slot + 2, tagged(ptag, f2u(j < G ? q[s][k] : 0.0f)));
         ++slot;
       }
     }
-    if (gt == 0) put_u64(TW.cntw(unit * R + j) + c, tagged(tag, n));
+    if (gt == 0) put_u64(TW.cntw(unit * R + j) + c, tagged(ptag, n));
   }
   // rows with more than kTopkSlots candidates in this chunk (ties, or rows whose
   // largest values crowd into one chunk): sort the chunk's candidate pairs in
@@ -904,10 +967,10 @@ __global__ __launch_bounds__(SmallShape<G>::kThreads) void k_accept_small_topk(P
       const uint32_t idx = pair_idx(pr);
       const float qv = j < G ? qrow[j * A.q_stride + idx] : 0.0f;
       uint64_t* cw = TW.candw(unit * R + j, c) + 3 * tid;
-      put_u64(cw, tagged(tag, (uint32_t)(pr >> 32)));
-      put_u64(cw + 1, tagged(tag, idx));
-      put_u64(cw + 2, tagged(tag, f2u(qv)));
-      if (tid == 0) put_u64(TW.cntw(unit * R + j) + c, tagged(tag, (uint32_t)kTopkSlots));
+      put_u64(cw, tagged(ptag, (uint32_t)(pr >> 32)));
+      put_u64(cw + 1, tagged(ptag, idx));
+      put_u64(cw + 2, tagged(ptag, f2u(qv)));
+      if (tid == 0) put_u64(TW.cntw(unit * R + j) + c, tagged(ptag, (uint32_t)kTopkSlots));
     }
   }
   __syncthreads();     // s_big is reused below
@@ -917,7 +980,8 @@ __global__ __launch_bounds__(SmallShape<G>::kThreads) void k_accept_small_topk(P
   // candidate counts of every (row, chunk) -> exclusive offsets (wave j: row j)
   if (wid < R) {
     uint32_t cnt[4][1];
-    read_tagged<4, 1>(TW.cntw(unit * R + wid), P.nchunk, lane, tag, cnt, sy, &s_bad);
+    read_tagged<4, 1>(TW.cntw(unit * R + wid), P.nchunk, lane, tag, cnt, sy, &s_fail, spent,
+                      limit);
     uint32_t run = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -961,22 +1025,26 @@ __global__ __launch_bounds__(SmallShape<G>::kThreads) void k_accept_small_topk(P
       }
     }
     uint64_t wv[kPer][3];
-    for (uint32_t spins = 0;; ++spins) {
+    for (;;) {
 #pragma unroll
       for (int i = 0; i < kPer; ++i)
 #pragma unroll
         for (int k = 0; k < 3; ++k) wv[i][k] = ad[i] ? get_u64(ad[i] + k) : tagged(tag, 0u);
-      bool ok = true;
+      bool ok = true, poisoned = false;
 #pragma unroll
       for (int i = 0; i < kPer; ++i)
 #pragma unroll
-        for (int k = 0; k < 3; ++k) ok = ok && (uint32_t)(wv[i][k] >> 32) == tag;
+        for (int k = 0; k < 3; ++k) {
+          const uint32_t t = (uint32_t)(wv[i][k] >> 32);
+          ok = ok && t == tag;
+          poisoned = poisoned || t == (tag | kPoison);
+        }
       if (ok) break;
-      if (spins == kSpinLimit) {
-        s_bad = 1;
-        __hip_atomic_store(&sy->err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (poisoned || spent >= limit || is_bad(&s_fail)) {
+        fail_wait(sy, &s_fail);
         break;
       }
+      ++spent;
       __builtin_amdgcn_s_sleep(1);
     }
 #pragma unroll
@@ -1024,12 +1092,14 @@ __global__ __launch_bounds__(SmallShape<G>::kThreads) void k_accept_small_topk(P
       uint32_t* bq = s_bigq + wid * 256;
       uint64_t v[4];
       uint32_t pl[4];
-      gather_cands<4>(TW, row, cn, off, P.nchunk, 0, n, tag, sy, &s_bad, lane, bp, bq, v, pl);
+      gather_cands<4>(TW, row, cn, off, P.nchunk, 0, n, tag, sy, &s_fail, spent, limit, lane, bp,
+                      bq, v, pl);
       wave_sort_desc<4>(v, pl, lane);
       for (int b0 = 4 * kWave; b0 < n; b0 += 3 * kWave) {
         uint64_t v2[4];
         uint32_t p2[4];
-        gather_cands<4>(TW, row, cn, off, P.nchunk, b0 - kWave, n, tag, sy, &s_bad, lane, bp,
+        gather_cands<4>(TW, row, cn, off, P.nchunk, b0 - kWave, n, tag, sy, &s_fail, spent, limit,
+                        lane, bp,
                         bq, v2, p2);
         v2[0] = v[0];
         p2[0] = pl[0];
@@ -1149,7 +1219,7 @@ __global__ __launch_bounds__(SmallShape<G>::kThreads) void k_accept_small_topk(P
     }
   }
   __syncthreads();
-  const bool bad = s_bad != 0;
+  const bool bad = s_bad != 0 || s_fail != 0;
   const int r = s_nacc;
   if (tid <= G) {
     int64_t v;

@@ -74,6 +74,7 @@ struct AttnArgs {
   int sk_nwg;                // balanced launch: workgroups
   int xcd_pack;              // per-tile grid: only workgroups x % xcd_pack == 0 work
   unsigned* tickets;         // fused kernel: split-merge tickets per (sequence, kv head)
+  int contig;                // keys are the call's own unpaged rows (no block table)
 };
 
 // The q/k-norm + RoPE + KV-store step run inside the per-tile kernel
@@ -212,6 +213,7 @@ __device__ __forceinline__ bf16x8_t fp8x8w_to_bf16(uint32_t lo, uint32_t hi) {
 // sequence's query start qs and lengths.
 struct TileRef {
   int b, kvh, qt, qs, Lq, Lk, rows;
+  int ks;  // first key row of the sequence (unpaged keys, AttnArgs::contig)
 };
 
 // from the sequence's bounds cu_q[b], cu_q[b + 1], cu_k[b], cu_k[b + 1]
@@ -225,6 +227,7 @@ __device__ __forceinline__ TileRef tile_ref_of(int b, int kvh, int qt, int G, in
   t.Lq = q1 - q0;
   t.Lk = k1 - k0;
   t.rows = t.Lq * G;
+  t.ks = k0;
   return t;
 }
 __device__ __forceinline__ TileRef tile_ref(const AttnArgs& a, int b, int kvh, int qt, int G) {
@@ -429,6 +432,12 @@ __device__ __forceinline__ void wave_walk(const AttnArgs& a, const TileRef& t, i
   // window ws of this wave -> cache row bases (bytes) of its K and V head rows;
   // false when its block is not a valid cache block (the window is skipped)
   auto window_base = [&](int ws, const uint8_t*& kb, const uint8_t*& vb) -> bool {
+    if (a.contig) {  // unpaged keys: row ks + key of the [tokens, Hkv, 128] k / v
+      const int64_t off = ((int64_t)(t.ks + ws) * a.c_st + (int64_t)kvh * a.c_sh) * esz;
+      kb = a.kc + off;
+      vb = a.vc + off;
+      return true;
+    }
     const int blk_idx = key_block(ws, a.bs_shift, a.block_size);
     const int bi = blk_idx - bt0;
     const int blk = (bi < nbt_used && bi < bt_cap && bt0 + bi < a.bt_width) ? s_bt[bi] : -1;
@@ -1364,6 +1373,7 @@ static int attn_prepare(const void* q, int64_t q_stride_tok, int64_t q_stride_he
   a.o_st = out_stride_tok;
   a.o_sh = out_stride_head;
   a.tickets = static_cast<unsigned*>(workspace);
+  a.contig = 0;
   return HS_OK;
 }
 
@@ -1397,6 +1407,21 @@ int hs_verify_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_he
                         int head_dim, int block_size, float softmax_scale, void* out,
                         int64_t out_stride_tok, int64_t out_stride_head, void* workspace,
                         size_t workspace_bytes, void* stream) {
+  // no block table: the keys are the call's own unpaged rows
+  // (flash_attn_varlen_func without block_table, attention.py:147-160):
+  // k_cache / v_cache are [tokens, num_kv_heads, 128] with sequence b's keys
+  // at rows cu_seqlens_k[b] .. cu_seqlens_k[b + 1] - 1, and the block
+  // arguments are ignored (the kernel's table prefetch reads cu_seqlens_k,
+  // whose values it does not use)
+  const bool contig = block_tables == nullptr;
+  if (contig) {
+    block_tables = cu_seqlens_k;
+    block_table_stride = 1;
+    block_table_width = 1;
+    num_blocks = 1;
+    block_size = kWin;
+    cache_stride_block = 0;
+  }
   AttnArgs a;
   size_t need = 0;
   const int prc = attn_prepare(q, q_stride_tok, q_stride_head, k_cache, v_cache, kv_dtype,
@@ -1407,10 +1432,11 @@ int hs_verify_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_he
                                softmax_scale, out, out_stride_tok, out_stride_head, workspace,
                                workspace_bytes, &a, &need);
   if (prc != HS_OK) return prc;
+  a.contig = contig ? 1 : 0;
   const int G = a.G;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   bool heads = false;
-  const int nwg = attn_sk_plan(num_seqs, num_kv_heads, a.qtiles, max_seqlen_k, &heads);
+  const int nwg = contig ? 0 : attn_sk_plan(num_seqs, num_kv_heads, a.qtiles, max_seqlen_k, &heads);
   if (nwg && workspace && workspace_bytes >= need &&
       (max_seqlen_k + block_size - 1) / block_size + 1 <= kSkBtCap) {
     const size_t slots = 2 * (size_t)nwg * kRows * (heads ? num_kv_heads : 1);
@@ -1473,7 +1499,7 @@ int hs_qk_norm_rope_attend(const void* qkv, int64_t token_stride, int num_tokens
                            size_t workspace_bytes, void* stream) {
   if (num_tokens <= 0) return num_tokens == 0 ? HS_OK : HS_ERR_INVALID;
   if (!qkv || !q_weight || !k_weight || !cos_sin || !positions || !slot_mapping || !q_out ||
-      cos_sin_rows <= 0)
+      cos_sin_rows <= 0 || !block_tables)
     return HS_ERR_INVALID;
   if (num_q_heads <= 0 || num_kv_heads <= 0) return HS_ERR_INVALID;
   if (head_dim != kD) return HS_ERR_UNSUPPORTED;

@@ -109,7 +109,7 @@ class SpecRunner:
                 u_draft=torch.zeros((g, B), dtype=torch.float32, device=dev),
                 u_acc=torch.zeros((B, g), dtype=torch.float32, device=dev),
                 elig=torch.zeros(B, dtype=torch.int32, device=dev),
-                graphs=None, last=None, graph_last=None)
+                graphs=None, last=None, graph_last=None, logits=None, graph_logits=None)
             self._per_gamma[g] = G
         return G
 
@@ -353,6 +353,7 @@ class SpecRunner:
                                           topk_le64=self.topk_le64)
         ops.spec_commit(st, g, out, olen, eligible=G.elig)
         G.last = (nacc, out, olen)
+        G.logits = logits  # the acceptance call's target rows (read by checks)
         self.last = G.last
 
     def step(self):
@@ -409,7 +410,7 @@ class SpecRunner:
         # the captured verify phase rebinds G.last to the graph's output tensors, which
         # hold nothing until the first replay: keep the eager step's outputs as the
         # last results and switch to the graph's on replay
-        eager_last = G.last
+        eager_last, eager_logits = G.last, G.logits
         gd, gv = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
         s = torch.cuda.Stream(device=self.device)
         s.wait_stream(torch.cuda.current_stream(self.device))
@@ -422,8 +423,9 @@ class SpecRunner:
         torch.cuda.synchronize()
         self._restore(snap)  # capture executed nothing, but keep the state exact
         G.graphs = (gd, gv)
-        G.graph_last = G.last
+        G.graph_last, G.graph_logits = G.last, G.logits
         G.last = self.last = eager_last
+        G.logits = eager_logits
 
     def replay(self):
         G = self._g()
@@ -431,6 +433,7 @@ class SpecRunner:
         gd.replay()
         gv.replay()
         G.last = self.last = G.graph_last
+        G.logits = G.graph_logits
 
     def _snapshot(self):
         st = self.state

@@ -4,19 +4,19 @@ Drop-in for mini_vllm/layers/attention.py: the same constructor
 Attention(num_heads, head_dim, scale, num_kv_heads), the same module
 attributes bound by the model runner (k_cache, v_cache, kv_cache_dtype) and
 the same store_kvcache(key, value, k_cache, v_cache, slot_mapping) function.
-forward(q, k, v) stores k/v at context.slot_mapping (attention.py:145) and then
-attends over the paged cache through context.block_tables:
-  * prefill / verify (context.is_prefill): cu_seqlens_q/k as given
-    (attention.py:147-160, bottom-right causal);
+forward(q, k, v) stores k/v at context.slot_mapping when a cache is bound
+(attention.py:145) and then attends:
+  * prefill / verify (context.is_prefill) with block tables: over the paged
+    cache, cu_seqlens_q/k as given (attention.py:147-160, bottom-right causal);
+  * prefill without block tables (no cached prefix): over the step's own k/v,
+    cu_seqlens_q/k as given (attention.py:147-160 with block_table None; no
+    cache needed, as in the reference's warm-up);
   * decode: one query per sequence with context.context_lens keys
     (attention.py:162-170); cu_seqlens_k is taken from context.cu_seqlens_k
     when the caller staged it on the device, else built from context_lens;
     the launch is sized by max_model_len when the runner set it, else by
     max_seqlen_k, else (the reference's decode context sets neither) by the
     block-table width times the block size.
-Prefill without block tables (the reference then attends over the step's own
-k/v, attention.py:147-149) is not supported: the kernel reads the paged cache
-only, so a runner stages block tables for every prefill.
 kv_cache_dtype "fp8" means float8_e4m3fn caches with per-tensor scales
 k_scale / v_scale, used by every phase (the reference keeps a separate BF16
 prefill cache for verify, attention.py:114-131; one FP8 cache keeps the
@@ -67,19 +67,20 @@ class Attention(nn.Module):
         if not (self.k_cache.numel() and self.v_cache.numel()):
             raise RuntimeError("Attention needs a bound KV cache (k_cache / v_cache)")
         if ctx.block_tables is None:
-            # the reference attends over the step's own k/v here (attention.py:147-149);
-            # this build's kernel reads the paged cache only, so the runner must stage
-            # block tables for every prefill (as SpecRunner and VerifyRunner do)
-            raise RuntimeError("Attention needs context.block_tables: prefill over the "
-                               "unpaged k/v of the step is not supported")
+            raise RuntimeError("Attention over the cache needs context.block_tables")
 
     def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
         ctx = get_context()
-        self._check_bound(ctx)
         k = k.view(-1, self.num_kv_heads, self.head_dim)
         v = v.view(-1, self.num_kv_heads, self.head_dim)
-        store_kvcache(k, v, self.k_cache, self.v_cache, ctx.slot_mapping, self.k_scale,
-                      self.v_scale)
+        if self.k_cache.numel() and self.v_cache.numel():
+            store_kvcache(k, v, self.k_cache, self.v_cache, ctx.slot_mapping, self.k_scale,
+                          self.v_scale)
+        if ctx.is_prefill and ctx.block_tables is None:
+            # attention.py:147-160 with block_table None: the step's own k / v
+            q = q.view(-1, self.num_heads, self.head_dim)
+            return _ops.verify_attention(q, k, v, None, ctx.cu_seqlens_q, ctx.cu_seqlens_k,
+                                         ctx.max_seqlen_q, ctx.max_seqlen_k, self.scale)
         return self.attend(q)
 
     def attend(self, q: torch.Tensor) -> torch.Tensor:

@@ -186,6 +186,20 @@ def accept_error(device, clear: bool = False) -> bool:
     return bad
 
 
+def accept_wait_budget(device, polls: int | None) -> None:
+    """Sets the wait budget of the single-launch acceptance on this device's
+    acceptance workspace (the 32-bit word at byte 12, include/hilda_spec.h):
+    `polls` polls per thread over all its waits of a launch, or the default with
+    None. For tests of the failure path: a small budget makes the kernels give
+    up their waits (every kernel still exits), and the calls report invalid
+    outputs. Creates the workspace if needed; ordered on the current stream."""
+    dev = torch.device("cuda", _dev_index(device))
+    lib = L.lib()
+    ws = workspace(dev, lib.hs_spec_accept_workspace_size(1, 1, 8), "spec_accept")
+    word = ws[12:16].view(torch.int32)
+    word.fill_(0 if polls is None else int(polls) + 1)
+
+
 def check_accepted(num_accepted: torch.Tensor, what: str = "spec_accept") -> None:
     """Raises if any entry of num_accepted (already on the host, or copied here)
     is negative: the acceptance kernel marked that sequence's outputs invalid."""
@@ -272,7 +286,7 @@ def _kv_code(cache: torch.Tensor) -> int:
 
 
 def verify_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
-                     block_tables: torch.Tensor, cu_seqlens_q: torch.Tensor,
+                     block_tables: torch.Tensor | None, cu_seqlens_q: torch.Tensor,
                      cu_seqlens_k: torch.Tensor, max_seqlen_q: int, max_seqlen_k: int,
                      softmax_scale: float, *, k_scale: float = 1.0, v_scale: float = 1.0,
                      out: torch.Tensor | None = None) -> torch.Tensor:
@@ -281,24 +295,40 @@ def verify_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     q [tokens, Hq, 128] bf16; k_cache/v_cache [num_blocks, block_size, Hkv, 128]
     bf16 or float8_e4m3fn (dequantised as code * k_scale / v_scale);
     block_tables int32 [B, W]; cu_seqlens_q/k int32 [B+1].
+    block_tables None: flash_attn_varlen_func without a block table
+    (attention.py:147-160 for a prefill with no cached prefix): k_cache and
+    v_cache are then the step's own k / v rows [tokens, Hkv, 128], sequence b's
+    keys at rows cu_seqlens_k[b] .. cu_seqlens_k[b + 1] - 1.
     """
     dev = _need_cuda(q, k_cache, v_cache, block_tables, cu_seqlens_q, cu_seqlens_k, out)
     if q.dtype != torch.bfloat16 or q.dim() != 3 or q.stride(2) != 1:
         raise ValueError("q must be [tokens, heads, head_dim] bf16 with contiguous head_dim")
     if k_cache.shape != v_cache.shape or k_cache.dtype != v_cache.dtype:
         raise ValueError("k_cache and v_cache must match")
-    if k_cache.stride() != v_cache.stride() or k_cache.stride(3) != 1:
-        raise ValueError("k_cache and v_cache need identical strides with contiguous head_dim")
-    nb, bs, Hkv, D = k_cache.shape
+    B = cu_seqlens_q.numel() - 1
+    cq = cu_seqlens_q.to(torch.int32).contiguous()
+    ck = cu_seqlens_k.to(torch.int32).contiguous()
+    if block_tables is None:
+        if k_cache.dim() != 3 or k_cache.stride() != v_cache.stride() or k_cache.stride(2) != 1:
+            raise ValueError("unpaged k / v must be [tokens, kv_heads, head_dim] with identical "
+                             "strides and contiguous head_dim")
+        Nk, Hkv, D = k_cache.shape
+        nb, bs, bt = 1, 32, None
+        s_blk, s_tok, s_head = 0, k_cache.stride(0), k_cache.stride(1)
+        bt_stride = bt_width = 1
+    else:
+        if k_cache.stride() != v_cache.stride() or k_cache.stride(3) != 1:
+            raise ValueError("k_cache and v_cache need identical strides with contiguous "
+                             "head_dim")
+        nb, bs, Hkv, D = k_cache.shape
+        bt = block_tables if block_tables.dtype == torch.int32 else block_tables.to(torch.int32)
+        if bt.dim() != 2 or bt.shape[0] < B or bt.stride(1) != 1:
+            bt = bt.contiguous()
+        s_blk, s_tok, s_head = k_cache.stride(0), k_cache.stride(1), k_cache.stride(2)
+        bt_stride, bt_width = bt.stride(0), bt.shape[1]
     N, Hq, Dq = q.shape
     if Dq != D:
         raise ValueError("head_dim mismatch")
-    B = cu_seqlens_q.numel() - 1
-    bt = block_tables if block_tables.dtype == torch.int32 else block_tables.to(torch.int32)
-    if bt.dim() != 2 or bt.shape[0] < B or bt.stride(1) != 1:
-        bt = bt.contiguous()
-    cq = cu_seqlens_q.to(torch.int32).contiguous()
-    ck = cu_seqlens_k.to(torch.int32).contiguous()
     if out is None:
         out = torch.empty((N, Hq, D), dtype=torch.bfloat16, device=dev)
     lib = L.lib()
@@ -307,9 +337,9 @@ def verify_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     ws = workspace(dev, nbytes, "attention")
     rc = lib.hs_verify_attention(
         q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(),
-        _kv_code(k_cache), k_cache.stride(0), k_cache.stride(1), k_cache.stride(2),
-        float(k_scale), float(v_scale), bt.data_ptr(), bt.stride(0), bt.shape[1], nb,
-        cq.data_ptr(), ck.data_ptr(), B, int(max_seqlen_q), int(max_seqlen_k), Hq, Hkv, D, bs,
+        _kv_code(k_cache), s_blk, s_tok, s_head, float(k_scale), float(v_scale),
+        None if bt is None else bt.data_ptr(), bt_stride, bt_width, nb, cq.data_ptr(),
+        ck.data_ptr(), B, int(max_seqlen_q), int(max_seqlen_k), Hq, Hkv, D, bs,
         float(softmax_scale), out.data_ptr(), out.stride(0), out.stride(1), ws.data_ptr(),
         ws.numel(), _stream(dev))
     L.check(rc, "hs_verify_attention")

@@ -97,12 +97,20 @@ int hs_version(void);
 /*                 per CU, gamma <= 7, aligned rows, vocab a multiple of 8)  */
 /*                 run as a single launch whose workgroups exchange data     */
 /*                 through the workspace: in reference mode, and in filtered */
-/*                 mode with HS_ACCEPT_TOPK_LE64 when vocab >= 64 * 2048. If one of its bounded waits ever   */
-/*                 ran out, or its launch counter was not left by a completed */
-/*                 call, that sequence's num_accepted is -1 and out_len 0,   */
-/*                 and the 32-bit word at byte offset 8 of the workspace is  */
-/*                 set to 1 (sticky until the caller clears it). Callers     */
-/*                 must check num_accepted >= 0 at their next synchronisation.*/
+/*                 mode with HS_ACCEPT_TOPK_LE64 when vocab >= 64 * 2048.    */
+/*                 Its waits are bounded: a thread polls at most a budget    */
+/*                 (2^20 polls, over all its waits of the launch; the 32-bit */
+/*                 word at byte offset 12 of the workspace, when nonzero,    */
+/*                 sets it to that value minus 1, for tests of this path),   */
+/*                 and a workgroup stops waiting at once when one of its     */
+/*                 waits has failed or its data came from one that failed.   */
+/*                 If a wait ran out, or the launch counter was not left by  */
+/*                 a completed call, the sequences concerned get             */
+/*                 num_accepted -1 and out_len 0 (a sequence's outputs are   */
+/*                 either all valid or marked so), and the 32-bit word at    */
+/*                 byte offset 8 of the workspace is set to 1 (sticky until  */
+/*                 the caller clears it). Callers must check num_accepted    */
+/*                 >= 0 at their next synchronisation.                       */
 /* ------------------------------------------------------------------------ */
 size_t hs_spec_accept_workspace_size(int batch, int gamma, int vocab);
 
@@ -156,7 +164,12 @@ int hs_sampler(const void* logits, int logits_dtype, int64_t logits_row_stride,
 /*               (block, token, head); fp8 values dequantise as code*scale.  */
 /* block_tables: int32 [num_seqs, block_table_width] (row stride given, at  */
 /*               most INT32_MAX elements); entries outside [0, num_blocks)  */
-/*               are treated as empty.                                       */
+/*               are treated as empty. NULL: the keys are the call's own    */
+/*               unpaged rows (flash_attn_varlen_func without block_table,   */
+/*               a prefill with no cached prefix): k_cache / v_cache are     */
+/*               [tokens, num_kv_heads, 128] with element strides (token,    */
+/*               head), sequence b's keys at rows cu_seqlens_k[b] ..         */
+/*               cu_seqlens_k[b + 1] - 1; block arguments are ignored.       */
 /* cu_seqlens_q/k: int32 [num_seqs + 1] prefix sums of query/key lengths.    */
 /* The workspace (size from hs_verify_attention_workspace_size) holds, after */
 /* 16 KiB of merge counters (zero-filled before the first call, left zero),  */

@@ -201,3 +201,112 @@ def test_store_kvcache(hv, attn, cuda, kv):
                            slots)
         np.testing.assert_array_equal(kc.view(torch.uint8).cpu().numpy(), ek)
         np.testing.assert_array_equal(vc.view(torch.uint8).cpu().numpy(), ev)
+
+
+# ---------------------------------------------------------------- unpaged prefill
+@pytest.mark.parametrize("cache", ["none", "bf16", "fp8"])
+def test_attention_forward_unpaged_prefill(hv, attn, cuda, cache):
+    """Attention.forward under the reference's prefill context without block tables
+    (model_runner.py:614-649: set_context(True, cu_seqlens_q, cu_seqlens_k,
+    max_seqlen_q, max_seqlen_k, slot_mapping, None, None) for prompts with no
+    cached prefix), ragged prompts of 1 to 1500 tokens: the output is
+    flash_attn_varlen_func over the step's own k / v (attention.py:147-160), here
+    the float64 oracle per sequence within 2e-2; with a bound cache the k / v rows
+    land at slot_mapping first (bf16: bit-exact; fp8: the oracle codec), with
+    none (the reference's warm-up) nothing is stored."""
+    from importlib import import_module
+    ctxm = import_module("hilda-vllm_amd.utils.context")
+    layer_mod = import_module("hilda-vllm_amd.layers.attention")
+    Hq, Hkv, D, bs = 16, 8, 128, 256
+    lens = [1, 37, 300, 1500, 4]
+    g = torch.Generator(device=cuda).manual_seed(11)
+    N = sum(lens)
+    q = torch.randn((N, Hq * D), generator=g, device=cuda).to(torch.bfloat16)
+    k = torch.randn((N, Hkv * D), generator=g, device=cuda).to(torch.bfloat16)
+    v = torch.randn((N, Hkv * D), generator=g, device=cuda).to(torch.bfloat16)
+    cu = torch.tensor([0] + list(np.cumsum(lens)), dtype=torch.int32, device=cuda)
+    layer = layer_mod.Attention(Hq, D, D ** -0.5, Hkv)
+    nblk = [(n + bs - 1) // bs for n in lens]
+    nb = sum(nblk) + 2
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(5)).tolist()
+    slots, o = [], 0
+    for n, m in zip(lens, nblk):
+        blocks = perm[o:o + m]
+        o += m
+        slots += [blocks[i // bs] * bs + i % bs for i in range(n)]
+    slots_t = torch.tensor(slots, dtype=torch.int32, device=cuda)
+    ksc = vsc = 1.0
+    if cache != "none":
+        dt = torch.bfloat16 if cache == "bf16" else torch.float8_e4m3fn
+        kc = torch.zeros((nb, bs, Hkv, D), dtype=dt, device=cuda)
+        vc = torch.zeros_like(kc)
+        layer.k_cache, layer.v_cache = kc, vc
+        if cache == "fp8":
+            ksc, vsc = 0.02, 0.015
+            layer.k_scale, layer.v_scale = ksc, vsc
+    print(f"unpaged prefill cache={cache} lens={lens}", flush=True)
+    ctxm.set_context(True, cu, cu, max(lens), max(lens), slots_t, None, None)
+    try:
+        out = layer(q, k, v)
+    finally:
+        ctxm.reset_context()
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy().reshape(N, Hq, D)
+    qn = q.float().cpu().numpy().reshape(N, Hq, D)
+    kn = k.float().cpu().numpy().reshape(N, Hkv, D)
+    vn = v.float().cpu().numpy().reshape(N, Hkv, D)
+    for b, n in enumerate(lens):
+        s0 = int(cu[b])
+        ref = attn.paged_attention(qn[s0:s0 + n], kn[None, s0:s0 + n], vn[None, s0:s0 + n],
+                                   np.zeros((1, 1), np.int64), np.array([0, n]),
+                                   np.array([0, n]), D ** -0.5)
+        err = np.abs(got[s0:s0 + n] - ref).max()
+        assert err <= TOL * max(1.0, np.abs(ref).max()), (b, n, err)
+    if cache == "none":
+        return
+    kc_h = layer.k_cache.view(torch.uint8).cpu().numpy() if cache == "fp8" else \
+        layer.k_cache.float().cpu().numpy()
+    vc_h = layer.v_cache.view(torch.uint8).cpu().numpy() if cache == "fp8" else \
+        layer.v_cache.float().cpu().numpy()
+    sl = np.array(slots)
+    if cache == "fp8":
+        kexp, vexp = attn.e4m3fn_quantize(kn, ksc), attn.e4m3fn_quantize(vn, vsc)
+    else:
+        kexp, vexp = kn, vn
+    np.testing.assert_array_equal(kc_h[sl // bs, sl % bs], kexp)
+    np.testing.assert_array_equal(vc_h[sl // bs, sl % bs], vexp)
+
+
+@pytest.mark.parametrize("qlens,klens", [([40, 200], [40, 200]), ([4], [2100])])
+def test_verify_attention_unpaged_matches_paged(hv, cuda, qlens, klens):
+    """The unpaged mode (no block table) and the paged kernel over a cache holding
+    the same rows give the same bits: the same windows and arithmetic, only the
+    row addresses differ. A ragged prefill, and 4 queries over 2100 keys (three
+    key splits and their combine); both shapes run the per-tile grid."""
+    Hq, Hkv, D, bs = 32, 8, 128, 256
+    g = torch.Generator(device=cuda).manual_seed(12 + sum(klens))
+    N, Nk = sum(qlens), sum(klens)
+    q = torch.randn((N, Hq, D), generator=g, device=cuda).to(torch.bfloat16)
+    k = torch.randn((Nk, Hkv, D), generator=g, device=cuda).to(torch.bfloat16)
+    v = torch.randn((Nk, Hkv, D), generator=g, device=cuda).to(torch.bfloat16)
+    cq = torch.tensor([0] + list(np.cumsum(qlens)), dtype=torch.int32, device=cuda)
+    ck = torch.tensor([0] + list(np.cumsum(klens)), dtype=torch.int32, device=cuda)
+    nblk = [(n + bs - 1) // bs for n in klens]
+    kc = torch.zeros((sum(nblk), bs, Hkv, D), dtype=torch.bfloat16, device=cuda)
+    vc = torch.zeros_like(kc)
+    B = len(klens)
+    bt = torch.full((B, max(nblk)), -1, dtype=torch.int32, device=cuda)
+    o = 0
+    for b, (n, m) in enumerate(zip(klens, nblk)):
+        bt[b, :m] = torch.arange(o, o + m, dtype=torch.int32)
+        s0 = int(ck[b])
+        for i in range(m):
+            rows = min(bs, n - i * bs)
+            kc[o + i, :rows] = k[s0 + i * bs:s0 + i * bs + rows]
+            vc[o + i, :rows] = v[s0 + i * bs:s0 + i * bs + rows]
+        o += m
+    print(f"unpaged vs paged q={qlens} k={klens}", flush=True)
+    a = hv.ops.verify_attention(q, k, v, None, cq, ck, max(qlens), max(klens), D ** -0.5)
+    p = hv.ops.verify_attention(q, kc, vc, bt, cq, ck, max(qlens), max(klens), D ** -0.5)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16), p.view(torch.int16))

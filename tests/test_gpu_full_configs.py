@@ -171,9 +171,12 @@ def _accept_both(hv, orc, w, cuda, mode):
     return ref
 
 
-@pytest.mark.parametrize("B,gamma", [(64, 3), (256, 5)])
+@pytest.mark.parametrize("B,gamma", [(64, 1), (64, 3), (64, 5), (256, 1), (256, 3), (256, 5)])
 @pytest.mark.parametrize("mode", ["reference", "filtered", "greedy"])
 def test_config1_full_size(hv, orc, cuda, B, gamma, mode):
+    """Config 1 over its grid B in {64, 256} x gamma in {1, 3, 5} (B = 8 is in
+    test_gpu_sampler.py): bf16 logits, per-sequence T / top-k / top-p, the three
+    modes; accepted counts, emitted tokens and lengths bit-exact vs the C oracle."""
     print(f"config1 full size B={B} gamma={gamma} {mode}", flush=True)
     w = hv.synthetic.accept_workload(B, gamma, seed=7000 + B + gamma, dtype="bf16",
                                      per_seq_settings=True,

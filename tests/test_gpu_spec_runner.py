@@ -9,6 +9,7 @@ than reference outputs):
 """
 import importlib
 
+import numpy as np
 import pytest
 import torch
 
@@ -399,14 +400,37 @@ def test_config4_shape_adaptive_fp8_to_8192(cuda):
     print("gamma histogram", {k: gammas.count(k) for k in sorted(set(gammas))}, flush=True)
 
 
+def _accept_matches_oracle(r, orc):
+    """The acceptance of the runner's last step against the C oracle on that step's
+    own inputs (model_runner.py:387-428): its target logits, draft probabilities and
+    tokens, temperatures and uniforms, read back after the step; accepted counts,
+    emitted tokens and lengths must be equal."""
+    G = r._g()
+    B, g, V = r.B, G.gamma, r.V
+    logits = G.logits.float().cpu().numpy().reshape(B, g + 1, V)
+    ref = orc.spec_accept(logits, G.draft_probs.cpu().numpy(),
+                          G.draft_tokens.cpu().numpy(), r.temps.cpu().numpy(),
+                          G.u_acc.cpu().numpy(), r.u_res.cpu().numpy())
+    nacc, out, olen = (t.cpu().numpy() for t in G.last)
+    np.testing.assert_array_equal(nacc, ref["num_accepted"])
+    np.testing.assert_array_equal(olen, ref["out_len"])
+    for b in range(B):
+        n = int(olen[b])
+        np.testing.assert_array_equal(out[b, :n], ref["out_tokens"][b, :n])
+    return nacc
+
+
 @pytest.mark.parametrize("draft_kind", ["qwen3-0.6b", "forced"])
-def test_config3_real_geometry_graph_matches_eager(cuda, draft_kind):
+def test_config3_real_geometry_graph_matches_eager(cuda, orc, draft_kind):
     """Config 3 at its real geometry: random-init Qwen3-8B target (36 layers,
     hidden 4096, 32 / 8 heads, FFN 12288, vocab 151936) with the Qwen3-0.6B draft
     or the forced-acceptance draft (the target's first 28 layers and LM head),
-    batch 1, gamma 3, T 0.6, a 64-token prompt. Six steps replayed from the
-    captured HIP graphs emit the same tokens as six eager steps; every step emits
-    1 to gamma + 1 tokens; the forced draft has drafts accepted."""
+    batch 1, gamma 3, T 0.6, a 64-token prompt, max_model_len 4096 (the
+    reference's). Six steps replayed from the captured HIP graphs emit the same
+    tokens as six eager steps; every step's acceptance (eager and replayed)
+    equals the C oracle on the step's own logits, draft probabilities and
+    uniforms; every step emits 1 to gamma + 1 tokens; the forced draft has
+    drafts accepted."""
     q3, sr = _mods()
     print(f"config 3 real geometry, draft {draft_kind}", flush=True)
     target = q3.Qwen3Host(q3.QWEN3_8B, device=cuda, seed=1)
@@ -415,19 +439,21 @@ def test_config3_real_geometry_graph_matches_eager(cuda, draft_kind):
     prompt = torch.randint(0, 10000, (64,), generator=torch.Generator().manual_seed(0)).tolist()
 
     def run(graphs):
-        r = sr.SpecRunner(target, draft, batch=1, gamma=3, max_model_len=160, temperature=0.6,
+        r = sr.SpecRunner(target, draft, batch=1, gamma=3, max_model_len=4096, temperature=0.6,
                           mode="reference", device=cuda)
         r.load_prompts([prompt])
         torch.manual_seed(3)
         r.prefill()
         torch.manual_seed(77)
         r.step()
+        _accept_matches_oracle(r, orc)
         if graphs:
             r.capture()
         lens = [r.lengths()[0]]
         for _ in range(6):
             r.replay() if graphs else r.step()
             torch.cuda.synchronize()
+            _accept_matches_oracle(r, orc)
             lens.append(r.lengths()[0])
         r.check()
         toks = r.tokens(0)
