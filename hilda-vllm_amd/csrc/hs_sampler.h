@@ -178,6 +178,10 @@ int launch_accept_small(const Problem& P, const AcceptArgs& A, const Work& W, co
                         hipStream_t stream);
 // the same for filtered mode when every sequence's top-k is in [1, kTopkMax]
 int small_topk_ok(const Problem& P, const AcceptArgs& A, int esz);
+// single-launch row sampler (reference mode, a few rows; spec_accept_small.hip)
+int small_sampler_ok(const Problem& P, const SampleOut& O, int esz);
+template <typename T>
+int launch_sample_small(const Problem& P, const Work& W, const SampleOut& O, hipStream_t stream);
 template <typename T>
 int launch_accept_small_topk(const Problem& P, const AcceptArgs& A, const Work& W,
                              const SampleOut& O, hipStream_t stream);

@@ -904,7 +904,8 @@ int hs_sampler(const void* logits, int logits_dtype, int64_t logits_row_stride, 
                void* stream) {
   if (rows <= 0 || vocab <= 0) return HS_ERR_INVALID;
   if (rows > kMaxRows) return HS_ERR_UNSUPPORTED;
-  mode &= ~HS_ACCEPT_CHAIN;  // the row sampler always runs the chain
+  const bool chain_only = (mode & HS_ACCEPT_CHAIN) != 0;
+  mode &= ~HS_ACCEPT_CHAIN;
   if (mode != HS_ACCEPT_REFERENCE && mode != HS_ACCEPT_FILTERED && mode != HS_ACCEPT_GREEDY)
     return HS_ERR_INVALID;
   if (logits_dtype != HS_F32 && logits_dtype != HS_BF16) return HS_ERR_INVALID;
@@ -947,6 +948,12 @@ int hs_sampler(const void* logits, int logits_dtype, int64_t logits_row_stride, 
   O.row_stats = row_stats;
   Work W = bind_work(workspace, L);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int esz = logits_dtype == HS_F32 ? 4 : 2;
+  // a few rows in reference mode: one launch (k_sample_small), the same bits
+  if (!chain_only && mode == HS_ACCEPT_REFERENCE && small_sampler_ok(P, O, esz)) {
+    if (logits_dtype == HS_F32) return launch_sample_small<float>(P, W, O, s);
+    return launch_sample_small<uint16_t>(P, W, O, s);
+  }
   if (logits_dtype == HS_F32) return run_sampler_chain<float>(P, A, W, mode, O, s);
   return run_sampler_chain<uint16_t>(P, A, W, mode, O, s);
 }

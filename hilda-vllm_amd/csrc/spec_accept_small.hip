@@ -1235,6 +1235,211 @@ __global__ __launch_bounds__(SmallShape<G>::kThreads) void k_accept_small_topk(P
   }
 }
 
+
+// Single-launch row sampler for a few rows (the draft step's probabilities
+// and token at small batch, model_runner.py:312-313 with sampler.py:13-25,
+// reference mode): one 256-thread workgroup per (chunk, row), every
+// workgroup resident at once (the host checks the CU count).
+//   A: the chunk's maximum and exact exp-sum of x = logit / T (the chain's
+//      chunk statistics), published as tagged words;
+//   B: every workgroup folds the row's normaliser from all chunks' words
+//      (fold_row_tagged), writes its chunk's probabilities p = e / S and
+//      publishes the chunk's fixed-point weight sum (k_sample_part's
+//      arithmetic);
+//   C: every workgroup locates the chunk holding the inverse-CDF point
+//      t = u * W from all weight sums; the workgroup owning it finds the
+//      token in its registers (k_sample_final's rule).
+// Waits, poisoned words and the invalid mark as in k_accept_small: the row's
+// chunk-0 workgroup marks the token -1 first, and only a workgroup whose
+// waits all succeeded writes it again.
+template <typename T>
+__global__ __launch_bounds__(kChunkThreads) void k_sample_small(Problem P, Work W, SampleOut O) {
+  __shared__ float s_m[kChunkThreads / kWave];
+  __shared__ uint64_t s_e[kChunkThreads / kWave];
+  __shared__ RowDesc s_desc;
+  __shared__ uint32_t s_tag;
+  __shared__ int s_bad;
+  __shared__ int s_cstar;
+  __shared__ uint64_t s_trel;
+  __shared__ long long s_tok;
+  const int c = blockIdx.x;
+  const int row = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t nwg = gridDim.x * gridDim.y;
+  SmallSync* sy = W.sync;
+  const int64_t i0 = chunk_elem(c, tid, 0);
+  const bool in = i0 < P.V;
+  const T* lrow = reinterpret_cast<const T*>(P.logits) + (int64_t)row * P.row_stride;
+  const uint32_t limit = spin_budget(sy);
+  uint32_t spent = 0;
+  if (O.sample && c == 0 && tid == 0)
+    __hip_atomic_store(&O.tokens[row], (int64_t)-1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+  // ---- phase A: chunk statistics ----
+  float x[8];
+  load8_row<T>(lrow, i0, in, x);
+  const float u = O.sample ? O.uniforms[row] : 0.0f;
+  const float Tt = P.temps[row];
+  const float rT = 1.0f / Tt;
+  const bool fastT = hs_rcp_ok(Tt);
+  __builtin_amdgcn_sched_barrier(0);
+  // the entry count (see k_accept_small)
+  uint64_t start = 0;
+  if (tid == 0) {
+    start = __hip_atomic_fetch_add(&sy->start, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if ((uint32_t)start == nwg - 1)
+      __hip_atomic_store(&sy->start, ((start >> 32) + 1) << 32, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+  }
+  const bool entry_bad = tid == 0 && (uint32_t)start >= nwg;
+  if (entry_bad) __hip_atomic_store(&sy->err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  float m = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    x[k] = hs_div_temp(x[k], Tt, rT, fastT);
+    if (in) m = fmaxf(m, x[k]);
+  }
+  m = wave_max_f32(m);
+  if (lane == 0) s_m[wid] = m;
+  if (tid == 0) {
+    s_tag = launch_tag(start);
+    s_bad = entry_bad ? 1 : 0;
+  }
+  __syncthreads();
+  const uint32_t tag = s_tag;
+  m = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
+  {
+    uint32_t hi = 0, lo = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (in) hs_fx44_split(hs_exp(x[k] - m), hi, lo);
+    const uint64_t e = wave_sum_u64(hs_join44(hi, lo));
+    if (lane == 0) s_e[wid] = e;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    // the invalid mark reaches memory before this workgroup's first word
+    if (c == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    const uint32_t ptag = s_bad ? (tag | kPoison) : tag;
+    const uint64_t es = s_e[0] + s_e[1] + s_e[2] + s_e[3];
+    uint64_t* sw = stat_words(W, row, P.nchunk) + c * 3;
+    put_u64(sw, tagged(ptag, f2u(m)));
+    put_u64(sw + 1, tagged(ptag, (uint32_t)es));
+    put_u64(sw + 2, tagged(ptag, (uint32_t)(es >> 32)));
+  }
+
+  // ---- phase B: normaliser, this chunk's probabilities and weight sum ----
+  if (wid == 0) {
+    const RowDesc dd = fold_row_tagged(P, W, row, tag, lane, &s_bad, spent, limit);
+    if (lane == 0) s_desc = dd;
+  }
+  __syncthreads();
+  const RowDesc D = s_desc;
+  if (c == 0 && O.row_stats && tid == 0) {
+    O.row_stats[2 * (int64_t)row] = D.m;
+    O.row_stats[2 * (int64_t)row + 1] = D.s;
+  }
+  const float rS = 1.0f / D.s;
+  const bool fastS = hs_rcp_ok(D.s);
+  uint64_t pw[8];
+  float pr[8];
+  uint64_t tp = 0;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    float p = 0.0f;
+    if (in) {
+      const float e = hs_exp(x[k] - D.m);
+      p = fastS ? hs_div_rcp(e, D.s, rS) : e / D.s;
+    }
+    pr[k] = p;
+    uint32_t hi = 0, lo = 0;
+    hs_fx44_split(p, hi, lo);
+    pw[k] = hs_join44(hi, lo);
+    tp += pw[k];
+  }
+  if (O.probs && in) {
+    float* pp = O.probs + (int64_t)row * O.probs_stride + i0;
+    *reinterpret_cast<float4*>(pp) = make_float4(pr[0], pr[1], pr[2], pr[3]);
+    *reinterpret_cast<float4*>(pp + 4) = make_float4(pr[4], pr[5], pr[6], pr[7]);
+  }
+  if (!O.sample) return;
+  tp = wave_sum_u64(tp);
+  if (lane == 0) s_e[wid] = tp;
+  __syncthreads();
+  if (tid == 0) {
+    const uint32_t ptag = s_bad ? (tag | kPoison) : tag;
+    const uint64_t bp = s_e[0] + s_e[1] + s_e[2] + s_e[3];
+    uint64_t* sw = samp_words(W, P.units, row, P.nchunk) + c * 2;
+    put_u64(sw, tagged(ptag, (uint32_t)bp));
+    put_u64(sw + 1, tagged(ptag, (uint32_t)(bp >> 32)));
+  }
+
+  // ---- phase C: chunk of the inverse-CDF point, token in its owner ----
+  if (wid == 0) {
+    uint32_t v[4][2];
+    read_tagged<4, 2>(samp_words(W, P.units, row, P.nchunk), P.nchunk, lane, tag, v, sy, &s_bad,
+                      spent, limit);
+    uint64_t cp[4], pt = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      cp[i] = ((uint64_t)v[i][1] << 32) | v[i][0];
+      pt += cp[i];
+    }
+    pt = wave_sum_u64(pt);
+    const uint64_t t = hs_mulshift24(hs_u24(u), pt);
+    int cstar = -1;
+    uint64_t before = 0, running = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (cstar < 0) {
+        const uint64_t incl = wave_incl_scan_u64(cp[i], lane);
+        const uint64_t mm = __ballot(running + incl > t);
+        if (mm) {
+          const int l = __ffsll((long long)mm) - 1;
+          cstar = i * kWave + l;
+          before = running + __shfl(incl, l, 64) - __shfl(cp[i], l, 64);
+        } else {
+          running += __shfl(incl, 63, 64);
+        }
+      }
+    }
+    if (lane == 0) {
+      s_cstar = cstar;
+      s_trel = t - before;
+      s_tok = -1;
+    }
+  }
+  __syncthreads();
+  const int cstar = s_cstar;
+  if (cstar != c && !(cstar < 0 && c == 0)) return;  // one writer per row
+  if (cstar == c) {
+    const uint64_t trel = s_trel;
+    uint64_t sv = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) sv += pw[k];
+    const uint64_t incl = wave_incl_scan_u64(sv, lane);
+    if (lane == 63) s_e[wid] = incl;
+    __syncthreads();
+    uint64_t off = 0;
+    for (int ww = 0; ww < wid; ++ww) off += s_e[ww];
+    const uint64_t lo = off + incl - sv;
+    if (lo <= trel && trel < off + incl) {
+      uint64_t acc = lo;
+      for (int k = 0; k < 8; ++k) {
+        acc += pw[k];
+        if (acc > trel) {
+          s_tok = (long long)(i0 + k);
+          break;
+        }
+      }
+    }
+    __syncthreads();
+  }
+  if (s_bad != 0) return;  // the token keeps its invalid mark
+  if (tid == 0)
+    __hip_atomic_store(&O.tokens[row], (int64_t)s_tok, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 }  // namespace
 
 int small_accept_ok(const Problem& P, const AcceptArgs& A, int mode, int esz) {
@@ -1316,6 +1521,34 @@ int launch_accept_small_topk(const Problem& P, const AcceptArgs& A, const Work& 
   }
   return hipGetLastError() == hipSuccess ? HS_OK : HS_ERR_LAUNCH;
 }
+
+int small_sampler_ok(const Problem& P, const SampleOut& O, int esz) {
+  if (P.V % 8 || ((uintptr_t)P.logits & 15) || ((P.row_stride * esz) % 16)) return 0;
+  if (O.probs && (((uintptr_t)O.probs & 15) || ((O.probs_stride * 4) % 16))) return 0;
+  if (O.out_kind != 0 || (!O.probs && !O.sample)) return 0;
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return 0;
+  // every workgroup resident at once (one 256-thread workgroup per CU at
+  // most), at most four chunks per lane in the folds, words within the region
+  const size_t tag_bytes = ((size_t)P.units * 3 + (size_t)P.units * 4) * (size_t)P.nchunk * 8;
+  return (P.nchunk <= 4 * kWave && (int64_t)P.nchunk * P.units <= cus &&
+          tag_bytes <= kSmallTagBytes) ? 1 : 0;
+}
+
+template <typename T>
+int launch_sample_small(const Problem& P, const Work& W, const SampleOut& O,
+                        hipStream_t stream) {
+  hipLaunchKernelGGL(k_sample_small<T>, dim3(P.nchunk, P.units), dim3(kChunkThreads), 0,
+                     stream, P, W, O);
+  return hipGetLastError() == hipSuccess ? HS_OK : HS_ERR_LAUNCH;
+}
+
+template int launch_sample_small<float>(const Problem&, const Work&, const SampleOut&,
+                                        hipStream_t);
+template int launch_sample_small<uint16_t>(const Problem&, const Work&, const SampleOut&,
+                                           hipStream_t);
 
 template int launch_accept_small<float>(const Problem&, const AcceptArgs&, const Work&,
                                         const SampleOut&, hipStream_t);

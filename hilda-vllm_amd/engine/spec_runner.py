@@ -325,13 +325,17 @@ class SpecRunner:
                 set_context(False, cq, ck, 1, 0, slots, None, st.block_tables)
                 h = self.draft(ids, pos)
             logits = self.draft.compute_logits(h)
+            # one sequence: the token goes straight to its draft slot (a column of
+            # several sequences is strided, so it goes through the scratch)
+            tok = G.draft_tokens[:, j] if self.B == 1 else self.tok_scratch
             if self.mode == "greedy":
-                ops.sample_rows(logits, mode="greedy", tokens_out=self.tok_scratch)
+                ops.sample_rows(logits, mode="greedy", tokens_out=tok)
             else:
                 ops.sample_rows(logits, self.temps, self.top_ks, self.top_ps, mode=mode,
                                 uniforms=G.u_draft[j], probs_out=G.draft_probs[:, j],
-                                tokens_out=self.tok_scratch)
-            G.draft_tokens[:, j].copy_(self.tok_scratch)
+                                tokens_out=tok)
+            if self.B != 1:
+                G.draft_tokens[:, j].copy_(self.tok_scratch)
         reset_context()
 
     def verify_phase(self):
@@ -396,8 +400,8 @@ class SpecRunner:
         outputs (fixed-gamma runs read nothing back per step; the flag is sticky).
         Synchronises with the device."""
         if ops.accept_error(self.device, clear=True):
-            raise RuntimeError("spec run: an acceptance call produced invalid outputs (a "
-                               "bounded wait inside the single-launch kernel ran out)")
+            raise RuntimeError("spec run: an acceptance or draft-sampler call produced invalid "
+                               "outputs (a bounded wait inside a single-launch kernel ran out)")
 
     # ------------------------------------------------------------------ graphs
     def capture(self):

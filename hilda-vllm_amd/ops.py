@@ -173,29 +173,36 @@ def spec_accept(target_logits: torch.Tensor, draft_probs: torch.Tensor | None,
 
 
 def accept_error(device, clear: bool = False) -> bool:
-    """True once a spec_accept call on this device's shared acceptance workspace
-    produced invalid outputs (num_accepted -1): the sticky 32-bit word at byte 8
-    of the workspace (include/hilda_spec.h). Synchronises with the device."""
-    ws = _WS.get((_dev_index(device), "spec_accept"))
-    if ws is None:
-        return False
-    word = ws[8:12]
-    bad = bool(word.cpu().any())
-    if clear and bad:
-        word.zero_()
+    """True once a spec_accept call (num_accepted -1) or a sample_rows call (token
+    -1) on this device's shared workspaces produced invalid outputs: the sticky
+    32-bit word at byte 8 of either workspace (include/hilda_spec.h).
+    Synchronises with the device."""
+    bad = False
+    for kind in ("spec_accept", "sampler"):
+        ws = _WS.get((_dev_index(device), kind))
+        if ws is None:
+            continue
+        word = ws[8:12]
+        if bool(word.cpu().any()):
+            bad = True
+            if clear:
+                word.zero_()
     return bad
 
 
-def accept_wait_budget(device, polls: int | None) -> None:
-    """Sets the wait budget of the single-launch acceptance on this device's
-    acceptance workspace (the 32-bit word at byte 12, include/hilda_spec.h):
-    `polls` polls per thread over all its waits of a launch, or the default with
-    None. For tests of the failure path: a small budget makes the kernels give
-    up their waits (every kernel still exits), and the calls report invalid
-    outputs. Creates the workspace if needed; ordered on the current stream."""
+def accept_wait_budget(device, polls: int | None, kind: str = "spec_accept") -> None:
+    """Sets the wait budget of the single-launch kernels on this device's
+    acceptance (kind "spec_accept") or row-sampler ("sampler") workspace (the
+    32-bit word at byte 12, include/hilda_spec.h): `polls` polls per thread over
+    all its waits of a launch, or the default with None. For tests of the
+    failure path: a small budget makes the kernels give up their waits (every
+    kernel still exits), and the calls report invalid outputs. Creates the
+    workspace if needed; ordered on the current stream."""
     dev = torch.device("cuda", _dev_index(device))
     lib = L.lib()
-    ws = workspace(dev, lib.hs_spec_accept_workspace_size(1, 1, 8), "spec_accept")
+    size = (lib.hs_spec_accept_workspace_size(1, 1, 8) if kind == "spec_accept"
+            else lib.hs_sampler_workspace_size(1, 8))
+    ws = workspace(dev, size, kind)
     word = ws[12:16].view(torch.int32)
     word.fill_(0 if polls is None else int(polls) + 1)
 
@@ -214,12 +221,16 @@ def sample_rows(logits: torch.Tensor, temperatures: torch.Tensor | None = None,
                 top_ks: torch.Tensor | None = None, top_ps: torch.Tensor | None = None, *,
                 mode="reference", uniforms: torch.Tensor | None = None, want_probs: bool = False,
                 out_kind: int = 0, row_stats: bool = False,
-                probs_out: torch.Tensor | None = None, tokens_out: torch.Tensor | None = None):
+                probs_out: torch.Tensor | None = None, tokens_out: torch.Tensor | None = None,
+                chain_only: bool = False):
     """Row sampler (Sampler.forward / draft probabilities).
 
     Returns dict(probs=[rows, V] f32 or None, tokens=[rows] int64 or None,
     row_stats=[rows, 2] or None). out_kind 1 returns the masked logits of the
-    top-k/top-p filters instead of probabilities.
+    top-k/top-p filters instead of probabilities. A few rows in reference mode
+    run as one launch; chain_only runs the launch chain instead (same bits).
+    A row whose single-launch draw could not complete (a bounded wait ran out)
+    gets token -1 and sets the sticky flag accept_error reads.
     """
     m = _mode(mode)
     dev = _need_cuda(logits, temperatures, top_ks, top_ps, uniforms)
@@ -268,7 +279,8 @@ def sample_rows(logits: torch.Tensor, temperatures: torch.Tensor | None = None,
 
     rc = lib.hs_sampler(p(lg), _logit_dtype(lg), lstride, rows, V, p(temperatures),
                         p(top_ks) if m == L.HS_ACCEPT_FILTERED else None,
-                        p(top_ps) if m == L.HS_ACCEPT_FILTERED else None, m, p(probs),
+                        p(top_ps) if m == L.HS_ACCEPT_FILTERED else None,
+                        m | (L.HS_ACCEPT_CHAIN if chain_only else 0), p(probs),
                         probs.stride(0) if probs is not None else 0, int(out_kind),
                         uniforms_ptr if m != L.HS_ACCEPT_GREEDY else None,
                         p(toks), p(stats), ws.data_ptr(), ws.numel(), _stream(dev))

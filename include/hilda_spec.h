@@ -8,20 +8,15 @@
  *
  * Workspaces: query the size with the matching *_workspace_size() function
  * and pass a buffer at least that large. Two calls that share one workspace
- * must not overlap in time. Three kinds:
- *  - hs_sampler: the workspace only carries partial results from one launch
- *    of a call to the next launch of the same call; it needs no
- *    initialisation.
- *  - hs_verify_attention and hs_qk_norm_rope_attend: likewise, except that
- *    its first 16 KiB hold counters of the fused call's in-kernel merge of
- *    key splits; they must be zero before the first call and every call
- *    leaves them zero. These two entry points may share a workspace with
- *    each other but not with any other entry point.
- *  - hs_spec_accept and hs_spec_commit: the workspace also carries state from
- *    one call to the next. It must be zero-filled before its first use, every
- *    call leaves it ready for the next (so the calls can be recorded into a
- *    HIP graph without a clearing step), and it must not be passed to any
- *    other entry point.
+ * must not overlap in time. A workspace is zero-filled before its first use
+ * and every call leaves it ready for the next (so the calls can be recorded
+ * into a HIP graph without a clearing step). Each entry point's workspace is
+ * its own, except that hs_verify_attention and hs_qk_norm_rope_attend may
+ * share one:
+ *  - hs_spec_accept, hs_sampler and hs_spec_commit carry state from one call
+ *    to the next (launch counters, the free-list scratch);
+ *  - hs_verify_attention / hs_qk_norm_rope_attend hold partial results of a
+ *    call after 16 KiB of merge counters that every call leaves zero.
  */
 #ifndef HILDA_SPEC_H
 #define HILDA_SPEC_H
@@ -57,8 +52,8 @@ extern "C" {
 /* Flag OR-ed into any mode of hs_spec_accept: run the launch chain (chunk    */
 /* statistics, filter passes, row filter, decision and draw) even where a     */
 /* single-launch kernel would serve the call. The results are the same bits;  */
-/* this is for testing and timing the paths. hs_sampler accepts and ignores   */
-/* it (it always runs the chain).                                             */
+/* this is for testing and timing the paths. OR-ed into the mode of          */
+/* hs_sampler it likewise forces that call's launch chain.                    */
 #define HS_ACCEPT_CHAIN 0x200
 
 /* Human-readable text for a status code (static storage). */
@@ -138,6 +133,15 @@ int hs_spec_accept(const void* target_logits, int logits_dtype, int64_t logits_r
 /* uniforms + tokens_out (optional, both or neither): one                    */
 /* uniform per row drives an inverse-CDF draw that replaces the exponential- */
 /* race draw of sampler.py:24.                                               */
+/* workspace: hs_sampler_workspace_size bytes, zero-filled before its first */
+/* use (every call leaves it ready for the next); not shared with other     */
+/* entry points. Reference-mode calls whose rows x ceil(vocab/2048)         */
+/* workgroups fit one per CU (vocab a multiple of 8, 16-byte aligned rows   */
+/* and probability rows, out_kind 0) run as a single launch whose           */
+/* workgroups exchange data through the workspace, with the bounded waits   */
+/* of hs_spec_accept's single launch (same budget word at byte offset 12,  */
+/* same sticky error word at byte offset 8); a row whose draw could not be  */
+/* completed gets token -1 (its probabilities are then unspecified).        */
 /* ------------------------------------------------------------------------ */
 size_t hs_sampler_workspace_size(int rows, int vocab);
 

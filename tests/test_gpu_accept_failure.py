@@ -86,3 +86,49 @@ def test_zero_wait_budget(hv, orc, cuda, kind):
     np.testing.assert_array_equal(out, ref["out_tokens"])
     np.testing.assert_array_equal(olen, ref["out_len"])
     assert not ops.accept_error(cuda)
+
+
+def test_sampler_zero_wait_budget(hv, orc, cuda):
+    """The single-launch row sampler under a zero wait budget: each row's token is
+    the oracle's or -1 (with the sticky error word set), each call returns at
+    once, and the default budget afterwards gives the oracle's tokens."""
+    ops = hv.ops
+    V, rows = 151936, 3
+    rng = np.random.default_rng(5)
+    logits = rng.standard_normal((rows, V), dtype=np.float32) * 2
+    T = np.array([0.6, 1.0, 0.8], np.float32)
+    u = rng.random(rows, dtype=np.float32)
+    ref = orc.sampler(logits, T, np.zeros(rows, np.int32), np.ones(rows, np.float32),
+                      mode="reference", uniforms=u)
+    lg = torch.from_numpy(logits).to(cuda)
+    Tt, ut = torch.from_numpy(T).to(cuda), torch.from_numpy(u).to(cuda)
+
+    def call():
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        r = ops.sample_rows(lg, Tt, mode="reference", uniforms=ut, want_probs=True)
+        toks = r["tokens"].cpu().numpy()
+        return toks, time.perf_counter() - t0
+
+    call()
+    ops.accept_error(cuda, clear=True)
+    print("sampler zero wait budget", flush=True)
+    ops.accept_wait_budget(cuda, 0, kind="sampler")
+    invalid = 0
+    try:
+        for _ in range(4):
+            toks, dt = call()
+            assert dt < 0.25, dt
+            for b in range(rows):
+                if toks[b] < 0:
+                    invalid += 1
+                else:
+                    assert toks[b] == ref["tokens"][b]
+        if invalid:
+            assert ops.accept_error(cuda)
+    finally:
+        ops.accept_wait_budget(cuda, None, kind="sampler")
+    ops.accept_error(cuda, clear=True)
+    toks, _ = call()
+    np.testing.assert_array_equal(toks, ref["tokens"])
+    assert not ops.accept_error(cuda)

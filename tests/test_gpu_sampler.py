@@ -365,3 +365,47 @@ def test_filter_segmented_passes_many_rows(hv, orc, cuda, dtype, unaligned):
     np.testing.assert_array_equal(r["probs"].cpu().numpy(), ref["probs"])
     np.testing.assert_array_equal(r["tokens"].cpu().numpy(), ref["tokens"])
     np.testing.assert_array_equal(r["row_stats"].cpu().numpy(), ref["row_stats"])
+
+
+@pytest.mark.parametrize("rows,dtype,temps", [(1, "bf16", [0.6]), (1, "f32", [1.0]),
+                                              (2, "f32", [1.3, 0.6]),
+                                              (3, "bf16", [0.6, 1.0, 2.0])])
+def test_sampler_single_launch_matches_chain_and_oracle(hv, orc, cuda, rows, dtype, temps):
+    """The single-launch row sampler (a few rows, reference mode: the draft step's
+    softmax(logits / T) and token, model_runner.py:312-313) writes the same
+    probabilities, tokens and row statistics as the launch chain, bit for bit, and
+    both equal the C oracle; the probabilities go to a strided view as the draft
+    phase writes them (draft_probs[:, j] of [rows, gamma, V]). Uniforms include
+    the range ends."""
+    V = 151936
+    rng = np.random.default_rng(100 + rows)
+    logits = rng.standard_normal((rows, V), dtype=np.float32) * 2
+    if dtype == "bf16":
+        bits = hv.synthetic.f32_to_bf16_bits(logits)
+        logits = (bits.astype(np.uint32) << 16).view(np.float32)
+        lg = torch.from_numpy(bits.view(np.int16)).to(cuda).view(torch.bfloat16)
+    else:
+        lg = torch.from_numpy(logits).to(cuda)
+    T = np.array(temps, np.float32)
+    for u_case in ("random", "ends"):
+        u = rng.random(rows, dtype=np.float32) if u_case == "random" else \
+            np.array([0.0, np.float32(1.0) - np.float32(2 ** -24), 0.5][:rows], np.float32)
+        ref = orc.sampler(logits, T, np.zeros(rows, np.int32), np.ones(rows, np.float32),
+                          mode="reference", uniforms=u)
+        got = []
+        for chain in (False, True):
+            big = torch.full((rows, 3, V), float("nan"), device=cuda)
+            tok = torch.full((rows,), -7, dtype=torch.int64, device=cuda)
+            print(f"sampler rows={rows} {dtype} u={u_case} chain={chain}", flush=True)
+            r = hv.ops.sample_rows(lg, torch.from_numpy(T).to(cuda), mode="reference",
+                                   uniforms=torch.from_numpy(u).to(cuda), probs_out=big[:, 1],
+                                   tokens_out=tok, row_stats=True, chain_only=chain)
+            torch.cuda.synchronize()
+            assert torch.isnan(big[:, 0]).all() and torch.isnan(big[:, 2]).all()
+            got.append((big[:, 1].cpu().numpy(), tok.cpu().numpy(),
+                        r["row_stats"].cpu().numpy()))
+        for probs, toks, stats in got:
+            np.testing.assert_array_equal(toks, ref["tokens"])
+            np.testing.assert_array_equal(stats, ref["row_stats"])
+            np.testing.assert_array_equal(probs, ref["probs"])
+    assert not hv.ops.accept_error(cuda)
