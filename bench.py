@@ -232,6 +232,58 @@ def bench_accept(args, torch, hv):
     return res
 
 
+def bench_sampler(args, torch, hv):
+    """The draft step's row sampler alone (model_runner.py:312-313 with
+    sampler.py:13-25): softmax(logits / T) of --batch rows written into one column of
+    a [B, 3, V] draft-probability buffer (as the draft phase writes it) and one token
+    per row drawn with an explicit uniform; --logits bf16 (default) or f32 ~ N(0, 2^2),
+    T = --temperature, reference mode (a few rows run as one launch; --chain forces the
+    launch chain). Inputs rotate over copies so every call reads HBM."""
+    dev = torch.device("cuda:0")
+    B = args.batch
+    esz = 2 if args.logits == "bf16" else 4
+    step_bytes = B * V * esz + B * V * 4 + B * 8  # logits read, probabilities and tokens written
+    copies = max(2, int(512e6 // (B * V * esz)) + 1)
+    gen = torch.Generator(device=dev).manual_seed(0)
+    lg = torch.randn((B, V), generator=gen, device=dev) * 2.0
+    if args.logits == "bf16":
+        lg = lg.to(torch.bfloat16)
+    bufs = [lg.clone() for _ in range(copies)]
+    del lg
+    probs = torch.empty((B, 3, V), dtype=torch.float32, device=dev)
+    toks = torch.empty(B, dtype=torch.int64, device=dev)
+    temps = torch.full((B,), args.temperature, device=dev)
+    u = torch.rand(B, generator=gen, device=dev)
+
+    def one_round():
+        for i in range(copies):
+            hv.ops.sample_rows(bufs[i], temps, mode="reference", uniforms=u,
+                               probs_out=probs[:, 1], tokens_out=toks, chain_only=args.chain)
+
+    reps_w = max(1, -(-args.warmup // copies))
+    reps = max(1, -(-args.steps // copies))
+    graph_time_us(torch, dev, one_round, reps_w)
+    us = graph_time_us(torch, dev, one_round, reps) / copies
+    achieved = step_bytes / (us * 1e-6) / 1e9
+    tag = f"sampler-b{B}-{args.logits}" + ("-chain" if args.chain else "")
+    kernel = "k_sample_small<bf16>" if args.logits == "bf16" else "k_sample_small<float>"
+    return {"metric": METRIC, "value": round(us, 3), "unit": "us/call (row sampler)",
+            "n_gpus": 1, "steps": reps * copies, "warmup": reps_w * copies,
+            "ms_per_step": round(us / 1e3, 6), "higher_is_better": False, "scaling": "weak",
+            "vs_baseline": None, "dtype": f"{args.logits} logits, f32 math",
+            "data": "synthetic (seeded N(0,2^2) logits)",
+            "config": {"workload": f"draft-step row sampler, B={B} V={V} {args.logits}, "
+                                   f"T={args.temperature}, reference mode",
+                       "chain_only": bool(args.chain), "input_copies_rotated": copies},
+            "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5),
+                         "traffic": None if args.chain else profiled_traffic(kernel, tag),
+                         "bytes_per_step": step_bytes,
+                         "kernels": "one hs_sampler call: k_sample_small for a few rows, "
+                                    "else the chain (chunk statistics, probabilities and "
+                                    "partial sums, final search)"}}
+
+
 def bench_attention(args, torch, hv):
     """Config 2: B=64 sequences x 4 verify queries, 16/8 heads, D=128, L ~ U[64, 2048],
     256-token blocks in a random permutation; bf16 or fp8-e4m3 cache."""
@@ -1120,8 +1172,8 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="spec",
-                    choices=["spec", "accept", "attention", "attention-b1", "gemm", "copy",
-                             "adaptive"])
+                    choices=["spec", "accept", "sampler", "attention", "attention-b1", "gemm",
+                             "copy", "adaptive"])
     ap.add_argument("--max-context", type=int, default=8192)
     ap.add_argument("--rocprof-summary", metavar="DIR", default=None,
                     help="print a text summary of a rocprofv3 CSV output directory and exit")
@@ -1149,7 +1201,7 @@ def main(argv=None):
     ap.add_argument("--no-forced", action="store_true",
                     help="spec workload: skip the forced-acceptance companion run")
     ap.add_argument("--chain", action="store_true",
-                    help="accept workload: force the launch chain (no single-launch kernel)")
+                    help="accept and sampler workloads: force the launch chain (no single-launch kernel)")
     ap.add_argument("--no-topk-hint", action="store_true",
                     help="accept workload: do not pass the top-k <= 64 promise (chain path)")
     args = ap.parse_args(argv)
@@ -1181,6 +1233,8 @@ def main(argv=None):
         res = bench_gemm(args, torch, hv)
     elif args.workload == "adaptive":
         res = bench_adaptive(args, torch, hv)
+    elif args.workload == "sampler":
+        res = bench_sampler(args, torch, hv)
     else:
         res = bench_accept(args, torch, hv)
     print(json.dumps(res))

@@ -116,15 +116,22 @@ class Qwen3Layer(nn.Module):
         ctx = get_context()
         attn._check_bound(ctx)
         if attn.calib is not None:
-            # FP8 calibration pass: amax of the K rows (after q/k-norm and RoPE) and V rows
-            _, kk = _ops.qk_norm_rope(qkv, g.num_heads, g.num_kv_heads, self.q_norm, self.k_norm,
-                                      self.rope.cos_sin, positions, g.rms_eps)
+            # FP8 calibration pass (a prefill with no cached prefix): amax of the K rows
+            # (after q/k-norm and RoPE) and V rows, and the attention over those bf16
+            # rows themselves (no cache store), so that later layers see the activations
+            # of an exact cache rather than of one quantised with unknown scales
+            qq, kk = _ops.qk_norm_rope(qkv, g.num_heads, g.num_kv_heads, self.q_norm, self.k_norm,
+                                       self.rope.cos_sin, positions, g.rms_eps)
             vv = qkv[:, self.q_size + self.kv_size:]
             torch.maximum(attn.calib, torch.stack([kk.abs().amax(), vv.abs().amax()]).float(),
                           out=attn.calib)
-        # q/k-norm + RoPE + KV store + attention: one launch for decode and verify steps
-        o = attn.attend_qkv(qkv, self.q_norm, self.k_norm, self.rope.cos_sin, positions,
-                            g.rms_eps)
+            vr = vv.reshape(-1, g.num_kv_heads, g.head_dim).contiguous()  # k's strides
+            o = _ops.verify_attention(qq, kk, vr, None, ctx.cu_seqlens_q, ctx.cu_seqlens_k,
+                                      ctx.max_seqlen_q, ctx.max_seqlen_k, attn.scale)
+        else:
+            # q/k-norm + RoPE + KV store + attention: one launch for decode and verify steps
+            o = attn.attend_qkv(qkv, self.q_norm, self.k_norm, self.rope.cos_sin, positions,
+                                g.rms_eps)
         h = _ops.linear(o.reshape(o.shape[0], -1), self.o)
         x, residual = _ops.linear_rmsnorm(h, self.ln2, g.rms_eps, self.gate_up, residual=residual,
                                           swiglu=True)

@@ -206,8 +206,11 @@ class SpecRunner:
 
     def _calibrate_fp8(self, ids, pos, cu, maxlen, slots):
         """Per-layer k/v scales of the FP8 target cache, headroom * amax / 448, from
-        the K (after q/k-norm and RoPE) and V rows of the prompt; one extra target
-        forward whose cache writes the real prefill then overwrites."""
+        the K (after q/k-norm and RoPE) and V rows of the prompt: one extra target
+        forward that attends over each layer's own bf16 K/V rows and stores nothing
+        (so every layer's amax is measured on undistorted activations). Tokens past
+        the prompt that exceed amax * headroom saturate at +-448 * scale:
+        kv_saturation() measures how many codes did."""
         layers = self.target.attention_layers()
         for a in layers:
             a.calib = torch.zeros(2, dtype=torch.float32, device=self.device)
@@ -224,6 +227,22 @@ class SpecRunner:
 
     def kv_scales(self) -> list[tuple[float, float]]:
         return [(a.k_scale, a.v_scale) for a in self.target.attention_layers()]
+
+    def kv_saturation(self) -> float:
+        """Fraction of the FP8 target cache's codes in use (the blocks of the running
+        sequences' tables) that sit at the e4m3fn saturation value +-448 (codes 0x7e,
+        0xfe): values the per-tensor scales clipped. 0 for a bf16 cache. Reads the
+        cache back (a diagnostic, synchronises)."""
+        if self.kv.dtype != torch.float8_e4m3fn:
+            return 0.0
+        nb = self.state.num_seq_blocks.cpu().tolist()
+        bt = self.state.block_tables.cpu()
+        used = sorted({int(bt[b, i]) for b in range(self.B) for i in range(nb[b])})
+        if not used:
+            return 0.0
+        codes = self.kv.view(torch.uint8)[:, :, torch.tensor(used, device=self.device)]
+        sat = ((codes & 0x7F) == 0x7E).sum().item()
+        return sat / codes.numel()
 
     # ------------------------------------------------------------------ preemption
     def preempt(self, b: int):

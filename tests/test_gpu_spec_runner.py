@@ -468,3 +468,44 @@ def test_config3_real_geometry_graph_matches_eager(cuda, orc, draft_kind):
     assert all(1 <= s <= 4 for s in steps), steps
     if draft_kind == "forced":
         assert sum(steps) > len(steps), steps  # some drafts accepted
+
+
+def test_fp8_calibration_matches_bf16_cache_amax(cuda):
+    """FP8 scale calibration (prefill without given scales) attends over each layer's
+    own bf16 K/V rows, so every layer's amax is taken on the activations of an exact
+    cache: the scales equal headroom * amax / 448 of the K and V rows that a
+    bf16-cache run of the same model and prompt stores, layer by layer. After a few
+    steps, kv_saturation() reports the share of clipped codes (in [0, 1))."""
+    q3, sr = _mods()
+    g = _small(q3, layers=3)
+    target = q3.Qwen3Host(g, device=cuda, seed=21)
+    draft = q3.Qwen3Host(g, device=cuda, seed=22)
+    prompt = torch.randint(0, 3000, (40,), generator=torch.Generator().manual_seed(4)).tolist()
+    print("fp8 calibration vs bf16 cache amax", flush=True)
+
+    def runner(kv):
+        r = sr.SpecRunner(target, draft, batch=1, gamma=3, max_model_len=256, temperature=0.6,
+                          mode="reference", kv_cache_dtype=kv, device=cuda)
+        r.load_prompts([prompt])
+        torch.manual_seed(1)
+        r.prefill()
+        torch.cuda.synchronize()
+        return r
+
+    r8 = runner("fp8")
+    scales = r8.kv_scales()
+    rb = runner("auto")
+    bt = rb.state.block_tables[0].cpu().tolist()
+    slots = [bt[p // rb.bs] * rb.bs + p % rb.bs for p in range(len(prompt))]
+    idx = torch.tensor(slots, device=cuda)
+    for i, (ks, vs) in enumerate(scales):
+        kr = rb.kv[0, i].reshape(-1, g.num_kv_heads, g.head_dim)[idx]
+        vr = rb.kv[1, i].reshape(-1, g.num_kv_heads, g.head_dim)[idx]
+        ek = kr.float().abs().amax().item() * r8.FP8_HEADROOM / 448.0
+        ev = vr.float().abs().amax().item() * r8.FP8_HEADROOM / 448.0
+        assert abs(ks - ek) <= 1e-6 * ek and abs(vs - ev) <= 1e-6 * ev, (i, ks, ek, vs, ev)
+    for _ in range(3):
+        r8.step()
+    sat = r8.kv_saturation()
+    assert 0.0 <= sat < 1.0
+    print(f"fp8 saturated share after 3 steps: {sat:.2e}", flush=True)
