@@ -136,7 +136,8 @@ struct Work {
 struct SampleOut {
   float* probs;
   int64_t probs_stride;
-  int out_kind;  // 0: probabilities, 1: logits/T inside the kept set, -inf outside
+  int out_kind;  // 0: probabilities, 1: logits/T inside the kept set, -inf outside,
+                 // 2: the unfiltered probabilities (the draw stays filtered)
   const float* uniforms;
   int64_t* tokens;
   int sample;

@@ -384,6 +384,11 @@ __global__ __launch_bounds__(kT) void k_sample_part(Problem P, AcceptArgs A, Wor
   float* pout = O.probs ? O.probs + (int64_t)row * O.probs_stride : nullptr;
   const bool p_vec = pout && ((reinterpret_cast<uintptr_t>(pout) & 15u) == 0);
   const bool masked = (O.out_kind == 1);
+  // out_kind 2: the row's unfiltered probabilities, exp(x - m) / s_full over
+  // every element (m, the row maximum, is always kept), beside the filtered draw
+  const bool full = (O.out_kind == 2);
+  const float rSf = 1.0f / D.s_full;
+  const bool fastSf = hs_rcp_ok(D.s_full);
   const int c_begin = (int)((int64_t)split * P.nchunk / P.nsplit);
   const int c_end = (int)((int64_t)(split + 1) * P.nchunk / P.nsplit);
 
@@ -396,16 +401,20 @@ __global__ __launch_bounds__(kT) void k_sample_part(Problem P, AcceptArgs A, Wor
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       const int64_t i = i0 + k;
-      float p = 0.0f, xm = -INFINITY;
+      float p = 0.0f, xm = -INFINITY, pf = 0.0f;
       if (i < P.V) {
         const float x = hs_div_temp(v[k], Tt, rT, fastT);
-        if (desc_keep(D, hs_key(x), i)) {
+        const bool kept = desc_keep(D, hs_key(x), i);
+        if (kept || full) {
           const float e = hs_exp(x - D.m);
-          p = fastS ? hs_div_rcp(e, D.s, rS) : e / D.s;
-          xm = x;
+          if (kept) {
+            p = fastS ? hs_div_rcp(e, D.s, rS) : e / D.s;
+            xm = x;
+          }
+          if (full) pf = fastSf ? hs_div_rcp(e, D.s_full, rSf) : e / D.s_full;
         }
       }
-      pr[k] = masked ? xm : p;
+      pr[k] = masked ? xm : (full ? pf : p);
       hs_fx44_split(p, phi, plo);
       if (residual) hs_fx44_split(fmaxf(p - q[k], 0.0f), whi, wlo);
     }
@@ -919,8 +928,10 @@ int hs_sampler(const void* logits, int logits_dtype, int64_t logits_row_stride, 
     if (!temperatures) return HS_ERR_INVALID;
     if (probs_out && probs_row_stride < vocab) return HS_ERR_INVALID;
   }
-  if (out_kind != 0 && out_kind != 1) return HS_ERR_INVALID;
+  if (out_kind < 0 || out_kind > 2) return HS_ERR_INVALID;
   if (mode == HS_ACCEPT_FILTERED && (!top_ks || !top_ps)) return HS_ERR_INVALID;
+  // reference mode keeps every element: its unfiltered probabilities are out_kind 0's
+  if (mode == HS_ACCEPT_REFERENCE && out_kind == 2) out_kind = 0;
   const int nchunk = nchunk_of(vocab);
   Layout L = make_layout(rows, rows, nchunk);
   if (workspace_bytes < L.total) return HS_ERR_WORKSPACE;

@@ -40,11 +40,13 @@ class SpecRunner:
                  mode: str = "reference", eos: int = -1, k_scale: float | None = None,
                  v_scale: float | None = None, device="cuda", adaptive: bool = False,
                  max_gamma: int | None = None):
-        if mode == "reference" and (0 < top_k < target.g.vocab or top_p < 1.0):
-            # the reference draws draft tokens from the filtered Sampler but keeps the
-            # unfiltered softmax as the draft probabilities (model_runner.py:312-313);
-            # hs_sampler has no output kind giving both, so such settings use "filtered"
-            raise ValueError("reference mode takes no top-k / top-p; use mode='filtered'")
+        filters = 0 < top_k < target.g.vocab or top_p < 1.0
+        # reference mode with top-k / top-p draws the draft tokens from the filtered
+        # Sampler and keeps the unfiltered softmax as the draft probabilities
+        # (model_runner.py:312-313): hs_sampler's output kind 2 gives both in one
+        # call; the acceptance compares against the unfiltered target (:398)
+        self.draft_out_kind = 2 if (mode == "reference" and filters) else 0
+        self.draft_mode = "filtered" if (mode == "filtered" or self.draft_out_kind) else "reference"
         self.target, self.draft = target, draft
         self.B, self.gamma = batch, gamma
         self.max_gamma = max(gamma, max_gamma or (8 if adaptive else gamma))
@@ -329,7 +331,6 @@ class SpecRunner:
         G = self._g()
         ops.spec_prealloc(st, G.gamma, out=G.elig)
         G.u_draft.uniform_()
-        mode = "filtered" if self.mode == "filtered" else "reference"
         for j in range(G.gamma):
             if j == 0:
                 # two queries: the previous token (fills the draft K/V the last step
@@ -350,7 +351,8 @@ class SpecRunner:
             if self.mode == "greedy":
                 ops.sample_rows(logits, mode="greedy", tokens_out=tok)
             else:
-                ops.sample_rows(logits, self.temps, self.top_ks, self.top_ps, mode=mode,
+                ops.sample_rows(logits, self.temps, self.top_ks, self.top_ps,
+                                mode=self.draft_mode, out_kind=self.draft_out_kind,
                                 uniforms=G.u_draft[j], probs_out=G.draft_probs[:, j],
                                 tokens_out=tok)
             if self.B != 1:

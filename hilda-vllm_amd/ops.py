@@ -227,7 +227,8 @@ def sample_rows(logits: torch.Tensor, temperatures: torch.Tensor | None = None,
 
     Returns dict(probs=[rows, V] f32 or None, tokens=[rows] int64 or None,
     row_stats=[rows, 2] or None). out_kind 1 returns the masked logits of the
-    top-k/top-p filters instead of probabilities. A few rows in reference mode
+    top-k/top-p filters instead of probabilities; out_kind 2 the unfiltered
+    probabilities beside the filtered draw (model_runner.py:312-313). A few rows in reference mode
     run as one launch; chain_only runs the launch chain instead (same bits).
     A row whose single-launch draw could not complete (a bounded wait ran out)
     gets token -1 and sets the sticky flag accept_error reads.

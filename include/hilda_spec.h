@@ -129,7 +129,12 @@ int hs_spec_accept(const void* target_logits, int logits_dtype, int64_t logits_r
 /* probs_out (optional): [rows, vocab] f32. out_kind 0 writes the           */
 /* probabilities of the (filtered) distribution; out_kind 1 writes logits/T  */
 /* inside the kept set and -inf outside it, i.e. the masked logits of        */
-/* Sampler._apply_top_k/_apply_top_p (sampler.py:27-49).                    */
+/* Sampler._apply_top_k/_apply_top_p (sampler.py:27-49); out_kind 2 writes  */
+/* the unfiltered softmax(logits/T) (bit-identical to a reference-mode      */
+/* call's probabilities) while the draw stays filtered: the draft step of   */
+/* reference-mode acceptance with top-k / top-p, which samples from Sampler  */
+/* but keeps torch.softmax(logits/T) as the draft probabilities             */
+/* (model_runner.py:312-313). In reference mode out_kind 2 is out_kind 0.   */
 /* uniforms + tokens_out (optional, both or neither): one                    */
 /* uniform per row drives an inverse-CDF draw that replaces the exponential- */
 /* race draw of sampler.py:24.                                               */

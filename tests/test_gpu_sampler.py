@@ -210,6 +210,40 @@ def test_sampler_probs_and_tokens(hv, orc, cuda, mode):
     np.testing.assert_array_equal(r["probs"].cpu().numpy(), ref["probs"])
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_sampler_unfiltered_probs_beside_filtered_draw(hv, orc, cuda, dtype):
+    """out_kind 2 (model_runner.py:312-313: the draft token from the filtered
+    Sampler, the draft probabilities from the unfiltered softmax(logits/T)): the
+    tokens equal the oracle's filtered draw and the probabilities the oracle's
+    reference-mode (unfiltered) rows, bit for bit; rows without a filter (k 0,
+    p 1) included, and the same call in reference mode equals out_kind 0."""
+    rng = np.random.default_rng(21)
+    rows, V = 6, 151936
+    logits = (rng.standard_normal((rows, V), dtype=np.float32) * 2)
+    if dtype == "bf16":
+        lg = torch.from_numpy(logits).to(cuda).to(torch.bfloat16)
+        logits = lg.float().cpu().numpy()
+    else:
+        lg = torch.from_numpy(logits).to(cuda)
+    temps = np.array([1.0, 0.6, 1.2, 0.9, 1.0, 0.5], np.float32)
+    tk = np.array([50, 0, 20, 1, 0, 5000], np.int32)
+    tp = np.array([0.9, 0.8, 1.0, 1.0, 1.0, 0.95], np.float32)
+    u = rng.random(rows, dtype=np.float32)
+    dev = {k: torch.from_numpy(v).to(cuda) for k, v in
+           dict(t=temps, k=tk, p=tp, u=u).items()}
+    r = hv.ops.sample_rows(lg, dev["t"], dev["k"], dev["p"], mode="filtered",
+                           uniforms=dev["u"], want_probs=True, out_kind=2)
+    filt = orc.sampler(logits, temps, tk, tp, mode="filtered", uniforms=u)
+    full = orc.sampler(logits, temps, mode="reference", uniforms=u)
+    np.testing.assert_array_equal(r["tokens"].cpu().numpy(), filt["tokens"])
+    np.testing.assert_array_equal(r["probs"].cpu().numpy(), full["probs"])
+    assert (filt["probs"] == 0).any() and not (full["probs"][:, :100] == 0).all()
+    r2 = hv.ops.sample_rows(lg, dev["t"], mode="reference", uniforms=dev["u"], want_probs=True,
+                            out_kind=2)
+    np.testing.assert_array_equal(r2["tokens"].cpu().numpy(), full["tokens"])
+    np.testing.assert_array_equal(r2["probs"].cpu().numpy(), full["probs"])
+
+
 def test_sampler_masked_logits_match_reference_kats(hv, cuda):
     """tests/test_sampler.py:6-44 of the reference, through the GPU filter."""
     x = torch.tensor([[5.0, 4.0, 3.0, 2.0]], device=cuda)

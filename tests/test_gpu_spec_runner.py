@@ -153,6 +153,61 @@ def test_filtered_topk_graph_replay_matches_eager(cuda):
         assert graph.tokens(b) == eager.tokens(b)
 
 
+def test_reference_mode_with_filters_keeps_unfiltered_draft_probs(cuda, orc):
+    """Reference mode with top-k 50 / top-p 0.9 (model_runner.py:312-313 and
+    :387-428): draft tokens come from the filtered Sampler, the draft
+    probabilities are the unfiltered softmax(logits/T), and the acceptance
+    compares them with the unfiltered target. Each step's draft rows have more
+    than 50 nonzero probabilities, each draft token ranks among its row's 50
+    largest, the acceptance equals the C oracle in reference mode on the step's
+    own inputs, and graph replays reproduce eager steps."""
+    q3, sr = _mods()
+    gt = _small(q3, layers=2, vocab=151936)
+    gd = _small(q3, layers=1, vocab=151936)
+
+    def make():
+        target = q3.Qwen3Host(gt, device=cuda, seed=31)
+        draft = q3.Qwen3Host(gd, device=cuda, seed=32)
+        r = sr.SpecRunner(target, draft, batch=2, gamma=3, max_model_len=400, block_size=32,
+                          temperature=0.8, top_k=50, top_p=0.9, mode="reference", device=cuda)
+        assert r.draft_out_kind == 2 and r.draft_mode == "filtered" and not r.topk_le64
+        r.load_prompts([[3, 4, 5, 6], list(range(300, 330))])
+        torch.manual_seed(8)
+        r.prefill()
+        return r
+
+    def check_step(r):
+        G = r._g()
+        q = G.draft_probs.cpu()
+        toks = G.draft_tokens.cpu()
+        for b in range(r.B):
+            for j in range(G.gamma):
+                row = q[b, j]
+                assert int((row > 0).sum()) > 50
+                assert abs(float(row.double().sum()) - 1.0) < 1e-4
+                assert int((row > row[int(toks[b, j])]).sum()) < 50
+        _accept_matches_oracle(r, orc)
+
+    eager = make()
+    torch.manual_seed(91)
+    for _ in range(5):
+        eager.step()
+        torch.cuda.synchronize()
+        check_step(eager)
+    graph = make()
+    torch.manual_seed(91)
+    graph.step()
+    graph.capture()
+    for _ in range(4):
+        graph.replay()
+        torch.cuda.synchronize()
+        check_step(graph)
+    graph.check()
+    assert graph.lengths() == eager.lengths()
+    for b in range(2):
+        assert graph.tokens(b) == eager.tokens(b)
+
+
 def test_fused_layer_matches_eager(cuda):
     """Fused kernels (RMSNorm inside the projections, qk-norm + RoPE + KV store,
     SwiGLU epilogue) vs the eager restatement of qwen3.py:72-185 (same attention
