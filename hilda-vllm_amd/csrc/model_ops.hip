@@ -5,8 +5,9 @@
 // PyTorch would launch ~45 tiny kernels per layer for them, which at batch 1
 // costs more than the layer's GEMMs. One launch each here:
 //   hs_rmsnorm       (optional residual add) + RMSNorm, one workgroup per row;
-//   hs_qk_norm_rope  per-head RMSNorm of q and k + neox RoPE, one wave per
-//                    (token, head): lane l owns the rotation pair (l, l + 64);
+//   hs_qk_norm_rope  per-head RMSNorm of q and k + neox RoPE, one 16-lane row
+//                    per (token, head): lane j holds dims 8j .. 8j + 7, all
+//                    lane exchanges in DPP;
 //   hs_qk_norm_rope_store  the same, with k written straight into its paged
 //                    cache slot and v copied there (bf16, or FP8 e4m3fn with a
 //                    per-tensor scale), replacing the separate store_kvcache
@@ -89,7 +90,9 @@ __global__ __launch_bounds__(kNT) void k_rmsnorm(const uint16_t* __restrict__ x,
   }
 }
 
-// one wave per (token, head); heads [0, Hq) are q, [Hq, Hq+Hkv) are k
+// One 16-lane row per (token, head), four heads per wave (norm_rope_row's
+// layout: lane j of a row holds dims 8j .. 8j + 7, read and written with one
+// 16-byte access); heads [0, Hq) are q, [Hq, Hq+Hkv) are k.
 __global__ __launch_bounds__(kNT) void k_qk_norm_rope(const uint16_t* __restrict__ qkv, int64_t ts,
                                                       int Hq, int Hkv,
                                                       const uint16_t* __restrict__ qw,
@@ -98,18 +101,22 @@ __global__ __launch_bounds__(kNT) void k_qk_norm_rope(const uint16_t* __restrict
                                                       const int64_t* __restrict__ positions,
                                                       float eps, uint16_t* __restrict__ qo,
                                                       uint16_t* __restrict__ ko, int N) {
-  const int wave = blockIdx.x * (kNT / 64) + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
   const int H = Hq + Hkv;
-  if (wave >= N * H) return;
-  const int tok = wave / H, h = wave % H;
+  const int64_t row = ((int64_t)blockIdx.x * kNT + threadIdx.x) >> 4;
+  const int j = threadIdx.x & 15;
+  if (row >= (int64_t)N * H) return;  // whole rows: the row's DPP partners are here
+  const int tok = (int)(row / H), h = (int)(row % H);
   const bool isq = h < Hq;
-  uint16_t y1, y2;
-  norm_rope_pair(qkv + tok * ts + h * 128, isq ? qw : kw, cos_sin + positions[tok] * 128, eps,
-                 lane, y1, y2);
+  uint16_t xh[8], w[8], y[8];
+  unpack8(*reinterpret_cast<const uint4*>(qkv + tok * ts + h * 128 + 8 * j), xh);
+  unpack8(*reinterpret_cast<const uint4*>((isq ? qw : kw) + 8 * j), w);
+  float x[8], c[8], sn[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) x[k] = bf(xh[k]);
+  load_rot8(cos_sin + positions[tok] * 128, j, c, sn);
+  norm_rope_row(x, w, c, sn, eps, j, y);
   uint16_t* dst = isq ? qo + ((int64_t)tok * Hq + h) * 128 : ko + ((int64_t)tok * Hkv + (h - Hq)) * 128;
-  dst[lane] = y1;
-  dst[lane + 64] = y2;
+  *reinterpret_cast<uint4*>(dst + 8 * j) = pack8(y);
 }
 
 struct NormRopeStoreArgs {
@@ -130,43 +137,52 @@ struct NormRopeStoreArgs {
   int block_size, num_blocks, N;
 };
 
-// one wave per (token, head) over the q, k and v heads of the fused qkv row:
-// q heads are normalised, rotated and written to qo; k heads are normalised,
-// rotated and stored at the token's cache slot; v heads are stored unchanged.
-// Slots < 0 (and blocks beyond num_blocks) store nothing, as store_kvcache.
+// One 16-lane row per (token, head) over the q, k and v heads of the fused qkv
+// row (four heads per wave, norm_rope_row's layout): q heads are normalised,
+// rotated and written to qo; k heads are normalised, rotated and stored at
+// the token's cache slot; v heads are stored unchanged. Slots < 0 (and blocks
+// beyond num_blocks) store nothing, as store_kvcache.
 template <bool kFp8>
 __global__ __launch_bounds__(kNT) void k_qk_norm_rope_store(NormRopeStoreArgs a) {
   // the argument block's three 64-byte lines requested together (latency-bound
   // at decode sizes)
   asm volatile("" ::"s"(a.qkv), "s"(a.qo), "s"(a.block_size));
-  const int wave = blockIdx.x * (kNT / 64) + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
   const int H = a.Hq + 2 * a.Hkv;
-  if (wave >= a.N * H) return;
-  const int tok = wave / H, h = wave % H;
-  const uint16_t* src = a.qkv + tok * a.ts + h * 128;
-  if (h < a.Hq) {
-    uint16_t y1, y2;
-    norm_rope_pair(src, a.qw, a.cos_sin + a.positions[tok] * 128, a.eps, lane, y1, y2);
-    uint16_t* dst = a.qo + ((int64_t)tok * a.Hq + h) * 128;
-    dst[lane] = y1;
-    dst[lane + 64] = y2;
+  const int64_t row = ((int64_t)blockIdx.x * kNT + threadIdx.x) >> 4;
+  const int j = threadIdx.x & 15;
+  if (row >= (int64_t)a.N * H) return;  // whole rows: the row's DPP partners are here
+  const int tok = (int)(row / H), h = (int)(row % H);
+  uint16_t xh[8];
+  unpack8(*reinterpret_cast<const uint4*>(a.qkv + tok * a.ts + h * 128 + 8 * j), xh);
+  const bool isv = h >= a.Hq + a.Hkv;
+  if (isv) {  // v: stored as it is
+    const int slot = a.slots[tok];
+    if (slot < 0) return;
+    const int blk = slot / a.block_size, off = slot % a.block_size;
+    if (blk >= a.num_blocks) return;
+    const int64_t elem = (int64_t)blk * a.c_sb + (int64_t)off * a.c_st +
+                         (int64_t)(h - a.Hq - a.Hkv) * a.c_sh;
+    store_row8<kFp8>(a.vc, elem, j, xh, a.v_scale);
+    return;
+  }
+  const bool isq = h < a.Hq;
+  uint16_t w[8], y[8];
+  unpack8(*reinterpret_cast<const uint4*>((isq ? a.qw : a.kw) + 8 * j), w);
+  float x[8], c[8], sn[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) x[k] = bf(xh[k]);
+  load_rot8(a.cos_sin + a.positions[tok] * 128, j, c, sn);
+  norm_rope_row(x, w, c, sn, a.eps, j, y);
+  if (isq) {
+    *reinterpret_cast<uint4*>(a.qo + ((int64_t)tok * a.Hq + h) * 128 + 8 * j) = pack8(y);
     return;
   }
   const int slot = a.slots[tok];
   if (slot < 0) return;
   const int blk = slot / a.block_size, off = slot % a.block_size;
   if (blk >= a.num_blocks) return;
-  const bool isk = h < a.Hq + a.Hkv;
-  const int kvh = isk ? h - a.Hq : h - a.Hq - a.Hkv;
-  const int64_t elem = (int64_t)blk * a.c_sb + (int64_t)off * a.c_st + (int64_t)kvh * a.c_sh;
-  if (isk) {
-    uint16_t y1, y2;
-    norm_rope_pair(src, a.kw, a.cos_sin + a.positions[tok] * 128, a.eps, lane, y1, y2);
-    store_pair<kFp8>(a.kc, elem, lane, y1, y2, a.k_scale);
-  } else {
-    store_pair<kFp8>(a.vc, elem, lane, src[lane], src[lane + 64], a.v_scale);
-  }
+  const int64_t elem = (int64_t)blk * a.c_sb + (int64_t)off * a.c_st + (int64_t)(h - a.Hq) * a.c_sh;
+  store_row8<kFp8>(a.kc, elem, j, y, a.k_scale);
 }
 
 __global__ __launch_bounds__(kNT) void k_silu_mul(const uint16_t* __restrict__ gu, int64_t gs,
@@ -228,8 +244,12 @@ int hs_qk_norm_rope(const void* qkv, int64_t token_stride, int num_q_heads, int 
       num_tokens < 0 || num_q_heads <= 0 || num_kv_heads <= 0)
     return HS_ERR_INVALID;
   if (head_dim != 128) return HS_ERR_UNSUPPORTED;
-  const int64_t waves = (int64_t)num_tokens * (num_q_heads + num_kv_heads);
-  hipLaunchKernelGGL(k_qk_norm_rope, dim3((unsigned)((waves + 3) / 4)), dim3(kNT), 0,
+  // 16-byte rows: every 8-element piece of a head is one load or store
+  if ((token_stride % 8) || (((uintptr_t)qkv | (uintptr_t)q_out | (uintptr_t)k_out |
+                             (uintptr_t)q_weight | (uintptr_t)k_weight | (uintptr_t)cos_sin) & 15))
+    return HS_ERR_UNSUPPORTED;
+  const int64_t rows = (int64_t)num_tokens * (num_q_heads + num_kv_heads);
+  hipLaunchKernelGGL(k_qk_norm_rope, dim3((unsigned)((rows + kNT / 16 - 1) / (kNT / 16))), dim3(kNT), 0,
                      reinterpret_cast<hipStream_t>(stream), static_cast<const uint16_t*>(qkv),
                      token_stride, num_q_heads, num_kv_heads,
                      static_cast<const uint16_t*>(q_weight),
@@ -255,7 +275,12 @@ int hs_qk_norm_rope_store(const void* qkv, int64_t token_stride, int num_q_heads
   if (kv_dtype != HS_BF16 && kv_dtype != HS_FP8_E4M3) return HS_ERR_INVALID;
   if (kv_dtype == HS_FP8_E4M3 && !(k_scale > 0.0f && v_scale > 0.0f)) return HS_ERR_INVALID;
   if (token_stride < (int64_t)(num_q_heads + 2 * num_kv_heads) * 128) return HS_ERR_INVALID;
-  if (((uintptr_t)qkv | (uintptr_t)q_out | (uintptr_t)k_cache | (uintptr_t)v_cache) & 1)
+  // 16-byte rows (8-byte fp8 rows): every 8-element piece of a head is one load or store
+  if ((token_stride % 8) || (cache_stride_block % 8) || (cache_stride_tok % 8) ||
+      (cache_stride_head % 8) ||
+      (((uintptr_t)qkv | (uintptr_t)q_out | (uintptr_t)q_weight | (uintptr_t)k_weight |
+        (uintptr_t)cos_sin) & 15) ||
+      (((uintptr_t)k_cache | (uintptr_t)v_cache) & (kv_dtype == HS_BF16 ? 15 : 7)))
     return HS_ERR_UNSUPPORTED;
   NormRopeStoreArgs a;
   a.qkv = static_cast<const uint16_t*>(qkv);
@@ -279,8 +304,8 @@ int hs_qk_norm_rope_store(const void* qkv, int64_t token_stride, int num_q_heads
   a.block_size = block_size;
   a.num_blocks = num_blocks;
   a.N = num_tokens;
-  const int64_t waves = (int64_t)num_tokens * (num_q_heads + 2 * num_kv_heads);
-  const dim3 grid((unsigned)((waves + 3) / 4));
+  const int64_t rows = (int64_t)num_tokens * (num_q_heads + 2 * num_kv_heads);
+  const dim3 grid((unsigned)((rows + kNT / 16 - 1) / (kNT / 16)));
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (kv_dtype == HS_FP8_E4M3)
     hipLaunchKernelGGL(k_qk_norm_rope_store<true>, grid, dim3(kNT), 0, s, a);

@@ -179,25 +179,51 @@ typedef short v4i16_t __attribute__((ext_vector_type(4)));
 typedef int v2i32_t __attribute__((ext_vector_type(2)));
 #define HS_LDS __attribute__((address_space(3)))
 
+// Per-lane byte offsets of a wave's window loads, the same for every window
+// of the wave (computed once): instruction i of a tile covers rows kk = i * R
+// + lane / L (R rows of L lanes each, 16 bytes per lane); `off` is the
+// lane's chunk of row kk (its swizzled position in the tile) and `off0` the
+// same chunk of row 0, the stand-in for rows past `hi`. The host keeps 32
+// token rows of the cache within 2 GiB.
+template <bool kFp8>
+struct WinOffs {
+  static constexpr int kLanesPerRow = (kFp8 ? 128 : 256) / 16;
+  static constexpr int kRowsPerInst = 64 / kLanesPerRow;
+  static constexpr int kInst = kWin / kRowsPerInst;
+  uint32_t off[kInst], off0[kInst];
+  int lrow;  // lane / kLanesPerRow
+};
+
+template <bool kFp8>
+__device__ __forceinline__ WinOffs<kFp8> win_offs(const AttnArgs& a, int lane) {
+  using W = WinOffs<kFp8>;
+  const int esz = kFp8 ? 1 : 2;
+  W w;
+  w.lrow = lane / W::kLanesPerRow;
+  const int sl = lane % W::kLanesPerRow;
+#pragma unroll
+  for (int i = 0; i < W::kInst; ++i) {
+    const int kk = i * W::kRowsPerInst + w.lrow;
+    const uint32_t c16 = (uint32_t)(sl ^ (kFp8 ? swz8(kk) : swz16(kk))) * 16u;
+    w.off[i] = (uint32_t)(kk * a.c_st * esz) + c16;
+    w.off0[i] = c16;
+  }
+  return w;
+}
+
 // Copies the K and V rows of one 32-key window into the wave's LDS tiles with
 // global->LDS loads (16 bytes per lane, each instruction covering whole rows).
 // Keys at or past `hi` re-read key ws (always valid) so every tile row holds
 // finite cache data; their scores are masked to -inf.
 template <bool kFp8>
-__device__ __forceinline__ void issue_window(const AttnArgs& a, const uint8_t* kbase,
-                                             const uint8_t* vbase, int ws, int hi,
-                                             uint8_t* tile_k, uint8_t* tile_v, int lane) {
-  constexpr int kRowB = kFp8 ? 128 : 256;
-  constexpr int kLanesPerRow = kRowB / 16;
-  constexpr int kRowsPerInst = 64 / kLanesPerRow;
-  const int esz = kFp8 ? 1 : 2;
+__device__ __forceinline__ void issue_window(const uint8_t* kbase, const uint8_t* vbase, int ws,
+                                             int hi, uint8_t* tile_k, uint8_t* tile_v,
+                                             const WinOffs<kFp8>& wo) {
+  using W = WinOffs<kFp8>;
+  const int lim = hi - ws;  // rows of the window below hi
 #pragma unroll
-  for (int i = 0; i < kWin / kRowsPerInst; ++i) {
-    const int kk = i * kRowsPerInst + lane / kLanesPerRow;
-    const int sl = lane % kLanesPerRow;
-    const int c = sl ^ (kFp8 ? swz8(kk) : swz16(kk));
-    const int key = (ws + kk < hi) ? kk : 0;
-    const int64_t off = ((int64_t)key * a.c_st) * esz + c * 16;
+  for (int i = 0; i < W::kInst; ++i) {
+    const uint32_t off = (i * W::kRowsPerInst + wo.lrow < lim) ? wo.off[i] : wo.off0[i];
     __builtin_amdgcn_global_load_lds(kbase + off, (HS_LDS void*)(tile_k + i * 1024), 16, 0, 0);
     __builtin_amdgcn_global_load_lds(vbase + off, (HS_LDS void*)(tile_v + i * 1024), 16, 0, 0);
   }
@@ -253,10 +279,7 @@ struct AttnLds {
   static constexpr int kTileB = kWin * kRowB;
   static constexpr int kKvBytes = kAW * 2 * kTileB;
   static constexpr int kOBytes = kAW * kRows * kOStride * 4;
-  // 16 zero bytes after the tiles and partials: the merge reads them in place
-  // of the partials of waves that held no keys
-  static constexpr int kZeroOff = kKvBytes > kOBytes ? kKvBytes : kOBytes;
-  static constexpr int kRawBytes = kZeroOff + 16;
+  static constexpr int kRawBytes = kKvBytes > kOBytes ? kKvBytes : kOBytes;
 };
 
 // Running softmax state of one wave: per query row (lane column n) the max
@@ -267,111 +290,314 @@ struct WaveAcc {
   f32x4_t oacc[8];
 };
 
-// The q/k-norm + RoPE + KV store of one (sequence, kv head) tile, by all the
-// workgroup's waves, each item one head in norm_rope_pair's layout (lane l
-// holds dims l and l + 64, so the bits equal hs_qk_norm_rope_store's): the
-// kv head's k and v rows of the sequence's query tokens go to their cache
-// slots (slots < 0 and blocks past num_blocks store nothing), the tile's q
-// rows to s_q (16 rows x 128 bf16). The host runs this only when one
-// workgroup holds every query row of the (sequence, kv head), so no other
-// workgroup reads these rows.
-// qkv_load issues every load of the wave's items (it = wid + kAW i, the k/v
-// tokens first so their stores go out first) at kernel start; the cos/sin
-// row is fetched at the position the token holds in its sequence
-// (Lk - Lq + i, clamped into the table) together with positions[], and
-// fetched again in qkv_finish where positions[] says otherwise. qkv_finish
-// computes and stores, waits for the stores and ends at a workgroup barrier.
-constexpr int kQkvItems = 4;  // up to 32 items: 16 q rows and at most 16 tokens
-struct QkvLoads {
-  int nrows, nitems;
-  int64_t pos[kQkvItems];
-  int guess[kQkvItems], slot[kQkvItems];
-  uint16_t x1[kQkvItems], x2[kQkvItems], w1[kQkvItems], w2[kQkvItems];
-  uint16_t v1[kQkvItems], v2[kQkvItems];
-  float c[kQkvItems], sn[kQkvItems];
+// The q/k-norm + RoPE of the fused kernel's (sequence, kv head) tile, in
+// norm_rope_row's layout (one 16-lane row per head, lane j holding dims 8j ..
+// 8j + 7, so the bits equal hs_qk_norm_rope_store's): the tile's q rows go to
+// s_q (16 rows x 128 bf16), the kv head's k and v rows of the sequence's query
+// tokens to s_new (token i's rows laid out as the tile row of key Lk - Lq + i,
+// the cache's bytes: bf16, or the e4m3fn codes the store writes) and to the
+// registers from which kv_store_all writes them to their cache slots (slots <
+// 0 and blocks past num_blocks store nothing). The host runs this only when
+// one workgroup holds every query row of the (sequence, kv head), so no other
+// workgroup of the split reads these rows.
+// Heads are wave items of 4 rows: the q rows first, then the k rows, then the
+// v rows of the query tokens, each kind from a wave boundary on; wave w takes
+// items w and w + 8 (two rounds cover 16 q rows and 16 tokens). qkv_load
+// issues every load of the wave's rows as soon as the sequence bounds are
+// known, each piece of a head one 16-byte load; the cos/sin row is fetched at
+// the position the token holds in its sequence (Lk - Lq + i, clamped into the
+// table) together with positions[], and fetched again in qkv_compute where
+// positions[] says otherwise.
+constexpr int kQkvRounds = 2;
+struct QkvRow {
+  int kind;  // 0: q row, 1: k of a token, 2: v of a token, -1: none
+  int idx;   // q row of the tile, or query token
+  int tok;   // token of the call
 };
+struct QkvLoads {
+  QkvRow row[kQkvRounds];
+  int64_t pos[kQkvRounds];
+  int guess[kQkvRounds], slot[kQkvRounds];
+  uint4 x[kQkvRounds], w[kQkvRounds];
+  float c[kQkvRounds][8], sn[kQkvRounds][8];
+};
+
+// the row of lane `lane` in wave item wi (4 rows per item)
+__device__ __forceinline__ QkvRow qkv_row(const TileRef& t, int nrows, int wi, int lane) {
+  const int wq = (nrows + 3) / 4, wk = (t.Lq + 3) / 4;
+  QkvRow r;
+  r.kind = -1;
+  r.idx = 0;
+  r.tok = t.qs;
+  int k, base, count;
+  if (wi < wq) {
+    k = 0, base = 0, count = nrows;
+  } else if (wi < wq + wk) {
+    k = 1, base = wq, count = t.Lq;
+  } else if (wi < wq + 2 * wk) {
+    k = 2, base = wq + wk, count = t.Lq;
+  } else {
+    return r;
+  }
+  const int i = 4 * (wi - base) + (lane >> 4);
+  if (i >= count) return r;
+  r.kind = k;
+  r.idx = i;
+  return r;
+}
 
 __device__ __forceinline__ void qkv_load(const AttnArgs& a, const QkvArgs& qa, const TileRef& t,
                                          int kvh, int G, QkvLoads& L) {
-  const int lane = threadIdx.x & 63;
+  const int lane = threadIdx.x & 63, j = lane & 15;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int r0 = t.qt * kRows;
-  L.nrows = t.rows - r0 < kRows ? t.rows - r0 : kRows;
-  L.nitems = t.Lq + L.nrows;  // k/v of each query token, then the q rows
-  // a zero the compiler cannot see as uniform: the slot loads stay vector
-  // loads whose values are not moved to scalar registers at once (which would
-  // wait for each item's loads before the next item's are issued)
-  int vzero;
-  asm volatile("v_mov_b32 %0, 0" : "=v"(vzero));
+  const int nrows = t.rows < kRows ? t.rows : kRows;
 #pragma unroll
-  for (int i = 0; i < kQkvItems; ++i) {
-    const int it = wid + kAW * i;
+  for (int i = 0; i < kQkvRounds; ++i) {
+    QkvRow r = qkv_row(t, nrows, wid + kAW * i, lane);
     L.slot[i] = -1;
-    if (it < L.nitems) {
-      const bool iskv = it < t.Lq;
-      const int r = r0 + (it - t.Lq);
-      const int qi = iskv ? it : r / G;
-      const int tok = t.qs + qi;
-      const int head = iskv ? qa.Hq + kvh : kvh * G + r % G;
-      const uint16_t* src = qa.qkv + (int64_t)tok * qa.ts + (int64_t)head * kD;
-      const uint16_t* w = iskv ? qa.kw : qa.qw;
-      int g = t.Lk - t.Lq + qi;
-      g = g < 0 ? 0 : (g >= qa.cs_rows ? qa.cs_rows - 1 : g);
-      L.guess[i] = g;
-      L.pos[i] = qa.positions[tok];
-      L.x1[i] = src[lane];
-      L.x2[i] = src[lane + 64];
-      L.w1[i] = w[lane];
-      L.w2[i] = w[lane + 64];
-      const float* cs = qa.cos_sin + (int64_t)g * kD;
-      L.c[i] = cs[lane];
-      L.sn[i] = cs[64 + lane];
-      if (iskv) {
-        L.slot[i] = qa.slots[tok + vzero];
-        const uint16_t* vs = src + (int64_t)a.Hkv * kD;
-        L.v1[i] = vs[lane];
-        L.v2[i] = vs[lane + 64];
+    if (r.kind >= 0) {
+      const int qi = r.kind == 0 ? r.idx / G : r.idx;
+      r.tok = t.qs + qi;
+      const int head = r.kind == 0 ? kvh * G + r.idx % G
+                                   : qa.Hq + (r.kind == 2 ? a.Hkv : 0) + kvh;
+      L.x[i] = *reinterpret_cast<const uint4*>(qa.qkv + (int64_t)r.tok * qa.ts +
+                                               (int64_t)head * kD + 8 * j);
+      L.pos[i] = qa.positions[r.tok];
+      if (r.kind != 2) {
+        L.w[i] = *reinterpret_cast<const uint4*>((r.kind == 0 ? qa.qw : qa.kw) + 8 * j);
+        int g = t.Lk - t.Lq + qi;
+        g = g < 0 ? 0 : (g >= qa.cs_rows ? qa.cs_rows - 1 : g);
+        L.guess[i] = g;
+        load_rot8(qa.cos_sin + (int64_t)g * kD, j, L.c[i], L.sn[i]);
       }
+      if (r.kind != 0) L.slot[i] = qa.slots[r.tok];
     }
+    L.row[i] = r;
+  }
+}
+
+// The cache stores of the wave's k/v rows: element offset of the row (-1:
+// nothing to store), the cache, and the lane's 8 bf16 values.
+struct KvStores {
+  int64_t elem[kQkvRounds];
+  bool isv[kQkvRounds];
+  uint16_t h[kQkvRounds][8];
+};
+
+// byte offset of dims 8j .. 8j + 7 of a tile row for window row kk (the
+// tile's 16-byte chunk swizzle; 8 fp8 codes are half a chunk)
+template <bool kFp8>
+__device__ __forceinline__ int tile_piece(int kk, int j) {
+  if constexpr (kFp8)
+    return (((j >> 1) ^ swz8(kk)) << 4) | ((j & 1) << 3);
+  else
+    return (j ^ swz16(kk)) << 4;
+}
+
+template <bool kFp8>
+__device__ __forceinline__ void qkv_compute(const AttnArgs& a, const QkvArgs& qa, const TileRef& t,
+                                            int kvh, QkvLoads& L, uint16_t* s_q, uint8_t* s_new,
+                                            KvStores& S) {
+  constexpr int kRowB = AttnLds<kFp8>::kRowB;
+  const int lane = threadIdx.x & 63, j = lane & 15;
+  const int knew = t.Lk - t.Lq;
+#pragma unroll
+  for (int i = 0; i < kQkvRounds; ++i) {
+    S.elem[i] = -1;
+    S.isv[i] = false;
+    const QkvRow r = L.row[i];
+    if (r.kind < 0) continue;
+    uint16_t xh[8], y[8];
+    unpack8(L.x[i], xh);
+    if (r.kind != 2) {
+      if (L.pos[i] != L.guess[i])  // the token sits elsewhere than its key index
+        load_rot8(qa.cos_sin + L.pos[i] * kD, j, L.c[i], L.sn[i]);
+      uint16_t w[8];
+      unpack8(L.w[i], w);
+      float x[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) x[k] = bf(xh[k]);
+      norm_rope_row(x, w, L.c[i], L.sn[i], qa.eps, j, y);
+    } else {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) y[k] = xh[k];
+    }
+    if (r.kind == 0) {
+      *reinterpret_cast<uint4*>(s_q + r.idx * kD + 8 * j) = pack8(y);
+      continue;
+    }
+    // token r.idx's k or v row as the tile row of key knew + r.idx (the fast
+    // case needs Lq <= kRows)
+    if (r.idx < kRows) {
+      const int kk = (knew + r.idx) & (kWin - 1);
+      uint8_t* dst = s_new + (r.kind == 2 ? kRows * kRowB : 0) + r.idx * kRowB + tile_piece<kFp8>(kk, j);
+      if constexpr (kFp8)
+        *reinterpret_cast<uint2*>(dst) = e4m3x8_of_bf16(y, r.kind == 2 ? qa.v_scale : qa.k_scale);
+      else
+        *reinterpret_cast<uint4*>(dst) = pack8(y);
+    }
+    // store_kvcache semantics: slots < 0 and blocks past num_blocks store nothing
+    if (L.slot[i] >= 0) {
+      const int blk = L.slot[i] / a.block_size, off = L.slot[i] % a.block_size;
+      if (blk < a.num_blocks)
+        S.elem[i] = (int64_t)blk * a.c_sb + (int64_t)off * a.c_st + (int64_t)kvh * a.c_sh;
+    }
+    S.isv[i] = r.kind == 2;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) S.h[i][k] = y[k];
   }
 }
 
 template <bool kFp8>
-__device__ __forceinline__ void qkv_finish(const AttnArgs& a, const QkvArgs& qa, const TileRef& t,
-                                           int kvh, QkvLoads& L, uint16_t* s_q) {
-  const int lane = threadIdx.x & 63;
-  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  uint8_t* kc = const_cast<uint8_t*>(a.kc);
-  uint8_t* vc = const_cast<uint8_t*>(a.vc);
+__device__ __forceinline__ void kv_store_all(const AttnArgs& a, const QkvArgs& qa,
+                                             const KvStores& S) {
+  const int j = threadIdx.x & 15;
 #pragma unroll
-  for (int i = 0; i < kQkvItems; ++i) {
-    const int it = wid + kAW * i;
-    if (it >= L.nitems) break;
-    if (L.pos[i] != L.guess[i]) {  // the token sits elsewhere than its key index
-      const float* cs = qa.cos_sin + L.pos[i] * kD;
-      L.c[i] = cs[lane];
-      L.sn[i] = cs[64 + lane];
+  for (int i = 0; i < kQkvRounds; ++i) {
+    if (S.elem[i] >= 0)
+      store_row8<kFp8>(const_cast<uint8_t*>(S.isv[i] ? a.vc : a.kc), S.elem[i], j, S.h[i],
+                       S.isv[i] ? qa.v_scale : qa.k_scale);
+  }
+}
+
+// Workgroup barrier that orders LDS only: global loads and stores in flight
+// stay in flight (a plain __syncthreads waits for all of them).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Reads window ws (keys ws .. ws + 31) from the wave's LDS tiles into the
+// MFMA operand registers: K as the A operand of S^T (row rho = n holds key
+// ws + 8*(n/4) + 4*kb + (n%4)) and V^T as the A operand of d-block db (lane
+// (n, g) holds V[8g .. 8g+7][16db + n], gathered with transposing LDS reads).
+// kNew: the rows of keys at or past knew come from the new-key rows nk / nv
+// instead (row key - knew, laid out as the tile row of that key; masked keys
+// past the last new row nlast read that row: finite data weighted 0).
+template <bool kFp8, bool kNew>
+__device__ __forceinline__ void window_read(const uint8_t* tile_k, const uint8_t* tile_v,
+                                            const uint8_t* nk, const uint8_t* nv, int ws,
+                                            int knew, int nlast, int lane, bf16x8_t (&ka)[2][4],
+                                            bf16x8_t (&va)[8]) {
+  constexpr int kRowB = AttnLds<kFp8>::kRowB;
+  const int n = lane & 15, g = lane >> 4;
+  // row base of window row kk in the tile or the new-key rows
+  auto row_of = [&](const uint8_t* tile, const uint8_t* nrow, int kk) -> const uint8_t* {
+    if constexpr (kNew) {
+      const int r = ws + kk - knew;
+      return r >= 0 ? nrow + (r < nlast ? r : nlast) * kRowB : tile + kk * kRowB;
+    } else {
+      return tile + kk * kRowB;
     }
-    uint16_t y1, y2;
-    norm_rope_vals(bf(L.x1[i]), bf(L.x2[i]), L.w1[i], L.w2[i], L.c[i], L.sn[i], qa.eps, y1, y2);
-    if (it >= t.Lq) {
-      const int row = it - t.Lq;
-      s_q[row * kD + lane] = y1;
-      s_q[row * kD + lane + 64] = y2;
-    } else if (L.slot[i] >= 0) {
-      // store_kvcache semantics: slots < 0 and blocks past num_blocks store nothing
-      const int blk = L.slot[i] / a.block_size, off = L.slot[i] % a.block_size;
-      if (blk < a.num_blocks) {
-        const int64_t elem = (int64_t)blk * a.c_sb + (int64_t)off * a.c_st + (int64_t)kvh * a.c_sh;
-        store_pair<kFp8>(kc, elem, lane, y1, y2, qa.k_scale);
-        store_pair<kFp8>(vc, elem, lane, L.v1[i], L.v2[i], qa.v_scale);
+  };
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    const int kk = 8 * (n >> 2) + 4 * kb + (n & 3);
+    const uint8_t* row = row_of(tile_k, nk, kk);
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds) {
+      if constexpr (kFp8) {
+        const int u = g + 4 * ds;  // 8-byte unit of dims 8g + 32ds
+        const int ph = (((u >> 1) ^ swz8(kk)) << 4) | ((u & 1) << 3);
+        const uint2 raw = *reinterpret_cast<const uint2*>(row + ph);
+        ka[kb][ds] = fp8x8w_to_bf16(raw.x, raw.y);
+      } else {
+        const int ph = ((g + 4 * ds) ^ swz16(kk)) << 4;
+        ka[kb][ds] = u4_to_bf16x8(*reinterpret_cast<const uint4*>(row + ph));
       }
     }
   }
-  // the cache stores have reached the L2 before any wave of the workgroup
-  // loads those rows (their lines were not read by this workgroup before)
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
+#pragma unroll
+  for (int db = 0; db < 8; ++db) {
+    if constexpr (kFp8) {
+      const int kk = 8 * g + (n >> 1);
+      const int ph = ((db ^ swz8(kk)) << 4) | ((n & 1) << 3);
+      const v2i32_t t = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+          (HS_LDS v2i32_t*)(row_of(tile_v, nv, kk) + ph));
+      va[db] = fp8x8w_to_bf16((uint32_t)t[0], (uint32_t)t[1]);
+    } else {
+      union {
+        v4i16_t h[2];
+        bf16x8_t v;
+      } u;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int kk = 8 * g + 4 * h + (n >> 2);
+        const int ph = (((2 * db + ((n & 3) >> 1)) ^ swz16(kk)) << 4) | ((n & 1) << 3);
+        u.h[h] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (HS_LDS v4i16_t*)(row_of(tile_v, nv, kk) + ph));
+      }
+      va[db] = u.v;
+    }
+  }
+}
+
+// A row's scores are exponentiated against a reference that trails its
+// running max by at most 2^kRefSlack (log2 units): O and the sum are rescaled
+// only when some row's max passes its reference by more, which after the
+// first window is rare. The normalised output is the same softmax.
+constexpr float kRefSlack = 8.0f;
+
+// One window's contribution to the wave's running softmax state: S^T = K Q^T
+// for the two 16-key blocks; the keys at or past hi, past the row's last
+// visible key lim_r and the rows past the tile are masked; the reference
+// update (m, the row's reference in scaled log2 units) and O^T = O^T + V^T P^T
+// with P^T = exp2(S^T scale - m) from registers.
+__device__ __forceinline__ void window_mma(const AttnArgs& a, int ws, int hi, int lim_r, bool r_ok,
+                                           int lane, const bf16x8_t (&ka)[2][4],
+                                           const bf16x8_t (&va)[8], const bf16x8_t (&qv)[4],
+                                           float& m, float& lsum, f32x4_t (&oacc)[8]) {
+  const int g = lane >> 4;
+  f32x4_t st[2];
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds)
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[kb][ds], qv[ds], acc, 0, 0, 0);
+    st[kb] = acc;
+  }
+  // lane holds row n, keys ws + 8g + 4kb + j (raw scores)
+  float sv[8];
+  float mloc = -INFINITY;
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float v = st[kb][j];
+      const int key = ws + 8 * g + 4 * kb + j;
+      if (!r_ok || key >= hi || key > lim_r) v = -INFINITY;
+      sv[kb * 4 + j] = v;
+      mloc = fmaxf(mloc, v);
+    }
+  mloc = row4_max(mloc) * a.scale_log2;  // the softmax scale is positive
+  const bool up = mloc > m + kRefSlack;
+  if (__builtin_amdgcn_ballot_w64(up)) {
+    const float m_new = up ? mloc : m;
+    const float alpha = (m_new == m) ? 1.0f : __builtin_amdgcn_exp2f(m - m_new);
+    m = m_new;
+    lsum *= alpha;
+#pragma unroll
+    for (int db = 0; db < 8; ++db) oacc[db] *= alpha;
+  }
+  const float base = (m == -INFINITY) ? 0.0f : m;
+  float psum = 0.0f;
+  union {
+    uint16_t h[8];
+    bf16x8_t v;
+  } pb;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[t], a.scale_log2, -base));
+    psum += p;
+    pb.h[t] = f32_to_bf16_rne(p);
+  }
+  lsum += psum;
+  // O^T[d][row] += V^T[d][keys 8g..8g+7] * P^T
+#pragma unroll
+  for (int db = 0; db < 8; ++db)
+    oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[db], pb.v, oacc[db], 0, 0, 0);
 }
 
 // Walks keys [lo, hi) of query tile t (hi clipped to the keys the tile's
@@ -382,18 +608,11 @@ __device__ __forceinline__ void qkv_finish(const AttnArgs& a, const QkvArgs& qa,
 // block lo / block_size on, up to bt_cap of them, filled by the caller.
 // kG: query heads per KV head as a compile-time constant (2, 4 or 8), or 0 to
 // read it from the arguments (any other group size).
-// kQkv: the tile's q rows and its new k/v rows are made here from the loads
-// the kernel issued at its start (qkv_finish, after the s_bt barrier): a
-// first window holding only earlier keys is issued before, one reaching the
-// sequence's query tokens after it.
-template <bool kFp8, int kG, bool kQkv = false>
+template <bool kFp8, int kG>
 __device__ __forceinline__ void wave_walk(const AttnArgs& a, const TileRef& t, int kvh, int lo,
                                           int hi, int ws0, int step, const int* s_bt, int bt_cap,
-                                          uint8_t* tile_k, uint8_t* tile_v, WaveAcc& acc,
-                                          const QkvArgs* qa = nullptr, QkvLoads* ql = nullptr,
-                                          uint16_t* s_q = nullptr) {
+                                          uint8_t* tile_k, uint8_t* tile_v, WaveAcc& acc) {
   const int G = kG ? kG : a.G;
-  constexpr int kRowB = AttnLds<kFp8>::kRowB;
   const int qs = t.qs, Lq = t.Lq, Lk = t.Lk, rows = t.rows;
   const int lane = threadIdx.x & 63;
   const int n = lane & 15;  // query row of this lane (B-operand column)
@@ -409,16 +628,14 @@ __device__ __forceinline__ void wave_walk(const AttnArgs& a, const TileRef& t, i
   const int qh = kvh * G + (r_ok ? r % G : 0);
   const int lim_r = Lk - Lq + qi;  // last visible key of this row
   bf16x8_t qv[4];
-  if constexpr (!kQkv) {
 #pragma unroll
-    for (int ds = 0; ds < 4; ++ds) {
-      if (r_ok) {
-        const uint16_t* qp =
-            a.q + (int64_t)(qs + qi) * a.q_st + (int64_t)qh * a.q_sh + ds * 32 + g * 8;
-        qv[ds] = u4_to_bf16x8(*reinterpret_cast<const uint4*>(qp));
-      } else {
-        qv[ds] = u4_to_bf16x8(make_uint4(0, 0, 0, 0));
-      }
+  for (int ds = 0; ds < 4; ++ds) {
+    if (r_ok) {
+      const uint16_t* qp =
+          a.q + (int64_t)(qs + qi) * a.q_st + (int64_t)qh * a.q_sh + ds * 32 + g * 8;
+      qv[ds] = u4_to_bf16x8(*reinterpret_cast<const uint4*>(qp));
+    } else {
+      qv[ds] = u4_to_bf16x8(make_uint4(0, 0, 0, 0));
     }
   }
 
@@ -449,26 +666,13 @@ __device__ __forceinline__ void wave_walk(const AttnArgs& a, const TileRef& t, i
     return true;
   };
 
+  const WinOffs<kFp8> wo = win_offs<kFp8>(a, lane);
   int ws = ws0;
   bool have = false;
-  // kQkv: keys from Lk - Lq on are the query tokens' own, stored by the prologue
-  const bool early = !kQkv || (ws + kWin < hi ? ws + kWin : hi) <= Lk - Lq;
-  if (ws < hi && early) {
+  if (ws < hi) {
     const uint8_t *kb, *vb;
     have = window_base(ws, kb, vb);
-    if (have) issue_window<kFp8>(a, kb, vb, ws, hi, tile_k, tile_v, lane);
-  }
-  if constexpr (kQkv) {
-    qkv_finish<kFp8>(a, *qa, t, kvh, *ql, s_q);
-#pragma unroll
-    for (int ds = 0; ds < 4; ++ds)
-      qv[ds] = r_ok ? u4_to_bf16x8(*reinterpret_cast<const uint4*>(s_q + n * kD + ds * 32 + g * 8))
-                    : u4_to_bf16x8(make_uint4(0, 0, 0, 0));
-    if (ws < hi && !early) {
-      const uint8_t *kb, *vb;
-      have = window_base(ws, kb, vb);
-      if (have) issue_window<kFp8>(a, kb, vb, ws, hi, tile_k, tile_v, lane);
-    }
+    if (have) issue_window<kFp8>(kb, vb, ws, hi, tile_k, tile_v, wo);
   }
   while (ws < hi) {
     const int ws_next = ws + step;
@@ -476,47 +680,7 @@ __device__ __forceinline__ void wave_walk(const AttnArgs& a, const TileRef& t, i
     bf16x8_t ka[2][4], va[8];
     if (cur) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      // K as the A operand: row rho = n holds key ws + 8*(n/4) + 4*kb + (n%4)
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const int kk = 8 * (n >> 2) + 4 * kb + (n & 3);
-        const uint8_t* row = tile_k + kk * kRowB;
-#pragma unroll
-        for (int ds = 0; ds < 4; ++ds) {
-          if constexpr (kFp8) {
-            const int u = g + 4 * ds;  // 8-byte unit of dims 8g + 32ds
-            const int ph = (((u >> 1) ^ swz8(kk)) << 4) | ((u & 1) << 3);
-            const uint2 raw = *reinterpret_cast<const uint2*>(row + ph);
-            ka[kb][ds] = fp8x8w_to_bf16(raw.x, raw.y);
-          } else {
-            const int ph = ((g + 4 * ds) ^ swz16(kk)) << 4;
-            ka[kb][ds] = u4_to_bf16x8(*reinterpret_cast<const uint4*>(row + ph));
-          }
-        }
-      }
-      // V^T as the A operand of d-block db: lane (i = n, g) holds V[8g .. 8g+7][16db + i],
-      // gathered from the row-major tile with transposing LDS reads
-#pragma unroll
-      for (int db = 0; db < 8; ++db) {
-        if constexpr (kFp8) {
-          const int kk = 8 * g + (n >> 1);
-          const int ph = ((db ^ swz8(kk)) << 4) | ((n & 1) << 3);
-          const v2i32_t t = __builtin_amdgcn_ds_read_tr8_b64_v2i32((HS_LDS v2i32_t*)(tile_v + kk * kRowB + ph));
-          va[db] = fp8x8w_to_bf16((uint32_t)t[0], (uint32_t)t[1]);
-        } else {
-          union {
-            v4i16_t h[2];
-            bf16x8_t v;
-          } u;
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            const int kk = 8 * g + 4 * h + (n >> 2);
-            const int ph = (((2 * db + ((n & 3) >> 1)) ^ swz16(kk)) << 4) | ((n & 1) << 3);
-            u.h[h] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((HS_LDS v4i16_t*)(tile_v + kk * kRowB + ph));
-          }
-          va[db] = u.v;
-        }
-      }
+      window_read<kFp8, false>(tile_k, tile_v, nullptr, nullptr, ws, 0, 0, lane, ka, va);
       // every LDS read of the tiles has returned before the next window overwrites them
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
@@ -524,56 +688,9 @@ __device__ __forceinline__ void wave_walk(const AttnArgs& a, const TileRef& t, i
     if (ws_next < hi) {
       const uint8_t *kb, *vb;
       have = window_base(ws_next, kb, vb);
-      if (have) issue_window<kFp8>(a, kb, vb, ws_next, hi, tile_k, tile_v, lane);
+      if (have) issue_window<kFp8>(kb, vb, ws_next, hi, tile_k, tile_v, wo);
     }
-    if (cur) {
-      // S^T = K Q^T for the two 16-key blocks
-      f32x4_t st[2];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ds = 0; ds < 4; ++ds)
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[kb][ds], qv[ds], acc, 0, 0, 0);
-        st[kb] = acc;
-      }
-      // lane holds row n, keys ws + 8g + 4kb + j
-      float sv[8];
-      float mloc = -INFINITY;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int key = ws + 8 * g + 4 * kb + j;
-          float v = st[kb][j] * a.scale_log2;
-          if (!r_ok || key >= hi || key > lim_r) v = -INFINITY;
-          sv[kb * 4 + j] = v;
-          mloc = fmaxf(mloc, v);
-        }
-      mloc = row4_max(mloc);
-      const float m_new = fmaxf(m, mloc);
-      const float base = (m_new == -INFINITY) ? 0.0f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f(m - base);
-      m = m_new;
-      float psum = 0.0f;
-      union {
-        uint16_t h[8];
-        bf16x8_t v;
-      } pb;
-#pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        const float p = __builtin_amdgcn_exp2f(sv[t] - base);
-        psum += p;
-        pb.h[t] = f32_to_bf16_rne(p);
-      }
-      lsum = lsum * alpha + psum;
-      // O^T[d][row] = alpha * O^T + V^T[d][keys 8g..8g+7] * P^T
-#pragma unroll
-      for (int db = 0; db < 8; ++db) {
-        oacc[db] *= alpha;
-        oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[db], pb.v, oacc[db], 0, 0, 0);
-      }
-    }
+    if (cur) window_mma(a, ws, hi, lim_r, r_ok, lane, ka, va, qv, m, lsum, oacc);
     ws = ws_next;
   }
   // per-row totals of this wave
@@ -584,35 +701,36 @@ __device__ __forceinline__ void wave_walk(const AttnArgs& a, const TileRef& t, i
   for (int db = 0; db < 8; ++db) acc.oacc[db] = oacc[db];
 }
 
-// Merge of the first NW waves' partials for one query row and dims d0..d0+3,
-// d0+64..d0+67: running max M, sum L and unnormalised output o (waves w >=
-// nact hold no keys and weigh 0).
-template <int NW>
-__device__ __forceinline__ void merge_waves(const float (*s_m)[kRows], const float (*s_l)[kRows],
-                                            const float* s_o, const float* s_zero, int wave_o,
-                                            int nact, int row, int d0, float& M, float& L,
-                                            float (&o)[8]) {
-  float mw[NW];
+// Merge of the 8 waves' partials for one query row and dims d0 .. d0 + 3:
+// running max M, sum L and unnormalised output o. Every wave's state is
+// there: a wave that held no keys has max -inf, sum 0 and output 0, so its
+// weight exp2(-inf - M) is 0. Waves in order, so every kernel sharing it
+// gives the same bits. s_m / s_l: [row][wave]; s_o: wave w's rows at w * wave_o.
+__device__ __forceinline__ void merge_waves(const float (*s_m)[kAW], const float (*s_l)[kAW],
+                                            const float* s_o, int wave_o, int row, int d0,
+                                            float& M, float& L, float (&o)[4]) {
+  const float4 m0 = *reinterpret_cast<const float4*>(&s_m[row][0]);
+  const float4 m1 = *reinterpret_cast<const float4*>(&s_m[row][4]);
+  const float4 l0 = *reinterpret_cast<const float4*>(&s_l[row][0]);
+  const float4 l1 = *reinterpret_cast<const float4*>(&s_l[row][4]);
+  float4 x[kAW];
+#pragma unroll
+  for (int w = 0; w < kAW; ++w)
+    x[w] = *reinterpret_cast<const float4*>(&s_o[w * wave_o + row * kOStride + d0]);
+  const float mw[kAW] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
+  const float lw[kAW] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
   M = -INFINITY;
 #pragma unroll
-  for (int w = 0; w < NW; ++w) {
-    mw[w] = w < nact ? s_m[w][row] : -INFINITY;
-    M = fmaxf(M, mw[w]);
-  }
+  for (int w = 0; w < kAW; ++w) M = fmaxf(M, mw[w]);
   const float Mb = (M == -INFINITY) ? 0.0f : M;
   L = 0.0f;
 #pragma unroll
-  for (int t = 0; t < 8; ++t) o[t] = 0.0f;
+  for (int t = 0; t < 4; ++t) o[t] = 0.0f;
 #pragma unroll
-  for (int w = 0; w < NW; ++w) {
+  for (int w = 0; w < kAW; ++w) {
     const float f = __builtin_amdgcn_exp2f(mw[w] - Mb);
-    L += (w < nact ? s_l[w][row] : 0.0f) * f;
-    const float* src0 = w < nact ? &s_o[w * wave_o + row * kOStride + d0] : s_zero;
-    const float* src1 = w < nact ? src0 + 64 : s_zero;
-    const float4 x0 = *reinterpret_cast<const float4*>(src0);
-    const float4 x1 = *reinterpret_cast<const float4*>(src1);
-    o[0] += x0.x * f; o[1] += x0.y * f; o[2] += x0.z * f; o[3] += x0.w * f;
-    o[4] += x1.x * f; o[5] += x1.y * f; o[6] += x1.z * f; o[7] += x1.w * f;
+    L += lw[w] * f;
+    o[0] += x[w].x * f; o[1] += x[w].y * f; o[2] += x[w].z * f; o[3] += x[w].w * f;
   }
 }
 
@@ -647,37 +765,24 @@ __device__ __forceinline__ void combine_splits(const AttnArgs& a, int b, int kvh
   *reinterpret_cast<uint4*>(a.out + (int64_t)(qs + oi) * a.o_st + (int64_t)oh * a.o_sh + d0) = ob.u;
 }
 
-// Attends query tile t over keys [klo, khi) with the 8 waves of the workgroup
-// (wave w takes windows w, w + 8, ...), merges the waves and writes the
-// normalised output (pslot < 0) or the unnormalised partial (o, running max,
-// sum) at partial slot pslot. s_bt as for wave_walk. s_raw holds the per-wave
-// K and V window tiles and, after the key loop, the per-wave partial outputs.
-// kQkv (the fused kernel, one query tile): the prologue runs inside the walk,
-// and a partial (the tile's keys span ns > 1 splits) is merged in the
-// kernel: the last of the tile's ns workgroups to take its ticket
-// (a.tickets[b * Hkv + kvh], zero between calls) merges them all.
-template <bool kFp8, int kG, bool kQkv = false>
-__device__ __forceinline__ void attend_keys(const AttnArgs& a, const TileRef& t, int klo, int khi,
-                                            int64_t pslot, uint8_t* s_raw, float (*s_m)[kRows],
-                                            float (*s_l)[kRows], const int* s_bt, int bt_cap,
-                                            const QkvArgs* qa = nullptr,
-                                            QkvLoads* ql = nullptr, uint16_t* s_q = nullptr,
-                                            int ns = 1) {
+// Merges the 8 waves' running states (acc) of query tile t, whose keys were
+// [klo, khi) with wave w on windows w, w + 8, ..., and writes the normalised
+// output (pslot < 0) or the unnormalised partial (o, running max, sum) at
+// partial slot pslot. s_raw holds the per-wave K and V window tiles, which
+// take the per-wave partial outputs here. kSplitMerge (the fused kernel): a
+// partial (the tile's keys span ns > 1 splits) is merged in the kernel: the
+// last of the tile's ns workgroups to take its ticket (a.tickets[b * Hkv +
+// kvh], zero between calls) merges them all.
+template <bool kFp8, int kG, bool kSplitMerge>
+__device__ __forceinline__ void merge_tile(const AttnArgs& a, const TileRef& t, int64_t pslot,
+                                           uint8_t* s_raw, float (*s_m)[kAW], float (*s_l)[kAW],
+                                           const WaveAcc& acc, int ns) {
   const int G = kG ? kG : a.G;
   constexpr int kTileB = AttnLds<kFp8>::kTileB;
   const int kvh = t.kvh, qs = t.qs, rows = t.rows;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int n = lane & 15, g = lane >> 4;
   const int r0 = t.qt * kRows;
-  uint8_t* tile_k = s_raw + wid * 2 * kTileB;
-  uint8_t* tile_v = tile_k + kTileB;
-  WaveAcc acc;
-  wave_walk<kFp8, kG, kQkv>(a, t, kvh, klo, khi, klo + wid * kWin, kAW * kWin, s_bt, bt_cap,
-                            tile_k, tile_v, acc, qa, ql, s_q);
-  // waves that hold keys (wave w starts at klo + 32w): the others have nothing
-  // to merge
-  const int nkeys = khi - klo;
-  const int nact = nkeys <= 0 ? 0 : (nkeys + kWin - 1) / kWin < kAW ? (nkeys + kWin - 1) / kWin : kAW;
   // bf16 tiles: a wave's partial output fits its own K/V tiles, which it has
   // finished reading (its last window's reads were waited on), so it needs no
   // barrier before writing it; fp8 tiles are smaller and the partials go over
@@ -685,62 +790,46 @@ __device__ __forceinline__ void attend_keys(const AttnArgs& a, const TileRef& t,
   constexpr bool kOwn = kRows * kOStride * 4 <= 2 * kTileB;
   constexpr int kWaveO = kOwn ? 2 * kTileB / 4 : kRows * kOStride;  // floats between waves
   float* s_o = reinterpret_cast<float*>(s_raw);
-  float* s_zero = reinterpret_cast<float*>(s_raw + AttnLds<kFp8>::kZeroOff);
-  if (tid == 0) *reinterpret_cast<float4*>(s_zero) = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (wid < nact && g == 0) {
-    s_m[wid][n] = acc.m;
-    s_l[wid][n] = acc.lsum;
+  if (g == 0) {
+    s_m[n][wid] = acc.m;
+    s_l[n][wid] = acc.lsum;
   }
-  if constexpr (!kOwn) __syncthreads();  // every wave is done with its tiles
-  if (wid < nact) {
+  if constexpr (!kOwn) lds_barrier();  // every wave is done with its tiles
 #pragma unroll
-    for (int db = 0; db < 8; ++db)
-      *reinterpret_cast<float4*>(&s_o[wid * kWaveO + n * kOStride + db * 16 + 4 * g]) =
-          make_float4(acc.oacc[db][0], acc.oacc[db][1], acc.oacc[db][2], acc.oacc[db][3]);
-  }
-  __syncthreads();
-  // merge the waves: thread handles row tid/16, dims 4(tid%16) .. +4 and
-  // 64 + 4(tid%16) .. +4 (the other threads have no row)
-  const int row = tid >> 4;
-  const int rr = r0 + row;
-  const bool act = tid < kRows * 16 && rr < rows;
-  if (act) {
-    const int d0 = (tid & 15) * 4;
-    // branch-free over the first 4 or all 8 waves, so that all LDS reads go
-    // out together: a wave without keys contributes weight 0 and reads the
-    // zero bytes (one address for every lane)
-    float M, L, o[8];
-    if (nact <= 4)
-      merge_waves<4>(s_m, s_l, s_o, s_zero, kWaveO, nact, row, d0, M, L, o);
-    else
-      merge_waves<kAW>(s_m, s_l, s_o, s_zero, kWaveO, nact, row, d0, M, L, o);
-    const int oi = rr / G, oh = kvh * G + rr % G;
-    if (pslot < 0) {
-      const float inv = (L > 0.0f) ? a.v_scale / L : 0.0f;
-      union {
-        uint16_t h[4];
-        uint2 u;
-      } ob0, ob1;
+  for (int db = 0; db < 8; ++db)
+    *reinterpret_cast<float4*>(&s_o[wid * kWaveO + n * kOStride + db * 16 + 4 * g]) =
+        make_float4(acc.oacc[db][0], acc.oacc[db][1], acc.oacc[db][2], acc.oacc[db][3]);
+  lds_barrier();
+  // merge the waves: thread handles row tid / 32, dims 4 (tid % 32) .. + 3
+  {
+    const int row = tid >> 5;
+    const int rr = r0 + row;
+    if (rr < rows) {
+      const int d0 = (tid & 31) * 4;
+      float M, L, o[4];
+      merge_waves(s_m, s_l, s_o, kWaveO, row, d0, M, L, o);
+      const int oi = rr / G, oh = kvh * G + rr % G;
+      if (pslot < 0) {
+        const float inv = (L > 0.0f) ? a.v_scale / L : 0.0f;
+        union {
+          uint16_t h[4];
+          uint2 u;
+        } ob;
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        ob0.h[t] = f32_to_bf16_rne(o[t] * inv);
-        ob1.h[t] = f32_to_bf16_rne(o[4 + t] * inv);
-      }
-      uint16_t* po = a.out + (int64_t)(qs + oi) * a.o_st + (int64_t)oh * a.o_sh + d0;
-      *reinterpret_cast<uint2*>(po) = ob0.u;
-      *reinterpret_cast<uint2*>(po + 64) = ob1.u;
-    } else {
-      const int64_t pidx = pslot * kRows + row;
-      float* po = a.part_o + pidx * kD + d0;
-      *reinterpret_cast<float4*>(po) = make_float4(o[0], o[1], o[2], o[3]);
-      *reinterpret_cast<float4*>(po + 64) = make_float4(o[4], o[5], o[6], o[7]);
-      if ((tid & 15) == 0) {
-        a.part_ml[pidx * 2] = M;
-        a.part_ml[pidx * 2 + 1] = L;
+        for (int t = 0; t < 4; ++t) ob.h[t] = f32_to_bf16_rne(o[t] * inv);
+        *reinterpret_cast<uint2*>(a.out + (int64_t)(qs + oi) * a.o_st + (int64_t)oh * a.o_sh +
+                                  d0) = ob.u;
+      } else {
+        const int64_t pidx = pslot * kRows + row;
+        *reinterpret_cast<float4*>(a.part_o + pidx * kD + d0) = make_float4(o[0], o[1], o[2], o[3]);
+        if ((tid & 31) == 0) {
+          a.part_ml[pidx * 2] = M;
+          a.part_ml[pidx * 2 + 1] = L;
+        }
       }
     }
   }
-  if constexpr (kQkv) {
+  if constexpr (kSplitMerge) {
     if (pslot >= 0) {
       // in-kernel merge of the ns splits: every thread's partial stores are
       // made visible at agent scope before the workgroup takes its ticket;
@@ -759,9 +848,29 @@ __device__ __forceinline__ void attend_keys(const AttnArgs& a, const TileRef& t,
       if (!s_last) return;
       __threadfence();
       if (tid == 0) __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (act) combine_splits(a, t.b, kvh, t.qt, qs, ns, row, rr, (tid & 15) * 8);
+      const int row = tid >> 4, rr = r0 + row;
+      if (tid < kRows * 16 && rr < rows)
+        combine_splits(a, t.b, kvh, t.qt, qs, ns, row, rr, (tid & 15) * 8);
     }
   }
+}
+
+// Attends query tile t over keys [klo, khi) with the 8 waves of the workgroup
+// (wave w takes windows w, w + 8, ...), merges the waves and writes the
+// normalised output (pslot < 0) or the unnormalised partial at partial slot
+// pslot (merge_tile). s_bt as for wave_walk.
+template <bool kFp8, int kG>
+__device__ __forceinline__ void attend_keys(const AttnArgs& a, const TileRef& t, int klo, int khi,
+                                            int64_t pslot, uint8_t* s_raw, float (*s_m)[kAW],
+                                            float (*s_l)[kAW], const int* s_bt, int bt_cap) {
+  constexpr int kTileB = AttnLds<kFp8>::kTileB;
+  const int wid = threadIdx.x >> 6;
+  uint8_t* tile_k = s_raw + wid * 2 * kTileB;
+  uint8_t* tile_v = tile_k + kTileB;
+  WaveAcc acc;
+  wave_walk<kFp8, kG>(a, t, t.kvh, klo, khi, klo + wid * kWin, kAW * kWin, s_bt, bt_cap, tile_k,
+                      tile_v, acc);
+  merge_tile<kFp8, kG, false>(a, t, pslot, s_raw, s_m, s_l, acc, 1);
 }
 
 // One launch = one workgroup per (kv head x query tile, split, sequence).
@@ -790,7 +899,7 @@ __global__ __launch_bounds__(kAT) void k_verify_attn(const int32_t* cu_q, const 
                                                      AttnArgs a) {
   const int G = kG ? kG : a.G;
   __shared__ __attribute__((aligned(16))) uint8_t s_raw[AttnLds<kFp8>::kRawBytes];
-  __shared__ float s_m[kAW][kRows], s_l[kAW][kRows];
+  __shared__ __attribute__((aligned(16))) float s_m[kRows][kAW], s_l[kRows][kAW];
   __shared__ int s_bt[kBtCap];
   if (blockIdx.x & ((1u << xcd_shift) - 1)) return;
   const int bx = blockIdx.x >> xcd_shift;
@@ -833,64 +942,175 @@ __global__ __launch_bounds__(kAT) void k_verify_attn(const int32_t* cu_q, const 
 }
 
 // k_verify_attn with the q/k-norm + RoPE + KV-store step of its tile's
-// tokens in the prologue (qkv_load at the start, qkv_finish after the
-// block-table barrier): the host launches it where one query tile holds
+// tokens in the prologue: the host launches it where one query tile holds
 // every query row of each (sequence, kv head). The grid is (kv head x xcd
 // pack, key split, sequence); split s holds keys [s * split_len, (s + 1) *
 // split_len) of the sequence, so a sequence whose keys fit one split is one
-// workgroup per kv head (which alone writes and reads its new k/v rows) and
-// the other splits' workgroups return at once; longer sequences write
-// partials that the last of their workgroups merges (attend_keys), every
-// workgroup of the sequence storing the new k/v rows before it reads them
-// (the same bytes). With xcd_shift = 3 the workgroups that work are those
-// with x % 8 == split % 8, so the kv heads of one split are dispatched to one
-// XCD and consecutive splits to different XCDs (placement only). Replaces
+// workgroup per kv head and the other splits' workgroups return at once;
+// longer sequences write partials that the last of their workgroups merges
+// (merge_tile). With xcd_shift = 3 the workgroups that work are those with
+// x % 8 == split % 8, so the kv heads of one split are dispatched to one XCD
+// and consecutive splits to different XCDs (placement only). Replaces
 // hs_qk_norm_rope_store + hs_verify_attention (+ the split combine) for
 // decode and verify steps.
+// Wave w walks windows w, w + 8, ... of the split as in k_verify_attn (the
+// same keys in the same order: bit-identical outputs). Nothing waits for a
+// workgroup barrier before the first window is in flight: each wave loads the
+// block-table entries of its own windows (lane j: window j) with the sequence
+// bounds and issues its first window as soon as they arrive, then the loads of
+// its q/k-norm + RoPE items. The query tokens' own keys (Lk - Lq .. Lk - 1)
+// are computed here; where every token's cache slot is the one the block table
+// gives its key (the fast case, every decode and verify step of the engine),
+// the windows read those rows from s_new, and the cache stores go out
+// unwaited. Otherwise (a padding slot, a token stored elsewhere) the stores
+// are waited for and a window reaching those keys reads them back from the
+// cache, as the two launches do.
 template <bool kFp8, int kG>
 __global__ __launch_bounds__(kAT) void k_verify_attn_qkv(const int32_t* cu_q, const int32_t* cu_k,
                                                          const int32_t* bt, int bt_stride,
                                                          int xcd_shift, int bs_shift,
                                                          int bt_width, int nbt_split, int split_len,
                                                          AttnArgs a, QkvArgs qa) {
+  constexpr int kRowB = AttnLds<kFp8>::kRowB;
+  constexpr int kTileB = AttnLds<kFp8>::kTileB;
   __shared__ __attribute__((aligned(16))) uint8_t s_raw[AttnLds<kFp8>::kRawBytes];
-  __shared__ float s_m[kAW][kRows], s_l[kAW][kRows];
-  __shared__ int s_bt[kBtCap];
+  __shared__ __attribute__((aligned(16))) float s_m[kRows][kAW], s_l[kRows][kAW];
   __shared__ __attribute__((aligned(16))) uint16_t s_q[kRows * kD];
+  // the query tokens' k rows, then their v rows (at most kRows tokens)
+  __shared__ __attribute__((aligned(16))) uint8_t s_new[2 * kRows * kRowB];
+  (void)nbt_split;
   const int G = kG ? kG : a.G;
   const unsigned xm = (1u << xcd_shift) - 1;
   if ((blockIdx.x & xm) != (blockIdx.y & xm)) return;
   const int kvh = blockIdx.x >> xcd_shift;
   const int split = blockIdx.y;
   const int b = blockIdx.z;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int cq0 = cu_q[b], cq1 = cu_q[b + 1], ck0 = cu_k[b], ck1 = cu_k[b + 1];
   const int lo = split * split_len;
-  const int bt0 = split == 0 ? 0 : key_block(lo, bs_shift, a.block_size);
-  int nbt = nbt_split;
-  if (nbt > bt_width - bt0) nbt = bt_width - bt0;
   const int32_t* btrow = bt + (int64_t)b * bt_stride;
-  const int bi = bt0 + tid < bt_width ? bt0 + tid : bt_width - 1;
-  const int bt_mine = btrow[bi];
-  asm volatile("" ::"s"(a.q), "s"(a.c_sh), "s"(a.scale_log2), "s"(a.sk_pre));
-  asm volatile("" ::"v"(bt_mine), "v"(cq0), "v"(cq1), "v"(ck0), "v"(ck1));
+  // block-table entry of this wave's window j (keys lo + 32 wid + 256 j) in
+  // lane j, clamped into the row (a window past the row is skipped below)
+  const int wbi = key_block(lo + kWin * wid + kAW * kWin * lane, bs_shift, a.block_size);
+  const int wbt = btrow[wbi < bt_width ? wbi : bt_width - 1];
+  // the argument block's lines are requested now, together (one field of each)
+  asm volatile("" ::"s"(a.q), "s"(a.c_sh), "s"(a.scale_log2), "s"(a.sk_pre), "s"(qa.qkv),
+               "s"(qa.cs_rows));
+  // one wait for the bounds and the table entries
+  asm volatile("" ::"v"(wbt), "v"(cq0), "v"(cq1), "v"(ck0), "v"(ck1));
   const TileRef t = tile_ref_of(b, kvh, 0, G, cq0, cq1, ck0, ck1);
-  if (tid < nbt) s_bt[tid] = bt_mine;
-  for (int i = tid + kAT; i < nbt; i += kAT) s_bt[i] = btrow[bt0 + i];
   // no query token or no key of this split: nothing to store or attend
   if (t.rows <= 0 || t.Lk <= 0 || lo >= t.Lk) return;
   int hi = lo + split_len;
   const int vis = tile_keys(t, G);
   if (vis < hi) hi = vis;
+  const int knew = t.Lk - t.Lq;  // first key of the query tokens
+  const int esz = kFp8 ? 1 : 2;
+  uint8_t* tile_k = s_raw + wid * 2 * kTileB;
+  uint8_t* tile_v = tile_k + kTileB;
+  // window j of this wave (first key wsj) -> its cache row bases; false when
+  // its block is not a valid cache block (the window is skipped)
+  auto window_base = [&](int j, int wsj, const uint8_t*& kb, const uint8_t*& vb) -> bool {
+    const int bi = key_block(wsj, bs_shift, a.block_size);
+    if (bi >= bt_width) return false;
+    const int blk = __builtin_amdgcn_readlane(wbt, j);
+    if (blk < 0 || blk >= a.num_blocks) return false;
+    const int64_t off = ((int64_t)blk * a.c_sb + (int64_t)(wsj - bi * a.block_size) * a.c_st +
+                         (int64_t)kvh * a.c_sh) * esz;
+    kb = a.kc + off;
+    vb = a.vc + off;
+    return true;
+  };
+  // the first window goes out as soon as the bounds and table entries are in,
+  // then the q/k-norm + RoPE rows' loads, and per lane i < Lq the slot of
+  // query token i and the table entry of its key
+  const WinOffs<kFp8> wo = win_offs<kFp8>(a, lane);
+  int ws = lo + kWin * wid;
+  const uint8_t* kb0 = a.kc;
+  const uint8_t* vb0 = a.vc;
+  bool have = ws < hi && window_base(0, ws, kb0, vb0);
+  if (have) issue_window<kFp8>(kb0, vb0, ws, hi, tile_k, tile_v, wo);
   QkvLoads ql;
   qkv_load(a, qa, t, kvh, G, ql);
+  const int fi = lane < t.Lq ? lane : t.Lq - 1;
+  const int fkey = knew + fi;
+  const int fbi = key_block(fkey, bs_shift, a.block_size);
+  const int fblk = btrow[fbi < bt_width ? fbi : bt_width - 1];
+  const int fslot = qa.slots[t.qs + fi];
+  KvStores S;
+  qkv_compute<kFp8>(a, qa, t, kvh, ql, s_q, s_new, S);
+  const bool ok = t.Lq <= kRows && fslot >= 0 && fbi < bt_width && fblk >= 0 && fblk < a.num_blocks &&
+                  fslot == fblk * a.block_size + (fkey - fbi * a.block_size);
+  const bool fast = __builtin_amdgcn_ballot_w64(!ok) == 0;  // the same in every wave
+  if (!fast) {
+    // the stores reach the L2 before any wave loads those rows
+    kv_store_all<kFp8>(a, qa, S);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
+  lds_barrier();  // s_q and s_new written
+  if (!fast && have) {
+    // the first window was loaded before the stores, which may have written
+    // any of its rows: load it again past this CU's L1
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    const uint8_t *kb, *vb;
+    window_base(0, ws, kb, vb);
+    issue_window<kFp8>(kb, vb, ws, hi, tile_k, tile_v, wo);
+  }
+  const int n = lane & 15, g = lane >> 4;
+  const int r = n;
+  const bool r_ok = r < t.rows;
+  const int lim_r = knew + (r_ok ? r / G : 0);  // last visible key of this row
+  bf16x8_t qv[4];
+#pragma unroll
+  for (int ds = 0; ds < 4; ++ds)
+    qv[ds] = r_ok ? u4_to_bf16x8(*reinterpret_cast<const uint4*>(s_q + n * kD + ds * 32 + g * 8))
+                  : u4_to_bf16x8(make_uint4(0, 0, 0, 0));
+  float m = -INFINITY, lsum = 0.0f;
+  f32x4_t oacc[8];
+#pragma unroll
+  for (int db = 0; db < 8; ++db) oacc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  // fast: keys from knew on read s_new
+  const int kn = fast ? knew : INT32_MAX;
+  const uint8_t* nk = s_new;
+  const uint8_t* nv = s_new + kRows * kRowB;
+  bool stored = !fast;
+  for (int j = 0; ws < hi; ++j) {
+    const int ws_next = ws + kAW * kWin;
+    const bool cur = have;
+    bf16x8_t ka[2][4], va[8];
+    if (cur) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      window_read<kFp8, true>(tile_k, tile_v, nk, nv, ws, kn, t.Lq - 1, lane, ka, va);
+      // every LDS read of the tiles has returned before the next window overwrites them
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+    if (!stored) {  // fast: nothing in this kernel reads the stored rows
+      kv_store_all<kFp8>(a, qa, S);
+      stored = true;
+    }
+    have = false;
+    if (ws_next < hi) {
+      const uint8_t *kb, *vb;
+      have = window_base(j + 1, ws_next, kb, vb);
+      // a window of query-token keys only reads s_new: nothing to load
+      if (have && ws_next < kn) issue_window<kFp8>(kb, vb, ws_next, hi, tile_k, tile_v, wo);
+    }
+    if (cur) window_mma(a, ws, hi, lim_r, r_ok, lane, ka, va, qv, m, lsum, oacc);
+    ws = ws_next;
+  }
+  if (!stored) kv_store_all<kFp8>(a, qa, S);
+  WaveAcc acc;
+  acc.m = m;
+  acc.lsum = row4_sum(lsum);
+#pragma unroll
+  for (int db = 0; db < 8; ++db) acc.oacc[db] = oacc[db];
   // splits holding keys (at most the launched ones: keys past the declared
   // maximum are not attended, as in the per-tile kernel)
   int ns = (t.Lk + split_len - 1) / split_len;
   if (ns > (int)gridDim.y) ns = (int)gridDim.y;
   const int64_t pslot = ns <= 1 ? -1 : ((int64_t)b * a.Hkv + kvh) * a.nsplit + split;
-  attend_keys<kFp8, kG, true>(a, t, lo, hi, pslot, s_raw, s_m, s_l, s_bt, kBtCap, &qa, &ql, s_q,
-                              ns);
+  merge_tile<kFp8, kG, true>(a, t, pslot, s_raw, s_m, s_l, acc, ns);
 }
 
 // Balanced launch: one workgroup per CU. The 32-key windows of all tiles
@@ -983,7 +1203,8 @@ __global__ __launch_bounds__(kAT) void k_verify_attn_sk(AttnArgs a) {
   const int G = kG ? kG : a.G;
   constexpr int kRaw = kHeads ? AttnLds<kFp8>::kKvBytes : AttnLds<kFp8>::kRawBytes;
   __shared__ __attribute__((aligned(16))) uint8_t s_raw[kRaw];
-  __shared__ float s_m[kHeads ? 1 : kAW][kRows], s_l[kHeads ? 1 : kAW][kRows];
+  __shared__ __attribute__((aligned(16))) float s_m[kHeads ? 1 : kRows][kAW],
+      s_l[kHeads ? 1 : kRows][kAW];
   __shared__ int s_bt[kSkBtCap];
   __shared__ int s_pre[kSkMaxTiles + 1];
   __shared__ int s_wsum[kAW];
@@ -1339,6 +1560,8 @@ static int attn_prepare(const void* q, int64_t q_stride_tok, int64_t q_stride_he
     return HS_ERR_UNSUPPORTED;
   if (((uintptr_t)q | (uintptr_t)out | (uintptr_t)k_cache | (uintptr_t)v_cache) & 15)
     return HS_ERR_UNSUPPORTED;
+  // a window's 32 token rows lie within 2 GiB of its first (32-bit load offsets)
+  if (cache_stride_tok * esz * kWin > INT32_MAX) return HS_ERR_UNSUPPORTED;
   const size_t need = *pneed = hs_verify_attention_workspace_size(num_seqs, num_q_heads, num_kv_heads,
                                                          max_seqlen_q, max_seqlen_k);
   AttnArgs& a = *pa;
@@ -1506,7 +1729,10 @@ int hs_qk_norm_rope_attend(const void* qkv, int64_t token_stride, int num_tokens
   if (kv_dtype != HS_BF16 && kv_dtype != HS_FP8_E4M3) return HS_ERR_INVALID;
   if (token_stride < (int64_t)(num_q_heads + 2 * num_kv_heads) * kD) return HS_ERR_INVALID;
   if (kv_dtype == HS_FP8_E4M3 && !(k_scale > 0.0f && v_scale > 0.0f)) return HS_ERR_INVALID;
-  if ((uintptr_t)qkv & 1) return HS_ERR_UNSUPPORTED;
+  // 16-byte pieces of every head (q/k-norm + RoPE rows of 16 lanes)
+  if ((token_stride % 8) || (((uintptr_t)qkv | (uintptr_t)q_weight | (uintptr_t)k_weight |
+                              (uintptr_t)cos_sin) & 15))
+    return HS_ERR_UNSUPPORTED;
   // q_out [num_tokens, Hq, 128]: the two-launch path's q, and the argument
   // checks' stand-in for q (the fused kernel does not write it)
   AttnArgs a;
