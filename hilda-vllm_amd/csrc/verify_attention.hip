@@ -229,6 +229,19 @@ __device__ __forceinline__ void issue_window(const uint8_t* kbase, const uint8_t
   }
 }
 
+// One tile (K or V) of issue_window: its 8 (bf16) or 4 (fp8) loads.
+template <bool kFp8>
+__device__ __forceinline__ void issue_tile(const uint8_t* base, int ws, int hi, uint8_t* tile,
+                                           const WinOffs<kFp8>& wo) {
+  using W = WinOffs<kFp8>;
+  const int lim = hi - ws;
+#pragma unroll
+  for (int i = 0; i < W::kInst; ++i) {
+    const uint32_t off = (i * W::kRowsPerInst + wo.lrow < lim) ? wo.off[i] : wo.off0[i];
+    __builtin_amdgcn_global_load_lds(base + off, (HS_LDS void*)(tile + i * 1024), 16, 0, 0);
+  }
+}
+
 // 8 fp8 e4m3fn values held as two dwords -> bf16x8
 __device__ __forceinline__ bf16x8_t fp8x8w_to_bf16(uint32_t lo, uint32_t hi) {
   return fp8x8_to_bf16(make_uint2(lo, hi));
@@ -270,17 +283,32 @@ __device__ __forceinline__ int tile_keys(const TileRef& t, int G) {
   return hi > 0 ? hi : 0;
 }
 
-// floats per row of a wave's partial output: rows 4 banks apart, so the
-// 16-byte writes (lanes = rows) and the merge's reads fall in distinct banks
-constexpr int kOStride = kD + 4;
+// LDS of the per-wave window tiles: the K tiles of the 8 waves in one array,
+// their V tiles in another (so the compiler tells a wave's K loads from its V
+// loads and waits for each on its own). After the key loop a wave's partial
+// output (16 rows x 128 floats, 8 KB) goes into its K tile (bf16), or into
+// 8 KB slots over both arrays (fp8 tiles are 4 KB).
 template <bool kFp8>
 struct AttnLds {
   static constexpr int kRowB = kFp8 ? 128 : 256;
   static constexpr int kTileB = kWin * kRowB;
-  static constexpr int kKvBytes = kAW * 2 * kTileB;
-  static constexpr int kOBytes = kAW * kRows * kOStride * 4;
-  static constexpr int kRawBytes = kKvBytes > kOBytes ? kKvBytes : kOBytes;
+  static constexpr int kArrB = kAW * kTileB;  // bytes of each of the K and V arrays
 };
+
+// wave w's partial output in the tile arrays
+template <bool kFp8>
+__device__ __forceinline__ float* wave_part(uint8_t* s_kt, uint8_t* s_vt, int w) {
+  constexpr int kTileB = AttnLds<kFp8>::kTileB;
+  constexpr int kPartB = kRows * kD * 4;
+  if constexpr (kTileB >= kPartB)
+    return reinterpret_cast<float*>(s_kt + w * kTileB);
+  else
+    return reinterpret_cast<float*>(w < kAW / 2 ? s_kt + w * kPartB : s_vt + (w - kAW / 2) * kPartB);
+}
+// float offset of (row, 4-float group c4) in a partial: groups XOR-swizzled by
+// the row, so the MFMA-layout writes (16 rows at one group) and the merge's
+// row reads hit distinct banks
+__device__ __forceinline__ int part_off(int row, int c4) { return row * kD + ((c4 ^ row) << 2); }
 
 // Running softmax state of one wave: per query row (lane column n) the max
 // (log2 domain) and the sum of the lane's exp2 terms, and O^T in the MFMA
@@ -468,33 +496,28 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// Reads window ws (keys ws .. ws + 31) from the wave's LDS tiles into the
-// MFMA operand registers: K as the A operand of S^T (row rho = n holds key
-// ws + 8*(n/4) + 4*kb + (n%4)) and V^T as the A operand of d-block db (lane
-// (n, g) holds V[8g .. 8g+7][16db + n], gathered with transposing LDS reads).
-// kNew: the rows of keys at or past knew come from the new-key rows nk / nv
-// instead (row key - knew, laid out as the tile row of that key; masked keys
-// past the last new row nlast read that row: finite data weighted 0).
 template <bool kFp8, bool kNew>
-__device__ __forceinline__ void window_read(const uint8_t* tile_k, const uint8_t* tile_v,
-                                            const uint8_t* nk, const uint8_t* nv, int ws,
-                                            int knew, int nlast, int lane, bf16x8_t (&ka)[2][4],
-                                            bf16x8_t (&va)[8]) {
+__device__ __forceinline__ const uint8_t* window_row(const uint8_t* tile, const uint8_t* nrow, int ws,
+                                                     int knew, int nlast, int kk) {
   constexpr int kRowB = AttnLds<kFp8>::kRowB;
+  if constexpr (kNew) {
+    const int r = ws + kk - knew;
+    return r >= 0 ? nrow + (r < nlast ? r : nlast) * kRowB : tile + kk * kRowB;
+  } else {
+    return tile + kk * kRowB;
+  }
+}
+
+// K of window ws as the A operand of S^T (row rho = n holds key ws + 8*(n/4)
+// + 4*kb + (n%4)), from the wave's K tile or, kNew, the new-key rows.
+template <bool kFp8, bool kNew>
+__device__ __forceinline__ void read_k(const uint8_t* tile_k, const uint8_t* nk, int ws, int knew,
+                                       int nlast, int lane, bf16x8_t (&ka)[2][4]) {
   const int n = lane & 15, g = lane >> 4;
-  // row base of window row kk in the tile or the new-key rows
-  auto row_of = [&](const uint8_t* tile, const uint8_t* nrow, int kk) -> const uint8_t* {
-    if constexpr (kNew) {
-      const int r = ws + kk - knew;
-      return r >= 0 ? nrow + (r < nlast ? r : nlast) * kRowB : tile + kk * kRowB;
-    } else {
-      return tile + kk * kRowB;
-    }
-  };
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
     const int kk = 8 * (n >> 2) + 4 * kb + (n & 3);
-    const uint8_t* row = row_of(tile_k, nk, kk);
+    const uint8_t* row = window_row<kFp8, kNew>(tile_k, nk, ws, knew, nlast, kk);
 #pragma unroll
     for (int ds = 0; ds < 4; ++ds) {
       if constexpr (kFp8) {
@@ -508,13 +531,23 @@ __device__ __forceinline__ void window_read(const uint8_t* tile_k, const uint8_t
       }
     }
   }
+}
+
+// V^T of window ws as the A operand of d-block db (lane (n, g) holds
+// V[8g .. 8g+7][16db + n]), gathered with transposing LDS reads.
+template <bool kFp8, bool kNew>
+__device__ __forceinline__ void read_v(const uint8_t* tile_v, const uint8_t* nv, int ws, int knew,
+                                       int nlast, int lane, bf16x8_t (&va)[8]) {
+  constexpr int kRowB = AttnLds<kFp8>::kRowB;
+  (void)kRowB;
+  const int n = lane & 15, g = lane >> 4;
 #pragma unroll
   for (int db = 0; db < 8; ++db) {
     if constexpr (kFp8) {
       const int kk = 8 * g + (n >> 1);
       const int ph = ((db ^ swz8(kk)) << 4) | ((n & 1) << 3);
       const v2i32_t t = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-          (HS_LDS v2i32_t*)(row_of(tile_v, nv, kk) + ph));
+          (HS_LDS v2i32_t*)(window_row<kFp8, kNew>(tile_v, nv, ws, knew, nlast, kk) + ph));
       va[db] = fp8x8w_to_bf16((uint32_t)t[0], (uint32_t)t[1]);
     } else {
       union {
@@ -526,11 +559,25 @@ __device__ __forceinline__ void window_read(const uint8_t* tile_k, const uint8_t
         const int kk = 8 * g + 4 * h + (n >> 2);
         const int ph = (((2 * db + ((n & 3) >> 1)) ^ swz16(kk)) << 4) | ((n & 1) << 3);
         u.h[h] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (HS_LDS v4i16_t*)(row_of(tile_v, nv, kk) + ph));
+            (HS_LDS v4i16_t*)(window_row<kFp8, kNew>(tile_v, nv, ws, knew, nlast, kk) + ph));
       }
       va[db] = u.v;
     }
   }
+}
+
+// Reads window ws (keys ws .. ws + 31) from the wave's LDS tiles into the
+// MFMA operand registers (read_k and read_v). kNew: the rows of keys at or
+// past knew come from the new-key rows nk / nv instead (row key - knew, laid
+// out as the tile row of that key; masked keys past the last new row nlast
+// read that row: finite data weighted 0).
+template <bool kFp8, bool kNew>
+__device__ __forceinline__ void window_read(const uint8_t* tile_k, const uint8_t* tile_v,
+                                            const uint8_t* nk, const uint8_t* nv, int ws,
+                                            int knew, int nlast, int lane, bf16x8_t (&ka)[2][4],
+                                            bf16x8_t (&va)[8]) {
+  read_k<kFp8, kNew>(tile_k, nk, ws, knew, nlast, lane, ka);
+  read_v<kFp8, kNew>(tile_v, nv, ws, knew, nlast, lane, va);
 }
 
 // A row's scores are exponentiated against a reference that trails its
@@ -539,15 +586,16 @@ __device__ __forceinline__ void window_read(const uint8_t* tile_k, const uint8_t
 // first window is rare. The normalised output is the same softmax.
 constexpr float kRefSlack = 8.0f;
 
-// One window's contribution to the wave's running softmax state: S^T = K Q^T
-// for the two 16-key blocks; the keys at or past hi, past the row's last
-// visible key lim_r and the rows past the tile are masked; the reference
-// update (m, the row's reference in scaled log2 units) and O^T = O^T + V^T P^T
-// with P^T = exp2(S^T scale - m) from registers.
-__device__ __forceinline__ void window_mma(const AttnArgs& a, int ws, int hi, int lim_r, bool r_ok,
-                                           int lane, const bf16x8_t (&ka)[2][4],
-                                           const bf16x8_t (&va)[8], const bf16x8_t (&qv)[4],
-                                           float& m, float& lsum, f32x4_t (&oacc)[8]) {
+// One window's contribution to the wave's running softmax state, in two
+// steps: mma_s, S^T = K Q^T for the two 16-key blocks, the keys at or past
+// hi, past the row's last visible key lim_r and the rows past the tile
+// masked, the reference update (m, the row's reference in scaled log2 units)
+// and P^T = exp2(S^T scale - m) in bf16; mma_pv, O^T += V^T P^T with P^T from
+// registers.
+__device__ __forceinline__ bf16x8_t mma_s(const AttnArgs& a, int ws, int hi, int lim_r, bool r_ok,
+                                          int lane, const bf16x8_t (&ka)[2][4],
+                                          const bf16x8_t (&qv)[4], float& m, float& lsum,
+                                          f32x4_t (&oacc)[8]) {
   const int g = lane >> 4;
   f32x4_t st[2];
 #pragma unroll
@@ -594,10 +642,22 @@ __device__ __forceinline__ void window_mma(const AttnArgs& a, int ws, int hi, in
     pb.h[t] = f32_to_bf16_rne(p);
   }
   lsum += psum;
-  // O^T[d][row] += V^T[d][keys 8g..8g+7] * P^T
+  return pb.v;
+}
+
+// O^T[d][row] += V^T[d][keys 8g..8g+7] * P^T
+__device__ __forceinline__ void mma_pv(const bf16x8_t (&va)[8], bf16x8_t pb, f32x4_t (&oacc)[8]) {
 #pragma unroll
   for (int db = 0; db < 8; ++db)
-    oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[db], pb.v, oacc[db], 0, 0, 0);
+    oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[db], pb, oacc[db], 0, 0, 0);
+}
+
+__device__ __forceinline__ void window_mma(const AttnArgs& a, int ws, int hi, int lim_r, bool r_ok,
+                                           int lane, const bf16x8_t (&ka)[2][4],
+                                           const bf16x8_t (&va)[8], const bf16x8_t (&qv)[4],
+                                           float& m, float& lsum, f32x4_t (&oacc)[8]) {
+  const bf16x8_t pb = mma_s(a, ws, hi, lim_r, r_ok, lane, ka, qv, m, lsum, oacc);
+  mma_pv(va, pb, oacc);
 }
 
 // Walks keys [lo, hi) of query tile t (hi clipped to the keys the tile's
@@ -705,9 +765,10 @@ __device__ __forceinline__ void wave_walk(const AttnArgs& a, const TileRef& t, i
 // running max M, sum L and unnormalised output o. Every wave's state is
 // there: a wave that held no keys has max -inf, sum 0 and output 0, so its
 // weight exp2(-inf - M) is 0. Waves in order, so every kernel sharing it
-// gives the same bits. s_m / s_l: [row][wave]; s_o: wave w's rows at w * wave_o.
+// gives the same bits. s_m / s_l: [row][wave]; wave w's partial at wave_part.
+template <bool kFp8>
 __device__ __forceinline__ void merge_waves(const float (*s_m)[kAW], const float (*s_l)[kAW],
-                                            const float* s_o, int wave_o, int row, int d0,
+                                            uint8_t* s_kt, uint8_t* s_vt, int row, int c4,
                                             float& M, float& L, float (&o)[4]) {
   const float4 m0 = *reinterpret_cast<const float4*>(&s_m[row][0]);
   const float4 m1 = *reinterpret_cast<const float4*>(&s_m[row][4]);
@@ -716,7 +777,7 @@ __device__ __forceinline__ void merge_waves(const float (*s_m)[kAW], const float
   float4 x[kAW];
 #pragma unroll
   for (int w = 0; w < kAW; ++w)
-    x[w] = *reinterpret_cast<const float4*>(&s_o[w * wave_o + row * kOStride + d0]);
+    x[w] = *reinterpret_cast<const float4*>(wave_part<kFp8>(s_kt, s_vt, w) + part_off(row, c4));
   const float mw[kAW] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
   const float lw[kAW] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
   M = -INFINITY;
@@ -768,14 +829,15 @@ __device__ __forceinline__ void combine_splits(const AttnArgs& a, int b, int kvh
 // Merges the 8 waves' running states (acc) of query tile t, whose keys were
 // [klo, khi) with wave w on windows w, w + 8, ..., and writes the normalised
 // output (pslot < 0) or the unnormalised partial (o, running max, sum) at
-// partial slot pslot. s_raw holds the per-wave K and V window tiles, which
-// take the per-wave partial outputs here. kSplitMerge (the fused kernel): a
+// partial slot pslot. The per-wave K and V window tiles (s_kt, s_vt) take the
+// per-wave partial outputs here. kSplitMerge (the fused kernel): a
 // partial (the tile's keys span ns > 1 splits) is merged in the kernel: the
 // last of the tile's ns workgroups to take its ticket (a.tickets[b * Hkv +
 // kvh], zero between calls) merges them all.
 template <bool kFp8, int kG, bool kSplitMerge>
 __device__ __forceinline__ void merge_tile(const AttnArgs& a, const TileRef& t, int64_t pslot,
-                                           uint8_t* s_raw, float (*s_m)[kAW], float (*s_l)[kAW],
+                                           uint8_t* s_kt, uint8_t* s_vt, float (*s_m)[kAW],
+                                           float (*s_l)[kAW],
                                            const WaveAcc& acc, int ns) {
   const int G = kG ? kG : a.G;
   constexpr int kTileB = AttnLds<kFp8>::kTileB;
@@ -783,21 +845,20 @@ __device__ __forceinline__ void merge_tile(const AttnArgs& a, const TileRef& t, 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int n = lane & 15, g = lane >> 4;
   const int r0 = t.qt * kRows;
-  // bf16 tiles: a wave's partial output fits its own K/V tiles, which it has
+  // bf16 tiles: a wave's partial output fits its own K tile, which it has
   // finished reading (its last window's reads were waited on), so it needs no
   // barrier before writing it; fp8 tiles are smaller and the partials go over
-  // the whole tile area after every wave is done with its tiles
-  constexpr bool kOwn = kRows * kOStride * 4 <= 2 * kTileB;
-  constexpr int kWaveO = kOwn ? 2 * kTileB / 4 : kRows * kOStride;  // floats between waves
-  float* s_o = reinterpret_cast<float*>(s_raw);
+  // both tile arrays after every wave is done with its tiles
+  constexpr bool kOwn = AttnLds<kFp8>::kTileB >= kRows * kD * 4;
   if (g == 0) {
     s_m[n][wid] = acc.m;
     s_l[n][wid] = acc.lsum;
   }
   if constexpr (!kOwn) lds_barrier();  // every wave is done with its tiles
+  float* part = wave_part<kFp8>(s_kt, s_vt, wid);
 #pragma unroll
   for (int db = 0; db < 8; ++db)
-    *reinterpret_cast<float4*>(&s_o[wid * kWaveO + n * kOStride + db * 16 + 4 * g]) =
+    *reinterpret_cast<float4*>(part + part_off(n, db * 4 + g)) =
         make_float4(acc.oacc[db][0], acc.oacc[db][1], acc.oacc[db][2], acc.oacc[db][3]);
   lds_barrier();
   // merge the waves: thread handles row tid / 32, dims 4 (tid % 32) .. + 3
@@ -805,9 +866,9 @@ __device__ __forceinline__ void merge_tile(const AttnArgs& a, const TileRef& t, 
     const int row = tid >> 5;
     const int rr = r0 + row;
     if (rr < rows) {
-      const int d0 = (tid & 31) * 4;
+      const int c4 = tid & 31, d0 = c4 * 4;
       float M, L, o[4];
-      merge_waves(s_m, s_l, s_o, kWaveO, row, d0, M, L, o);
+      merge_waves<kFp8>(s_m, s_l, s_kt, s_vt, row, c4, M, L, o);
       const int oi = rr / G, oh = kvh * G + rr % G;
       if (pslot < 0) {
         const float inv = (L > 0.0f) ? a.v_scale / L : 0.0f;
@@ -861,16 +922,17 @@ __device__ __forceinline__ void merge_tile(const AttnArgs& a, const TileRef& t, 
 // pslot (merge_tile). s_bt as for wave_walk.
 template <bool kFp8, int kG>
 __device__ __forceinline__ void attend_keys(const AttnArgs& a, const TileRef& t, int klo, int khi,
-                                            int64_t pslot, uint8_t* s_raw, float (*s_m)[kAW],
+                                            int64_t pslot, uint8_t* s_kt, uint8_t* s_vt,
+                                            float (*s_m)[kAW],
                                             float (*s_l)[kAW], const int* s_bt, int bt_cap) {
   constexpr int kTileB = AttnLds<kFp8>::kTileB;
   const int wid = threadIdx.x >> 6;
-  uint8_t* tile_k = s_raw + wid * 2 * kTileB;
-  uint8_t* tile_v = tile_k + kTileB;
+  uint8_t* tile_k = s_kt + wid * kTileB;
+  uint8_t* tile_v = s_vt + wid * kTileB;
   WaveAcc acc;
   wave_walk<kFp8, kG>(a, t, t.kvh, klo, khi, klo + wid * kWin, kAW * kWin, s_bt, bt_cap, tile_k,
                       tile_v, acc);
-  merge_tile<kFp8, kG, false>(a, t, pslot, s_raw, s_m, s_l, acc, 1);
+  merge_tile<kFp8, kG, false>(a, t, pslot, s_kt, s_vt, s_m, s_l, acc, 1);
 }
 
 // One launch = one workgroup per (kv head x query tile, split, sequence).
@@ -898,7 +960,8 @@ __global__ __launch_bounds__(kAT) void k_verify_attn(const int32_t* cu_q, const 
                                                      int bs_shift, int bt_width, int nbt_split,
                                                      AttnArgs a) {
   const int G = kG ? kG : a.G;
-  __shared__ __attribute__((aligned(16))) uint8_t s_raw[AttnLds<kFp8>::kRawBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t s_kt[AttnLds<kFp8>::kArrB];
+  __shared__ __attribute__((aligned(16))) uint8_t s_vt[AttnLds<kFp8>::kArrB];
   __shared__ __attribute__((aligned(16))) float s_m[kRows][kAW], s_l[kRows][kAW];
   __shared__ int s_bt[kBtCap];
   if (blockIdx.x & ((1u << xcd_shift) - 1)) return;
@@ -938,7 +1001,7 @@ __global__ __launch_bounds__(kAT) void k_verify_attn(const int32_t* cu_q, const 
   if (vis < hi) hi = vis;
   const int64_t pslot =
       t.Lk <= split_len ? -1 : (((int64_t)b * a.Hkv + kvh) * qtiles + qt) * a.nsplit + split;
-  attend_keys<kFp8, kG>(a, t, lo, hi, pslot, s_raw, s_m, s_l, s_bt, kBtCap);
+  attend_keys<kFp8, kG>(a, t, lo, hi, pslot, s_kt, s_vt, s_m, s_l, s_bt, kBtCap);
 }
 
 // k_verify_attn with the q/k-norm + RoPE + KV-store step of its tile's
@@ -973,7 +1036,8 @@ __global__ __launch_bounds__(kAT) void k_verify_attn_qkv(const int32_t* cu_q, co
                                                          AttnArgs a, QkvArgs qa) {
   constexpr int kRowB = AttnLds<kFp8>::kRowB;
   constexpr int kTileB = AttnLds<kFp8>::kTileB;
-  __shared__ __attribute__((aligned(16))) uint8_t s_raw[AttnLds<kFp8>::kRawBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t s_kt[AttnLds<kFp8>::kArrB];
+  __shared__ __attribute__((aligned(16))) uint8_t s_vt[AttnLds<kFp8>::kArrB];
   __shared__ __attribute__((aligned(16))) float s_m[kRows][kAW], s_l[kRows][kAW];
   __shared__ __attribute__((aligned(16))) uint16_t s_q[kRows * kD];
   // the query tokens' k rows, then their v rows (at most kRows tokens)
@@ -1007,8 +1071,8 @@ __global__ __launch_bounds__(kAT) void k_verify_attn_qkv(const int32_t* cu_q, co
   if (vis < hi) hi = vis;
   const int knew = t.Lk - t.Lq;  // first key of the query tokens
   const int esz = kFp8 ? 1 : 2;
-  uint8_t* tile_k = s_raw + wid * 2 * kTileB;
-  uint8_t* tile_v = tile_k + kTileB;
+  uint8_t* tile_k = s_kt + wid * kTileB;
+  uint8_t* tile_v = s_vt + wid * kTileB;
   // window j of this wave (first key wsj) -> its cache row bases; false when
   // its block is not a valid cache block (the window is skipped)
   auto window_base = [&](int j, int wsj, const uint8_t*& kb, const uint8_t*& vb) -> bool {
@@ -1030,7 +1094,10 @@ __global__ __launch_bounds__(kAT) void k_verify_attn_qkv(const int32_t* cu_q, co
   const uint8_t* kb0 = a.kc;
   const uint8_t* vb0 = a.vc;
   bool have = ws < hi && window_base(0, ws, kb0, vb0);
-  if (have) issue_window<kFp8>(kb0, vb0, ws, hi, tile_k, tile_v, wo);
+  if (have) {  // K first, so that its scores can start while V lands
+    issue_tile<kFp8>(kb0, ws, hi, tile_k, wo);
+    issue_tile<kFp8>(vb0, ws, hi, tile_v, wo);
+  }
   QkvLoads ql;
   qkv_load(a, qa, t, kvh, G, ql);
   const int fi = lane < t.Lq ? lane : t.Lq - 1;
@@ -1055,7 +1122,8 @@ __global__ __launch_bounds__(kAT) void k_verify_attn_qkv(const int32_t* cu_q, co
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     const uint8_t *kb, *vb;
     window_base(0, ws, kb, vb);
-    issue_window<kFp8>(kb, vb, ws, hi, tile_k, tile_v, wo);
+    issue_tile<kFp8>(kb, ws, hi, tile_k, wo);
+    issue_tile<kFp8>(vb, ws, hi, tile_v, wo);
   }
   const int n = lane & 15, g = lane >> 4;
   const int r = n;
@@ -1074,31 +1142,41 @@ __global__ __launch_bounds__(kAT) void k_verify_attn_qkv(const int32_t* cu_q, co
   const int kn = fast ? knew : INT32_MAX;
   const uint8_t* nk = s_new;
   const uint8_t* nv = s_new + kRows * kRowB;
-  bool stored = !fast;
+  const bool stored = !fast;
+  // Each window streams its K tile, then its V tile; window j + 1's K goes
+  // out as soon as K_j is in registers and its V as soon as V_j is, so the
+  // next window's loads overlap this window's scores, softmax and P V. Every
+  // tile read waits for all loads in flight (loads into LDS cannot be waited
+  // for one by one across the loop: the compiler would wait for all anyway).
   for (int j = 0; ws < hi; ++j) {
     const int ws_next = ws + kAW * kWin;
     const bool cur = have;
-    bf16x8_t ka[2][4], va[8];
+    const uint8_t *kbn = nullptr, *vbn = nullptr;
+    const bool have_next = ws_next < hi && window_base(j + 1, ws_next, kbn, vbn);
+    // a window of query-token keys only reads s_new: nothing to load
+    const bool load_next = have_next && ws_next < kn;
     if (cur) {
+      bf16x8_t ka[2][4], va[8];
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      window_read<kFp8, true>(tile_k, tile_v, nk, nv, ws, kn, t.Lq - 1, lane, ka, va);
-      // every LDS read of the tiles has returned before the next window overwrites them
+      read_k<kFp8, true>(tile_k, nk, ws, kn, t.Lq - 1, lane, ka);
+      // every LDS read of the tile has returned before the next window overwrites it
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      if (load_next) issue_tile<kFp8>(kbn, ws_next, hi, tile_k, wo);
+      const bf16x8_t pb = mma_s(a, ws, hi, lim_r, r_ok, lane, ka, qv, m, lsum, oacc);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      read_v<kFp8, true>(tile_v, nv, ws, kn, t.Lq - 1, lane, va);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      if (load_next) issue_tile<kFp8>(vbn, ws_next, hi, tile_v, wo);
+      mma_pv(va, pb, oacc);
+    } else if (load_next) {
+      issue_tile<kFp8>(kbn, ws_next, hi, tile_k, wo);
+      issue_tile<kFp8>(vbn, ws_next, hi, tile_v, wo);
     }
-    if (!stored) {  // fast: nothing in this kernel reads the stored rows
-      kv_store_all<kFp8>(a, qa, S);
-      stored = true;
-    }
-    have = false;
-    if (ws_next < hi) {
-      const uint8_t *kb, *vb;
-      have = window_base(j + 1, ws_next, kb, vb);
-      // a window of query-token keys only reads s_new: nothing to load
-      if (have && ws_next < kn) issue_window<kFp8>(kb, vb, ws_next, hi, tile_k, tile_v, wo);
-    }
-    if (cur) window_mma(a, ws, hi, lim_r, r_ok, lane, ka, va, qv, m, lsum, oacc);
+    have = have_next;
     ws = ws_next;
   }
+  // fast: nothing in this kernel reads the stored rows; they go out after the
+  // key loop, while the waves merge
   if (!stored) kv_store_all<kFp8>(a, qa, S);
   WaveAcc acc;
   acc.m = m;
@@ -1110,7 +1188,7 @@ __global__ __launch_bounds__(kAT) void k_verify_attn_qkv(const int32_t* cu_q, co
   int ns = (t.Lk + split_len - 1) / split_len;
   if (ns > (int)gridDim.y) ns = (int)gridDim.y;
   const int64_t pslot = ns <= 1 ? -1 : ((int64_t)b * a.Hkv + kvh) * a.nsplit + split;
-  merge_tile<kFp8, kG, true>(a, t, pslot, s_raw, s_m, s_l, acc, ns);
+  merge_tile<kFp8, kG, true>(a, t, pslot, s_kt, s_vt, s_m, s_l, acc, ns);
 }
 
 // Balanced launch: one workgroup per CU. The 32-key windows of all tiles
@@ -1159,15 +1237,16 @@ __device__ __forceinline__ int sk_tiles(const AttnArgs& a) {
 // output (pslot < 0) or the unnormalised partial at partial slot pslot.
 template <bool kFp8, int kG>
 __device__ __forceinline__ void attend_heads(const AttnArgs& a, const TileRef& t, int klo, int khi,
-                                             int64_t pslot, uint8_t* s_raw, const int* s_bt,
+                                             int64_t pslot, uint8_t* s_kt, uint8_t* s_vt,
+                                             const int* s_bt,
                                              int bt_cap) {
   const int G = kG ? kG : a.G;
   constexpr int kTileB = AttnLds<kFp8>::kTileB;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int n = lane & 15, g = lane >> 4;
   const int kvh = wid;
-  uint8_t* tile_k = s_raw + wid * 2 * kTileB;
-  uint8_t* tile_v = tile_k + kTileB;
+  uint8_t* tile_k = s_kt + wid * kTileB;
+  uint8_t* tile_v = s_vt + wid * kTileB;
   WaveAcc acc;
   wave_walk<kFp8, kG>(a, t, kvh, klo, khi, klo, kWin, s_bt, bt_cap, tile_k, tile_v, acc);
   const int r = t.qt * kRows + n;
@@ -1201,8 +1280,8 @@ __device__ __forceinline__ void attend_heads(const AttnArgs& a, const TileRef& t
 template <bool kFp8, int kG, bool kHeads>
 __global__ __launch_bounds__(kAT) void k_verify_attn_sk(AttnArgs a) {
   const int G = kG ? kG : a.G;
-  constexpr int kRaw = kHeads ? AttnLds<kFp8>::kKvBytes : AttnLds<kFp8>::kRawBytes;
-  __shared__ __attribute__((aligned(16))) uint8_t s_raw[kRaw];
+  __shared__ __attribute__((aligned(16))) uint8_t s_kt[AttnLds<kFp8>::kArrB];
+  __shared__ __attribute__((aligned(16))) uint8_t s_vt[AttnLds<kFp8>::kArrB];
   __shared__ __attribute__((aligned(16))) float s_m[kHeads ? 1 : kRows][kAW],
       s_l[kHeads ? 1 : kRows][kAW];
   __shared__ int s_bt[kSkBtCap];
@@ -1279,9 +1358,9 @@ __global__ __launch_bounds__(kAT) void k_verify_attn_sk(AttnArgs a) {
     for (int i = tid; i < nbt && i < kSkBtCap && bt0 + i < a.bt_width; i += kAT)
       s_bt[i] = a.bt[(int64_t)b * a.bt_stride + bt0 + i];
     if constexpr (kHeads)
-      attend_heads<kFp8, kG>(a, t, klo, khi, pslot, s_raw, s_bt, kSkBtCap);
+      attend_heads<kFp8, kG>(a, t, klo, khi, pslot, s_kt, s_vt, s_bt, kSkBtCap);
     else
-      attend_keys<kFp8, kG>(a, t, klo, khi, pslot, s_raw, s_m, s_l, s_bt, kSkBtCap);
+      attend_keys<kFp8, kG>(a, t, klo, khi, pslot, s_kt, s_vt, s_m, s_l, s_bt, kSkBtCap);
     w = seg_end;
     ++seg;
   }
