@@ -962,12 +962,13 @@ def _accept_args(**kw):
 
 def bookkeeping_probe(torch, hv, context: int = PROBE_CONTEXT - 4, gamma: int = 3,
                       out_len: int = 2, reps: int = 20):
-    """The spec step's bookkeeping launches at batch 1 (hs_spec_prealloc at the start of
-    the draft phase, hs_verify_prepare at the start of the verify phase, hs_spec_commit
-    after the acceptance), graph-timed together from a sequence of `context` tokens;
+    """The spec step's bookkeeping launches at batch 1, as the fixed-gamma runner makes
+    them: hs_verify_prepare at the start of the verify phase and hs_spec_commit_next
+    after the acceptance (the commit, then the next step's pre-allocation and first
+    draft-step staging), graph-timed together from a sequence of `context` tokens;
     every replay commits `out_len` tokens (one accepted draft and the resample, the
     typical outcome). Returns (µs per step, bytes per step): the state words, the
-    staging rows and the committed tokens the three launches read and write."""
+    staging rows and the committed tokens the launches read and write."""
     dev = torch.device("cuda:0")
     bs = 256
     end = context + (reps + 2) * out_len + gamma + 2
@@ -995,16 +996,21 @@ def bookkeeping_probe(torch, hv, context: int = PROBE_CONTEXT - 4, gamma: int = 
     out = torch.randint(0, V, (1, gamma + 1), dtype=torch.int64, device=dev)
     olen = torch.full((1,), out_len, dtype=torch.int32, device=dev)
 
+    stage0 = (torch.empty(2, dtype=torch.int64, device=dev), torch.empty(2, dtype=torch.int64, device=dev),
+              torch.empty(2, dtype=torch.int32, device=dev), torch.empty(2, dtype=torch.int32, device=dev),
+              torch.empty(2, dtype=torch.int32, device=dev))
+    hv.ops.spec_prealloc(st, gamma, out=elig)  # the step before the first replay
+
     def step():
-        hv.ops.spec_prealloc(st, gamma, out=elig)
         hv.ops.verify_prepare(st, draft, gamma)
-        hv.ops.spec_commit(st, gamma, out, olen, eligible=elig)
+        hv.ops.spec_commit_next(st, gamma, out, olen, elig, gamma, stage0, lookback=True)
 
     us = graph_time_us(torch, dev, step, reps)
     R = gamma + 1
     nbytes = (4 * 6 + 4 * W  # prealloc: lengths, counts, free header, table row, ref counts
               + 8 + gamma * 8 + R * (8 + 8 + 4) + 2 * 2 * 4  # prepare: ids, positions, slots, cu
-              + R * 8 + 4 + out_len * 8 + 4 * 6)  # commit: emitted tokens in, tokens appended
+              + R * 8 + 4 + out_len * 8 + 4 * 6  # commit: emitted tokens in, tokens appended
+              + 2 * (8 + 8 + 4) + 2 * 2 * 4)  # next draft step 0: ids, positions, slots, cu
     return us, nbytes
 
 
@@ -1032,10 +1038,10 @@ def inscope_step_probe(torch, hv, attn_roof: dict, layers: int):
             "parts": {"attention": {"launches": layers, "bytes": attn_bytes,
                                     "us": round(attn_us, 2)},
                       "acceptance": {"bytes": acc_bytes, "us": round(acc_us, 2)},
-                      "bookkeeping": {"launches": 3, "bytes": bk_bytes, "us": round(bk_us, 2)}},
+                      "bookkeeping": {"launches": 2, "bytes": bk_bytes, "us": round(bk_us, 2)}},
             "what": f"verify+accept step without the projection weights: {layers} fused "
-                    f"attention launches at L={PROBE_CONTEXT}, the acceptance call, prealloc + "
-                    "verify staging + commit; graph-timed per part"}
+                    f"attention launches at L={PROBE_CONTEXT}, the acceptance call, verify staging + "
+                    "commit (with the next step's pre-allocation and draft staging); graph-timed per part"}
 
 
 def profiled_traffic(kernel: str, workload: str):

@@ -50,12 +50,17 @@ __device__ __forceinline__ int ring_at(const hs_spec_state& s, int pos) {
 // ---------------------------------------------------------------------------
 // pre-allocation: llm_engine.py:111-128
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kCT) void k_prealloc(hs_spec_state s, int gamma, int32_t* eligible,
-                                                  int32_t* status) {
-  __shared__ int s_need[kCT];
-  __shared__ int s_off[kCT];
-  __shared__ int s_ok[kCT];
-  __shared__ int s_take;
+struct PreallocLds {
+  int need[kCT], off[kCT], ok[kCT];
+  int take;
+};
+
+__device__ void prealloc_body(const hs_spec_state& s, int gamma, int32_t* eligible,
+                              int32_t* status, PreallocLds& L) {
+  int* s_need = L.need;
+  int* s_off = L.off;
+  int* s_ok = L.ok;
+  int& s_take = L.take;
   const int tid = threadIdx.x;
   for (int base = 0; base < s.B; base += kCT) {
     const int b = base + tid;
@@ -116,6 +121,12 @@ __global__ __launch_bounds__(kCT) void k_prealloc(hs_spec_state s, int gamma, in
   }
 }
 
+__global__ __launch_bounds__(kCT) void k_prealloc(hs_spec_state s, int gamma, int32_t* eligible,
+                                                  int32_t* status) {
+  __shared__ PreallocLds L;
+  prealloc_body(s, gamma, eligible, status, L);
+}
+
 // ---------------------------------------------------------------------------
 // verify staging: model_runner.py:339-362
 // ---------------------------------------------------------------------------
@@ -165,12 +176,10 @@ __global__ __launch_bounds__(kCT) void k_prepare(hs_spec_state s, const int64_t*
 // 0 feeds the two last tokens (positions len-2, len-1): after a step that
 // accepted every draft, the draft model never saw the last accepted draft,
 // and this fills that KV slot.
-__global__ __launch_bounds__(kCT) void k_draft_prepare(hs_spec_state s, const int64_t* draft,
-                                                       int draft_stride, int step, int lookback,
-                                                       int64_t* input_ids, int64_t* positions,
-                                                       int32_t* slot_mapping, int32_t* cu_q,
-                                                       int32_t* cu_k) {
-  __shared__ int s_w[kCW];
+__device__ void draft_prepare_body(const hs_spec_state& s, const int64_t* draft, int draft_stride,
+                                   int step, int lookback, int64_t* input_ids, int64_t* positions,
+                                   int32_t* slot_mapping, int32_t* cu_q, int32_t* cu_k,
+                                   int* s_w) {
   const int tid = threadIdx.x;
   const int R = (step == 0 && lookback) ? 2 : 1;
   int carry = 0;
@@ -210,6 +219,16 @@ __global__ __launch_bounds__(kCT) void k_draft_prepare(hs_spec_state s, const in
   }
 }
 
+__global__ __launch_bounds__(kCT) void k_draft_prepare(hs_spec_state s, const int64_t* draft,
+                                                       int draft_stride, int step, int lookback,
+                                                       int64_t* input_ids, int64_t* positions,
+                                                       int32_t* slot_mapping, int32_t* cu_q,
+                                                       int32_t* cu_k) {
+  __shared__ int s_w[kCW];
+  draft_prepare_body(s, draft, draft_stride, step, lookback, input_ids, positions, slot_mapping,
+                     cu_q, cu_k, s_w);
+}
+
 // ---------------------------------------------------------------------------
 // commit + rollback: llm_engine.py:146-195, block_manager.py:84-92
 // ---------------------------------------------------------------------------
@@ -221,12 +240,10 @@ struct CommitWs {
   int32_t* seq;     // [5 * B] per-sequence scratch
 };
 
-__global__ __launch_bounds__(kCT) void k_commit(hs_spec_state s, int gamma, const int32_t* nacc,
-                                                const int64_t* out_tokens, const int32_t* out_len,
-                                                const int32_t* eligible, int32_t* appended,
-                                                int32_t* dirty, int dirty_mode, CommitWs w) {
-  __shared__ int s_w[kCW];
-  __shared__ int s_tot[2];
+__device__ void commit_body(const hs_spec_state& s, int gamma, const int64_t* out_tokens,
+                            const int32_t* out_len, const int32_t* eligible, int32_t* appended,
+                            int32_t* dirty, int dirty_mode, const CommitWs& w, int* s_w,
+                            int* s_tot) {
   const int tid = threadIdx.x;
   const int R = gamma + 1;
   int32_t* s_nblk = w.seq;             // table length at entry
@@ -234,7 +251,6 @@ __global__ __launch_bounds__(kCT) void k_commit(hs_spec_state s, int gamma, cons
   int32_t* s_ntrim = w.seq + 2 * s.B;  // blocks trimmed from the tail
   int32_t* s_odeal = w.seq + 3 * s.B;  // first event of the sequence's releases
   int32_t* s_otrim = w.seq + 4 * s.B;
-  (void)nacc;
 
   // phase 1: append tokens, stop at EOS / max_tokens, count release events
   for (int b = tid; b < s.B; b += kCT) {
@@ -360,6 +376,38 @@ __global__ __launch_bounds__(kCT) void k_commit(hs_spec_state s, int gamma, cons
   if (tid == 0) s.free_hdr[1] = count0 + carry;
 }
 
+__global__ __launch_bounds__(kCT) void k_commit(hs_spec_state s, int gamma, const int64_t* out_tokens,
+                                                const int32_t* out_len, const int32_t* eligible,
+                                                int32_t* appended, int32_t* dirty, int dirty_mode,
+                                                CommitWs w) {
+  __shared__ int s_w[kCW];
+  __shared__ int s_tot[2];
+  commit_body(s, gamma, out_tokens, out_len, eligible, appended, dirty, dirty_mode, w, s_w,
+              s_tot);
+}
+
+// The commit of a step, then the next step's pre-allocation (into eligible,
+// which the commit has read) and its first draft step's staging, in one
+// workgroup: the state each part reads is the one the previous part left
+// (their writes are ordered by the workgroup barriers between them).
+__global__ __launch_bounds__(kCT) void k_commit_next(hs_spec_state s, int gamma,
+                                                     const int64_t* out_tokens,
+                                                     const int32_t* out_len, int32_t* eligible,
+                                                     CommitWs w, int next_gamma, int32_t* status,
+                                                     int lookback, int64_t* input_ids,
+                                                     int64_t* positions, int32_t* slot_mapping,
+                                                     int32_t* cu_q, int32_t* cu_k) {
+  __shared__ int s_w[kCW];
+  __shared__ int s_tot[2];
+  __shared__ PreallocLds L;
+  commit_body(s, gamma, out_tokens, out_len, eligible, nullptr, nullptr, 0, w, s_w, s_tot);
+  __syncthreads();
+  prealloc_body(s, next_gamma, eligible, status, L);
+  __syncthreads();
+  draft_prepare_body(s, nullptr, 0, 0, lookback, input_ids, positions, slot_mapping, cu_q, cu_k,
+                     s_w);
+}
+
 // zero the K/V rows of the given slots in every (kv, layer) plane
 __global__ __launch_bounds__(256) void k_zero_slots(uint8_t* cache, int64_t plane_bytes,
                                                     int planes, int64_t slot_bytes,
@@ -446,9 +494,34 @@ int hs_spec_commit(const hs_spec_state* state, int gamma, const int32_t* num_acc
   w.ev_blk = p + 2 * (size_t)state->num_blocks;
   w.ev_free = w.ev_blk + (size_t)state->B * state->W;
   w.seq = w.ev_free + (size_t)state->B * state->W;
+  (void)num_accepted;
   hipLaunchKernelGGL(k_commit, dim3(1), dim3(kCT), 0, reinterpret_cast<hipStream_t>(stream),
-                     *state, gamma, num_accepted, out_tokens, out_len, eligible, appended,
-                     dirty_slots, dirty_mode, w);
+                     *state, gamma, out_tokens, out_len, eligible, appended, dirty_slots,
+                     dirty_mode, w);
+  return hipGetLastError() == hipSuccess ? HS_OK : HS_ERR_LAUNCH;
+}
+
+int hs_spec_commit_next(const hs_spec_state* state, int gamma, const int64_t* out_tokens,
+                        const int32_t* out_len, int32_t* eligible, void* workspace,
+                        size_t workspace_bytes, int next_gamma, int32_t* status, int lookback,
+                        int64_t* input_ids, int64_t* positions, int32_t* slot_mapping,
+                        int32_t* cu_seqlens_q, int32_t* cu_seqlens_k, void* stream) {
+  if (!state_ok(state) || gamma < 0 || next_gamma < 0 || !out_tokens || !out_len ||
+      !eligible || !workspace || !input_ids || !positions || !slot_mapping || !cu_seqlens_q ||
+      !cu_seqlens_k || (lookback != 0 && lookback != 1))
+    return HS_ERR_INVALID;
+  if (workspace_bytes < hs_spec_commit_workspace_size(state->B, state->W, state->num_blocks))
+    return HS_ERR_WORKSPACE;
+  int32_t* p = static_cast<int32_t*>(workspace);
+  CommitWs w;
+  w.dec = p;
+  w.last = p + state->num_blocks;
+  w.ev_blk = p + 2 * (size_t)state->num_blocks;
+  w.ev_free = w.ev_blk + (size_t)state->B * state->W;
+  w.seq = w.ev_free + (size_t)state->B * state->W;
+  hipLaunchKernelGGL(k_commit_next, dim3(1), dim3(kCT), 0, reinterpret_cast<hipStream_t>(stream),
+                     *state, gamma, out_tokens, out_len, eligible, w, next_gamma, status,
+                     lookback, input_ids, positions, slot_mapping, cu_seqlens_q, cu_seqlens_k);
   return hipGetLastError() == hipSuccess ? HS_OK : HS_ERR_LAUNCH;
 }
 

@@ -39,7 +39,7 @@ class SpecRunner:
                  temperature: float = 1.0, top_k: int = 0, top_p: float = 1.0,
                  mode: str = "reference", eos: int = -1, k_scale: float | None = None,
                  v_scale: float | None = None, device="cuda", adaptive: bool = False,
-                 max_gamma: int | None = None):
+                 max_gamma: int | None = None, chain_steps: bool | None = None):
         filters = 0 < top_k < target.g.vocab or top_p < 1.0
         # reference mode with top-k / top-p draws the draft tokens from the filtered
         # Sampler and keeps the unfiltered softmax as the draft probabilities
@@ -93,6 +93,14 @@ class SpecRunner:
         self.sampler = Sampler()
         self._per_gamma: dict[int, SimpleNamespace] = {}
         self.controller = AdaptiveGamma(gamma, max_gamma=self.max_gamma) if adaptive else None
+        # fixed gamma: each step's commit also pre-allocates the next step and stages its
+        # first draft step (hs_spec_commit_next), so the next draft phase starts with
+        # the draft forward; _staged says the state already holds that
+        self.chain_steps = (not adaptive) if chain_steps is None else bool(chain_steps)
+        if self.chain_steps and adaptive:
+            raise ValueError("chained steps need a fixed gamma (the next step's gamma is "
+                             "known when the commit runs)")
+        self._staged = False
         self.history: list[tuple[int, int, int]] = []  # (gamma, accepted, proposed) per step
         self.preempted: list[int] = []  # sequences out of the batch until readmit(), next first
         self.last = None
@@ -142,6 +150,7 @@ class SpecRunner:
         """Allocates prompt blocks from the front of the free list (block_manager.py:59-82
         without prefix reuse: random prompts never share a full block)."""
         assert len(prompts) == self.B
+        self._staged = False
         st = self.state
         free = list(range(self.num_blocks))
         tables, nblk = [], []
@@ -254,6 +263,9 @@ class SpecRunner:
         so prealloc and commit skip it) until readmit() has recomputed its KV; its
         tokens and max_tokens stay. Like waiting.appendleft, the last one preempted
         comes back first."""
+        if self._staged:
+            raise RuntimeError("preempt between chained steps: build the runner with "
+                               "adaptive=True or chain_steps=False")
         st = self.state
         n = int(st.num_seq_blocks[b])
         table = st.block_tables[b, :n].cpu().tolist()
@@ -281,6 +293,9 @@ class SpecRunner:
         preempted for lack of blocks returns only once others have released some;
         the target and draft K/V of every token but the last, which the next step
         processes, are recomputed by prefill. Returns how many returned."""
+        if self._staged:
+            raise RuntimeError("readmit between chained steps: build the runner with "
+                               "adaptive=True or chain_steps=False")
         st = self.state
         back = 0
         while self.preempted:
@@ -329,14 +344,18 @@ class SpecRunner:
         (model_runner.py:294-318)."""
         st = self.state
         G = self._g()
-        ops.spec_prealloc(st, G.gamma, out=G.elig)
+        if not self._staged:
+            ops.spec_prealloc(st, G.gamma, out=G.elig)
         G.u_draft.uniform_()
         for j in range(G.gamma):
             if j == 0:
                 # two queries: the previous token (fills the draft K/V the last step
                 # left out when it accepted every draft) and the last token
-                ids, pos, slots, cq, ck = ops.draft_prepare(st, None, 0, out=self.d_stage0,
-                                                            lookback=True)
+                if self._staged:  # the previous commit staged them
+                    ids, pos, slots, cq, ck = self.d_stage0
+                else:
+                    ids, pos, slots, cq, ck = ops.draft_prepare(st, None, 0, out=self.d_stage0,
+                                                                lookback=True)
                 set_context(True, cq, ck, 2, 0, slots, None, st.block_tables)
                 h = self.draft(ids, pos)[1::2]
             else:
@@ -376,7 +395,11 @@ class SpecRunner:
                                           G.u_acc, self.u_res, mode=self.mode,
                                           top_ks=self.top_ks, top_ps=self.top_ps,
                                           topk_le64=self.topk_le64)
-        ops.spec_commit(st, g, out, olen, eligible=G.elig)
+        if self.chain_steps:
+            ops.spec_commit_next(st, g, out, olen, G.elig, g, self.d_stage0, lookback=True)
+            self._staged = True
+        else:
+            ops.spec_commit(st, g, out, olen, eligible=G.elig)
         G.last = (nacc, out, olen)
         G.logits = logits  # the acceptance call's target rows (read by checks)
         self.last = G.last

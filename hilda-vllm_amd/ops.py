@@ -486,6 +486,31 @@ def spec_commit(state: SpecStateTensors, gamma: int, out_tokens: torch.Tensor,
     return app, dirty
 
 
+def spec_commit_next(state: SpecStateTensors, gamma: int, out_tokens: torch.Tensor,
+                     out_len: torch.Tensor, eligible: torch.Tensor, next_gamma: int,
+                     stage0: tuple, lookback: bool = True) -> None:
+    """spec_commit(eligible=eligible) then, in the same launch, the next step's
+    spec_prealloc(next_gamma, out=eligible) and draft_prepare(step 0, lookback)
+    into the staging tensors `stage0` (ids, positions, slots, cu_q, cu_k):
+    llm_engine.py:146-195 and :111-128, model_runner.py:294-310."""
+    dev = state.context_lens.device
+    if eligible.dtype != torch.int32 or eligible.numel() != state.B or not eligible.is_contiguous():
+        raise ValueError("eligible must be a contiguous int32 [B] tensor")
+    R = 2 if lookback else 1
+    ids, pos, slots, cq, ck = stage0
+    if (ids.numel() != state.B * R or pos.numel() != state.B * R or slots.numel() != state.B * R
+            or cq.numel() != state.B + 1 or ck.numel() != state.B + 1):
+        raise ValueError("staging tensors do not match the batch")
+    ot = out_tokens.to(torch.int64).contiguous()
+    ol = out_len.to(torch.int32).contiguous()
+    st = state.struct()
+    L.check(L.lib().hs_spec_commit_next(
+        ctypes_ref(st), int(gamma), ot.data_ptr(), ol.data_ptr(), eligible.data_ptr(),
+        state.commit_ws.data_ptr(), state.commit_ws.numel(), int(next_gamma), None, int(R == 2),
+        ids.data_ptr(), pos.data_ptr(), slots.data_ptr(), cq.data_ptr(), ck.data_ptr(),
+        _stream(dev)), "hs_spec_commit_next")
+
+
 def zero_kv_slots(cache: torch.Tensor, slots: torch.Tensor) -> None:
     """Zero the rows of `slots` in every plane of a [P..., num_blocks, block_size, H, D] cache
     (cleanup_rejected_kv_slots, model_runner.py:467-481)."""

@@ -323,6 +323,20 @@ int hs_spec_commit(const hs_spec_state* state, int gamma, const int32_t* num_acc
                    int32_t* appended, int32_t* dirty_slots, int dirty_mode, void* workspace,
                    size_t workspace_bytes, void* stream);
 
+/* hs_spec_commit (without appended / dirty slots) followed, in the same     */
+/* launch, by the next step's hs_spec_prealloc(next_gamma) into eligible     */
+/* (read by the commit first) and hs_draft_prepare(step 0, lookback) into    */
+/* the given staging buffers: the end of one speculative step and the        */
+/* start of the next, llm_engine.py:146-195 then :111-128 and                */
+/* model_runner.py:294-310, for callers that know the next step's gamma.     */
+/* No reference counterpart: the reference runs these as separate host       */
+/* steps; here they are one graph node instead of three.                     */
+int hs_spec_commit_next(const hs_spec_state* state, int gamma, const int64_t* out_tokens,
+                        const int32_t* out_len, int32_t* eligible, void* workspace,
+                        size_t workspace_bytes, int next_gamma, int32_t* status, int lookback,
+                        int64_t* input_ids, int64_t* positions, int32_t* slot_mapping,
+                        int32_t* cu_seqlens_q, int32_t* cu_seqlens_k, void* stream);
+
 /* Zeroes row_bytes at every slot of slots[] (entries < 0 skipped) in each of */
 /* num_planes planes (e.g. the 2*L (K|V, layer) planes of a                  */
 /* [2, L, num_blocks, block_size, H, D] cache): byte offset                  */

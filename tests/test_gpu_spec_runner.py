@@ -22,17 +22,25 @@ def _mods():
     return q3, sr
 
 
+def _hv():
+    return importlib.import_module("hilda-vllm_amd")
+
+
 def _small(q3, layers=2, hidden=512, heads=4, kv=2, vocab=3000):
     return q3.Qwen3Geometry(num_layers=layers, hidden=hidden, num_heads=heads, num_kv_heads=kv,
                             ffn=1024, vocab=vocab, max_position=4096)
 
 
 def _check_state(runner):
+    """Block accounting between steps: every sequence holds ceil(len / block) blocks,
+    or, when the last commit already pre-allocated the next step (chained steps),
+    ceil((len + gamma + 1) / block)."""
     st = runner.state
     nb = st.num_seq_blocks.cpu()
     lens = st.context_lens.cpu()
+    extra = runner.gamma + 1 if runner._staged else 0
     for b in range(runner.B):
-        need = (int(lens[b]) + runner.bs - 1) // runner.bs
+        need = (int(lens[b]) + extra + runner.bs - 1) // runner.bs
         assert int(nb[b]) == need
     used = int(nb.sum())
     assert int(st.free_hdr[1]) + used == runner.num_blocks
@@ -110,6 +118,50 @@ def test_graph_replay_matches_eager(cuda):
     assert graph.lengths() == eager.lengths()
     for b in range(2):
         assert graph.tokens(b) == eager.tokens(b)
+
+
+def test_chained_steps_match_separate_bookkeeping(cuda):
+    """hs_spec_commit_next (the commit, then the next step's pre-allocation and first
+    draft-step staging in one launch) against hs_spec_commit + hs_spec_prealloc +
+    hs_draft_prepare as separate launches: the same tokens every step, and at the
+    end the same device state once the separate runner has pre-allocated and staged
+    its next step too (llm_engine.py:111-195, model_runner.py:294-310)."""
+    q3, sr = _mods()
+    gt = _small(q3, layers=2)
+    gd = _small(q3, layers=1)
+
+    def make(chain):
+        target = q3.Qwen3Host(gt, device=cuda, seed=31)
+        draft = q3.Qwen3Host(gd, device=cuda, seed=32)
+        r = sr.SpecRunner(target, draft, batch=3, gamma=3, max_model_len=300, block_size=32,
+                          temperature=0.9, mode="reference", device=cuda, chain_steps=chain)
+        r.load_prompts([[3, 4, 5, 6], list(range(200, 262)), [9] * 30])
+        torch.manual_seed(7)
+        r.prefill()
+        return r
+
+    sep, chn = make(False), make(True)
+    for step in range(8):
+        torch.manual_seed(100 + step)
+        sep.step()
+        torch.manual_seed(100 + step)
+        chn.step()
+        print(f"chained step {step}: lengths {chn.lengths()}", flush=True)
+        assert chn.lengths() == sep.lengths()
+        for b in range(3):
+            assert chn.tokens(b) == sep.tokens(b)
+        _check_state(chn)
+        _check_state(sep)
+    hv = _hv()
+    G = sep._g()
+    hv.ops.spec_prealloc(sep.state, G.gamma, out=G.elig)
+    stage = hv.ops.draft_prepare(sep.state, None, 0, lookback=True)
+    torch.cuda.synchronize()
+    for f in sep.state.FIELDS:
+        assert torch.equal(getattr(sep.state, f), getattr(chn.state, f)), f
+    assert torch.equal(G.elig, chn._g().elig)
+    for x, y in zip(stage, chn.d_stage0):
+        assert torch.equal(x, y)
 
 
 def test_filtered_topk_graph_replay_matches_eager(cuda):
