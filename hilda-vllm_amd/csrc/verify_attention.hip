@@ -799,21 +799,71 @@ __device__ __forceinline__ void merge_waves(const float (*s_m)[kAW], const float
 // (b, kvh, qt) (query start qs) and writes its normalised output, dims d0 ..
 // d0 + 7: k_attn_combine's arithmetic, shared with the fused kernel's
 // in-kernel merge so that both give the same bits.
+// Partials read by another workgroup of the same launch (the fused kernel's
+// in-kernel split merge) move with agent-scope atomic stores and loads: the
+// stores write through to the coherent level before the writer's ticket is
+// taken, the loads do not hit a stale line of another XCD's L2, and no
+// fence has to write back or invalidate a whole L2 (an agent-scope fence on
+// this GPU does both, ~17 us per launch measured). Partials merged by a
+// later launch use plain accesses.
+template <bool kCoherent>
+__device__ __forceinline__ void part_store4(float* p, float x, float y, float z, float w) {
+  if constexpr (kCoherent) {
+    __hip_atomic_store(reinterpret_cast<uint64_t*>(p),
+                       (uint64_t)__float_as_uint(x) | ((uint64_t)__float_as_uint(y) << 32),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(reinterpret_cast<uint64_t*>(p + 2),
+                       (uint64_t)__float_as_uint(z) | ((uint64_t)__float_as_uint(w) << 32),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    *reinterpret_cast<float4*>(p) = make_float4(x, y, z, w);
+  }
+}
+template <bool kCoherent>
+__device__ __forceinline__ void part_store2(float* p, float x, float y) {
+  if constexpr (kCoherent)
+    __hip_atomic_store(reinterpret_cast<uint64_t*>(p),
+                       (uint64_t)__float_as_uint(x) | ((uint64_t)__float_as_uint(y) << 32),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else
+    *reinterpret_cast<float2*>(p) = make_float2(x, y);
+}
+template <bool kCoherent>
+__device__ __forceinline__ float2 part_load2(const float* p) {
+  if constexpr (kCoherent) {
+    const uint64_t u = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+    return make_float2(__uint_as_float((uint32_t)u), __uint_as_float((uint32_t)(u >> 32)));
+  } else {
+    return *reinterpret_cast<const float2*>(p);
+  }
+}
+
+// merges the ns key splits of row `row` (query row rr) of one (sequence, kv
+// head, query tile), dims d0 .. d0 + 7, and writes the normalised output
+template <bool kCoherent>
 __device__ __forceinline__ void combine_splits(const AttnArgs& a, int b, int kvh, int qt, int qs,
                                                int ns, int row, int rr, int d0) {
   const int64_t base = (((int64_t)b * a.Hkv + kvh) * a.qtiles + qt) * a.nsplit;
   float M = -INFINITY;
-  for (int s = 0; s < ns; ++s) M = fmaxf(M, a.part_ml[((base + s) * kRows + row) * 2]);
+  for (int s = 0; s < ns; ++s)
+    M = fmaxf(M, part_load2<kCoherent>(a.part_ml + ((base + s) * kRows + row) * 2).x);
   const float Mb = (M == -INFINITY) ? 0.0f : M;
   float L = 0.0f, o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   for (int s = 0; s < ns; ++s) {
     const int64_t pidx = (base + s) * kRows + row;
-    const float f = __builtin_amdgcn_exp2f(a.part_ml[pidx * 2] - Mb);
-    L += a.part_ml[pidx * 2 + 1] * f;
-    const float4 x0 = *reinterpret_cast<const float4*>(a.part_o + pidx * kD + d0);
-    const float4 x1 = *reinterpret_cast<const float4*>(a.part_o + pidx * kD + d0 + 4);
-    o[0] += x0.x * f; o[1] += x0.y * f; o[2] += x0.z * f; o[3] += x0.w * f;
-    o[4] += x1.x * f; o[5] += x1.y * f; o[6] += x1.z * f; o[7] += x1.w * f;
+    const float2 ml = part_load2<kCoherent>(a.part_ml + pidx * 2);
+    const float f = __builtin_amdgcn_exp2f(ml.x - Mb);
+    L += ml.y * f;
+    float x[8];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float2 v = part_load2<kCoherent>(a.part_o + pidx * kD + d0 + 2 * k);
+      x[2 * k] = v.x;
+      x[2 * k + 1] = v.y;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) o[k] += x[k] * f;
   }
   const float inv = (L > 0.0f) ? a.v_scale / L : 0.0f;
   const int oi = rr / a.G, oh = kvh * a.G + rr % a.G;
@@ -882,36 +932,32 @@ __device__ __forceinline__ void merge_tile(const AttnArgs& a, const TileRef& t, 
                                   d0) = ob.u;
       } else {
         const int64_t pidx = pslot * kRows + row;
-        *reinterpret_cast<float4*>(a.part_o + pidx * kD + d0) = make_float4(o[0], o[1], o[2], o[3]);
-        if ((tid & 31) == 0) {
-          a.part_ml[pidx * 2] = M;
-          a.part_ml[pidx * 2 + 1] = L;
-        }
+        part_store4<kSplitMerge>(a.part_o + pidx * kD + d0, o[0], o[1], o[2], o[3]);
+        if ((tid & 31) == 0) part_store2<kSplitMerge>(a.part_ml + pidx * 2, M, L);
       }
     }
   }
   if constexpr (kSplitMerge) {
     if (pslot >= 0) {
-      // in-kernel merge of the ns splits: every thread's partial stores are
-      // made visible at agent scope before the workgroup takes its ticket;
-      // the last workgroup acquires them all and merges
+      // in-kernel merge of the ns splits: every thread's partial stores
+      // (agent-scope, written through) have completed before the workgroup
+      // takes its ticket; the last workgroup reads them all at agent scope
+      // and merges
       __shared__ int s_last;
       unsigned* ticket = a.tickets + (int64_t)t.b * a.Hkv + kvh;
-      __threadfence();
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
       if (tid == 0) {
-        __threadfence();
         const unsigned prev =
             __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_last = prev + 1 == (unsigned)ns;
       }
       __syncthreads();
       if (!s_last) return;
-      __threadfence();
       if (tid == 0) __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       const int row = tid >> 4, rr = r0 + row;
       if (tid < kRows * 16 && rr < rows)
-        combine_splits(a, t.b, kvh, t.qt, qs, ns, row, rr, (tid & 15) * 8);
+        combine_splits<true>(a, t.b, kvh, t.qt, qs, ns, row, rr, (tid & 15) * 8);
     }
   }
 }
@@ -1455,7 +1501,7 @@ __global__ __launch_bounds__(kRows * 16) void k_attn_combine(AttnArgs a) {
   const int row = tid >> 4;
   const int rr = r0 + row;
   if (rr >= rows) return;
-  combine_splits(a, b, kvh, qt, qs, ns, row, rr, (tid & 15) * 8);
+  combine_splits<false>(a, b, kvh, qt, qs, ns, row, rr, (tid & 15) * 8);
 }
 
 template <bool kFp8>
