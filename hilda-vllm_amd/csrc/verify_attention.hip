@@ -329,14 +329,17 @@ struct WaveAcc {
 // one workgroup holds every query row of the (sequence, kv head), so no other
 // workgroup of the split reads these rows.
 // Heads are wave items of 4 rows: the q rows first, then the k rows, then the
-// v rows of the query tokens, each kind from a wave boundary on; wave w takes
-// items w and w + 8 (two rounds cover 16 q rows and 16 tokens). qkv_load
-// issues every load of the wave's rows as soon as the sequence bounds are
-// known, each piece of a head one 16-byte load; the cos/sin row is fetched at
+// v rows of the query tokens, each kind from a wave boundary on; prologue
+// wave p takes items p, p + 4 and p + 8 (three rounds cover 16 q rows and the
+// k and v rows of 16 tokens). qkv_load issues every load of the wave's rows as
+// soon as the sequence bounds are known, each piece of a head one 16-byte
+// load; the cos/sin row is fetched at
 // the position the token holds in its sequence (Lk - Lq + i, clamped into the
 // table) together with positions[], and fetched again in qkv_compute where
 // positions[] says otherwise.
-constexpr int kQkvRounds = 2;
+constexpr int kPW = 4;  // prologue waves of the fused kernel
+constexpr int kQkvRounds = 3;
+constexpr int kQkvT = (kAW + kPW) * 64;  // threads of a fused workgroup
 struct QkvRow {
   int kind;  // 0: q row, 1: k of a token, 2: v of a token, -1: none
   int idx;   // q row of the tile, or query token
@@ -346,7 +349,8 @@ struct QkvLoads {
   QkvRow row[kQkvRounds];
   int64_t pos[kQkvRounds];
   int guess[kQkvRounds], slot[kQkvRounds];
-  uint4 x[kQkvRounds], w[kQkvRounds];
+  uint4 x[kQkvRounds];
+  uint4 wq, wk;  // the lane's pieces of the q and k norm weights
   float c[kQkvRounds][8], sn[kQkvRounds][8];
 };
 
@@ -375,32 +379,37 @@ __device__ __forceinline__ QkvRow qkv_row(const TileRef& t, int nrows, int wi, i
 }
 
 __device__ __forceinline__ void qkv_load(const AttnArgs& a, const QkvArgs& qa, const TileRef& t,
-                                         int kvh, int G, QkvLoads& L) {
+                                         int kvh, int G, int pw, QkvLoads& L) {
   const int lane = threadIdx.x & 63, j = lane & 15;
-  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nrows = t.rows < kRows ? t.rows : kRows;
+  const int items = (nrows + 3) / 4 + 2 * ((t.Lq + 3) / 4);
+  // the norm weights' pieces of this lane, once for every round
+  L.wq = *reinterpret_cast<const uint4*>(qa.qw + 8 * j);
+  L.wk = *reinterpret_cast<const uint4*>(qa.kw + 8 * j);
+  // An item holds rows of one kind, so the round's branches are the wave's;
+  // within an item a lane without a row loads the item's first row, so every
+  // load of the round goes out before the first wait.
 #pragma unroll
   for (int i = 0; i < kQkvRounds; ++i) {
-    QkvRow r = qkv_row(t, nrows, wid + kAW * i, lane);
-    L.slot[i] = -1;
-    if (r.kind >= 0) {
-      const int qi = r.kind == 0 ? r.idx / G : r.idx;
-      r.tok = t.qs + qi;
-      const int head = r.kind == 0 ? kvh * G + r.idx % G
-                                   : qa.Hq + (r.kind == 2 ? a.Hkv : 0) + kvh;
-      L.x[i] = *reinterpret_cast<const uint4*>(qa.qkv + (int64_t)r.tok * qa.ts +
-                                               (int64_t)head * kD + 8 * j);
-      L.pos[i] = qa.positions[r.tok];
-      if (r.kind != 2) {
-        L.w[i] = *reinterpret_cast<const uint4*>((r.kind == 0 ? qa.qw : qa.kw) + 8 * j);
-        int g = t.Lk - t.Lq + qi;
-        g = g < 0 ? 0 : (g >= qa.cs_rows ? qa.cs_rows - 1 : g);
-        L.guess[i] = g;
-        load_rot8(qa.cos_sin + (int64_t)g * kD, j, L.c[i], L.sn[i]);
-      }
-      if (r.kind != 0) L.slot[i] = qa.slots[r.tok];
-    }
+    QkvRow r = qkv_row(t, nrows, pw + kPW * i, lane);
     L.row[i] = r;
+    if (pw + kPW * i >= items) continue;
+    // lane 0 holds the item's first row
+    const int kind = __builtin_amdgcn_readfirstlane(r.kind);
+    const int idx = r.kind < 0 ? 0 : r.idx;
+    const int qi = kind == 0 ? idx / G : idx;
+    const int tok = t.qs + qi;
+    L.row[i].tok = tok;
+    const int head = kind == 0 ? kvh * G + idx % G : qa.Hq + (kind == 2 ? a.Hkv : 0) + kvh;
+    L.x[i] = *reinterpret_cast<const uint4*>(qa.qkv + (int64_t)tok * qa.ts + (int64_t)head * kD + 8 * j);
+    if (kind != 0) L.slot[i] = qa.slots[tok];
+    if (kind != 2) {
+      L.pos[i] = qa.positions[tok];
+      int g = t.Lk - t.Lq + qi;
+      g = g < 0 ? 0 : (g >= qa.cs_rows ? qa.cs_rows - 1 : g);
+      L.guess[i] = g;
+      load_rot8(qa.cos_sin + (int64_t)g * kD, j, L.c[i], L.sn[i]);
+    }
   }
 }
 
@@ -429,6 +438,11 @@ __device__ __forceinline__ void qkv_compute(const AttnArgs& a, const QkvArgs& qa
   constexpr int kRowB = AttnLds<kFp8>::kRowB;
   const int lane = threadIdx.x & 63, j = lane & 15;
   const int knew = t.Lk - t.Lq;
+  // nothing computed from the loaded positions moves above this point (the
+  // compiler would otherwise compare them with the guesses right after the
+  // loads and wait there, before the next round's loads go out)
+#pragma unroll
+  for (int i = 0; i < kQkvRounds; ++i) asm volatile("" : "+v"(L.pos[i]), "+v"(L.guess[i]));
 #pragma unroll
   for (int i = 0; i < kQkvRounds; ++i) {
     S.elem[i] = -1;
@@ -441,7 +455,7 @@ __device__ __forceinline__ void qkv_compute(const AttnArgs& a, const QkvArgs& qa
       if (L.pos[i] != L.guess[i])  // the token sits elsewhere than its key index
         load_rot8(qa.cos_sin + L.pos[i] * kD, j, L.c[i], L.sn[i]);
       uint16_t w[8];
-      unpack8(L.w[i], w);
+      unpack8(r.kind == 0 ? L.wq : L.wk, w);
       float x[8];
 #pragma unroll
       for (int k = 0; k < 8; ++k) x[k] = bf(xh[k]);
@@ -1062,20 +1076,22 @@ __global__ __launch_bounds__(kAT) void k_verify_attn(const int32_t* cu_q, const 
 // and consecutive splits to different XCDs (placement only). Replaces
 // hs_qk_norm_rope_store + hs_verify_attention (+ the split combine) for
 // decode and verify steps.
-// Wave w walks windows w, w + 8, ... of the split as in k_verify_attn (the
-// same keys in the same order: bit-identical outputs). Nothing waits for a
-// workgroup barrier before the first window is in flight: each wave loads the
-// block-table entries of its own windows (lane j: window j) with the sequence
-// bounds and issues its first window as soon as they arrive, then the loads of
-// its q/k-norm + RoPE items. The query tokens' own keys (Lk - Lq .. Lk - 1)
-// are computed here; where every token's cache slot is the one the block table
-// gives its key (the fast case, every decode and verify step of the engine),
-// the windows read those rows from s_new, and the cache stores go out
-// unwaited. Otherwise (a padding slot, a token stored elsewhere) the stores
-// are waited for and a window reaching those keys reads them back from the
-// cache, as the two launches do.
+// Waves 0-7 walk windows w, w + 8, ... of the split as in k_verify_attn (the
+// same keys in the same order: bit-identical outputs); waves 8-11 run the
+// q/k-norm + RoPE prologue. Nothing waits for a workgroup barrier before the
+// first window is in flight: each attention wave loads the block-table
+// entries of its own windows (lane j: window j) with the sequence bounds and
+// issues its first window as soon as they arrive. The prologue waves load and
+// compute the query rows and the query tokens' own keys (Lk - Lq .. Lk - 1)
+// meanwhile; their waits are for their own loads (a wave with window loads
+// into LDS in flight could only wait for all of them). Where every token's
+// cache slot is the one the block table gives its key (the fast case, every
+// decode and verify step of the engine), the windows read those rows from
+// s_new, and the cache stores go out unwaited. Otherwise (a padding slot, a
+// token stored elsewhere) the stores are waited for and a window reaching
+// those keys reads them back from the cache, as the two launches do.
 template <bool kFp8, int kG>
-__global__ __launch_bounds__(kAT) void k_verify_attn_qkv(const int32_t* cu_q, const int32_t* cu_k,
+__global__ __launch_bounds__(kQkvT) void k_verify_attn_qkv(const int32_t* cu_q, const int32_t* cu_k,
                                                          const int32_t* bt, int bt_stride,
                                                          int xcd_shift, int bs_shift,
                                                          int bt_width, int nbt_split, int split_len,
@@ -1088,6 +1104,7 @@ __global__ __launch_bounds__(kAT) void k_verify_attn_qkv(const int32_t* cu_q, co
   __shared__ __attribute__((aligned(16))) uint16_t s_q[kRows * kD];
   // the query tokens' k rows, then their v rows (at most kRows tokens)
   __shared__ __attribute__((aligned(16))) uint8_t s_new[2 * kRows * kRowB];
+  __shared__ int s_fast;
   (void)nbt_split;
   const int G = kG ? kG : a.G;
   const unsigned xm = (1u << xcd_shift) - 1;
@@ -1116,6 +1133,39 @@ __global__ __launch_bounds__(kAT) void k_verify_attn_qkv(const int32_t* cu_q, co
   const int vis = tile_keys(t, G);
   if (vis < hi) hi = vis;
   const int knew = t.Lk - t.Lq;  // first key of the query tokens
+  if (wid >= kAW) {
+    // prologue wave: q/k-norm + RoPE of its rows into s_q and s_new, the
+    // fast-case check (every query token's slot is its key's table entry),
+    // and the cache stores. It has no window loads in flight, so its waits
+    // are for its own loads only. It ends after the barrier: the attention
+    // waves' later barriers count the surviving waves.
+    const int pw = wid - kAW;
+    QkvLoads ql;
+    qkv_load(a, qa, t, kvh, G, pw, ql);
+    const int fi = lane < t.Lq ? lane : t.Lq - 1;
+    const int fkey = knew + fi;
+    const int fbi = key_block(fkey, bs_shift, a.block_size);
+    const int fblk = btrow[fbi < bt_width ? fbi : bt_width - 1];
+    const int fslot = qa.slots[t.qs + fi];
+    // the attention waves issue their first windows after this barrier, so
+    // these loads are ahead of the windows in the CU's memory pipeline
+    lds_barrier();
+    KvStores S;
+    qkv_compute<kFp8>(a, qa, t, kvh, ql, s_q, s_new, S);
+    const bool ok = t.Lq <= kRows && fslot >= 0 && fbi < bt_width && fblk >= 0 &&
+                    fblk < a.num_blocks && fslot == fblk * a.block_size + (fkey - fbi * a.block_size);
+    const bool fast = __builtin_amdgcn_ballot_w64(!ok) == 0;  // the same in every wave
+    if (!fast) {
+      // the stores reach the L2 before any attention wave loads those rows
+      kv_store_all<kFp8>(a, qa, S);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    if (pw == 0 && lane == 0) s_fast = fast ? 1 : 0;
+    lds_barrier();  // s_q, s_new and s_fast written
+    // fast: nothing in this kernel reads the stored rows
+    if (fast) kv_store_all<kFp8>(a, qa, S);
+    return;
+  }
   const int esz = kFp8 ? 1 : 2;
   uint8_t* tile_k = s_kt + wid * kTileB;
   uint8_t* tile_v = s_vt + wid * kTileB;
@@ -1132,10 +1182,10 @@ __global__ __launch_bounds__(kAT) void k_verify_attn_qkv(const int32_t* cu_q, co
     vb = a.vc + off;
     return true;
   };
-  // the first window goes out as soon as the bounds and table entries are in,
-  // then the q/k-norm + RoPE rows' loads, and per lane i < Lq the slot of
-  // query token i and the table entry of its key
+  // the first window goes out as soon as the bounds and table entries are in
+  // and the prologue waves have issued their loads
   const WinOffs<kFp8> wo = win_offs<kFp8>(a, lane);
+  lds_barrier();
   int ws = lo + kWin * wid;
   const uint8_t* kb0 = a.kc;
   const uint8_t* vb0 = a.vc;
@@ -1144,24 +1194,8 @@ __global__ __launch_bounds__(kAT) void k_verify_attn_qkv(const int32_t* cu_q, co
     issue_tile<kFp8>(kb0, ws, hi, tile_k, wo);
     issue_tile<kFp8>(vb0, ws, hi, tile_v, wo);
   }
-  QkvLoads ql;
-  qkv_load(a, qa, t, kvh, G, ql);
-  const int fi = lane < t.Lq ? lane : t.Lq - 1;
-  const int fkey = knew + fi;
-  const int fbi = key_block(fkey, bs_shift, a.block_size);
-  const int fblk = btrow[fbi < bt_width ? fbi : bt_width - 1];
-  const int fslot = qa.slots[t.qs + fi];
-  KvStores S;
-  qkv_compute<kFp8>(a, qa, t, kvh, ql, s_q, s_new, S);
-  const bool ok = t.Lq <= kRows && fslot >= 0 && fbi < bt_width && fblk >= 0 && fblk < a.num_blocks &&
-                  fslot == fblk * a.block_size + (fkey - fbi * a.block_size);
-  const bool fast = __builtin_amdgcn_ballot_w64(!ok) == 0;  // the same in every wave
-  if (!fast) {
-    // the stores reach the L2 before any wave loads those rows
-    kv_store_all<kFp8>(a, qa, S);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  }
-  lds_barrier();  // s_q and s_new written
+  lds_barrier();  // the prologue waves wrote s_q, s_new and s_fast
+  const bool fast = __builtin_amdgcn_readfirstlane(s_fast) != 0;
   if (!fast && have) {
     // the first window was loaded before the stores, which may have written
     // any of its rows: load it again past this CU's L1
@@ -1188,7 +1222,6 @@ __global__ __launch_bounds__(kAT) void k_verify_attn_qkv(const int32_t* cu_q, co
   const int kn = fast ? knew : INT32_MAX;
   const uint8_t* nk = s_new;
   const uint8_t* nv = s_new + kRows * kRowB;
-  const bool stored = !fast;
   // Each window streams its K tile, then its V tile; window j + 1's K goes
   // out as soon as K_j is in registers and its V as soon as V_j is, so the
   // next window's loads overlap this window's scores, softmax and P V. Every
@@ -1221,9 +1254,6 @@ __global__ __launch_bounds__(kAT) void k_verify_attn_qkv(const int32_t* cu_q, co
     have = have_next;
     ws = ws_next;
   }
-  // fast: nothing in this kernel reads the stored rows; they go out after the
-  // key loop, while the waves merge
-  if (!stored) kv_store_all<kFp8>(a, qa, S);
   WaveAcc acc;
   acc.m = m;
   acc.lsum = row4_sum(lsum);
@@ -1532,13 +1562,13 @@ static void launch_attn_qkv(int G, dim3 grid, hipStream_t s, const AttnArgs& a,
   if (nbt > kBtCap) nbt = kBtCap;
   const int sl = a.split_len;
   switch (G) {
-    case 2: hipLaunchKernelGGL((k_verify_attn_qkv<kFp8, 2>), grid, dim3(kAT), 0, s, a.cu_q, a.cu_k, a.bt,
+    case 2: hipLaunchKernelGGL((k_verify_attn_qkv<kFp8, 2>), grid, dim3(kQkvT), 0, s, a.cu_q, a.cu_k, a.bt,
                                  bts, xs, a.bs_shift, a.bt_width, nbt, sl, a, qa); break;
-    case 4: hipLaunchKernelGGL((k_verify_attn_qkv<kFp8, 4>), grid, dim3(kAT), 0, s, a.cu_q, a.cu_k, a.bt,
+    case 4: hipLaunchKernelGGL((k_verify_attn_qkv<kFp8, 4>), grid, dim3(kQkvT), 0, s, a.cu_q, a.cu_k, a.bt,
                                  bts, xs, a.bs_shift, a.bt_width, nbt, sl, a, qa); break;
-    case 8: hipLaunchKernelGGL((k_verify_attn_qkv<kFp8, 8>), grid, dim3(kAT), 0, s, a.cu_q, a.cu_k, a.bt,
+    case 8: hipLaunchKernelGGL((k_verify_attn_qkv<kFp8, 8>), grid, dim3(kQkvT), 0, s, a.cu_q, a.cu_k, a.bt,
                                  bts, xs, a.bs_shift, a.bt_width, nbt, sl, a, qa); break;
-    default: hipLaunchKernelGGL((k_verify_attn_qkv<kFp8, 0>), grid, dim3(kAT), 0, s, a.cu_q, a.cu_k, a.bt,
+    default: hipLaunchKernelGGL((k_verify_attn_qkv<kFp8, 0>), grid, dim3(kQkvT), 0, s, a.cu_q, a.cu_k, a.bt,
                                   bts, xs, a.bs_shift, a.bt_width, nbt, sl, a, qa); break;
   }
 }
