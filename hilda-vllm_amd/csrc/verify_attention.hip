@@ -607,10 +607,14 @@ constexpr float kRefSlack = 8.0f;
 // and P^T = exp2(S^T scale - m) in bf16; mma_pv, O^T += V^T P^T with P^T from
 // registers.
 __device__ __forceinline__ bf16x8_t mma_s(const AttnArgs& a, int ws, int hi, int lim_r, bool r_ok,
-                                          int lane, const bf16x8_t (&ka)[2][4],
+                                          int kfull, int lane, const bf16x8_t (&ka)[2][4],
                                           const bf16x8_t (&qv)[4], float& m, float& lsum,
                                           f32x4_t (&oacc)[8]) {
   const int g = lane >> 4;
+  // keys below kfull are below hi and visible to every row of the tile: a
+  // window of such keys needs no mask (rows past the tile hold zero queries,
+  // finite scores, and are never written out)
+  const bool full = ws + kWin <= kfull;
   f32x4_t st[2];
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
@@ -622,26 +626,38 @@ __device__ __forceinline__ bf16x8_t mma_s(const AttnArgs& a, int ws, int hi, int
   }
   // lane holds row n, keys ws + 8g + 4kb + j (raw scores)
   float sv[8];
-  float mloc = -INFINITY;
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float v = st[kb][j];
-      const int key = ws + 8 * g + 4 * kb + j;
-      if (!r_ok || key >= hi || key > lim_r) v = -INFINITY;
-      sv[kb * 4 + j] = v;
-      mloc = fmaxf(mloc, v);
-    }
+    for (int j = 0; j < 4; ++j) sv[kb * 4 + j] = st[kb][j];
+  if (!full) {
+    // a branch of its own (the empty asm keeps the compiler from computing
+    // the mask for every window and selecting)
+    asm volatile("; masked window");
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int key = ws + 8 * g + 4 * kb + j;
+        if (!r_ok || key >= hi || key > lim_r) sv[kb * 4 + j] = -INFINITY;
+      }
+  }
+  float mloc = -INFINITY;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) mloc = fmaxf(mloc, sv[t]);
   mloc = row4_max(mloc) * a.scale_log2;  // the softmax scale is positive
   const bool up = mloc > m + kRefSlack;
   if (__builtin_amdgcn_ballot_w64(up)) {
     const float m_new = up ? mloc : m;
-    const float alpha = (m_new == m) ? 1.0f : __builtin_amdgcn_exp2f(m - m_new);
-    m = m_new;
-    lsum *= alpha;
+    // a row whose reference is still -inf has seen no key: its sums are exact
+    // zeros and need no rescale (the first window of every wave)
+    if (__builtin_amdgcn_ballot_w64(up && m != -INFINITY)) {
+      const float alpha = (m_new == m) ? 1.0f : __builtin_amdgcn_exp2f(m - m_new);
+      lsum *= alpha;
 #pragma unroll
-    for (int db = 0; db < 8; ++db) oacc[db] *= alpha;
+      for (int db = 0; db < 8; ++db) oacc[db] *= alpha;
+    }
+    m = m_new;
   }
   const float base = (m == -INFINITY) ? 0.0f : m;
   float psum = 0.0f;
@@ -667,10 +683,10 @@ __device__ __forceinline__ void mma_pv(const bf16x8_t (&va)[8], bf16x8_t pb, f32
 }
 
 __device__ __forceinline__ void window_mma(const AttnArgs& a, int ws, int hi, int lim_r, bool r_ok,
-                                           int lane, const bf16x8_t (&ka)[2][4],
+                                           int kfull, int lane, const bf16x8_t (&ka)[2][4],
                                            const bf16x8_t (&va)[8], const bf16x8_t (&qv)[4],
                                            float& m, float& lsum, f32x4_t (&oacc)[8]) {
-  const bf16x8_t pb = mma_s(a, ws, hi, lim_r, r_ok, lane, ka, qv, m, lsum, oacc);
+  const bf16x8_t pb = mma_s(a, ws, hi, lim_r, r_ok, kfull, lane, ka, qv, m, lsum, oacc);
   mma_pv(va, pb, oacc);
 }
 
@@ -701,6 +717,8 @@ __device__ __forceinline__ void wave_walk(const AttnArgs& a, const TileRef& t, i
   const int qi = r_ok ? r / G : 0;
   const int qh = kvh * G + (r_ok ? r % G : 0);
   const int lim_r = Lk - Lq + qi;  // last visible key of this row
+  // keys below kfull: visible to every row of the tile, below hi
+  const int kfull = min(hi, Lk - Lq + r0 / G + 1);
   bf16x8_t qv[4];
 #pragma unroll
   for (int ds = 0; ds < 4; ++ds) {
@@ -764,7 +782,7 @@ __device__ __forceinline__ void wave_walk(const AttnArgs& a, const TileRef& t, i
       have = window_base(ws_next, kb, vb);
       if (have) issue_window<kFp8>(kb, vb, ws_next, hi, tile_k, tile_v, wo);
     }
-    if (cur) window_mma(a, ws, hi, lim_r, r_ok, lane, ka, va, qv, m, lsum, oacc);
+    if (cur) window_mma(a, ws, hi, lim_r, r_ok, kfull, lane, ka, va, qv, m, lsum, oacc);
     ws = ws_next;
   }
   // per-row totals of this wave
@@ -1209,6 +1227,7 @@ __global__ __launch_bounds__(kQkvT) void k_verify_attn_qkv(const int32_t* cu_q, 
   const int r = n;
   const bool r_ok = r < t.rows;
   const int lim_r = knew + (r_ok ? r / G : 0);  // last visible key of this row
+  const int kfull = min(hi, knew + 1);  // keys every row sees, below hi
   bf16x8_t qv[4];
 #pragma unroll
   for (int ds = 0; ds < 4; ++ds)
@@ -1241,7 +1260,7 @@ __global__ __launch_bounds__(kQkvT) void k_verify_attn_qkv(const int32_t* cu_q, 
       // every LDS read of the tile has returned before the next window overwrites it
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       if (load_next) issue_tile<kFp8>(kbn, ws_next, hi, tile_k, wo);
-      const bf16x8_t pb = mma_s(a, ws, hi, lim_r, r_ok, lane, ka, qv, m, lsum, oacc);
+      const bf16x8_t pb = mma_s(a, ws, hi, lim_r, r_ok, kfull, lane, ka, qv, m, lsum, oacc);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       read_v<kFp8, true>(tile_v, nv, ws, kn, t.Lq - 1, lane, va);
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
