@@ -966,12 +966,15 @@ def bookkeeping_probe(torch, hv, context: int = PROBE_CONTEXT - 4, gamma: int = 
     them: hs_verify_prepare at the start of the verify phase and hs_spec_commit_next
     after the acceptance (the commit, then the next step's pre-allocation and first
     draft-step staging), graph-timed together from a sequence of `context` tokens;
-    every replay commits `out_len` tokens (one accepted draft and the resample, the
-    typical outcome). Returns (µs per step, bytes per step): the state words, the
-    staging rows and the committed tokens the launches read and write."""
+    every step commits `out_len` tokens (one accepted draft and the resample, the
+    typical outcome). One graph holds `per_graph` steps, so a replay keeps the GPU
+    busy longer than the host takes to launch the next one. Returns (µs per step,
+    bytes per step): the state words, the staging rows and the committed tokens the
+    launches read and write."""
     dev = torch.device("cuda:0")
     bs = 256
-    end = context + (reps + 2) * out_len + gamma + 2
+    per_graph = 32
+    end = context + (reps + 3) * per_graph * out_len + gamma + 2
     W = (end + bs - 1) // bs + 1
     st = hv.ops.SpecStateTensors(1, W, end + 8, W + 2, bs, -1, dev)
     nblk = (context + bs - 1) // bs
@@ -1001,11 +1004,12 @@ def bookkeeping_probe(torch, hv, context: int = PROBE_CONTEXT - 4, gamma: int = 
               torch.empty(2, dtype=torch.int32, device=dev))
     hv.ops.spec_prealloc(st, gamma, out=elig)  # the step before the first replay
 
-    def step():
-        hv.ops.verify_prepare(st, draft, gamma)
-        hv.ops.spec_commit_next(st, gamma, out, olen, elig, gamma, stage0, lookback=True)
+    def steps():
+        for _ in range(per_graph):
+            hv.ops.verify_prepare(st, draft, gamma)
+            hv.ops.spec_commit_next(st, gamma, out, olen, elig, gamma, stage0, lookback=True)
 
-    us = graph_time_us(torch, dev, step, reps)
+    us = graph_time_us(torch, dev, steps, reps) / per_graph
     R = gamma + 1
     nbytes = (4 * 6 + 4 * W  # prealloc: lengths, counts, free header, table row, ref counts
               + 8 + gamma * 8 + R * (8 + 8 + 4) + 2 * 2 * 4  # prepare: ids, positions, slots, cu

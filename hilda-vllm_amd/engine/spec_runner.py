@@ -87,7 +87,6 @@ class SpecRunner:
         self.top_ps = torch.full((batch,), float(top_p), **f32)
         self.topk_le64 = mode == "filtered" and 1 <= int(top_k) <= 64
         self.tok_scratch = torch.zeros(batch, dtype=torch.int64, device=dev)
-        self.u_res = torch.zeros(batch, **f32)
         self.d_stage = self._stage_bufs(batch)
         self.d_stage0 = self._stage_bufs(2 * batch)
         self.sampler = Sampler()
@@ -112,18 +111,28 @@ class SpecRunner:
         G = self._per_gamma.get(g)
         if G is None:
             dev, B = self.device, self.B
+            # every uniform of a step in one buffer, drawn by one launch at the start
+            # of the draft phase: the draft steps' draws [g, B], the acceptance
+            # uniforms [B, g] and the resample uniforms [B]
+            u_all = torch.zeros(2 * g * B + B, dtype=torch.float32, device=dev)
             G = SimpleNamespace(
                 gamma=g,
                 draft_tokens=torch.zeros((B, g), dtype=torch.int64, device=dev),
                 draft_probs=torch.zeros((B, g, self.V), dtype=torch.float32, device=dev),
-                u_draft=torch.zeros((g, B), dtype=torch.float32, device=dev),
-                u_acc=torch.zeros((B, g), dtype=torch.float32, device=dev),
+                u_all=u_all,
+                u_draft=u_all[:g * B].view(g, B),
+                u_acc=u_all[g * B:2 * g * B].view(B, g),
+                u_res=u_all[2 * g * B:],
                 elig=torch.zeros(B, dtype=torch.int32, device=dev),
                 graphs=None, last=None, graph_last=None, logits=None, graph_logits=None)
             self._per_gamma[g] = G
         return G
 
     # buffers of the current gamma (the fixed-gamma interface)
+    @property
+    def u_res(self):
+        return self._g().u_res
+
     @property
     def draft_tokens(self):
         return self._g().draft_tokens
@@ -346,7 +355,7 @@ class SpecRunner:
         G = self._g()
         if not self._staged:
             ops.spec_prealloc(st, G.gamma, out=G.elig)
-        G.u_draft.uniform_()
+        G.u_all.uniform_()  # this step's draft, acceptance and resample uniforms
         for j in range(G.gamma):
             if j == 0:
                 # two queries: the previous token (fills the draft K/V the last step
@@ -389,10 +398,9 @@ class SpecRunner:
         h = self.target(ids, pos)
         reset_context()
         logits = self.target.compute_logits(h).view(self.B, g + 1, self.V)
-        G.u_acc.uniform_()
-        self.u_res.uniform_()
+        # the uniforms were drawn at the start of the draft phase
         nacc, out, olen = ops.spec_accept(logits, G.draft_probs, G.draft_tokens, self.temps,
-                                          G.u_acc, self.u_res, mode=self.mode,
+                                          G.u_acc, G.u_res, mode=self.mode,
                                           top_ks=self.top_ks, top_ps=self.top_ps,
                                           topk_le64=self.topk_le64)
         if self.chain_steps:
