@@ -962,10 +962,11 @@ def _accept_args(**kw):
 
 def bookkeeping_probe(torch, hv, context: int = PROBE_CONTEXT - 4, gamma: int = 3,
                       out_len: int = 2, reps: int = 20):
-    """The spec step's bookkeeping launches at batch 1, as the fixed-gamma runner makes
-    them: hs_verify_prepare at the start of the verify phase and hs_spec_commit_next
-    after the acceptance (the commit, then the next step's pre-allocation and first
-    draft-step staging), graph-timed together from a sequence of `context` tokens;
+    """The spec step's bookkeeping at batch 1, as the fixed-gamma runner makes it: one
+    hs_spec_commit_next after the acceptance (the commit, then the next step's
+    pre-allocation, first draft-step staging and verify staging; the draft steps
+    write the draft tokens' ids in place), graph-timed from a sequence of `context`
+    tokens;
     every step commits `out_len` tokens (one accepted draft and the resample, the
     typical outcome). One graph holds `per_graph` steps, so a replay keeps the GPU
     busy longer than the host takes to launch the next one. Returns (µs per step,
@@ -1002,17 +1003,21 @@ def bookkeeping_probe(torch, hv, context: int = PROBE_CONTEXT - 4, gamma: int = 
     stage0 = (torch.empty(2, dtype=torch.int64, device=dev), torch.empty(2, dtype=torch.int64, device=dev),
               torch.empty(2, dtype=torch.int32, device=dev), torch.empty(2, dtype=torch.int32, device=dev),
               torch.empty(2, dtype=torch.int32, device=dev))
+    R = gamma + 1
+    vstage = (torch.empty(R, dtype=torch.int64, device=dev), torch.empty(R, dtype=torch.int64, device=dev),
+              torch.empty(R, dtype=torch.int32, device=dev), torch.empty(2, dtype=torch.int32, device=dev),
+              torch.empty(2, dtype=torch.int32, device=dev))
     hv.ops.spec_prealloc(st, gamma, out=elig)  # the step before the first replay
+    vstage[0][1:].copy_(draft[0])  # the draft steps' in-place ids
 
     def steps():
         for _ in range(per_graph):
-            hv.ops.verify_prepare(st, draft, gamma)
-            hv.ops.spec_commit_next(st, gamma, out, olen, elig, gamma, stage0, lookback=True)
+            hv.ops.spec_commit_next(st, gamma, out, olen, elig, gamma, stage0, lookback=True,
+                                    stage_verify=vstage)
 
     us = graph_time_us(torch, dev, steps, reps) / per_graph
-    R = gamma + 1
     nbytes = (4 * 6 + 4 * W  # prealloc: lengths, counts, free header, table row, ref counts
-              + 8 + gamma * 8 + R * (8 + 8 + 4) + 2 * 2 * 4  # prepare: ids, positions, slots, cu
+              + 8 + R * (8 + 4) + 8 + 2 * 2 * 4  # verify staging: last id, positions, slots, cu
               + R * 8 + 4 + out_len * 8 + 4 * 6  # commit: emitted tokens in, tokens appended
               + 2 * (8 + 8 + 4) + 2 * 2 * 4)  # next draft step 0: ids, positions, slots, cu
     return us, nbytes
@@ -1042,10 +1047,10 @@ def inscope_step_probe(torch, hv, attn_roof: dict, layers: int):
             "parts": {"attention": {"launches": layers, "bytes": attn_bytes,
                                     "us": round(attn_us, 2)},
                       "acceptance": {"bytes": acc_bytes, "us": round(acc_us, 2)},
-                      "bookkeeping": {"launches": 2, "bytes": bk_bytes, "us": round(bk_us, 2)}},
+                      "bookkeeping": {"launches": 1, "bytes": bk_bytes, "us": round(bk_us, 2)}},
             "what": f"verify+accept step without the projection weights: {layers} fused "
-                    f"attention launches at L={PROBE_CONTEXT}, the acceptance call, verify staging + "
-                    "commit (with the next step's pre-allocation and draft staging); graph-timed per part"}
+                    f"attention launches at L={PROBE_CONTEXT}, the acceptance call, the commit (with "
+                    "the next step's pre-allocation, draft staging and verify staging); graph-timed per part"}
 
 
 def profiled_traffic(kernel: str, workload: str):

@@ -66,7 +66,7 @@ SIGNATURES.update({
     "hs_spec_commit_workspace_size": (_sz, [_i32, _i32, _i32]),
     "hs_spec_commit": (_i32, [_sp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _sz, _vp]),
     "hs_spec_commit_next": (_i32, [_sp, _i32, _vp, _vp, _vp, _vp, _sz, _i32, _vp, _i32, _vp, _vp,
-                                   _vp, _vp, _vp, _vp]),
+                                   _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "hs_zero_kv_slots": (_i32, [_vp, _i64, _i32, _i64, _i64, _i64, _vp, _i32, _vp]),
     "hs_linear": (_i32, [_vp, _i64, _vp, _i32, _i32, _i32, _i32, _vp, _i64, _vp]),
     "hs_rmsnorm": (_i32, [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _i32, _i32, _f32, _vp]),

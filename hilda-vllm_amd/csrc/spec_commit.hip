@@ -130,11 +130,12 @@ __global__ __launch_bounds__(kCT) void k_prealloc(hs_spec_state s, int gamma, in
 // ---------------------------------------------------------------------------
 // verify staging: model_runner.py:339-362
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kCT) void k_prepare(hs_spec_state s, const int64_t* draft, int gamma,
-                                                 int64_t* input_ids, int64_t* positions,
-                                                 int32_t* slot_mapping, int32_t* cu_q,
-                                                 int32_t* cu_k) {
-  __shared__ int s_w[kCW];
+// draft NULL: the draft tokens' ids (rows 1 .. gamma of each sequence) are
+// left as they are (written in place by the draft steps' sampler)
+__device__ void verify_prepare_body(const hs_spec_state& s, const int64_t* draft, int gamma,
+                                    int64_t* input_ids, int64_t* positions,
+                                    int32_t* slot_mapping, int32_t* cu_q, int32_t* cu_k,
+                                    int* s_w) {
   const int tid = threadIdx.x;
   const int R = gamma + 1;
   int carry = 0;
@@ -146,15 +147,14 @@ __global__ __launch_bounds__(kCT) void k_prepare(hs_spec_state s, const int64_t*
       lk = len + gamma;
       const int nblk = s.num_seq_blocks[b];
       for (int j = 0; j < R; ++j) {
-        const int64_t tok = (j == 0) ? s.tokens[(int64_t)b * s.T + len - 1]
-                                     : draft[(int64_t)b * gamma + j - 1];
         const int pos = len - 1 + j;
         const int bi = pos / s.block_size;
         const int slot = (bi < nblk) ? s.block_tables[(int64_t)b * s.W + bi] * s.block_size +
                                            pos % s.block_size
                                      : -1;
         const int64_t o = (int64_t)b * R + j;
-        input_ids[o] = tok;
+        if (j == 0) input_ids[o] = s.tokens[(int64_t)b * s.T + len - 1];
+        else if (draft) input_ids[o] = draft[(int64_t)b * gamma + j - 1];
         positions[o] = pos;
         slot_mapping[o] = slot;
       }
@@ -169,6 +169,14 @@ __global__ __launch_bounds__(kCT) void k_prepare(hs_spec_state s, const int64_t*
     cu_q[s.B] = s.B * R;
     cu_k[s.B] = carry;
   }
+}
+
+__global__ __launch_bounds__(kCT) void k_prepare(hs_spec_state s, const int64_t* draft, int gamma,
+                                                 int64_t* input_ids, int64_t* positions,
+                                                 int32_t* slot_mapping, int32_t* cu_q,
+                                                 int32_t* cu_k) {
+  __shared__ int s_w[kCW];
+  verify_prepare_body(s, draft, gamma, input_ids, positions, slot_mapping, cu_q, cu_k, s_w);
 }
 
 // draft step staging: model_runner.py:294-310 (step j feeds the previous draft
@@ -387,16 +395,24 @@ __global__ __launch_bounds__(kCT) void k_commit(hs_spec_state s, int gamma, cons
 }
 
 // The commit of a step, then the next step's pre-allocation (into eligible,
-// which the commit has read) and its first draft step's staging, in one
+// which the commit has read), its first draft step's staging and, when v_ids
+// is given, its verify staging without the draft tokens' ids, in one
 // workgroup: the state each part reads is the one the previous part left
 // (their writes are ordered by the workgroup barriers between them).
+struct VerifyStage {
+  int64_t* ids;
+  int64_t* pos;
+  int32_t* slots;
+  int32_t* cu_q;
+  int32_t* cu_k;
+};
 __global__ __launch_bounds__(kCT) void k_commit_next(hs_spec_state s, int gamma,
                                                      const int64_t* out_tokens,
                                                      const int32_t* out_len, int32_t* eligible,
                                                      CommitWs w, int next_gamma, int32_t* status,
                                                      int lookback, int64_t* input_ids,
                                                      int64_t* positions, int32_t* slot_mapping,
-                                                     int32_t* cu_q, int32_t* cu_k) {
+                                                     int32_t* cu_q, int32_t* cu_k, VerifyStage v) {
   __shared__ int s_w[kCW];
   __shared__ int s_tot[2];
   __shared__ PreallocLds L;
@@ -406,6 +422,10 @@ __global__ __launch_bounds__(kCT) void k_commit_next(hs_spec_state s, int gamma,
   __syncthreads();
   draft_prepare_body(s, nullptr, 0, 0, lookback, input_ids, positions, slot_mapping, cu_q, cu_k,
                      s_w);
+  if (v.ids) {
+    __syncthreads();  // s_w is reused
+    verify_prepare_body(s, nullptr, next_gamma, v.ids, v.pos, v.slots, v.cu_q, v.cu_k, s_w);
+  }
 }
 
 // zero the K/V rows of the given slots in every (kv, layer) plane
@@ -505,11 +525,19 @@ int hs_spec_commit_next(const hs_spec_state* state, int gamma, const int64_t* ou
                         const int32_t* out_len, int32_t* eligible, void* workspace,
                         size_t workspace_bytes, int next_gamma, int32_t* status, int lookback,
                         int64_t* input_ids, int64_t* positions, int32_t* slot_mapping,
-                        int32_t* cu_seqlens_q, int32_t* cu_seqlens_k, void* stream) {
+                        int32_t* cu_seqlens_q, int32_t* cu_seqlens_k, int64_t* v_input_ids,
+                        int64_t* v_positions, int32_t* v_slot_mapping, int32_t* v_cu_seqlens_q,
+                        int32_t* v_cu_seqlens_k, void* stream) {
   if (!state_ok(state) || gamma < 0 || next_gamma < 0 || !out_tokens || !out_len ||
       !eligible || !workspace || !input_ids || !positions || !slot_mapping || !cu_seqlens_q ||
       !cu_seqlens_k || (lookback != 0 && lookback != 1))
     return HS_ERR_INVALID;
+  // the verify staging outputs: all or none
+  const int nv = (v_input_ids != nullptr) + (v_positions != nullptr) +
+                 (v_slot_mapping != nullptr) + (v_cu_seqlens_q != nullptr) +
+                 (v_cu_seqlens_k != nullptr);
+  if (nv != 0 && nv != 5) return HS_ERR_INVALID;
+  VerifyStage v{v_input_ids, v_positions, v_slot_mapping, v_cu_seqlens_q, v_cu_seqlens_k};
   if (workspace_bytes < hs_spec_commit_workspace_size(state->B, state->W, state->num_blocks))
     return HS_ERR_WORKSPACE;
   int32_t* p = static_cast<int32_t*>(workspace);
@@ -521,7 +549,7 @@ int hs_spec_commit_next(const hs_spec_state* state, int gamma, const int64_t* ou
   w.seq = w.ev_free + (size_t)state->B * state->W;
   hipLaunchKernelGGL(k_commit_next, dim3(1), dim3(kCT), 0, reinterpret_cast<hipStream_t>(stream),
                      *state, gamma, out_tokens, out_len, eligible, w, next_gamma, status,
-                     lookback, input_ids, positions, slot_mapping, cu_seqlens_q, cu_seqlens_k);
+                     lookback, input_ids, positions, slot_mapping, cu_seqlens_q, cu_seqlens_k, v);
   return hipGetLastError() == hipSuccess ? HS_OK : HS_ERR_LAUNCH;
 }
 

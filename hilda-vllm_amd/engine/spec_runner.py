@@ -100,6 +100,10 @@ class SpecRunner:
             raise ValueError("chained steps need a fixed gamma (the next step's gamma is "
                              "known when the commit runs)")
         self._staged = False
+        # one sequence: the commit also stages the next verify step (all but the
+        # draft tokens' ids, which the draft steps write straight into the verify
+        # input ids), so the verify phase starts with the target forward
+        self._stage_verify = self.chain_steps and batch == 1
         self.history: list[tuple[int, int, int]] = []  # (gamma, accepted, proposed) per step
         self.preempted: list[int] = []  # sequences out of the batch until readmit(), next first
         self.last = None
@@ -115,9 +119,14 @@ class SpecRunner:
             # of the draft phase: the draft steps' draws [g, B], the acceptance
             # uniforms [B, g] and the resample uniforms [B]
             u_all = torch.zeros(2 * g * B + B, dtype=torch.float32, device=dev)
+            v_stage = self._stage_bufs(B * (g + 1))
+            # one sequence: the draft tokens are rows 1 .. g of the verify input ids
+            draft_tokens = (v_stage[0].view(1, g + 1)[:, 1:] if B == 1 else
+                            torch.zeros((B, g), dtype=torch.int64, device=dev))
             G = SimpleNamespace(
                 gamma=g,
-                draft_tokens=torch.zeros((B, g), dtype=torch.int64, device=dev),
+                v_stage=v_stage,
+                draft_tokens=draft_tokens,
                 draft_probs=torch.zeros((B, g, self.V), dtype=torch.float32, device=dev),
                 u_all=u_all,
                 u_draft=u_all[:g * B].view(g, B),
@@ -393,7 +402,10 @@ class SpecRunner:
         st = self.state
         G = self._g()
         g = G.gamma
-        ids, pos, slots, cq, ck = ops.verify_prepare(st, G.draft_tokens, g)
+        if self._staged and self._stage_verify:  # the previous commit staged it
+            ids, pos, slots, cq, ck = G.v_stage
+        else:
+            ids, pos, slots, cq, ck = ops.verify_prepare(st, G.draft_tokens, g, out=G.v_stage)
         set_context(True, cq, ck, g + 1, 0, slots, None, st.block_tables)
         h = self.target(ids, pos)
         reset_context()
@@ -404,7 +416,8 @@ class SpecRunner:
                                           top_ks=self.top_ks, top_ps=self.top_ps,
                                           topk_le64=self.topk_le64)
         if self.chain_steps:
-            ops.spec_commit_next(st, g, out, olen, G.elig, g, self.d_stage0, lookback=True)
+            ops.spec_commit_next(st, g, out, olen, G.elig, g, self.d_stage0, lookback=True,
+                                 stage_verify=G.v_stage if self._stage_verify else None)
             self._staged = True
         else:
             ops.spec_commit(st, g, out, olen, eligible=G.elig)

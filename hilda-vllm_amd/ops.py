@@ -439,24 +439,40 @@ def spec_prealloc(state: SpecStateTensors, gamma: int, out: torch.Tensor | None 
     return elig
 
 
-def verify_prepare(state: SpecStateTensors, draft_tokens: torch.Tensor, gamma: int):
+def verify_prepare(state: SpecStateTensors, draft_tokens: torch.Tensor, gamma: int,
+                   out: tuple | None = None):
     """model_runner.py:339-362 on the device.
 
-    Returns (input_ids, positions, slot_mapping, cu_seqlens_q, cu_seqlens_k)."""
+    Returns (input_ids, positions, slot_mapping, cu_seqlens_q, cu_seqlens_k); `out`
+    may pass preallocated tensors of those shapes (the draft tokens may be a view
+    into out's input_ids: each id is read before it is written)."""
     dev = state.context_lens.device
     B, R = state.B, gamma + 1
-    ids = torch.empty(B * R, dtype=torch.int64, device=dev)
-    pos = torch.empty(B * R, dtype=torch.int64, device=dev)
-    slots = torch.empty(B * R, dtype=torch.int32, device=dev)
-    cq = torch.empty(B + 1, dtype=torch.int32, device=dev)
-    ck = torch.empty(B + 1, dtype=torch.int32, device=dev)
+    if out is None:
+        out = (torch.empty(B * R, dtype=torch.int64, device=dev),
+               torch.empty(B * R, dtype=torch.int64, device=dev),
+               torch.empty(B * R, dtype=torch.int32, device=dev),
+               torch.empty(B + 1, dtype=torch.int32, device=dev),
+               torch.empty(B + 1, dtype=torch.int32, device=dev))
+    _check_verify_stage(state, gamma, out)
+    ids, pos, slots, cq, ck = out
     dt = draft_tokens.to(torch.int64).contiguous() if gamma > 0 else None
     st = state.struct()
     L.check(L.lib().hs_verify_prepare(ctypes_ref(st), None if dt is None else dt.data_ptr(),
                                       int(gamma), ids.data_ptr(), pos.data_ptr(),
                                       slots.data_ptr(), cq.data_ptr(), ck.data_ptr(),
                                       _stream(dev)), "hs_verify_prepare")
-    return ids, pos, slots, cq, ck
+    return out
+
+
+def _check_verify_stage(state: SpecStateTensors, gamma: int, out: tuple) -> None:
+    ids, pos, slots, cq, ck = out
+    B, R = state.B, gamma + 1
+    want = ((ids, B * R, torch.int64), (pos, B * R, torch.int64), (slots, B * R, torch.int32),
+            (cq, B + 1, torch.int32), (ck, B + 1, torch.int32))
+    for t, n, dt in want:
+        if t.numel() != n or t.dtype != dt or not t.is_contiguous():
+            raise ValueError("verify staging tensors do not match the batch and gamma")
 
 
 def spec_commit(state: SpecStateTensors, gamma: int, out_tokens: torch.Tensor,
@@ -488,11 +504,15 @@ def spec_commit(state: SpecStateTensors, gamma: int, out_tokens: torch.Tensor,
 
 def spec_commit_next(state: SpecStateTensors, gamma: int, out_tokens: torch.Tensor,
                      out_len: torch.Tensor, eligible: torch.Tensor, next_gamma: int,
-                     stage0: tuple, lookback: bool = True) -> None:
+                     stage0: tuple, lookback: bool = True,
+                     stage_verify: tuple | None = None) -> None:
     """spec_commit(eligible=eligible) then, in the same launch, the next step's
     spec_prealloc(next_gamma, out=eligible) and draft_prepare(step 0, lookback)
     into the staging tensors `stage0` (ids, positions, slots, cu_q, cu_k):
-    llm_engine.py:146-195 and :111-128, model_runner.py:294-310."""
+    llm_engine.py:146-195 and :111-128, model_runner.py:294-310. With
+    `stage_verify` (verify_prepare's five outputs for next_gamma), also the next
+    step's verify staging (model_runner.py:339-362) except the draft tokens' ids,
+    which the draft steps write in place."""
     dev = state.context_lens.device
     if eligible.dtype != torch.int32 or eligible.numel() != state.B or not eligible.is_contiguous():
         raise ValueError("eligible must be a contiguous int32 [B] tensor")
@@ -501,6 +521,10 @@ def spec_commit_next(state: SpecStateTensors, gamma: int, out_tokens: torch.Tens
     if (ids.numel() != state.B * R or pos.numel() != state.B * R or slots.numel() != state.B * R
             or cq.numel() != state.B + 1 or ck.numel() != state.B + 1):
         raise ValueError("staging tensors do not match the batch")
+    vp = (None,) * 5
+    if stage_verify is not None:
+        _check_verify_stage(state, next_gamma, stage_verify)
+        vp = tuple(t.data_ptr() for t in stage_verify)
     ot = out_tokens.to(torch.int64).contiguous()
     ol = out_len.to(torch.int32).contiguous()
     st = state.struct()
@@ -508,7 +532,7 @@ def spec_commit_next(state: SpecStateTensors, gamma: int, out_tokens: torch.Tens
         ctypes_ref(st), int(gamma), ot.data_ptr(), ol.data_ptr(), eligible.data_ptr(),
         state.commit_ws.data_ptr(), state.commit_ws.numel(), int(next_gamma), None, int(R == 2),
         ids.data_ptr(), pos.data_ptr(), slots.data_ptr(), cq.data_ptr(), ck.data_ptr(),
-        _stream(dev)), "hs_spec_commit_next")
+        *vp, _stream(dev)), "hs_spec_commit_next")
 
 
 def zero_kv_slots(cache: torch.Tensor, slots: torch.Tensor) -> None:

@@ -329,13 +329,19 @@ int hs_spec_commit(const hs_spec_state* state, int gamma, const int32_t* num_acc
 /* the given staging buffers: the end of one speculative step and the        */
 /* start of the next, llm_engine.py:146-195 then :111-128 and                */
 /* model_runner.py:294-310, for callers that know the next step's gamma.     */
+/* v_*: optional (all five or none), the next step's hs_verify_prepare       */
+/* (model_runner.py:339-362) outputs except the ids of the draft tokens      */
+/* (rows 1 .. next_gamma of each sequence, left unwritten for the draft      */
+/* steps to fill in place).                                                  */
 /* No reference counterpart: the reference runs these as separate host       */
-/* steps; here they are one graph node instead of three.                     */
+/* steps; here they are one graph node instead of four.                      */
 int hs_spec_commit_next(const hs_spec_state* state, int gamma, const int64_t* out_tokens,
                         const int32_t* out_len, int32_t* eligible, void* workspace,
                         size_t workspace_bytes, int next_gamma, int32_t* status, int lookback,
                         int64_t* input_ids, int64_t* positions, int32_t* slot_mapping,
-                        int32_t* cu_seqlens_q, int32_t* cu_seqlens_k, void* stream);
+                        int32_t* cu_seqlens_q, int32_t* cu_seqlens_k, int64_t* v_input_ids,
+                        int64_t* v_positions, int32_t* v_slot_mapping, int32_t* v_cu_seqlens_q,
+                        int32_t* v_cu_seqlens_k, void* stream);
 
 /* Zeroes row_bytes at every slot of slots[] (entries < 0 skipped) in each of */
 /* num_planes planes (e.g. the 2*L (K|V, layer) planes of a                  */

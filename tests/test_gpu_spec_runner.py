@@ -120,35 +120,40 @@ def test_graph_replay_matches_eager(cuda):
         assert graph.tokens(b) == eager.tokens(b)
 
 
-def test_chained_steps_match_separate_bookkeeping(cuda):
+@pytest.mark.parametrize("batch", [1, 3])
+def test_chained_steps_match_separate_bookkeeping(cuda, batch):
     """hs_spec_commit_next (the commit, then the next step's pre-allocation and first
-    draft-step staging in one launch) against hs_spec_commit + hs_spec_prealloc +
-    hs_draft_prepare as separate launches: the same tokens every step, and at the
-    end the same device state once the separate runner has pre-allocated and staged
-    its next step too (llm_engine.py:111-195, model_runner.py:294-310)."""
+    draft-step staging in one launch; with one sequence also the next verify staging,
+    the draft tokens written straight into the verify input ids) against
+    hs_spec_commit + hs_spec_prealloc + hs_draft_prepare (+ hs_verify_prepare) as
+    separate launches: the same tokens every step, and at the end the same device
+    state and staging once the separate runner has pre-allocated and staged its next
+    step too (llm_engine.py:111-195, model_runner.py:294-310, 339-362)."""
     q3, sr = _mods()
     gt = _small(q3, layers=2)
     gd = _small(q3, layers=1)
+    prompts = [[3, 4, 5, 6], list(range(200, 262)), [9] * 30][-batch:]
 
     def make(chain):
         target = q3.Qwen3Host(gt, device=cuda, seed=31)
         draft = q3.Qwen3Host(gd, device=cuda, seed=32)
-        r = sr.SpecRunner(target, draft, batch=3, gamma=3, max_model_len=300, block_size=32,
+        r = sr.SpecRunner(target, draft, batch=batch, gamma=3, max_model_len=300, block_size=32,
                           temperature=0.9, mode="reference", device=cuda, chain_steps=chain)
-        r.load_prompts([[3, 4, 5, 6], list(range(200, 262)), [9] * 30])
+        r.load_prompts(prompts)
         torch.manual_seed(7)
         r.prefill()
         return r
 
     sep, chn = make(False), make(True)
+    assert chn._stage_verify == (batch == 1) and not sep._stage_verify
     for step in range(8):
         torch.manual_seed(100 + step)
         sep.step()
         torch.manual_seed(100 + step)
         chn.step()
-        print(f"chained step {step}: lengths {chn.lengths()}", flush=True)
+        print(f"chained step {step} (B={batch}): lengths {chn.lengths()}", flush=True)
         assert chn.lengths() == sep.lengths()
-        for b in range(3):
+        for b in range(batch):
             assert chn.tokens(b) == sep.tokens(b)
         _check_state(chn)
         _check_state(sep)
@@ -156,12 +161,21 @@ def test_chained_steps_match_separate_bookkeeping(cuda):
     G = sep._g()
     hv.ops.spec_prealloc(sep.state, G.gamma, out=G.elig)
     stage = hv.ops.draft_prepare(sep.state, None, 0, lookback=True)
+    vstage = hv.ops.verify_prepare(sep.state, G.draft_tokens, G.gamma)
     torch.cuda.synchronize()
     for f in sep.state.FIELDS:
         assert torch.equal(getattr(sep.state, f), getattr(chn.state, f)), f
     assert torch.equal(G.elig, chn._g().elig)
     for x, y in zip(stage, chn.d_stage0):
         assert torch.equal(x, y)
+    if batch == 1:
+        # the staged verify rows: all but the draft tokens' ids, which the next
+        # draft phase writes
+        R = G.gamma + 1
+        ids, *rest = chn._g().v_stage
+        assert torch.equal(ids[0::R], vstage[0][0::R])
+        for x, y in zip(vstage[1:], rest):
+            assert torch.equal(x, y)
 
 
 def test_filtered_topk_graph_replay_matches_eager(cuda):
