@@ -1212,7 +1212,13 @@ __global__ __launch_bounds__(kQkvT) void k_verify_attn_qkv(const int32_t* cu_q, 
     issue_tile<kFp8>(kb0, ws, hi, tile_k, wo);
     issue_tile<kFp8>(vb0, ws, hi, tile_v, wo);
   }
-  lds_barrier();  // the prologue waves wrote s_q, s_new and s_fast
+  // the prologue waves wrote s_q, s_new and s_fast. A barrier that orders LDS
+  // only: the compiler's LDS release would first wait for this wave's window
+  // loads into LDS, so the barrier would open when the last wave's first window
+  // had landed; here each wave waits for its own window after it (the first
+  // read below and the loop wait for its loads), and the waves whose windows
+  // land first start first.
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   const bool fast = __builtin_amdgcn_readfirstlane(s_fast) != 0;
   if (!fast && have) {
     // the first window was loaded before the stores, which may have written
