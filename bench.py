@@ -621,7 +621,7 @@ def bench_spec(args, torch, hv):
     t0 = time.perf_counter()
     target = q3.Qwen3Host(q3.QWEN3_8B, device=dev, seed=1)
     if args.draft == "forced":
-        draft = q3.Qwen3Host(q3.QWEN3_8B, share_from=target, num_layers=28)
+        draft = q3.Qwen3Host(q3.QWEN3_8B, share_from=target, num_layers=args.draft_layers)
     else:
         draft = q3.Qwen3Host(q3.QWEN3_0_6B, device=dev, seed=2)
     torch.cuda.synchronize()
@@ -733,8 +733,10 @@ def bench_adaptive(args, torch, hv):
     what all sequences need at the end (block pressure: sequences wait for blocks
     until others finish; when none can proceed the longest is preempted and later
     recomputed by prefill, scheduler.py:231-238,313-320). Random-init 8B target /
-    0.6B draft, T=0.6, reference acceptance, gamma from 3 adapted in [1, 7]
-    (llm_engine.py:197-208 with the range of the config)."""
+    0.6B draft (or, with --draft forced, the target's first 28 layers and LM head, so
+    that drafts are accepted often enough for gamma to move up), T=0.6, reference
+    acceptance, gamma from 3 adapted in [1, 7] (llm_engine.py:197-208 with the range
+    of the config)."""
     import importlib as _il
     import numpy as np
     q3 = _il.import_module("hilda-vllm_amd.engine.qwen3_host")
@@ -748,7 +750,10 @@ def bench_adaptive(args, torch, hv):
     need = sum(-(-(ctx + 9) // bs) for _ in range(B))
     num_blocks = max(int(0.75 * need), sum(-(-int(n) // bs) for n in plens) + B)
     target = q3.Qwen3Host(q3.QWEN3_8B, device=dev, seed=1)
-    draft = q3.Qwen3Host(q3.QWEN3_0_6B, device=dev, seed=2)
+    if args.draft == "forced":
+        draft = q3.Qwen3Host(q3.QWEN3_8B, share_from=target, num_layers=args.draft_layers)
+    else:
+        draft = q3.Qwen3Host(q3.QWEN3_0_6B, device=dev, seed=2)
     runner = sr.SpecRunner(target, draft, batch=B, gamma=3, max_model_len=ctx + 16, block_size=bs,
                            kv_cache_dtype="fp8", num_blocks=num_blocks, temperature=0.6,
                            mode="reference", adaptive=True, max_gamma=7, device=dev)
@@ -796,7 +801,9 @@ def bench_adaptive(args, torch, hv):
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16, fp8-e4m3 KV",
             "data": "synthetic (random-init weights, uniform-random prompt ids)",
             "config": {"workload": "config 4: adaptive gamma, FP8 KV, block pressure", "batch": B,
-                       "max_context": ctx, "num_blocks": num_blocks, "blocks_needed_at_end": need},
+                       "max_context": ctx, "num_blocks": num_blocks, "blocks_needed_at_end": need,
+                       "draft": f"target's first {args.draft_layers} layers + LM head"
+                       if args.draft == "forced" else "Qwen3-0.6B"},
             "tokens_emitted": emitted,
             "all_finished": bool(runner.state.finished.all()) and not runner.preempted,
             "preemptions": preemptions, "readmissions": readmitted,
@@ -1202,6 +1209,8 @@ def main(argv=None):
     ap.add_argument("--top-k", type=int, default=0)
     ap.add_argument("--top-p", type=float, default=1.0)
     ap.add_argument("--draft", default="qwen3-0.6b", choices=["qwen3-0.6b", "forced"])
+    ap.add_argument("--draft-layers", type=int, default=28,
+                    help="--draft forced: the target's first N layers (36: the target itself)")
     ap.add_argument("--kv", default="auto", choices=["auto", "fp8"])
     ap.add_argument("--attn-fused", action="store_true",
                     help="attention-b1: the fused launch (hs_qk_norm_rope_attend) of the spec step")
