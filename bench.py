@@ -34,8 +34,8 @@ verify-attention launch the step runs once per layer (hs_qk_norm_rope_attend:
 q/k-norm + RoPE of the 4 qkv rows, their K/V stored, then the attention) at the
 batch-1 verify shape with context 320 (64 prompt + 256 generated tokens);
 roofline_inscope_step is the verify+accept step's own work (36 such launches,
-the acceptance call, the bookkeeping launches) against its bytes, without the
-projection weights; roofline_gemm is the gate/up projection of the target (the
+the acceptance with the step's bookkeeping in one launch) against its bytes,
+without the projection weights; roofline_gemm is the gate/up projection of the target (the
 largest share of the step's kernel time, a weight stream) and roofline_step the
 whole verify phase against the weights it streams. accept and attention: the
 whole call. cpu_baseline times the torch-CPU restatement of the reference loop
@@ -967,22 +967,10 @@ def _accept_args(**kw):
     return ns
 
 
-def bookkeeping_probe(torch, hv, context: int = PROBE_CONTEXT - 4, gamma: int = 3,
-                      out_len: int = 2, reps: int = 20):
-    """The spec step's bookkeeping at batch 1, as the fixed-gamma runner makes it: one
-    hs_spec_commit_next after the acceptance (the commit, then the next step's
-    pre-allocation, first draft-step staging and verify staging; the draft steps
-    write the draft tokens' ids in place), graph-timed from a sequence of `context`
-    tokens;
-    every step commits `out_len` tokens (one accepted draft and the resample, the
-    typical outcome). One graph holds `per_graph` steps, so a replay keeps the GPU
-    busy longer than the host takes to launch the next one. Returns (µs per step,
-    bytes per step): the state words, the staging rows and the committed tokens the
-    launches read and write."""
-    dev = torch.device("cuda:0")
+def _probe_state(torch, hv, dev, context: int, end: int):
+    """A batch-1 sequence of `context` tokens (random ids, never finishing) in a
+    256-token-block state with blocks for `end` tokens free behind it."""
     bs = 256
-    per_graph = 32
-    end = context + (reps + 3) * per_graph * out_len + gamma + 2
     W = (end + bs - 1) // bs + 1
     st = hv.ops.SpecStateTensors(1, W, end + 8, W + 2, bs, -1, dev)
     nblk = (context + bs - 1) // bs
@@ -1002,18 +990,52 @@ def bookkeeping_probe(torch, hv, context: int = PROBE_CONTEXT - 4, gamma: int = 
     ref = torch.zeros(W + 2, dtype=torch.int32)
     ref[:nblk] = 1
     st.ref_count.copy_(ref)
+    return st
+
+
+def _probe_stages(torch, dev, gamma: int):
+    """Staging buffers of the next draft step (look-back: two rows) and the next
+    verify step (gamma + 1 rows) at batch 1."""
+    R = gamma + 1
+    i64 = dict(dtype=torch.int64, device=dev)
+    i32 = dict(dtype=torch.int32, device=dev)
+    stage0 = (torch.empty(2, **i64), torch.empty(2, **i64), torch.empty(2, **i32),
+              torch.empty(2, **i32), torch.empty(2, **i32))
+    vstage = (torch.empty(R, **i64), torch.empty(R, **i64), torch.empty(R, **i32),
+              torch.empty(2, **i32), torch.empty(2, **i32))
+    return stage0, vstage
+
+
+def _bookkeeping_bytes(W: int, gamma: int, out_len: int) -> int:
+    """State words, staging rows and committed tokens one batch-1 step's bookkeeping
+    reads and writes."""
+    R = gamma + 1
+    return (4 * 6 + 4 * W  # prealloc: lengths, counts, free header, table row, ref counts
+            + 8 + R * (8 + 4) + 8 + 2 * 2 * 4  # verify staging: last id, positions, slots, cu
+            + R * 8 + 4 + out_len * 8 + 4 * 6  # commit: emitted tokens in, tokens appended
+            + 2 * (8 + 8 + 4) + 2 * 2 * 4)  # next draft step 0: ids, positions, slots, cu
+
+
+def bookkeeping_probe(torch, hv, context: int = PROBE_CONTEXT - 4, gamma: int = 3,
+                      out_len: int = 2, reps: int = 20):
+    """The spec step's bookkeeping at batch 1 as its own launch: one
+    hs_spec_commit_next after the acceptance (the commit, then the next step's
+    pre-allocation, first draft-step staging and verify staging; the draft steps
+    write the draft tokens' ids in place), as the fixed-gamma runner makes it when
+    the acceptance cannot take it (batch above 1), graph-timed from a sequence of
+    `context` tokens; every step commits `out_len` tokens (one accepted draft and the
+    resample, the typical outcome). One graph holds `per_graph` steps, so a replay
+    keeps the GPU busy longer than the host takes to launch the next one. Returns
+    (µs per step, bytes per step)."""
+    dev = torch.device("cuda:0")
+    per_graph = 32
+    end = context + (reps + 3) * per_graph * out_len + gamma + 2
+    st = _probe_state(torch, hv, dev, context, end)
     elig = torch.empty(1, dtype=torch.int32, device=dev)
     draft = torch.randint(0, V, (1, gamma), dtype=torch.int64, device=dev)
     out = torch.randint(0, V, (1, gamma + 1), dtype=torch.int64, device=dev)
     olen = torch.full((1,), out_len, dtype=torch.int32, device=dev)
-
-    stage0 = (torch.empty(2, dtype=torch.int64, device=dev), torch.empty(2, dtype=torch.int64, device=dev),
-              torch.empty(2, dtype=torch.int32, device=dev), torch.empty(2, dtype=torch.int32, device=dev),
-              torch.empty(2, dtype=torch.int32, device=dev))
-    R = gamma + 1
-    vstage = (torch.empty(R, dtype=torch.int64, device=dev), torch.empty(R, dtype=torch.int64, device=dev),
-              torch.empty(R, dtype=torch.int32, device=dev), torch.empty(2, dtype=torch.int32, device=dev),
-              torch.empty(2, dtype=torch.int32, device=dev))
+    stage0, vstage = _probe_stages(torch, dev, gamma)
     hv.ops.spec_prealloc(st, gamma, out=elig)  # the step before the first replay
     vstage[0][1:].copy_(draft[0])  # the draft steps' in-place ids
 
@@ -1023,41 +1045,87 @@ def bookkeeping_probe(torch, hv, context: int = PROBE_CONTEXT - 4, gamma: int = 
                                     stage_verify=vstage)
 
     us = graph_time_us(torch, dev, steps, reps) / per_graph
-    nbytes = (4 * 6 + 4 * W  # prealloc: lengths, counts, free header, table row, ref counts
-              + 8 + R * (8 + 4) + 8 + 2 * 2 * 4  # verify staging: last id, positions, slots, cu
-              + R * 8 + 4 + out_len * 8 + 4 * 6  # commit: emitted tokens in, tokens appended
-              + 2 * (8 + 8 + 4) + 2 * 2 * 4)  # next draft step 0: ids, positions, slots, cu
-    return us, nbytes
+    return us, _bookkeeping_bytes(st.W, gamma, out_len)
+
+
+def accept_commit_probe(torch, hv, reps: int = 2):
+    """The batch-1 step's acceptance with its bookkeeping, as the fixed-gamma runner
+    makes it: one hs_spec_accept_commit_next per step, a single launch (the
+    workgroup that writes the acceptance outputs commits them, pre-allocates and
+    stages the next step). Inputs are rotated as in bench_accept so that every call
+    reads its rows from HBM; the sequence starts at PROBE_CONTEXT - 4 tokens and
+    grows by the tokens each call emits. Returns (µs per step, bytes per step: the
+    acceptance's rows and the bookkeeping's words, the latter at the typical two
+    emitted tokens, accepted mean)."""
+    dev = torch.device("cuda:0")
+    args = _accept_args()
+    g = args.gamma
+    R = g + 1
+    step_bytes = R * V * 2 + g * V * 4
+    copies = max(2, int(512e6 // step_bytes) + 1)
+    target, q, s = _accept_inputs(torch, hv, dev, args)
+    bufs = [(target.clone(), q.clone()) for _ in range(copies)]
+    del target, q
+    context = PROBE_CONTEXT - 4
+    end = context + copies * (reps + 3) * R + R + 2
+    st = _probe_state(torch, hv, dev, context, end)
+    elig = torch.empty(1, dtype=torch.int32, device=dev)
+    stage0, vstage = _probe_stages(torch, dev, g)
+    hv.ops.spec_prealloc(st, g, out=elig)
+    cn = dict(state=st, eligible=elig, next_gamma=g, stage0=stage0, lookback=True,
+              stage_verify=vstage)
+    outs = []
+
+    def one_round():
+        outs.clear()
+        for i in range(copies):
+            lg, qq = bufs[i]
+            outs.append(hv.ops.spec_accept(lg, qq, s["draft_tokens"], s["temperatures"],
+                                           s["u_accept"], s["u_resample"], commit_next=cn))
+
+    us = graph_time_us(torch, dev, one_round, reps) / copies
+    hv.ops.check_accepted(outs[-1][0], "accept_commit_probe")
+    emitted = float(sum(int(o[2][0]) for o in outs)) / len(outs)
+    return us, step_bytes + _bookkeeping_bytes(st.W, g, 2), round(emitted, 3)
 
 
 def inscope_step_probe(torch, hv, attn_roof: dict, layers: int):
     """The verify+accept step's own work at batch 1, gamma 3, context PROBE_CONTEXT:
     `layers` fused attention launches (q/k-norm + RoPE + KV store + attention, each
-    `attn_roof`'s bytes and graph-timed average), the fused acceptance call (bf16
-    target rows and f32 draft rows, (gamma+1)V*2 + gamma*V*4 bytes; inputs rotated so
-    every call reads HBM) and the bookkeeping launches (bookkeeping_probe). The
-    projection and LM-head weights are left out. achieved = in-scope bytes over the
-    sum of those kernels' graph-timed durations (each including its graph node's
-    dispatch gap, as in the step)."""
+    `attn_roof`'s bytes and graph-timed average), then the acceptance (bf16 target
+    rows and f32 draft rows, (gamma+1)V*2 + gamma*V*4 bytes; inputs rotated so every
+    call reads HBM) with the step's bookkeeping in the same launch
+    (accept_commit_probe). The projection and LM-head weights are left out. achieved
+    = in-scope bytes over the sum of those kernels' graph-timed durations (each
+    including its graph node's dispatch gap, as in the step). The acceptance and the
+    bookkeeping as separate launches are reported beside it."""
     acc = bench_accept(_accept_args(), torch, hv)
     acc_us = acc["value"]
     acc_bytes = acc["roofline"]["bytes_per_step"]
     bk_us, bk_bytes = bookkeeping_probe(torch, hv)
+    ac_us, ac_bytes, emitted = accept_commit_probe(torch, hv)
     attn_us = layers * attn_roof["avg_launch_us"]
     attn_bytes = layers * attn_roof["bytes_per_launch"]
-    nbytes = attn_bytes + acc_bytes + bk_bytes
-    us = attn_us + acc_us + bk_us
+    nbytes = attn_bytes + ac_bytes
+    us = attn_us + ac_us
     achieved = nbytes / (us * 1e-6) / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 5), "bytes_per_step": nbytes,
             "us_per_step": round(us, 2),
             "parts": {"attention": {"launches": layers, "bytes": attn_bytes,
                                     "us": round(attn_us, 2)},
-                      "acceptance": {"bytes": acc_bytes, "us": round(acc_us, 2)},
-                      "bookkeeping": {"launches": 1, "bytes": bk_bytes, "us": round(bk_us, 2)}},
+                      "acceptance_and_bookkeeping": {"launches": 1, "bytes": ac_bytes,
+                                                     "us": round(ac_us, 2),
+                                                     "emitted_mean": emitted},
+                      "as_two_launches": {"acceptance_us": round(acc_us, 2),
+                                          "acceptance_bytes": acc_bytes,
+                                          "bookkeeping_us": round(bk_us, 2),
+                                          "bookkeeping_bytes": bk_bytes}},
             "what": f"verify+accept step without the projection weights: {layers} fused "
-                    f"attention launches at L={PROBE_CONTEXT}, the acceptance call, the commit (with "
-                    "the next step's pre-allocation, draft staging and verify staging); graph-timed per part"}
+                    f"attention launches at L={PROBE_CONTEXT}, then the acceptance with the "
+                    "commit, the next step's pre-allocation, draft staging and verify staging "
+                    "in one launch; graph-timed per part (as_two_launches: the acceptance and "
+                    "the bookkeeping timed as separate launches, not summed)"}
 
 
 def profiled_traffic(kernel: str, workload: str):

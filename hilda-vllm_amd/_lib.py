@@ -59,7 +59,21 @@ class SpecState(ctypes.Structure):
 
 
 _sp = ctypes.POINTER(SpecState)
+
+
+class CommitNextArgs(ctypes.Structure):
+    """Mirror of hs_commit_next_args (include/hilda_spec.h)."""
+    _fields_ = [("state", _sp), ("eligible", _vp), ("workspace", _vp),
+                ("workspace_bytes", ctypes.c_size_t), ("next_gamma", ctypes.c_int32),
+                ("lookback", ctypes.c_int32)] + [(n, _vp) for n in (
+        "status", "input_ids", "positions", "slot_mapping", "cu_seqlens_q", "cu_seqlens_k",
+        "v_input_ids", "v_positions", "v_slot_mapping", "v_cu_seqlens_q", "v_cu_seqlens_k")]
+
+
 SIGNATURES.update({
+    "hs_spec_accept_commit_next": (_i32, [_vp, _i32, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _vp,
+                                          _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp,
+                                          _sz, ctypes.POINTER(CommitNextArgs), _vp]),
     "hs_spec_prealloc": (_i32, [_sp, _i32, _vp, _vp, _vp]),
     "hs_verify_prepare": (_i32, [_sp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
     "hs_draft_prepare": (_i32, [_sp, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),

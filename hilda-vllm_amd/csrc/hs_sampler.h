@@ -172,11 +172,13 @@ int launch_filter(const Problem& P, const Work& W, float* row_stats, bool wave,
                   hipStream_t stream);
 
 // single-launch acceptance (reference mode) for grids that fit one workgroup
-// per CU (spec_accept_small.hip)
+// per CU (spec_accept_small.hip); cn (batch 1 only, else NULL): the step's
+// bookkeeping (hs_bookkeeping.h) run by the workgroup that writes the outputs
+struct CommitNext;
 int small_accept_ok(const Problem& P, const AcceptArgs& A, int mode, int esz);
 template <typename T>
 int launch_accept_small(const Problem& P, const AcceptArgs& A, const Work& W, const SampleOut& O,
-                        hipStream_t stream);
+                        const CommitNext* cn, hipStream_t stream);
 // the same for filtered mode when every sequence's top-k is in [1, kTopkMax]
 int small_topk_ok(const Problem& P, const AcceptArgs& A, int esz);
 // single-launch row sampler (reference mode, a few rows; spec_accept_small.hip)

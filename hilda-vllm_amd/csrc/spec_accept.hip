@@ -29,6 +29,7 @@
 #include <stdint.h>
 #include <string.h>
 
+#include "hs_bookkeeping.h"
 #include "hs_device.h"
 #include "hs_sampler.h"
 #include "hs_sampler_dev.h"
@@ -829,14 +830,17 @@ size_t hs_spec_accept_workspace_size(int batch, int gamma, int vocab) {
   return make_layout(batch, batch * (gamma + 1), nchunk_of(vocab)).total;
 }
 
-int hs_spec_accept(const void* target_logits, int logits_dtype, int64_t logits_row_stride,
-                   const float* draft_probs, int64_t draft_row_stride,
-                   const int64_t* draft_tokens, const float* temperatures,
-                   const int32_t* top_ks, const float* top_ps,
-                   const float* u_accept, const float* u_resample,
-                   int batch, int gamma, int vocab, int mode,
-                   int32_t* num_accepted, int64_t* out_tokens, int32_t* out_len,
-                   float* row_stats, void* workspace, size_t workspace_bytes, void* stream) {
+// hs_spec_accept; with cn, also the step's bookkeeping: in the acceptance's
+// single launch at batch 1 (*fused = 1), else left to the caller (*fused = 0)
+static int accept_impl(const void* target_logits, int logits_dtype, int64_t logits_row_stride,
+                       const float* draft_probs, int64_t draft_row_stride,
+                       const int64_t* draft_tokens, const float* temperatures,
+                       const int32_t* top_ks, const float* top_ps, const float* u_accept,
+                       const float* u_resample, int batch, int gamma, int vocab, int mode,
+                       int32_t* num_accepted, int64_t* out_tokens, int32_t* out_len,
+                       float* row_stats, void* workspace, size_t workspace_bytes,
+                       const CommitNext* cn, int* fused, void* stream) {
+  *fused = 0;
   if (batch <= 0 || gamma <= 0 || gamma > kMaxGamma || vocab <= 0) return HS_ERR_INVALID;
   if (batch > kMaxRows) return HS_ERR_UNSUPPORTED;
   const bool topk_le64 = (mode & HS_ACCEPT_TOPK_LE64) != 0;
@@ -890,8 +894,10 @@ int hs_spec_accept(const void* target_logits, int logits_dtype, int64_t logits_r
   Work W = bind_work(workspace, L);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (!chain_only && small_accept_ok(P, A, mode, logits_dtype == HS_F32 ? 4 : 2)) {
-    if (logits_dtype == HS_F32) return launch_accept_small<float>(P, A, W, O, s);
-    return launch_accept_small<uint16_t>(P, A, W, O, s);
+    const CommitNext* c = (cn && batch == 1) ? cn : nullptr;
+    *fused = c ? 1 : 0;
+    if (logits_dtype == HS_F32) return launch_accept_small<float>(P, A, W, O, c, s);
+    return launch_accept_small<uint16_t>(P, A, W, O, c, s);
   }
   if (!chain_only && topk_le64 && small_topk_ok(P, A, logits_dtype == HS_F32 ? 4 : 2)) {
     if (logits_dtype == HS_F32) return launch_accept_small_topk<float>(P, A, W, O, s);
@@ -899,6 +905,52 @@ int hs_spec_accept(const void* target_logits, int logits_dtype, int64_t logits_r
   }
   if (logits_dtype == HS_F32) return run_sampler_chain<float>(P, A, W, mode, O, s);
   return run_sampler_chain<uint16_t>(P, A, W, mode, O, s);
+}
+
+int hs_spec_accept(const void* target_logits, int logits_dtype, int64_t logits_row_stride,
+                   const float* draft_probs, int64_t draft_row_stride,
+                   const int64_t* draft_tokens, const float* temperatures,
+                   const int32_t* top_ks, const float* top_ps,
+                   const float* u_accept, const float* u_resample,
+                   int batch, int gamma, int vocab, int mode,
+                   int32_t* num_accepted, int64_t* out_tokens, int32_t* out_len,
+                   float* row_stats, void* workspace, size_t workspace_bytes, void* stream) {
+  int fused = 0;
+  return accept_impl(target_logits, logits_dtype, logits_row_stride, draft_probs,
+                     draft_row_stride, draft_tokens, temperatures, top_ks, top_ps, u_accept,
+                     u_resample, batch, gamma, vocab, mode, num_accepted, out_tokens, out_len,
+                     row_stats, workspace, workspace_bytes, nullptr, &fused, stream);
+}
+
+int hs_spec_accept_commit_next(const void* target_logits, int logits_dtype,
+                               int64_t logits_row_stride, const float* draft_probs,
+                               int64_t draft_row_stride, const int64_t* draft_tokens,
+                               const float* temperatures, const int32_t* top_ks,
+                               const float* top_ps, const float* u_accept,
+                               const float* u_resample, int batch, int gamma, int vocab, int mode,
+                               int32_t* num_accepted, int64_t* out_tokens, int32_t* out_len,
+                               float* row_stats, void* workspace, size_t workspace_bytes,
+                               const hs_commit_next_args* next, void* stream) {
+  if (!next || !next->state || next->state->B != batch) return HS_ERR_INVALID;
+  const hs_commit_next_args& n = *next;
+  CommitNext c;
+  int rc = make_commit_next(n.state, gamma, n.eligible, n.workspace, n.workspace_bytes,
+                            n.next_gamma, n.status, n.lookback, n.input_ids, n.positions,
+                            n.slot_mapping, n.cu_seqlens_q, n.cu_seqlens_k, n.v_input_ids,
+                            n.v_positions, n.v_slot_mapping, n.v_cu_seqlens_q, n.v_cu_seqlens_k,
+                            &c);
+  if (rc != HS_OK) return rc;
+  int fused = 0;
+  rc = accept_impl(target_logits, logits_dtype, logits_row_stride, draft_probs, draft_row_stride,
+                   draft_tokens, temperatures, top_ks, top_ps, u_accept, u_resample, batch,
+                   gamma, vocab, mode, num_accepted, out_tokens, out_len, row_stats, workspace,
+                   workspace_bytes, &c, &fused, stream);
+  if (rc != HS_OK || fused) return rc;
+  return hs_spec_commit_next(n.state, gamma, out_tokens, out_len, n.eligible, n.workspace,
+                             n.workspace_bytes, n.next_gamma, n.status, n.lookback, n.input_ids,
+                             n.positions, n.slot_mapping, n.cu_seqlens_q, n.cu_seqlens_k,
+                             n.v_input_ids, n.v_positions, n.v_slot_mapping, n.v_cu_seqlens_q,
+                             n.v_cu_seqlens_k, stream);
 }
 
 size_t hs_sampler_workspace_size(int rows, int vocab) {

@@ -34,7 +34,9 @@
 // error flag is set and the outputs are marked invalid if one runs out).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <string.h>
 
+#include "hs_bookkeeping.h"
 #include "hs_device.h"
 #include "hs_sampler.h"
 #include "hs_sampler_dev.h"
@@ -217,10 +219,13 @@ __device__ __forceinline__ RowDesc fold_row_tagged(const Problem& P, const Work&
 }
 
 // G: drafts per sequence (gamma), a compile-time constant so that the rows
-// live in registers and every load is unconditional
-template <typename T, int G>
+// live in registers and every load is unconditional. kCommit (batch 1): the
+// workgroup that writes the outputs then runs the step's bookkeeping C with
+// them (commit_next_body).
+template <typename T, int G, bool kCommit>
 __global__ __launch_bounds__(SmallShape<G>::kThreads) void k_accept_small(Problem P, AcceptArgs A,
-                                                                          Work W, SampleOut O) {
+                                                                          Work W, SampleOut O,
+                                                                          CommitNext C) {
   using S = SmallShape<G>;
   constexpr int R = S::R, NG = S::NG, RPG = S::RPG, NW = S::NW;
   __shared__ float s_m[NW][RPG];
@@ -235,6 +240,9 @@ __global__ __launch_bounds__(SmallShape<G>::kThreads) void k_accept_small(Proble
   __shared__ int s_use_res;
   __shared__ long long s_tok;
   __shared__ int s_bad;
+  __shared__ int64_t s_otok[R];
+  __shared__ int32_t s_olen;
+  __shared__ B1Plan s_plan[kCommit ? kWave : 1];
 
   const int c = blockIdx.x;
   const int unit = blockIdx.y;
@@ -288,6 +296,14 @@ __global__ __launch_bounds__(SmallShape<G>::kThreads) void k_accept_small(Proble
   // keeps the scheduler from hoisting uses of the small inputs (and their
   // waits) above the row loads
   __builtin_amdgcn_sched_barrier(0);
+  // kCommit: the last wave (idle while the exchanges below are waited for)
+  // reads the bookkeeping's state words and table row now and the second round
+  // before phase B, and plans the commit of the accepted drafts and one more
+  // token while phase C's exchange is waited for; the writer then stores it
+  constexpr int kFW = NW - 1;
+  B1Pre pre{};
+  if constexpr (kCommit)
+    if (wid == kFW) b1_load1(C, pre);
   // logit and draft probability at every draft token (decision inputs, wave
   // 0), then the entry count: this workgroup joins the launch, and the last
   // one to enter advances the epoch for the next launch (every workgroup of
@@ -365,6 +381,9 @@ __global__ __launch_bounds__(SmallShape<G>::kThreads) void k_accept_small(Proble
       }
     }
   }
+
+  if constexpr (kCommit)
+    if (wid == kFW) b1_load2(C, pre);
 
   // ---- phase B: row normalisers, decision, weights of this chunk ----
   if (wid < R) {
@@ -458,6 +477,15 @@ __global__ __launch_bounds__(SmallShape<G>::kThreads) void k_accept_small(Proble
     put_u64(sw + 3, tagged(ptag, (uint32_t)(bp >> 32)));
   }
 
+  // (the plan waits in LDS, one entry per lane of the wave)
+  if constexpr (kCommit) {
+    if (wid == kFW) {
+      B1Plan q;
+      b1_plan(C, pre, r + 1, s_dt, q);
+      s_plan[lane] = q;
+    }
+  }
+
   // ---- phase C: chunk of the inverse-CDF point, token in its owner ----
   if (wid == 0) {
     uint64_t cw[4], cp[4];
@@ -546,10 +574,21 @@ __global__ __launch_bounds__(SmallShape<G>::kThreads) void k_accept_small(Proble
     else v = -1;
     __hip_atomic_store(&A.tok_out[(int64_t)unit * R + tid], v, __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
+    if constexpr (kCommit) s_otok[tid] = v;
   }
   if (tid == 0) {
     __hip_atomic_store(&A.len_out[unit], r + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_store(&A.nacc_out[unit], r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if constexpr (kCommit) s_olen = r + 1;
+  }
+  if constexpr (kCommit) {
+    // the step's bookkeeping, from the outputs just written (this is the
+    // only workgroup that reaches here: one unit, one writer)
+    __shared__ CommitNextLds<S::kThreads> s_cn;
+    __syncthreads();
+    B1Plan q{};
+    if (wid == kFW) q = s_plan[lane];
+    commit_next_planned<S::kThreads>(C, q, kFW, s_otok, &s_olen, s_cn);
   }
 }
 
@@ -1463,13 +1502,21 @@ int small_accept_ok(const Problem& P, const AcceptArgs& A, int mode, int esz) {
 
 template <typename T>
 int launch_accept_small(const Problem& P, const AcceptArgs& A, const Work& W, const SampleOut& O,
-                        hipStream_t stream) {
+                        const CommitNext* cn, hipStream_t stream) {
+  if (cn && P.units != 1) return HS_ERR_UNSUPPORTED;
+  CommitNext C;
+  if (cn) C = *cn;
+  else memset(&C, 0, sizeof(C));
   const dim3 grid(P.nchunk, P.units);
   switch (A.gamma) {
-#define HS_SMALL_CASE(G)                                                               \
-  case G:                                                                              \
-    hipLaunchKernelGGL((k_accept_small<T, G>), grid, dim3(SmallShape<G>::kThreads), 0, \
-                       stream, P, A, W, O);                                            \
+#define HS_SMALL_CASE(G)                                                                      \
+  case G:                                                                                     \
+    if (cn)                                                                                   \
+      hipLaunchKernelGGL((k_accept_small<T, G, true>), grid, dim3(SmallShape<G>::kThreads), 0, \
+                         stream, P, A, W, O, C);                                              \
+    else                                                                                      \
+      hipLaunchKernelGGL((k_accept_small<T, G, false>), grid, dim3(SmallShape<G>::kThreads),  \
+                         0, stream, P, A, W, O, C);                                           \
     break;
     HS_SMALL_CASE(1)
     HS_SMALL_CASE(2)
@@ -1551,12 +1598,12 @@ template int launch_sample_small<uint16_t>(const Problem&, const Work&, const Sa
                                            hipStream_t);
 
 template int launch_accept_small<float>(const Problem&, const AcceptArgs&, const Work&,
-                                        const SampleOut&, hipStream_t);
+                                        const SampleOut&, const CommitNext*, hipStream_t);
 template int launch_accept_small_topk<float>(const Problem&, const AcceptArgs&, const Work&,
                                              const SampleOut&, hipStream_t);
 template int launch_accept_small_topk<uint16_t>(const Problem&, const AcceptArgs&, const Work&,
                                                 const SampleOut&, hipStream_t);
 template int launch_accept_small<uint16_t>(const Problem&, const AcceptArgs&, const Work&,
-                                           const SampleOut&, hipStream_t);
+                                           const SampleOut&, const CommitNext*, hipStream_t);
 
 }  // namespace hs

@@ -410,14 +410,17 @@ class SpecRunner:
         h = self.target(ids, pos)
         reset_context()
         logits = self.target.compute_logits(h).view(self.B, g + 1, self.V)
-        # the uniforms were drawn at the start of the draft phase
+        # the uniforms were drawn at the start of the draft phase; chained steps
+        # run this step's bookkeeping with the acceptance (one launch at batch 1)
+        cn = None
+        if self.chain_steps:
+            cn = dict(state=st, eligible=G.elig, next_gamma=g, stage0=self.d_stage0,
+                      lookback=True, stage_verify=G.v_stage if self._stage_verify else None)
         nacc, out, olen = ops.spec_accept(logits, G.draft_probs, G.draft_tokens, self.temps,
                                           G.u_acc, G.u_res, mode=self.mode,
                                           top_ks=self.top_ks, top_ps=self.top_ps,
-                                          topk_le64=self.topk_le64)
+                                          topk_le64=self.topk_le64, commit_next=cn)
         if self.chain_steps:
-            ops.spec_commit_next(st, g, out, olen, G.elig, g, self.d_stage0, lookback=True,
-                                 stage_verify=G.v_stage if self._stage_verify else None)
             self._staged = True
         else:
             ops.spec_commit(st, g, out, olen, eligible=G.elig)

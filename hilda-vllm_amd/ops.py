@@ -92,8 +92,16 @@ def spec_accept(target_logits: torch.Tensor, draft_probs: torch.Tensor | None,
                 u_accept: torch.Tensor | None, u_resample: torch.Tensor | None, *,
                 mode="reference", top_ks: torch.Tensor | None = None,
                 top_ps: torch.Tensor | None = None, row_stats: bool = False,
-                topk_le64: bool = False, chain_only: bool = False):
+                topk_le64: bool = False, chain_only: bool = False,
+                commit_next: dict | None = None):
     """Fused acceptance sampler (drop-in for model_runner.py:387-428).
+
+    commit_next: spec_commit_next's arguments after out_len, as a dict (state,
+    eligible, next_gamma, stage0, and optionally lookback, stage_verify): the
+    call then also runs that bookkeeping on this step's outputs
+    (hs_spec_accept_commit_next). At batch 1 with the single-launch kernel it
+    runs inside the acceptance launch; if that launch's bounded waits fail, the
+    bookkeeping does not run (num_accepted -1 as below).
 
     topk_le64 (filtered mode): the caller knows every entry of top_ks is in
     [1, 64]; small batches then run as one launch. A sequence breaking that
@@ -156,17 +164,25 @@ def spec_accept(target_logits: torch.Tensor, draft_probs: torch.Tensor | None,
     def p(t):
         return None if t is None else t.data_ptr()
 
-    rc = lib.hs_spec_accept(p(lg), _logit_dtype(lg), lstride, p(q), qstride, p(dt),
-                            p(temperatures) if m != L.HS_ACCEPT_GREEDY else None,
-                            p(top_ks) if m == L.HS_ACCEPT_FILTERED else None,
-                            p(top_ps) if m == L.HS_ACCEPT_FILTERED else None,
-                            p(u_accept) if m != L.HS_ACCEPT_GREEDY else None,
-                            p(u_resample) if m != L.HS_ACCEPT_GREEDY else None,
-                            B, gamma, V, m | (L.HS_ACCEPT_TOPK_LE64 if topk_le64 else 0)
-                            | (L.HS_ACCEPT_CHAIN if chain_only else 0),
-                            p(nacc), p(out), p(olen), p(stats), ws.data_ptr(),
-                            ws.numel(), _stream(dev))
-    L.check(rc, "hs_spec_accept")
+    args = (p(lg), _logit_dtype(lg), lstride, p(q), qstride, p(dt),
+            p(temperatures) if m != L.HS_ACCEPT_GREEDY else None,
+            p(top_ks) if m == L.HS_ACCEPT_FILTERED else None,
+            p(top_ps) if m == L.HS_ACCEPT_FILTERED else None,
+            p(u_accept) if m != L.HS_ACCEPT_GREEDY else None,
+            p(u_resample) if m != L.HS_ACCEPT_GREEDY else None,
+            B, gamma, V, m | (L.HS_ACCEPT_TOPK_LE64 if topk_le64 else 0)
+            | (L.HS_ACCEPT_CHAIN if chain_only else 0),
+            p(nacc), p(out), p(olen), p(stats), ws.data_ptr(), ws.numel())
+    if commit_next is None:
+        L.check(lib.hs_spec_accept(*args, _stream(dev)), "hs_spec_accept")
+    else:
+        cn = dict(commit_next)
+        if cn["state"].B != B:
+            raise ValueError("commit_next state does not match the batch")
+        na, keep = _commit_next_args(gamma=gamma, **cn)
+        L.check(lib.hs_spec_accept_commit_next(*args, ctypes_ref(na), _stream(dev)),
+                "hs_spec_accept_commit_next")
+        del keep
     if row_stats:
         return nacc, out, olen, stats
     return nacc, out, olen
@@ -514,6 +530,25 @@ def spec_commit_next(state: SpecStateTensors, gamma: int, out_tokens: torch.Tens
     step's verify staging (model_runner.py:339-362) except the draft tokens' ids,
     which the draft steps write in place."""
     dev = state.context_lens.device
+    na, keep = _commit_next_args(state, gamma, eligible, next_gamma, stage0, lookback,
+                                 stage_verify)
+    ot = out_tokens.to(torch.int64).contiguous()
+    ol = out_len.to(torch.int32).contiguous()
+    L.check(L.lib().hs_spec_commit_next(
+        na.state, int(gamma), ot.data_ptr(), ol.data_ptr(), na.eligible, na.workspace,
+        na.workspace_bytes, na.next_gamma, na.status, na.lookback, na.input_ids, na.positions,
+        na.slot_mapping, na.cu_seqlens_q, na.cu_seqlens_k, na.v_input_ids, na.v_positions,
+        na.v_slot_mapping, na.v_cu_seqlens_q, na.v_cu_seqlens_k, _stream(dev)),
+        "hs_spec_commit_next")
+    del keep
+
+
+def _commit_next_args(state: SpecStateTensors, gamma: int, eligible: torch.Tensor,
+                      next_gamma: int, stage0: tuple, lookback: bool = True,
+                      stage_verify: tuple | None = None):
+    """Checks spec_commit_next's arguments and packs them as hs_commit_next_args;
+    returns it and the objects its pointers refer to (keep them alive for the call)."""
+    import ctypes
     if eligible.dtype != torch.int32 or eligible.numel() != state.B or not eligible.is_contiguous():
         raise ValueError("eligible must be a contiguous int32 [B] tensor")
     R = 2 if lookback else 1
@@ -525,14 +560,12 @@ def spec_commit_next(state: SpecStateTensors, gamma: int, out_tokens: torch.Tens
     if stage_verify is not None:
         _check_verify_stage(state, next_gamma, stage_verify)
         vp = tuple(t.data_ptr() for t in stage_verify)
-    ot = out_tokens.to(torch.int64).contiguous()
-    ol = out_len.to(torch.int32).contiguous()
     st = state.struct()
-    L.check(L.lib().hs_spec_commit_next(
-        ctypes_ref(st), int(gamma), ot.data_ptr(), ol.data_ptr(), eligible.data_ptr(),
-        state.commit_ws.data_ptr(), state.commit_ws.numel(), int(next_gamma), None, int(R == 2),
-        ids.data_ptr(), pos.data_ptr(), slots.data_ptr(), cq.data_ptr(), ck.data_ptr(),
-        *vp, _stream(dev)), "hs_spec_commit_next")
+    na = L.CommitNextArgs(ctypes.pointer(st), eligible.data_ptr(), state.commit_ws.data_ptr(),
+                          state.commit_ws.numel(), int(next_gamma), int(R == 2), None,
+                          ids.data_ptr(), pos.data_ptr(), slots.data_ptr(), cq.data_ptr(),
+                          ck.data_ptr(), *vp)
+    return na, (st,)
 
 
 def zero_kv_slots(cache: torch.Tensor, slots: torch.Tensor) -> None:

@@ -343,6 +343,52 @@ int hs_spec_commit_next(const hs_spec_state* state, int gamma, const int64_t* ou
                         int64_t* v_positions, int32_t* v_slot_mapping, int32_t* v_cu_seqlens_q,
                         int32_t* v_cu_seqlens_k, void* stream);
 
+/* The bookkeeping half of hs_spec_accept_commit_next: hs_spec_commit_next's  */
+/* arguments after out_len, with the same meaning (state->B = batch).         */
+typedef struct hs_commit_next_args {
+  const hs_spec_state* state;
+  int32_t* eligible;
+  void* workspace;
+  size_t workspace_bytes;
+  int32_t next_gamma;
+  int32_t lookback;
+  int32_t* status;
+  int64_t* input_ids;
+  int64_t* positions;
+  int32_t* slot_mapping;
+  int32_t* cu_seqlens_q;
+  int32_t* cu_seqlens_k;
+  int64_t* v_input_ids;
+  int64_t* v_positions;
+  int32_t* v_slot_mapping;
+  int32_t* v_cu_seqlens_q;
+  int32_t* v_cu_seqlens_k;
+} hs_commit_next_args;
+
+/* hs_spec_accept, then hs_spec_commit_next(next->state, gamma, out_tokens,  */
+/* out_len, next->...) on the same stream: a speculative step's acceptance   */
+/* (model_runner.py:387-428), commit and rollback (llm_engine.py:146-195),   */
+/* the next step's pre-allocation (:111-128) and its staging                 */
+/* (model_runner.py:294-310, :339-362). With batch 1 and the acceptance's    */
+/* single launch (reference mode, the conditions under hs_spec_accept), the  */
+/* workgroup that writes the acceptance outputs runs the bookkeeping after   */
+/* them: one launch in all. If that launch's bounded waits fail, the         */
+/* sequence gets num_accepted -1 as in hs_spec_accept and the bookkeeping    */
+/* does not run (state, eligible and staging keep their values; the two      */
+/* launches would commit no token and stage the next step). Otherwise the    */
+/* results are those of the two calls.                                       */
+/* No reference counterpart: the reference runs acceptance and bookkeeping   */
+/* as separate host steps; here a batch-1 step's are one graph node.         */
+int hs_spec_accept_commit_next(const void* target_logits, int logits_dtype,
+                               int64_t logits_row_stride, const float* draft_probs,
+                               int64_t draft_row_stride, const int64_t* draft_tokens,
+                               const float* temperatures, const int32_t* top_ks,
+                               const float* top_ps, const float* u_accept,
+                               const float* u_resample, int batch, int gamma, int vocab, int mode,
+                               int32_t* num_accepted, int64_t* out_tokens, int32_t* out_len,
+                               float* row_stats, void* workspace, size_t workspace_bytes,
+                               const hs_commit_next_args* next, void* stream);
+
 /* Zeroes row_bytes at every slot of slots[] (entries < 0 skipped) in each of */
 /* num_planes planes (e.g. the 2*L (K|V, layer) planes of a                  */
 /* [2, L, num_blocks, block_size, H, D] cache): byte offset                  */
