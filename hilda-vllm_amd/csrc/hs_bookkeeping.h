@@ -596,7 +596,7 @@ __device__ void b1_plan(const CommitNext& c, const B1Pre& P, int n, const int64_
   const int h = dpos >= 0 ? dpos : 0;  // at least len0 - 1 for lanes below R0
   const int jt = h - len0;             // index among the appended tokens
   Q.dlast = jt >= n - 1;
-  Q.dtok = jt < 0 ? P.hist : toks[jt < n - 1 ? jt : 0];
+  Q.dtok = jt < 0 ? P.hist : toks[(jt >= 0 && jt < n - 1) ? jt : 0];
   Q.dpos = dpos;
   Q.dsl = slot_of(dpos);
   Q.vpos = len - 1 + lane;
