@@ -420,6 +420,9 @@ __global__ __launch_bounds__(SmallShape<G>::kThreads) void k_accept_small(Proble
   const bool residual = (s_kind == kKindResidual);
   const bool mine = grp == r % NG;  // this group holds row r
   uint64_t w[8], pw[8];
+  // this thread's residual / plain weight sums, then its first offsets within
+  // the chunk (mine)
+  uint64_t lo_w = 0, lo_p = 0;
   if (mine) {
     const RowDesc D = s_desc[r];
     const float rS = 1.0f / D.s;
@@ -458,6 +461,8 @@ __global__ __launch_bounds__(SmallShape<G>::kThreads) void k_accept_small(Proble
       tw += w[k];
       tp += pw[k];
     }
+    lo_w = tw;
+    lo_p = tp;
     tw = wave_sum_u64(tw);
     tp = wave_sum_u64(tp);
     if (lane == 0) {
@@ -477,6 +482,19 @@ __global__ __launch_bounds__(SmallShape<G>::kThreads) void k_accept_small(Proble
     put_u64(sw + 3, tagged(ptag, (uint32_t)(bp >> 32)));
   }
 
+  // each thread's offsets within the chunk for the token search of the chunk's
+  // owner (known only after the exchange below), from the wave scans and the
+  // earlier waves' sums, once this chunk's sums are published
+  if (mine) {
+    const uint64_t iw = wave_incl_scan_u64(lo_w, lane), ip = wave_incl_scan_u64(lo_p, lane);
+    uint64_t ow = iw - lo_w, op = ip - lo_p;
+    for (int ww = 0; ww < gw; ++ww) {
+      ow += s_e[ww][0];
+      op += s_e[4 + ww][0];
+    }
+    lo_w = ow;
+    lo_p = op;
+  }
   // (the plan waits in LDS, one entry per lane of the wave)
   if constexpr (kCommit) {
     if (wid == kFW) {
@@ -534,29 +552,17 @@ __global__ __launch_bounds__(SmallShape<G>::kThreads) void k_accept_small(Proble
   const int cstar = s_cstar;
   if (cstar != c && !(cstar < 0 && c == 0)) return;  // one writer per unit
   if (cstar == c) {
+    // the element whose weight range [acc, acc + weight) holds trel (zero
+    // weights hold nothing): one in the chunk
     const uint64_t trel = s_trel;
     const bool use_res = s_use_res != 0;
-    uint64_t sv = 0, incl = 0;
     if (mine) {
+      uint64_t acc = use_res ? lo_w : lo_p;
 #pragma unroll
-      for (int k = 0; k < 8; ++k) sv += use_res ? w[k] : pw[k];
-      incl = wave_incl_scan_u64(sv, lane);
-      if (lane == 63) s_e[gw][0] = incl;
-    }
-    __syncthreads();
-    if (mine) {
-      uint64_t off = 0;
-      for (int ww = 0; ww < gw; ++ww) off += s_e[ww][0];
-      const uint64_t lo = off + incl - sv;
-      if (lo <= trel && trel < off + incl) {
-        uint64_t acc = lo;
-        for (int k = 0; k < 8; ++k) {
-          acc += use_res ? w[k] : pw[k];
-          if (acc > trel) {
-            s_tok = (long long)(i0 + k);
-            break;
-          }
-        }
+      for (int k = 0; k < 8; ++k) {
+        const uint64_t v = use_res ? w[k] : pw[k];
+        if (acc <= trel && trel < acc + v) s_tok = (long long)(i0 + k);
+        acc += v;
       }
     }
     __syncthreads();
@@ -1403,6 +1409,7 @@ __global__ __launch_bounds__(kChunkThreads) void k_sample_small(Problem P, Work 
     *reinterpret_cast<float4*>(pp + 4) = make_float4(pr[4], pr[5], pr[6], pr[7]);
   }
   if (!O.sample) return;
+  uint64_t lo = tp;  // this thread's sum, then its first offset within the chunk
   tp = wave_sum_u64(tp);
   if (lane == 0) s_e[wid] = tp;
   __syncthreads();
@@ -1412,6 +1419,15 @@ __global__ __launch_bounds__(kChunkThreads) void k_sample_small(Problem P, Work 
     uint64_t* sw = samp_words(W, P.units, row, P.nchunk) + c * 2;
     put_u64(sw, tagged(ptag, (uint32_t)bp));
     put_u64(sw + 1, tagged(ptag, (uint32_t)(bp >> 32)));
+  }
+
+  // this thread's offset within the chunk for the owner's token search (known
+  // only after the exchange below), once the chunk's sum is published
+  {
+    const uint64_t ip = wave_incl_scan_u64(lo, lane);
+    uint64_t o = ip - lo;
+    for (int ww = 0; ww < wid; ++ww) o += s_e[ww];
+    lo = o;
   }
 
   // ---- phase C: chunk of the inverse-CDF point, token in its owner ----
@@ -1453,25 +1469,13 @@ __global__ __launch_bounds__(kChunkThreads) void k_sample_small(Problem P, Work 
   const int cstar = s_cstar;
   if (cstar != c && !(cstar < 0 && c == 0)) return;  // one writer per row
   if (cstar == c) {
+    // the element whose weight range [acc, acc + weight) holds trel
     const uint64_t trel = s_trel;
-    uint64_t sv = 0;
+    uint64_t acc = lo;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) sv += pw[k];
-    const uint64_t incl = wave_incl_scan_u64(sv, lane);
-    if (lane == 63) s_e[wid] = incl;
-    __syncthreads();
-    uint64_t off = 0;
-    for (int ww = 0; ww < wid; ++ww) off += s_e[ww];
-    const uint64_t lo = off + incl - sv;
-    if (lo <= trel && trel < off + incl) {
-      uint64_t acc = lo;
-      for (int k = 0; k < 8; ++k) {
-        acc += pw[k];
-        if (acc > trel) {
-          s_tok = (long long)(i0 + k);
-          break;
-        }
-      }
+    for (int k = 0; k < 8; ++k) {
+      if (acc <= trel && trel < acc + pw[k]) s_tok = (long long)(i0 + k);
+      acc += pw[k];
     }
     __syncthreads();
   }
