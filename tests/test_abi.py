@@ -69,6 +69,35 @@ def test_spec_accept_rejects_bad_arguments_on_host(hv):
     del common
 
 
+def test_accept_commit_next_rejects_bad_arguments_on_host(hv):
+    """hs_spec_accept_commit_next checks the bookkeeping arguments as
+    hs_spec_commit_next does, then the acceptance's as hs_spec_accept does, before
+    any launch."""
+    L = hv._lib
+    lib = L.lib()
+    buf = ctypes.create_string_buffer(4096)
+    p = ctypes.cast(buf, ctypes.c_void_p).value
+    st = L.SpecState(*([p] * 11), 1, 4, 64, 8, 16, 0, 2)  # B=1, W=4, T=64, 8 blocks of 16
+
+    def args(lookback=1, elig=p, ws_bytes=1 << 20, vids=None, next_gamma=3):
+        return L.CommitNextArgs(ctypes.pointer(st), elig, p, ws_bytes, next_gamma, lookback, None,
+                                p, p, p, p, p, vids, None, None, None, None)
+
+    def call(na, B=1, g=3):
+        return lib.hs_spec_accept_commit_next(p, 1, 100, p, 100, p, p, p, p, p, p, B, g, 100, 0,
+                                              p, p, p, None, p, 1 << 20,
+                                              None if na is None else ctypes.byref(na), None)
+
+    assert call(None) == -1  # no bookkeeping arguments
+    assert call(args(), B=2) == -1  # a state of another batch
+    assert call(args(lookback=2)) == -1
+    assert call(args(elig=None)) == -1
+    assert call(args(next_gamma=-1)) == -1
+    assert call(args(vids=p)) == -1  # the verify staging outputs: all five or none
+    assert call(args(ws_bytes=8)) == -2
+    assert call(args(), g=0) == -1  # the acceptance's own checks
+
+
 def test_sampler_rejects_bad_arguments_on_host(hv):
     lib = hv._lib.lib()
     buf = ctypes.create_string_buffer(64)
