@@ -55,7 +55,7 @@ class SpecState(ctypes.Structure):
         "num_seq_blocks", "tokens", "free_ring", "free_hdr", "ref_count")] + [
         ("B", ctypes.c_int32), ("W", ctypes.c_int32), ("T", ctypes.c_int32),
         ("num_blocks", ctypes.c_int32), ("block_size", ctypes.c_int32), ("pad", ctypes.c_int32),
-        ("eos", ctypes.c_int64)]
+        ("eos", ctypes.c_int64), ("block_hash", ctypes.c_void_p)]
 
 
 _sp = ctypes.POINTER(SpecState)

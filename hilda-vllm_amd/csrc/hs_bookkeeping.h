@@ -47,6 +47,55 @@ __device__ __forceinline__ int ring_at(const hs_spec_state& s, int pos) {
 }
 
 // ---------------------------------------------------------------------------
+// block hash: BlockManager.compute_hash, block_manager.py:36-41
+// ---------------------------------------------------------------------------
+// xxh64 with seed 0 (the xxHash specification, XXH64) of the previous block's
+// hash as 8 little-endian bytes, when there is one (prefix != -1), then n
+// tokens as int64: whole 8-byte words, so no 4-byte or 1-byte tail round.
+constexpr uint64_t kXP1 = 11400714785074694791ull, kXP2 = 14029467366897019727ull;
+constexpr uint64_t kXP3 = 1609587929392839161ull, kXP4 = 9650029242287828579ull;
+constexpr uint64_t kXP5 = 2870177450012600261ull;
+__device__ __forceinline__ uint64_t xxh_rotl(uint64_t x, int r) {
+  return (x << r) | (x >> (64 - r));
+}
+__device__ __forceinline__ uint64_t xxh_round(uint64_t acc, uint64_t in) {
+  return xxh_rotl(acc + in * kXP2, 31) * kXP1;
+}
+__device__ uint64_t block_hash_of(int64_t prefix, const int64_t* toks, int n) {
+  const bool pre = prefix != -1;
+  const int total = n + (pre ? 1 : 0);
+  auto word = [&](int i) -> uint64_t {
+    return pre ? (i == 0 ? (uint64_t)prefix : (uint64_t)toks[i - 1]) : (uint64_t)toks[i];
+  };
+  uint64_t h;
+  int i = 0;
+  if (total >= 4) {
+    uint64_t v1 = kXP1 + kXP2, v2 = kXP2, v3 = 0, v4 = 0ull - kXP1;
+    for (; i + 4 <= total; i += 4) {
+      v1 = xxh_round(v1, word(i));
+      v2 = xxh_round(v2, word(i + 1));
+      v3 = xxh_round(v3, word(i + 2));
+      v4 = xxh_round(v4, word(i + 3));
+    }
+    h = xxh_rotl(v1, 1) + xxh_rotl(v2, 7) + xxh_rotl(v3, 12) + xxh_rotl(v4, 18);
+    h = (h ^ xxh_round(0, v1)) * kXP1 + kXP4;
+    h = (h ^ xxh_round(0, v2)) * kXP1 + kXP4;
+    h = (h ^ xxh_round(0, v3)) * kXP1 + kXP4;
+    h = (h ^ xxh_round(0, v4)) * kXP1 + kXP4;
+  } else {
+    h = kXP5;
+  }
+  h += (uint64_t)total * 8;
+  for (; i < total; ++i) h = xxh_rotl(h ^ xxh_round(0, word(i)), 27) * kXP1 + kXP4;
+  h ^= h >> 33;
+  h *= kXP2;
+  h ^= h >> 29;
+  h *= kXP3;
+  h ^= h >> 32;
+  return h;
+}
+
+// ---------------------------------------------------------------------------
 // pre-allocation: llm_engine.py:111-128
 // ---------------------------------------------------------------------------
 template <int NT>
@@ -108,6 +157,7 @@ __device__ void prealloc_body(const hs_spec_state& s, int gamma, int32_t* eligib
           const int blk = ring_at(s, head + s_off[tid] + k);
           s.block_tables[(int64_t)b * s.W + cur + k] = blk;
           s.ref_count[blk] = 1;
+          if (s.block_hash) s.block_hash[blk] = -1;  // Block.reset
         }
         s.num_seq_blocks[b] = cur + need;
       }
@@ -362,6 +412,54 @@ __device__ void commit_body(const hs_spec_state& s, int gamma, const int64_t* ou
     }
   }
   if (tid == 0) s.free_hdr[1] = count0 + carry;
+  if (!s.block_hash) return;
+
+  // phase 7: rehash (llm_engine.py:182-194) the tables of the sequences that
+  // took part and did not finish: a full block without a hash gets one (the
+  // previous block's hash as prefix), a partial block loses its hash. 7a: one
+  // thread per (sequence, entry) clears and finds each sequence's first full
+  // block without a hash (s_first, over s_nblk's words); 7b: the sequence's
+  // thread hashes from there on, in table order (each hash is the next one's
+  // prefix).
+  int32_t* s_first = w.seq;
+  __syncthreads();
+  for (int b = tid; b < s.B; b += NT) s_first[b] = 0x7fffffff;
+  __syncthreads();
+  const int bs = s.block_size;
+  auto rehashed = [&](int b) {
+    return !(eligible && !eligible[b]) && !s.finished[b];
+  };
+  for (int64_t p = tid; p < (int64_t)s.B * s.W; p += NT) {
+    const int b = (int)(p / s.W), bi = (int)(p % s.W);
+    const int nblk = s.num_seq_blocks[b];
+    if (bi >= nblk || !rehashed(b)) continue;
+    const int blk = s.block_tables[(int64_t)b * s.W + bi];
+    if (blk < 0 || blk >= s.num_blocks) continue;
+    const bool full = bi < nblk - 1 || s.context_lens[b] % bs == 0;
+    const int64_t h = s.block_hash[blk];
+    if (!full && h != -1) s.block_hash[blk] = -1;
+    if (full && h == -1) atomicMin(&s_first[b], bi);
+  }
+  __syncthreads();
+  for (int b = tid; b < s.B; b += NT) {
+    const int f = s_first[b];
+    if (f == 0x7fffffff) continue;
+    const int nblk = s.num_seq_blocks[b];
+    const int len = s.context_lens[b];
+    const int32_t* row = s.block_tables + (int64_t)b * s.W;
+    int64_t prev = f > 0 ? s.block_hash[row[f - 1]] : -1;
+    for (int bi = f; bi < nblk; ++bi) {
+      if (!(bi < nblk - 1 || len % bs == 0)) break;  // the partial last block
+      const int blk = row[bi];
+      int64_t h = s.block_hash[blk];
+      if (h == -1) {
+        if ((int64_t)(bi + 1) * bs > s.T) break;  // tokens past the history
+        h = (int64_t)block_hash_of(prev, s.tokens + (int64_t)b * s.T + (int64_t)bi * bs, bs);
+        s.block_hash[blk] = h;
+      }
+      prev = h;
+    }
+  }
 }
 
 // The commit of a step, then the next step's pre-allocation (into eligible,
@@ -454,7 +552,8 @@ struct B1Pre {
   int tb[4];
   int ring, tblk, ref;
   int64_t hist;
-  int bad;  // lane with an entry out of range
+  int bad;    // lane with an entry out of range
+  int bh[4];  // low words of the table entries' block hashes (state with hashes)
 };
 
 __device__ __forceinline__ void b1_load1(const CommitNext& c, B1Pre& P) {
@@ -500,6 +599,17 @@ __device__ __forceinline__ void b1_load2(const CommitNext& c, B1Pre& P) {
   P.bad = t && !in;
   P.ref = s.ref_count[in ? P.tblk : 0];  // used for lanes below the trim count
   P.hist = s.tokens[(len0 >= 1 && len0 <= s.T) ? len0 - 1 : 0];
+  // the low word of each table entry's hash: -1 has 0xffffffff there, so a hash
+  // whose low word is that reads as none (the rehash then takes the workgroup
+  // path, which reads whole hashes)
+  if (s.block_hash) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int blk = P.tb[q];
+      P.bh[q] = reinterpret_cast<const int32_t*>(
+          s.block_hash)[2 * (int64_t)(blk >= 0 && blk < N ? blk : 0)];
+    }
+  }
 }
 
 // The one-wave path's results for a commit of n tokens, all but the last of
@@ -555,6 +665,19 @@ __device__ void b1_plan(const CommitNext& c, const B1Pre& P, int n, const int64_
   const int needed2 = (len + c.next_gamma + 1 + bs - 1) / bs;
   const int need = needed2 - needed;
   if (need > kB1Take || (need > 0 && needed2 > s.W)) return;
+  // a rehash with work to do (a full block without a hash, a partial one with a
+  // hash: llm_engine.py:182-194) takes the workgroup path
+  if (s.block_hash) {
+    bool work = false;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int bi = lane + 64 * q;
+      const bool full = bi < needed - 1 || len % bs == 0;
+      const bool none = P.bh[q] == -1;
+      if (bi < needed && (full == none)) work = true;
+    }
+    if (__ballot(work) != 0) return;
+  }
   // the tail blocks released (lane e: entry nblk0 - 1 - e)
   const bool trims = lane < ntrim;
   const int tblk = P.tblk, ref = P.ref;
@@ -640,6 +763,7 @@ __device__ bool b1_store(const CommitNext& c, const B1Plan& Q, const int64_t* to
   if (lane < Q.take) {
     s.block_tables[Q.needed + lane] = Q.tk;
     s.ref_count[Q.tk] = 1;
+    if (s.block_hash) s.block_hash[Q.tk] = -1;  // Block.reset
   }
 #pragma unroll
   for (int q = 0; q < 4; ++q) {

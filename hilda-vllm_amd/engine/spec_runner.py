@@ -199,6 +199,7 @@ class SpecRunner:
         for t in tables:
             ref[t] = 1
         st.ref_count.copy_(ref)
+        st.block_hash.fill_(-1)  # the first commit hashes the full prompt blocks
         self.prompts = prompts
         del dev
 
@@ -330,6 +331,7 @@ class SpecRunner:
                                            dtype=torch.int32))
             idx = torch.tensor(blocks, dtype=torch.int64, device=self.device)
             st.ref_count.index_fill_(0, idx, 1)
+            st.block_hash.index_fill_(0, idx, -1)  # Block.reset
             st.block_tables[b, :need] = idx.to(torch.int32)
             st.num_seq_blocks[b] = need
             self._prefill_rows(b, n - 1)

@@ -407,11 +407,13 @@ class SpecStateTensors:
     Fields mirror Sequence / BlockManager (sequence.py:14-132,
     block_manager.py:26-115): context_lens, num_prompt, max_tokens, ignore_eos,
     finished, block_tables [B, W] (-1 padded), num_seq_blocks, tokens [B, T],
-    free_ring [num_blocks] + free_hdr (head, count), ref_count [num_blocks].
+    free_ring [num_blocks] + free_hdr (head, count), ref_count [num_blocks],
+    block_hash [num_blocks] int64 (the blocks' prefix hashes, -1 for none).
     """
 
     FIELDS = ("context_lens", "num_prompt", "max_tokens", "ignore_eos", "finished",
-              "block_tables", "num_seq_blocks", "tokens", "free_ring", "free_hdr", "ref_count")
+              "block_tables", "num_seq_blocks", "tokens", "free_ring", "free_hdr", "ref_count",
+              "block_hash")
 
     def __init__(self, B: int, W: int, T: int, num_blocks: int, block_size: int, eos: int,
                  device):
@@ -429,6 +431,7 @@ class SpecStateTensors:
         self.free_ring = torch.arange(num_blocks, **i32)
         self.free_hdr = torch.tensor([0, num_blocks], **i32)
         self.ref_count = torch.zeros(num_blocks, **i32)
+        self.block_hash = torch.full((num_blocks,), -1, dtype=torch.int64, device=device)
         self.commit_ws = torch.zeros(
             L.lib().hs_spec_commit_workspace_size(B, W, num_blocks), dtype=torch.uint8,
             device=device)

@@ -253,6 +253,14 @@ int hs_store_kvcache(const void* key, int64_t key_stride_tok, int64_t key_stride
 /* token history tokens [B, T] (T must exceed the longest sequence), the     */
 /* free-block deque as a ring free_ring[num_blocks] with free_hdr = {head,    */
 /* count} (pop at head, append at head+count), and ref_count[num_blocks].    */
+/* block_hash (optional, NULL: no hashing): [num_blocks] int64, a block's    */
+/* prefix hash (BlockManager.compute_hash, block_manager.py:36-41: xxh64,    */
+/* seed 0, of the previous block's hash as 8 little-endian bytes, when there */
+/* is one, then the block's tokens as int64) or -1. Pre-allocation resets    */
+/* the blocks it takes to -1 (Block.reset); the commit then rehashes the     */
+/* tables of the sequences that took part and did not finish, as            */
+/* llm_engine.py:182-194 does (full blocks without a hash get one, partial   */
+/* blocks lose theirs). The registry hash_to_block_id stays the host's.      */
 /* All pointers are device pointers; the struct itself lives on the host.    */
 /* ------------------------------------------------------------------------ */
 typedef struct hs_spec_state {
@@ -270,6 +278,7 @@ typedef struct hs_spec_state {
   int32_t B, W, T, num_blocks, block_size;
   int32_t pad;
   int64_t eos;
+  int64_t* block_hash;
 } hs_spec_state;
 
 /* Pre-allocation of blocks for len + gamma + 1 tokens,                      */

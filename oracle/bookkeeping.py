@@ -7,8 +7,8 @@ a deque) of:
   * BlockManager.allocate / deallocate, mini_vllm/engine/block_manager.py:
     35-92 (prefix hashing with xxhash64 as in :36-41);
   * the spec block of LLMEngine.step, mini_vllm/engine/llm_engine.py:
-    pre-allocation :111-128, apply :146-164, trim :170-181 (the rehash at
-    :182-194 is host-side hashing and not part of the device state);
+    pre-allocation :111-128, apply :146-164, trim :170-181 and the rehash of
+    the remaining blocks :182-194 (xxhash64, the reference's own dependency);
   * the verify staging of run_verify, model_runner.py:339-362;
   * the dirty-slot range of cleanup_rejected_kv_slots, model_runner.py:445-464.
 """
@@ -217,4 +217,24 @@ class BookState:
                     if block.ref_count == 0:
                         self.used.discard(block_id)
                         self.free.append(block_id)
+                self.rehash(seq)
         return appended, dirty
+
+    # llm_engine.py:182-194: full blocks without a hash get one (the previous
+    # block's hash as prefix), a partial last block loses its hash
+    def rehash(self, seq):
+        bs = self.block_size
+        for bi, block_id in enumerate(seq.block_table):
+            block = self.blocks[block_id]
+            is_last = bi == len(seq.block_table) - 1
+            full = (not is_last) or (len(seq) % bs == 0)
+            if full and block.hash == -1:
+                token_ids = seq.block(bi, bs)
+                prefix = self.blocks[seq.block_table[bi - 1]].hash if bi > 0 else -1
+                h = self.compute_hash(token_ids, prefix)
+                block.hash = h
+                block.token_ids = token_ids
+                self.hash_to_block_id[h] = block_id
+            elif not full and block.hash != -1:
+                block.hash = -1
+                block.token_ids = []

@@ -4,8 +4,8 @@ Random multi-step runs drive the oracle (oracle/bookkeeping.py, the
 reference's own data structures) and the device state through the same
 pre-allocation, staging and commit steps; after every step the whole device
 state must equal the oracle's: lengths, token histories, block tables, free
-deque contents in order, reference counts, finished flags, staging outputs and
-dirty slots (bit-exact integers).
+deque contents in order, reference counts, finished flags, staging outputs,
+dirty slots and block hashes (bit-exact integers).
 """
 import numpy as np
 import pytest
@@ -39,7 +39,13 @@ def to_device(hv, bm, seqs, W, T, dev):
     st.free_ring.copy_(torch.from_numpy(ring))
     st.free_hdr.copy_(torch.tensor([0, len(bm.free)], dtype=torch.int32))
     st.ref_count.copy_(torch.tensor([b.ref_count for b in bm.blocks], dtype=torch.int32))
+    st.block_hash.copy_(torch.tensor([as_i64(b.hash) for b in bm.blocks], dtype=torch.int64))
     return st
+
+
+def as_i64(h):
+    """A block hash (xxh64 digest, or -1) as the device's int64."""
+    return h - (1 << 64) if h >= (1 << 63) else h
 
 
 def assert_same_state(st, bm, seqs):
@@ -65,6 +71,9 @@ def assert_same_state(st, bm, seqs):
     used = sorted({b for s in seqs for b in s.block_table})
     for b in used:
         assert refs[b] == bm.blocks[b].ref_count, (b, refs[b], bm.blocks[b].ref_count)
+    # every block's hash (xxh64 by the xxhash library in the oracle), free ones included
+    hashes = st.block_hash.cpu().tolist()
+    assert hashes == [as_i64(b.hash) for b in bm.blocks]
 
 
 @pytest.mark.parametrize("seed", range(6))
