@@ -325,7 +325,8 @@ int hs_draft_prepare(const hs_spec_state* state, const int64_t* draft_tokens, in
 /* 0 sat out the step (llm_engine.py:120-121) and take no tokens; NULL means */
 /* every row took part.                                                      */
 /* The workspace must be zero-filled before its first use; every call leaves */
-/* it zero-filled.                                                           */
+/* the counters it reads zero-filled again (its other words are scratch,     */
+/* written before they are read), so it is ready for the next call.          */
 size_t hs_spec_commit_workspace_size(int batch, int table_width, int num_blocks);
 int hs_spec_commit(const hs_spec_state* state, int gamma, const int32_t* num_accepted,
                    const int64_t* out_tokens, const int32_t* out_len, const int32_t* eligible,
