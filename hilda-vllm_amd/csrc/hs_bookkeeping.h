@@ -517,8 +517,9 @@ __device__ void commit_next_body(const CommitNext& c, const int64_t* out_tokens,
 // commit_next_body for one sequence, in one wave
 // ---------------------------------------------------------------------------
 // The common step of a one-sequence state: not finished, eligible, not ending
-// in this step, a table row of at most 256 entries, at most kB1Take blocks to
-// take, staging rows within a wave. The results equal commit_next_body's; the
+// in this step, no rehash work (with block hashes: no block that has just
+// become full, no partial block with a hash), a table row of at most 256
+// entries, at most kB1Take blocks to take, staging rows within a wave. The results equal commit_next_body's; the
 // wave reads the state in two rounds of loads (the state words and the table
 // row; the free-list front, the history token and the reference counts of the
 // tail blocks the commit may release) instead of commit_next_body's chain of
@@ -541,8 +542,9 @@ __device__ __forceinline__ int b1_row_at(const int (&tb)[4], int bi) {
 // i + 64 q, clamped into the row: only entries below the row length are used);
 // b1_load2, from those, the free-list front (lane k: entry head + k), the tail
 // blocks a commit of at least one token may release, last first (lane e: table
-// entry nblk0 - 1 - e), their reference counts and the history token before
-// the appended ones. Every load is unconditional, from a clamped in-range
+// entry nblk0 - 1 - e), their reference counts, the history token before the
+// appended ones and (with block hashes) the low words of the table entries'
+// hashes. Every load is unconditional, from a clamped in-range
 // index where its own one is not needed or not valid, so that nothing waits
 // for it before its use in b1_plan (a conditional load would be waited for
 // where its branch joins). Nothing changes the state between the loads and
